@@ -1,0 +1,285 @@
+"""ctypes binding for the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
+
+The C functions restate the reference's scalar Rust kernels; see the header of
+prism_oracle.c for what pins each one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+KIND_Q8_0 = 8
+KIND_Q2_K = 10
+KIND_Q8_K = 15
+KIND_PQ2 = 142
+KIND_PTQ1 = 143
+
+Q8_SOURCE = 0
+Q8_PINNED = 1
+Q8_PINNED_NATIVE = 2
+
+OK = 0
+ERR_INVALID_INPUT = -1
+ERR_RESOURCE = -2
+ERR_NONFINITE = -3
+ERR_UNSUPPORTED = -5
+
+LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_Q8_K: (256, 292), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28)}
+
+# numpy mirrors of the C structs (tools/ternary/src/lib.rs:27-39; src/kernels.rs:528-535)
+Q8K_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (256,)), ("sums", "<i2", (16,))])
+Q8_DTYPE = np.dtype([("scale", "<f4"), ("sum", "<f4"), ("values", "i1", (32,))])
+assert Q8K_DTYPE.itemsize == 292 and Q8_DTYPE.itemsize == 40
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what} failed with code {code}")
+        self.code = code
+
+
+def build() -> None:
+    """Compile liboracle.so with oracle/Makefile."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        S = ctypes.c_size_t
+        I = ctypes.c_int
+        U = ctypes.c_uint32
+        sig = {
+            "po_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
+            "po_half_to_float_bits": (ctypes.c_uint32, [ctypes.c_uint16]),
+            "po_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
+            "po_round_f16": (ctypes.c_float, [ctypes.c_float]),
+            "po_decode_ptq_trits": (None, [P, P]),
+            "po_pack_ptq": (I, [P, P]),
+            "po_unpack_ptq": (I, [P, P]),
+            "po_quantize_q8k": (I, [P, S, I, P]),
+            "po_quantize_q8_0": (I, [P, S, I, P]),
+            "po_quantize_row": (I, [U, P, S, P, S]),
+            "po_decode_row": (I, [U, S, P, P]),
+            "po_dot_pq2": (I, [P, S, P, I, P]),
+            "po_dot_q8_groups": (I, [U, P, S, P, P]),
+            "po_dot_q8_groups_pinned": (I, [U, P, S, P, P]),
+            "po_dot_q2k": (I, [P, S, P, P]),
+            "po_dot_q8_0": (I, [P, S, P, P]),
+            "po_dot_ptq1_q8k": (I, [P, S, P, P]),
+            "po_packed_dot": (I, [U, S, P, S, P, S, P]),
+            "po_activation_contract": (I, [U, S, I]),
+            "po_matvec": (I, [U, S, S, P, P, I, P, I]),
+            "po_project_q8k": (I, [U, S, S, P, P, I, P, I]),
+            "po_project_q8": (I, [U, S, S, P, P, I, P, I]),
+            "po_vector_exp": (ctypes.c_float, [ctypes.c_float]),
+            "po_swiglu": (None, [P, P, S, I]),
+            "po_ffn": (I, [U, S, S, P, P, P, P, P, I, P, P, I]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(np.frombuffer(bytes(a), dtype=np.uint8) if isinstance(a, (bytes, bytearray)) else a, dtype=np.uint8)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != OK:
+        raise OracleError(rc, what)
+
+
+def half_to_float(h: int) -> float:
+    return lib().po_half_to_float(h)
+
+
+def half_to_float_bits(h: int) -> int:
+    return lib().po_half_to_float_bits(h)
+
+
+def float_to_half(f: float) -> int:
+    return lib().po_float_to_half(f)
+
+
+def decode_ptq_trits(block) -> np.ndarray:
+    b = _u8(block)
+    assert b.size == 28
+    out = np.zeros(128, np.int16)
+    lib().po_decode_ptq_trits(_p(b), _p(out))
+    return out
+
+
+def pack_ptq(pq2) -> bytes:
+    b = _u8(pq2)
+    out = np.zeros(28, np.uint8)
+    _check(lib().po_pack_ptq(_p(b), _p(out)), "pack_ptq")
+    return out.tobytes()
+
+
+def unpack_ptq(ptq) -> bytes:
+    b = _u8(ptq)
+    out = np.zeros(34, np.uint8)
+    _check(lib().po_unpack_ptq(_p(b), _p(out)), "unpack_ptq")
+    return out.tobytes()
+
+
+def quantize_q8k(x, pinned: bool) -> np.ndarray:
+    x = _f32(x)
+    out = np.zeros(x.size // 256, Q8K_DTYPE)
+    _check(lib().po_quantize_q8k(_p(x), x.size, int(pinned), _p(out)), "quantize_q8k")
+    return out
+
+
+def quantize_q8_0(x, contract: int) -> np.ndarray:
+    x = _f32(x)
+    out = np.zeros(x.size // 32, Q8_DTYPE)
+    _check(lib().po_quantize_q8_0(_p(x), x.size, contract, _p(out)), "quantize_q8_0")
+    return out
+
+
+def quantize_row(kind: int, x) -> bytes:
+    x = _f32(x)
+    g, bb = LAYOUT[kind]
+    out = np.zeros(x.size // g * bb, np.uint8)
+    _check(lib().po_quantize_row(kind, _p(x), x.size, _p(out), out.size), "quantize_row")
+    return out.tobytes()
+
+
+def decode_row(kind: int, count: int, data) -> np.ndarray:
+    d = _u8(data)
+    out = np.zeros(count, np.float32)
+    _check(lib().po_decode_row(kind, count, _p(d), _p(out)), "decode_row")
+    return out
+
+
+def _f(fn, *args) -> float:
+    out = np.zeros(1, np.float32)
+    _check(fn(*args, _p(out)), fn.__name__)
+    return out
+
+
+def dot_pq2(row, act: np.ndarray, fused: bool) -> np.float32:
+    r = _u8(row)
+    return _f(lib().po_dot_pq2, _p(r), r.size // 34, _p(act), int(fused))[0]
+
+
+def dot_q8_groups(kind: int, row, act: np.ndarray, pinned: bool = False) -> np.float32:
+    r = _u8(row)
+    bb = 34 if kind == KIND_PQ2 else 28
+    fn = lib().po_dot_q8_groups_pinned if pinned else lib().po_dot_q8_groups
+    return _f(fn, kind, _p(r), r.size // bb, _p(act))[0]
+
+
+def dot_q2k(row, act: np.ndarray) -> np.float32:
+    r = _u8(row)
+    return _f(lib().po_dot_q2k, _p(r), r.size // 84, _p(act))[0]
+
+
+def dot_q8_0(row, act: np.ndarray) -> np.float32:
+    r = _u8(row)
+    return _f(lib().po_dot_q8_0, _p(r), r.size // 34, _p(act))[0]
+
+
+def dot_ptq1_q8k(row, act: np.ndarray) -> np.float32:
+    r = _u8(row)
+    return _f(lib().po_dot_ptq1_q8k, _p(r), r.size // 28, _p(act))[0]
+
+
+def packed_dot(kind: int, count: int, weights, activations) -> np.float32:
+    w = _u8(weights)
+    a = _u8(activations)
+    return _f(lib().po_packed_dot, kind, count, _p(w), w.size, _p(a), a.size)[0]
+
+
+def activation_contract(kind: int, cols: int, pinned: bool) -> int:
+    return lib().po_activation_contract(kind, cols, int(pinned))
+
+
+def matvec(kind: int, cols: int, rows: int, w, x, pinned: bool = False, threads: int = 1) -> np.ndarray:
+    w = _u8(w)
+    x = _f32(x)
+    out = np.zeros(rows, np.float32)
+    _check(lib().po_matvec(kind, cols, rows, _p(w), _p(x), int(pinned), _p(out), threads), "matvec")
+    return out
+
+
+def matvec_rc(kind: int, cols: int, rows: int, w, x, pinned: bool = False, threads: int = 1):
+    """Like matvec but returns (code, output) instead of raising."""
+    w = _u8(w)
+    x = _f32(x)
+    out = np.full(rows, 7.0, np.float32)
+    rc = lib().po_matvec(kind, cols, rows, _p(w), _p(x), int(pinned), _p(out), threads)
+    return rc, out
+
+
+def project_q8k(kind: int, cols: int, rows: int, w, act: np.ndarray, fused: bool, threads: int = 1) -> np.ndarray:
+    w = _u8(w)
+    out = np.zeros(rows, np.float32)
+    _check(lib().po_project_q8k(kind, cols, rows, _p(w), _p(act), int(fused), _p(out), threads), "project_q8k")
+    return out
+
+
+def project_q8(kind: int, cols: int, rows: int, w, act: np.ndarray, pinned: bool, threads: int = 1) -> np.ndarray:
+    w = _u8(w)
+    out = np.zeros(rows, np.float32)
+    _check(lib().po_project_q8(kind, cols, rows, _p(w), _p(act), int(pinned), _p(out), threads), "project_q8")
+    return out
+
+
+def vector_exp(x: float) -> float:
+    return lib().po_vector_exp(x)
+
+
+def swiglu(gate, up, pinned: bool) -> np.ndarray:
+    g = _f32(gate)
+    u = _f32(up).copy()
+    lib().po_swiglu(_p(g), _p(u), g.size, int(pinned))
+    return u
+
+
+def ffn(kind: int, hidden: int, ffn_dim: int, wg, wu, wd, x, residual=None, pinned: bool = False, threads: int = 1):
+    wg, wu, wd = _u8(wg), _u8(wu), _u8(wd)
+    x = _f32(x)
+    out = np.zeros(hidden, np.float32)
+    h = np.zeros(ffn_dim, np.float32)
+    res = _f32(residual) if residual is not None else None
+    rc = lib().po_ffn(kind, hidden, ffn_dim, _p(wg), _p(wu), _p(wd), _p(x), _p(res) if res is not None else None,
+                      int(pinned), _p(out), _p(h), threads)
+    _check(rc, "ffn")
+    return out, h
+
+
+def prefill(kind: int, cols: int, rows: int, w, X, pinned: bool = False, threads: int = 1) -> np.ndarray:
+    """Tiled prefill semantics: each token row equals its own matvec (src/kernels/prefill.rs:829-887)."""
+    X = _f32(X)
+    return np.stack([matvec(kind, cols, rows, w, X[m], pinned, threads) for m in range(X.shape[0])])

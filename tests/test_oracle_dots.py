@@ -1,0 +1,296 @@
+"""Pin the oracle's row dots and matvec to the reference's captures and known answers.
+
+Mirrors src/kernels.rs:5293-5385, tests/kernels.rs:206-309, tests/kquants.rs:15-72,
+tests/upstream_prism/pq2.rs and tests/upstream_prism/codec_assertions.rs:602-1060.
+"""
+
+import numpy as np
+import pytest
+
+import fixtures_util as fx
+
+
+def _bits(v) -> int:
+    return int(np.float32(v).view(np.uint32))
+
+
+def test_pinned_pq2_accumulation_matches_native_binary_capture(oracle):
+    # src/kernels.rs:5293-5329
+    w = bytearray([0xAA] * 68)
+    w[0:2] = (0x3C01).to_bytes(2, "little")
+    w[34:36] = (0x3787).to_bytes(2, "little")
+    act = np.zeros(1, oracle.Q8K_DTYPE)
+    act["scale"] = np.uint32(0x3DA00001).view(np.float32)
+    act["values"][0, :128] = 3
+    act["values"][0, 128:] = -13
+    act["sums"][0, :8] = 48
+    act["sums"][0, 8:] = -208
+    assert _bits(oracle.dot_pq2(bytes(w), act, fused=True)) == 0xC1F90B01
+    assert _bits(oracle.dot_pq2(bytes(w), act, fused=False)) == 0xC1F90B02
+
+
+def test_pinned_ptq1_accumulation_matches_native_binary_capture(oracle):
+    # src/kernels.rs:5331-5385
+    blob = fx.read("swift-ptq1-dot-parity.bin")
+    meta = fx.load_json("swift-ptq1-dot-parity.json")
+    assert fx.sha256(blob) == meta["fixture_sha256"]
+    cur = 0
+    for case in range(2):
+        width = int.from_bytes(blob[cur:cur + 4], "little")
+        expected = int.from_bytes(blob[cur + 4:cur + 8], "little")
+        wb = width // 128 * 28
+        weights = blob[cur + 8: cur + 8 + wb]
+        acts = blob[cur + 8 + wb: cur + 8 + wb + width // 32 * 34]
+        cur += 8 + wb + width // 32 * 34
+        q8 = np.zeros(width // 32, oracle.Q8_DTYPE)
+        for i in range(width // 32):
+            q8[i]["scale"] = oracle.half_to_float(int.from_bytes(acts[34 * i:34 * i + 2], "little"))
+            q8[i]["values"] = np.frombuffer(acts[34 * i + 2:34 * i + 34], np.int8)
+        assert _bits(oracle.dot_q8_groups(oracle.KIND_PTQ1, weights, q8, pinned=True)) == expected
+        src = _bits(oracle.dot_q8_groups(oracle.KIND_PTQ1, weights, q8, pinned=False))
+        assert src != expected
+        assert src == meta["fixtures"][case]["source_bits"]
+        # The byte-level public entry (packed_dot) uses the source order too.
+        assert _bits(oracle.packed_dot(oracle.KIND_PTQ1, width, weights, acts)) == src
+    assert cur == len(blob)
+
+
+def test_pq2_matvec_uses_q8k_ties_even_and_per_half_scales(oracle):
+    # tests/kernels.rs:206-226
+    first = fx.pq2_block(0x3C00, [(1, 2), (2, 2), (3, 2)])
+    second = fx.pq2_block(0x3800, [(0, 0)])
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[2], x[3], x[128], x[255] = 127.0, 0.5, 1.5, 2.5, -1.5, -127.0
+    out = oracle.matvec(oracle.KIND_PQ2, 256, 1, first + second, x)
+    assert out.tolist() == [5.0]
+
+
+def test_pq2_native_symbol_three_zero_scale_and_zero_activations(oracle):
+    # tests/kernels.rs:228-245
+    w = fx.pq2_block(0x3C00, [(0, 3)]) + fx.pq2_block(0, [(0, 3)])
+    assert oracle.decode_row(oracle.KIND_PQ2, 256, w)[0] == 2.0
+    x = np.zeros(256, np.float32)
+    x[0] = -127.0
+    assert oracle.matvec(oracle.KIND_PQ2, 256, 1, w, x).tolist() == [-254.0]
+    assert oracle.matvec(oracle.KIND_PQ2, 256, 1, w, np.zeros(256, np.float32)).tolist() == [0.0]
+
+
+def test_ptq1_matvec_uses_q8_0_round_away_and_32_wide_scales(oracle):
+    # tests/kernels.rs:247-262
+    blk = oracle.pack_ptq(fx.pq2_block(0x4000, [(1, 2), (2, 2), (33, 2)]))
+    x = np.zeros(128, np.float32)
+    x[0], x[1], x[2], x[32], x[33] = 127.0, 0.5, 1.5, 63.5, 0.25
+    assert oracle.matvec(oracle.KIND_PTQ1, 128, 1, blk, x).tolist() == [7.0]
+
+
+def test_ptq1_activation_scales_are_rounded_to_fp16(oracle):
+    # tests/kernels.rs:264-275
+    blk = oracle.pack_ptq(fx.pq2_block(0x3C00, [(0, 2)]))
+    x = np.zeros(128, np.float32)
+    x[0] = 1.0
+    assert oracle.matvec(oracle.KIND_PTQ1, 128, 1, blk, x)[0] == np.float32(0.99993896)
+
+
+def test_pq2_odd_group_rows_use_native_q8_0_fallback(oracle):
+    # tests/kernels.rs:277-307
+    first = fx.pq2_block(0x4000, [(1, 2), (2, 3), (33, 2)])
+    x = np.zeros(128, np.float32)
+    x[0], x[1], x[2], x[32], x[33] = 127.0, 0.5, 1.5, 63.5, 0.25
+    assert oracle.matvec(oracle.KIND_PQ2, 128, 1, first, x).tolist() == [11.0]
+    second = fx.pq2_block(0x3800, [(1, 2), (2, 3), (33, 2)])
+    third = fx.pq2_block(0x3C00, [(1, 2), (2, 3), (33, 2)])
+    w = first + second + third
+    xx = np.concatenate([x, x, x])
+    assert oracle.matvec(oracle.KIND_PQ2, 384, 1, w, xx).tolist() == [19.25]
+    rc, out = oracle.matvec_rc(oracle.KIND_PQ2, 383, 1, w, xx[:383])
+    assert rc != 0 and out.tolist() == [0.0]
+
+
+def test_upstream_pq2_row_shapes_relative_rms(oracle):
+    # tests/upstream_prism/pq2.rs: 15 shapes, reference in f64, threshold 0.05.  The published
+    # worst (0.00678327, tools/prism/upstream/baseline.json:37) was measured on an earlier corpus
+    # (fixture sha 9e9c5b96..., :39), not on this pq2-inputs.bin (sha a37e4e61...), so only the
+    # threshold and this corpus' own worst value (shape K=512, N=16) are asserted.
+    worst = 0.0
+    shapes = fx.pq2_inputs()
+    assert len(shapes) == 15
+    for k, m, n, packed, act in shapes:
+        dec = np.zeros((m, k), np.float64)
+        for i in range(m):
+            for b in range(k // 128):
+                blk = packed[(i * (k // 128) + b) * 34:(i * (k // 128) + b + 1) * 34]
+                sc = np.float64(np.uint16(int.from_bytes(blk[:2], "little")).view(np.float16))
+                codes = np.array([(blk[2 + j // 4] >> (2 * (j % 4))) & 3 for j in range(128)])
+                assert (codes != 3).all()
+                dec[i, b * 128:(b + 1) * 128] = sc * (codes - 1)
+        A = act.reshape(n, k).astype(np.float64)
+        ref = (A @ dec.T).astype(np.float32).astype(np.float64)  # [n, m], rounded to f32 like upstream
+        got = np.stack([oracle.matvec(oracle.KIND_PQ2, k, m, packed, act[j * k:(j + 1) * k]) for j in range(n)])
+        err = np.sqrt(((got.astype(np.float64) - ref) ** 2).sum() / (ref ** 2).sum())
+        assert err < 0.05
+        worst = max(worst, err)
+    assert f"{worst:.7f}" == "0.0067834"
+
+
+def test_q2k_native_decode_and_generic_dot(oracle):
+    # tests/kquants.rs:15-72 restricted to TypeId 10.
+    data = fx.load_json("upstream-kquants-q2k.json")
+    assert len(data["Cases"]) == 5
+    for case in data["Cases"]:
+        count = case["Count"]
+        w = fx.hexbytes(case["OutputHex"])
+        dec = oracle.decode_row(oracle.KIND_Q2_K, count, w)
+        assert dec.tobytes() == fx.hexbytes(case["DecodedHex"]), case["Name"]
+        got = oracle.packed_dot(oracle.KIND_Q2_K, count, w, fx.hexbytes(case["ActivationsHex"]))
+        assert np.float32(got).tobytes() == fx.hexbytes(case["GenericDotHex"]), case["Name"]
+
+
+def test_q2k_dot_matches_unpack_reference_identity(oracle):
+    # src/kernels/kquants.rs:478-532: direct dot == dot via unpack (8-lane integer split).
+    rng = np.random.default_rng(11)
+    nb = 3
+    w = bytearray(rng.integers(0, 256, nb * 84, dtype=np.uint8).tobytes())
+    for b in range(nb):
+        w[b * 84 + 80:b * 84 + 82] = (0x3555).to_bytes(2, "little")
+        w[b * 84 + 82:b * 84 + 84] = (0xB955).to_bytes(2, "little")
+    act = np.zeros(nb, oracle.Q8K_DTYPE)
+    for b in range(nb):
+        v = rng.integers(-127, 128, 256).astype(np.int8)
+        act[b]["values"] = v
+        act[b]["sums"] = v.reshape(16, 16).astype(np.int32).sum(1)
+        act[b]["scale"] = np.float32(0.03125 * (b + 1))
+    # Independent evaluation through unpacking (order of kquants.rs:478-512 for kind 10).
+    total = np.float32(0)
+    for b in range(nb):
+        p = w[b * 84:(b + 1) * 84]
+        q = np.array([(p[16 + i // 128 * 32 + i % 32] >> (2 * (i % 128 // 32))) & 3 for i in range(256)], np.int64)
+        sc = np.array([p[i // 16] & 15 for i in range(256)], np.int64)
+        mn = np.array([p[g] >> 4 for g in range(16)], np.int64)
+        isum = int((sc * q * act[b]["values"].astype(np.int64)).sum())
+        msum = int((act[b]["sums"].astype(np.int64) * mn).sum())
+        d = np.float32(np.uint16(0x3555).view(np.float16))
+        m = np.float32(np.uint16(0xB955).view(np.float16))
+        s = act[b]["scale"]
+        total = np.float32(total + np.float32(np.float32(np.float32(s * d) * np.float32(isum))
+                                              - np.float32(np.float32(s * m) * np.float32(msum))))
+    assert _bits(oracle.dot_q2k(bytes(w), act)) == _bits(total)
+
+
+def test_q8_0_dot_exact_when_every_product_is_representable(oracle):
+    # No fixture pins the Q8_0 x Q8_0 value: with power-of-two scales every rounding step is
+    # exact, so the ordered chain must equal the exact f64 sum (catches dropped terms, index
+    # or operand mix-ups, wrong scale pairing).
+    rng = np.random.default_rng(5)
+    nb = 64
+    w = bytearray()
+    wsc = []
+    # Scales in {1,2,4} x {1,2} and |codes| <= 15 keep every partial sum an integer below 2^24.
+    for b in range(nb):
+        e = int(rng.integers(0, 3))
+        h = int(np.float16(2.0 ** e).view(np.uint16))
+        wsc.append(2.0 ** e)
+        w += h.to_bytes(2, "little") + rng.integers(-15, 16, 32).astype(np.int8).tobytes()
+    act = np.zeros(nb, oracle.Q8_DTYPE)
+    for b in range(nb):
+        act[b]["scale"] = np.float32(2.0 ** int(rng.integers(0, 2)))
+        act[b]["values"] = rng.integers(-15, 16, 32).astype(np.int8)
+    exact = 0.0
+    for b in range(nb):
+        codes = np.frombuffer(bytes(w[b * 34 + 2:b * 34 + 34]), np.int8).astype(np.int64)
+        exact += wsc[b] * float(act[b]["scale"]) * int((codes * act[b]["values"].astype(np.int64)).sum())
+    assert float(oracle.dot_q8_0(bytes(w), act)) == exact
+
+
+def test_ptq1_q8k_dot_equals_pq2_unfused_on_lossless_codec(oracle):
+    rng = np.random.default_rng(9)
+    nb = 8
+    pq2 = b""
+    for _ in range(nb):
+        blk = bytearray(fx.pq2_block(int(np.float16(abs(rng.normal(0, 0.02))).view(np.uint16)), []))
+        codes = rng.integers(0, 3, 128)
+        for i, c in enumerate(codes):
+            blk[2 + i // 4] = (blk[2 + i // 4] & ~(3 << (2 * (i % 4))) & 0xFF) | (int(c) << (2 * (i % 4)))
+        pq2 += bytes(blk)
+    ptq = b"".join(oracle.pack_ptq(pq2[34 * i:34 * (i + 1)]) for i in range(nb))
+    act = oracle.quantize_q8k(rng.standard_normal(nb * 128).astype(np.float32), pinned=False)
+    assert _bits(oracle.dot_ptq1_q8k(ptq, act)) == _bits(oracle.dot_pq2(pq2, act, fused=False))
+
+
+def _lcg99_cases(trials):
+    # tests/upstream_prism/codec_assertions.rs:612-620,763-790 (LCG, trial generation).
+    state = [99]
+
+    def nxt():
+        state[0] = (state[0] * 1103515245 + 12345) & 0xFFFFFFFF
+        return (state[0] >> 16) & 0xFFFF
+
+    cases = []
+    for _ in range(trials):
+        packed = bytes(nxt() & 0xFF for _ in range(26))
+        scale = np.float32(0.01) + np.float32(nxt() % 1000) / np.float32(50000.0)
+        acts = []
+        for _ in range(4):
+            s = np.float32(0.005) + np.float32(nxt() % 1000) / np.float32(80000.0)
+            vals = np.array([(nxt() % 255) - 127 for _ in range(32)], np.int8)
+            acts.append((s, vals))
+        cases.append((packed, scale, acts))
+    return cases
+
+
+def test_upstream_lcg99_ptq1_integer_group_sums(oracle):
+    # The integer group sums under the decoder equal the upstream scalar-trit transcription.
+    for packed, _, acts in _lcg99_cases(500):
+        blk = packed + (0x3C00).to_bytes(2, "little")
+        trits = oracle.decode_ptq_trits(blk).astype(np.int64)
+        for g in range(4):
+            # scalar_trit element map (codec_assertions.rs:647-663)
+            ref = 0
+            for e in range(32):
+                el = 32 * g + e
+                if el < 80:
+                    byte, digit = packed[el & 15], el >> 4
+                elif el < 120:
+                    byte, digit = packed[16 + ((el - 80) & 7)], (el - 80) >> 3
+                else:
+                    byte, digit = packed[24 + ((el - 120) & 1)], (el - 120) >> 1
+                v = byte
+                for i in range(4):
+                    if i < digit:
+                        v = (v * 3) & 0xFF
+                ref += (((v * 3) >> 8) - 1) * int(acts[g][1][e])
+            assert ref == int((trits[32 * g:32 * g + 32] * acts[g][1].astype(np.int64)).sum())
+        # Isolate each group through the oracle's float path with unit scales.
+        for g in range(4):
+            q8 = np.zeros(4, oracle.Q8_DTYPE)
+            q8[g]["scale"] = 1.0
+            q8[g]["values"] = acts[g][1]
+            got = oracle.dot_q8_groups(oracle.KIND_PTQ1, blk, q8)
+            assert got == np.float32(int((trits[32 * g:32 * g + 32] * acts[g][1].astype(np.int64)).sum()))
+
+
+def test_matvec_threads_do_not_change_bits(oracle):
+    rng = np.random.default_rng(1)
+    rows, cols = 37, 512
+    for kind in (oracle.KIND_PQ2, oracle.KIND_PTQ1, oracle.KIND_Q8_0):
+        w = oracle.quantize_row(kind, rng.normal(0, 0.02, rows * cols).astype(np.float32))
+        x = rng.standard_normal(cols).astype(np.float32)
+        for pinned in (False, True):
+            a = oracle.matvec(kind, cols, rows, w, x, pinned, threads=1)
+            b = oracle.matvec(kind, cols, rows, w, x, pinned, threads=5)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_nonfinite_weight_scale_is_an_error_and_clears_output(oracle):
+    rng = np.random.default_rng(2)
+    w = bytearray(oracle.quantize_row(oracle.KIND_PTQ1, rng.normal(0, 0.02, 4 * 256).astype(np.float32)))
+    w[28 * 5 + 26:28 * 5 + 28] = (0x7C00).to_bytes(2, "little")
+    rc, out = oracle.matvec_rc(oracle.KIND_PTQ1, 256, 4, bytes(w), rng.standard_normal(256).astype(np.float32))
+    assert rc == oracle.ERR_NONFINITE and not out.any()
+
+
+def test_vector_exp_close_to_expf(oracle):
+    rng = np.random.default_rng(4)
+    xs = rng.uniform(-80, 80, 4000).astype(np.float32)
+    got = np.array([oracle.vector_exp(float(x)) for x in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64))
+    assert np.max(np.abs(got / ref - 1)) < 4e-7
