@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X packed quantized matmul path.
+
+Headline workload (one "step"): the Qwen35-shaped dense FFN decode step at batch 1
+with Q2_K weights -- quantize x (f32 -> Q8_K), gate and up matvecs 2048->6144,
+SwiGLU, quantize h, down matvec 6144->2048 -- in the public (source) arithmetic
+contract.  Weights are rotated over >= 1 GiB of distinct device copies so every
+step streams them from HBM; steps are captured in HIP graphs on the library's
+stream and timed with HIP events on that stream.
+
+Prints ONE JSON line on rank 0 (the only rank: this build runs on one GPU).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "prism-inference_amd"))
+
+import numpy as np  # noqa: E402
+
+import hiprt  # noqa: E402
+import prism_hip as ph  # noqa: E402
+import synth  # noqa: E402
+
+METRIC = "packed matvec HBM GB/s (% peak); prefill int8 TOPS; decode tokens/s at batch 1"
+PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+PEAK_I8 = 5.0e15  # MI355X dense int8 MFMA, ops/s
+ROTATE_BYTES = 1 << 30
+HIDDEN, FFN = 2048, 6144
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def chunk_for(k: int) -> int:
+    for c in (8, 4, 2, 1):
+        if k % c == 0:
+            return c
+    return 1
+
+
+class Rotation:
+    """`copies` device copies of one packed tensor (identical bytes, distinct addresses)."""
+
+    def __init__(self, ctx: ph.Context, kind: int, rows: int, cols: int, data: np.ndarray, copies: int):
+        self.nbytes = data.size
+        self.buf = hiprt.DeviceBuffer(self.nbytes * copies)
+        self.buf.upload(data)
+        for i in range(1, copies):
+            hiprt.copy_d2d(self.buf.ptr + i * self.nbytes, self.buf.ptr, self.nbytes)
+        self.ids = [ctx.weight_device(kind, cols, rows, _View(self.buf.ptr + i * self.nbytes, self.nbytes))
+                    for i in range(copies)]
+
+
+class _View:
+    def __init__(self, ptr: int, nbytes: int):
+        self.ptr, self.nbytes = ptr, nbytes
+
+    def data_ptr(self):
+        return self.ptr
+
+    def numel(self):
+        return self.nbytes
+
+    def element_size(self):
+        return 1
+
+
+def ffn_step_bytes() -> int:
+    """Algorithmic HBM bytes of one FFN step: packed weights at native block size, the f32
+    input, gate/up/down f32 outputs and the f32 SwiGLU vector read by its quantizer."""
+    w = 3 * FFN * HIDDEN // 256 * 84
+    return w + 4 * HIDDEN + 2 * 4 * FFN + 4 * FFN + 4 * HIDDEN
+
+
+def bench_ffn(ctx: ph.Context, steps: int, warmup: int):
+    per_copy = 3 * FFN * HIDDEN // 256 * 84
+    chunk = chunk_for(steps)
+    copies = math.ceil(ROTATE_BYTES / per_copy / chunk) * chunk
+    log(f"ffn: {copies} weight copies ({copies * per_copy / 2**30:.2f} GiB), graph chunk {chunk}")
+    g = Rotation(ctx, ph.KIND_Q2_K, FFN, HIDDEN, synth.q2k_weights(FFN, HIDDEN, seed=101), copies)
+    u = Rotation(ctx, ph.KIND_Q2_K, FFN, HIDDEN, synth.q2k_weights(FFN, HIDDEN, seed=102), copies)
+    d = Rotation(ctx, ph.KIND_Q2_K, HIDDEN, FFN, synth.q2k_weights(HIDDEN, FFN, seed=103), copies)
+    x = hiprt.DeviceBuffer.from_numpy(synth.activations(HIDDEN, seed=104))
+    out = hiprt.DeviceBuffer(4 * HIDDEN)
+    stream = ctx.stream()
+    ctx.ffn_chain_device(g.ids[0], u.ids[0], d.ids[0], x, None, False, out)  # allocates scratch
+    assert ctx.sync() == 0
+
+    def enqueue(j):
+        def run():
+            for i in range(chunk):
+                c = j * chunk + i
+                ctx.ffn_chain_device(g.ids[c], u.ids[c], d.ids[c], x, None, False, out, None, stream)
+        return run
+
+    graphs = [hiprt.Graph(stream, enqueue(j)) for j in range(copies // chunk)]
+    for i in range(max(warmup // chunk, len(graphs))):
+        graphs[i % len(graphs)].launch()
+    assert ctx.sync() == 0
+    e0, e1 = hiprt.Event(), hiprt.Event()
+    hiprt.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps // chunk):
+        graphs[i % len(graphs)].launch()
+    e1.record(stream)
+    e1.synchronize()
+    hiprt.synchronize()
+    wall = time.perf_counter() - t0
+    rc = ctx.sync()
+    assert rc == 0, ctx.last_error
+    y = out.to_numpy(np.float32)
+    assert np.isfinite(y).all()
+    ms = e0.elapsed_ms(e1) / steps
+    return ms, wall / steps * 1e3, copies
+
+
+def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launches: int = 200):
+    """Per-launch duration of one matvec kernel (prepared Q8_K/Q8_0 activation already in HBM),
+    bracketed by HIP events on the library stream, weights rotated over >= 1 GiB."""
+    w = synth.weights(kind, rows, cols, seed=7)
+    copies = max(2, math.ceil(ROTATE_BYTES / w.size))
+    rot = Rotation(ctx, kind, rows, cols, w, copies)
+    contract = 0 if kind in (ph.KIND_Q2_K,) or (kind == ph.KIND_PQ2 and cols % 256 == 0) else 1
+    x = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=8))
+    if contract == 0:
+        act = hiprt.DeviceBuffer(cols // 256 * 292)
+        ctx.quantize_q8k_device(x, cols, 1, False, act)
+        path, act_bytes = ph.PATH_Q8K, cols // 256 * 292
+    else:
+        act = hiprt.DeviceBuffer(cols // 32 * 40)
+        ctx.quantize_q8_device(x, cols, 1, ph.Q8_SOURCE, act)
+        path, act_bytes = ph.PATH_Q8, cols // 32 * 34
+    out = hiprt.DeviceBuffer(4 * rows)
+    stream = ctx.stream()
+    for i in range(min(copies, 8)):
+        ctx.project_device(rot.ids[i], path, act, 1, False, out, stream)
+    assert ctx.sync() == 0
+    evs = [hiprt.Event() for _ in range(2 * launches)]
+    for i in range(launches):
+        evs[2 * i].record(stream)
+        ctx.project_device(rot.ids[i % copies], path, act, 1, False, out, stream)
+        evs[2 * i + 1].record(stream)
+    evs[-1].synchronize()
+    assert ctx.sync() == 0
+    durs = np.array([evs[2 * i].elapsed_ms(evs[2 * i + 1]) for i in range(launches)])
+    nbytes = w.size + act_bytes + 4 * rows
+    t = float(np.median(durs)) * 1e-3
+    for wid in rot.ids:
+        ctx.release(wid)
+    rot.buf.free()
+    return {"kind": kind, "rows": rows, "cols": cols, "bytes_per_launch": int(nbytes),
+            "avg_us": float(durs.mean()) * 1e3, "median_us": t * 1e6, "GBps": nbytes / t / 1e9,
+            "frac_hbm": nbytes / t / PEAK_HBM}
+
+
+def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 3):
+    w = synth.ptq1_weights(rows, cols, seed=9)
+    wbuf = hiprt.DeviceBuffer.from_numpy(w)
+    wid = ctx.weight_device(ph.KIND_PTQ1, cols, rows, _View(wbuf.ptr, w.size))
+    X = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=10, tokens=M))
+    out = hiprt.DeviceBuffer(4 * rows * M)
+    stream = ctx.stream()
+    ctx.project_device(wid, ph.PATH_F32, X, M, False, out, stream)
+    assert ctx.sync() == 0
+    e0, e1 = hiprt.Event(), hiprt.Event()
+    e0.record(stream)
+    for _ in range(reps):
+        ctx.project_device(wid, ph.PATH_F32, X, M, False, out, stream)
+    e1.record(stream)
+    e1.synchronize()
+    assert ctx.sync() == 0
+    t = e0.elapsed_ms(e1) / reps * 1e-3
+    ops = 2.0 * M * rows * cols
+    ctx.release(wid)
+    return {"M": M, "ms": t * 1e3, "TOPS": ops / t / 1e12, "frac_int8_peak": ops / t / PEAK_I8}
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    wg = synth.q2k_weights(FFN, HIDDEN, seed=101)
+    wu = synth.q2k_weights(FFN, HIDDEN, seed=102)
+    wd = synth.q2k_weights(HIDDEN, FFN, seed=103)
+    x = synth.activations(HIDDEN, seed=104)
+    oracle.ffn(oracle.KIND_Q2_K, HIDDEN, FFN, wg, wu, wd, x, None, False, threads)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        oracle.ffn(oracle.KIND_Q2_K, HIDDEN, FFN, wg, wu, wd, x, None, False, threads)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": ffn_step_bytes() / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": dt * 1e3,
+            "sample": f"{n} FFN decode steps (Q2_K 2048->6144->2048, source contract) on one weight copy, "
+                      f"scalar C restatement, rows split over {threads} threads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path would shard by output rows, see DESIGN.md)", file=sys.stderr)
+        return 2
+    if hiprt.device_count() < 1:
+        print("bench.py: no HIP device", file=sys.stderr)
+        return 1
+    ctx = ph.Context(0)
+    log(ctx.identity)
+    ms, wall_ms, copies = bench_ffn(ctx, args.steps, args.warmup)
+    nbytes = ffn_step_bytes()
+    value = nbytes / (ms * 1e-3) / 1e9
+    log(f"ffn step: {ms * 1e3:.2f} us/step (wall {wall_ms * 1e3:.2f}), {value:.1f} GB/s")
+    kern = bench_matvec_kernel(ctx, ph.KIND_Q2_K, FFN, HIDDEN)
+    log(f"q2k matvec {FFN}x{HIDDEN}: {kern['median_us']:.2f} us, {kern['GBps']:.1f} GB/s")
+    extras = {}
+    if not args.no_extras:
+        extras["matvec"] = []
+        for kind, rows, cols in [(ph.KIND_PTQ1, 2048, 2048), (ph.KIND_PQ2, 2048, 2048), (ph.KIND_Q2_K, HIDDEN, FFN),
+                                 (ph.KIND_PTQ1, 12288, 4096), (ph.KIND_Q2_K, 12288, 4096), (ph.KIND_Q8_0, 12288, 4096),
+                                 (ph.KIND_PTQ1, 151936, 4096), (ph.KIND_Q2_K, 151936, 4096),
+                                 (ph.KIND_Q8_0, 151936, 4096)]:
+            r = bench_matvec_kernel(ctx, kind, rows, cols, launches=100)
+            log(f"matvec kind={kind} {rows}x{cols}: {r['median_us']:.2f} us, {r['GBps']:.1f} GB/s")
+            extras["matvec"].append(r)
+        extras["prefill_ptq1_6144x2048"] = []
+        for M in (128, 512):
+            r = bench_prefill(ctx, M)
+            log(f"prefill M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
+            extras["prefill_ptq1_6144x2048"].append(r)
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int2xint8->int32, f32 chain",
+        "data": "synthetic (seeded; weights rotated over distinct device copies)",
+        "config": {"workload": "Qwen35-shaped dense FFN decode step, batch 1: Q2_K gate/up 2048->6144, "
+                               "SwiGLU, down 6144->2048, source contract",
+                   "hidden": HIDDEN, "ffn": FFN, "format": "Q2_K x Q8_K", "weight_copies": copies,
+                   "bytes_per_step": nbytes, "frac_hbm_peak": round(value * 1e9 / PEAK_HBM, 4),
+                   "tokens_per_s": round(1e3 / ms, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(kern["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(kern["frac_hbm"], 4), "traffic": None,
+                     "kernel": f"Q2_K x Q8_K matvec {FFN}x{HIDDEN}", "bytes_per_launch": kern["bytes_per_launch"],
+                     "avg_launch_us": round(kern["median_us"], 3)},
+        "cpu_baseline": cpu,
+    }
+    if extras:
+        line["extras"] = extras
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

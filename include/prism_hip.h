@@ -1,0 +1,186 @@
+/*
+ * prism_hip.h -- C ABI of the MI355X (gfx950) packed quantized matmul path.
+ *
+ * This library replaces the device side of the reference's projection-executor
+ * boundary (trait Pq2ProjectionExecutor, src/kernels/projection.rs:16-355) and the
+ * GGML MUL_MAT backend op for packed weights (src/backend/ops.rs:444-466).  Every
+ * entry point takes plain pointers and sizes; no C++ or torch type crosses it.
+ *
+ * Conventions (mirroring src/kernels/projection.rs:8-15,46-57,797-806,859-866):
+ *  - Calls are synchronous unless the name ends in _device; host pointers are only
+ *    read during the call and never retained.
+ *  - Every projection writes exactly rows*tokens f32 values.  On any error the
+ *    output is zero-filled (the reference clears its Vec) and a negative code is
+ *    returned; nothing is replayed on the CPU.
+ *  - A non-finite output, weight scale or activation is PRISM_ERR_NONFINITE.
+ *  - A device fault latches: every later supports*() returns 0 and calls fail
+ *    with PRISM_ERR_DEVICE_FAULT (tools/adreno-vulkan/src/executor.rs:1507-1530).
+ *  - One context per host thread; contexts create no host threads.  Streams are
+ *    internal (default priority).
+ *
+ * Arithmetic contract: results are bit-identical to the reference's scalar CPU
+ * kernels for the same prepared activations and the same source/pinned choice
+ * (src/kernels.rs:941-1248, src/kernels/kquants.rs:162-197,346-430).  SwiGLU
+ * outputs follow libm exp and are compared with a tolerance.
+ */
+#ifndef PRISM_HIP_H
+#define PRISM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Tensor kinds: GGML type ids (src/kernels.rs:75-87, src/backend.rs:99-141). */
+#define PRISM_KIND_Q8_0 8u
+#define PRISM_KIND_Q2_K 10u
+#define PRISM_KIND_PQ2 142u
+#define PRISM_KIND_PTQ1 143u
+
+/* Error codes. */
+#define PRISM_OK 0
+#define PRISM_ERR_INVALID_INPUT (-1)
+#define PRISM_ERR_RESOURCE (-2)
+#define PRISM_ERR_NONFINITE (-3)
+#define PRISM_ERR_DEVICE_FAULT (-4)
+#define PRISM_ERR_UNSUPPORTED (-5)
+
+/* Activation paths for prism_hip_supports (project / project_q8 / project_f32). */
+#define PRISM_PATH_Q8K 0
+#define PRISM_PATH_Q8 1
+#define PRISM_PATH_F32 2
+
+/* Q8_0 activation contracts (src/kernels.rs:552-617). */
+#define PRISM_Q8_SOURCE 0        /* public matvec: d=max/127, round half away     */
+#define PRISM_Q8_PINNED 1        /* pinned generic: same d, ties to even           */
+#define PRISM_Q8_PINNED_NATIVE 2 /* pinned PTQ1: d=max*0x3c010204, inv=127/max, RNE */
+
+/* Q8_K activation block, tools/ternary/src/lib.rs:27-39 (#[repr(C)], 292 bytes). */
+typedef struct prism_q8k_block {
+    float scale;
+    int8_t values[256];
+    int16_t sums[16];
+} prism_q8k_block;
+
+/* Prepared Q8_0 activation block, src/kernels.rs:528-535 (in-memory form, 40 bytes). */
+typedef struct prism_q8_block {
+    float scale; /* binary16-rounded */
+    float sum;   /* binary16-rounded scaled code sum (unused by these dots) */
+    int8_t values[32];
+} prism_q8_block;
+
+typedef struct prism_hip_ctx prism_hip_ctx;
+typedef int64_t prism_weight_id; /* >= 1 on success, negative error code otherwise */
+
+/* ---- lifecycle -------------------------------------------------------------- */
+
+/* Opens device `device` (HIP ordinal).  max_resident_bytes bounds the weights the
+ * context may own (0 = no bound).  flags must be 0.  Returns NULL on failure. */
+prism_hip_ctx *prism_hip_create(int device, uint64_t max_resident_bytes, uint32_t flags);
+void prism_hip_destroy(prism_hip_ctx *ctx);
+/* Pq2ProjectionExecutor::identity (src/kernels/projection.rs:17-18). */
+const char *prism_hip_identity(const prism_hip_ctx *ctx);
+/* Message of the last failed call on this context ("" if none). */
+const char *prism_hip_last_error(const prism_hip_ctx *ctx);
+/* 1 once a device fault has latched. */
+int prism_hip_faulted(const prism_hip_ctx *ctx);
+/* Pq2ProjectionExecutor::operation_capacity (projection.rs:20-28): 0 when faulted,
+ * UINT64_MAX otherwise (submissions are not rationed). */
+uint64_t prism_hip_operation_capacity(const prism_hip_ctx *ctx);
+/* Pq2ProjectionExecutor::operation_count (projection.rs:30-36): cols*rows for a
+ * supported projection, -1 (unknown) otherwise. */
+int64_t prism_hip_operation_count(const prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows);
+
+/* ---- eligibility -------------------------------------------------------------- */
+
+/* supports / supports_q8 / supports_f32 (projection.rs:38-44,59-66,89-92), decided
+ * from geometry alone before any launch.  Returns 1 or 0. */
+int prism_hip_supports(const prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows, int path);
+
+/* ---- weights ------------------------------------------------------------------ */
+
+/* Upload-or-lookup of a packed row-major tensor [rows][cols] (bytes must equal
+ * rows*cols/QK*block_bytes, src/kernels.rs:121-142).  `key` identifies the tensor
+ * (the reference keys device copies by tensor identity,
+ * tools/adreno-vulkan/src/executor.rs:686-760): acquiring an existing key with the
+ * same geometry returns its id without copying. */
+prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *ctx, uint64_t key, uint32_t kind, uint64_t cols,
+                                         uint64_t rows, const void *host, uint64_t bytes);
+/* Registers caller-owned device memory holding the packed tensor (no copy).  The
+ * caller keeps it alive until release. */
+prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows,
+                                             const void *device_ptr, uint64_t bytes);
+int prism_hip_weight_release(prism_hip_ctx *ctx, prism_weight_id w);
+int prism_hip_weight_release_all(prism_hip_ctx *ctx);
+uint64_t prism_hip_resident_bytes(const prism_hip_ctx *ctx);
+
+/* ---- executor projections (host pointers, synchronous) ------------------------ */
+
+/* Pq2ProjectionExecutor::project (projection.rs:46-57): PQ2 with cols%256==0 and
+ * prepared Q8_K codes, `fused` selects mul_add accumulation.  Also accepts Q2_K
+ * (kquants::dot) and PTQ1 (dot_ptq1_q8k, src/kernels.rs:999-1037).  act holds
+ * tokens*cols/256 blocks; out receives [tokens][rows]. */
+int prism_hip_project_q8k(prism_hip_ctx *ctx, prism_weight_id w, const prism_q8k_block *act, uint64_t nblocks,
+                          uint32_t tokens, int fused, float *out);
+/* Pq2ProjectionExecutor::project_q8 (projection.rs:68-87): PTQ1 or odd-group PQ2
+ * with prepared Q8_0 codes; `pinned` selects the four-lane FMA order for PTQ1.
+ * Also accepts Q8_0 weights (dot_legacy, src/kernels.rs:1204-1248). */
+int prism_hip_project_q8(prism_hip_ctx *ctx, prism_weight_id w, const prism_q8_block *act, uint64_t nblocks,
+                         uint32_t tokens, int pinned, float *out);
+/* Pq2ProjectionExecutor::project_f32 (projection.rs:94-107) generalised to every
+ * kind: quantizes on the GPU with the activation contract matvec_into would use
+ * (ActivationContract::for_tensor, src/kernels.rs:1663-1673) then projects.
+ * x holds tokens*cols floats. */
+int prism_hip_project_f32(prism_hip_ctx *ctx, prism_weight_id w, const float *x, uint32_t tokens, int pinned,
+                          float *out);
+/* project_f32_group (projection.rs:115-130): n (1..8) siblings sharing one input. */
+int prism_hip_project_f32_group(prism_hip_ctx *ctx, const prism_weight_id *ws, uint32_t n, const float *x,
+                                int pinned, float *const *outs);
+/* project_f32_ffn_swiglu (projection.rs:206-222): out[ffn] = SwiGLU(gate(x), up(x)). */
+int prism_hip_ffn_swiglu(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
+                         float *out);
+/* project_f32_ffn_chain (projection.rs:250-287) without the Hadamard transform:
+ * out[hidden] = down(SwiGLU(gate(x), up(x))) (+ residual if non-NULL).  Accepts
+ * PQ2 and Q2_K triples. */
+int prism_hip_ffn_chain(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                        const float *x, const float *residual, int pinned, float *out);
+/* Tiled prefill (src/kernels/prefill.rs:200-725): X[tokens][cols] -> out[tokens][rows];
+ * every token row is bit-identical to its own project_f32. */
+int prism_hip_prefill(prism_hip_ctx *ctx, prism_weight_id w, const float *x, uint32_t tokens, int pinned,
+                      float *out);
+
+/* ---- backend op ----------------------------------------------------------------- */
+
+/* ggml_mul_mat for a packed A (src/backend/call.rs:808-823, ops.rs:444-466): for each
+ * of the ncols activation columns b[j][cols], out[j][rows] = kernels::matvec(A, b[j])
+ * (public source contract). */
+int prism_hip_mul_mat(prism_hip_ctx *ctx, prism_weight_id a, const float *b, uint32_t ncols, float *out);
+
+/* ---- device-pointer dispatch (stream ordered; check with prism_hip_sync) -------- */
+
+/* Quantize tokens*cols device floats into device Q8_K blocks / Q8_0 blocks. */
+int prism_hip_quantize_q8k_device(prism_hip_ctx *ctx, const float *x, uint64_t cols, uint32_t tokens, int pinned,
+                                  prism_q8k_block *out, void *stream);
+int prism_hip_quantize_q8_device(prism_hip_ctx *ctx, const float *x, uint64_t cols, uint32_t tokens, int contract,
+                                 prism_q8_block *out, void *stream);
+/* Project device activations (path = PRISM_PATH_Q8K or PRISM_PATH_Q8 blocks, or
+ * PRISM_PATH_F32 floats quantized on the fly) into device out[tokens][rows]. */
+int prism_hip_project_device(prism_hip_ctx *ctx, prism_weight_id w, int path, const void *act, uint32_t tokens,
+                             int pinned, float *out, void *stream);
+/* FFN chain on device pointers (h may be NULL; when set it receives the SwiGLU vector). */
+int prism_hip_ffn_chain_device(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                               const float *x, const float *residual, int pinned, float *out, float *h,
+                               void *stream);
+/* Waits for `stream` (NULL = the context stream) and reports any error the
+ * device-side checks raised since the last sync (non-finite values, scale
+ * overflow).  Clears the device error flag. */
+int prism_hip_sync(prism_hip_ctx *ctx, void *stream);
+/* The context's internal stream (a hipStream_t), for ordering caller work. */
+void *prism_hip_stream(prism_hip_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

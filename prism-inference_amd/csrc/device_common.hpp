@@ -1,0 +1,79 @@
+// device_common.hpp -- gfx950 device helpers shared by the packed-matvec kernels.
+//
+// Exactness rules for everything in this directory:
+//  * compiled without -ffast-math; f32 denormals and correctly rounded division
+//    stay on (hipcc defaults), contraction is disabled (-ffp-contract=off) and
+//    __builtin_fmaf appears only where the reference uses mul_add;
+//  * integer block dots are exact int32 (v_dot4_i32_i8), in any order;
+//  * the binary32 scale/accumulate chain of each output row runs serially in
+//    block order in one lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace prism {
+
+// Kinds (src/kernels.rs:75-87).
+constexpr uint32_t kQ8_0 = 8, kQ2_K = 10, kPQ2 = 142, kPTQ1 = 143;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Q8_K / Q8_0 activation blocks (tools/ternary/src/lib.rs:27-39, src/kernels.rs:528-535).
+struct Q8KBlock {
+    float scale;
+    int8_t values[256];
+    int16_t sums[16];
+};
+struct Q8Block {
+    float scale;
+    float sum;
+    int8_t values[32];
+};
+static_assert(sizeof(Q8KBlock) == 292, "Q8_K layout");
+static_assert(sizeof(Q8Block) == 40, "Q8_0 layout");
+
+__device__ __forceinline__ bool finite(float v) { return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u; }
+
+// Exact binary16 -> binary32 (v_cvt_f32_f16 is exact, subnormals included).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+// binary32 -> binary16 -> binary32 with ties to even (src/kernels.rs:2824-2830).
+__device__ __forceinline__ float round_f16(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// Bytes [lo.b2, lo.b3, hi.b0, hi.b1]: a dword starting two bytes into `lo`.
+__device__ __forceinline__ uint32_t align2(uint32_t hi, uint32_t lo) { return __builtin_amdgcn_alignbyte(hi, lo, 2); }
+
+// Raw buffer resource over [base, base+bytes): loads past the end return zero,
+// so partial tiles can never fault.  Word 3 is the gfx9 raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ u32x3 bload3(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b96(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ u32x2 bload2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ uint32_t bload1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+}
+
+__device__ __forceinline__ void raise_error(int *flag, int bits) {
+    if (flag) __hip_atomic_fetch_or(flag, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace prism

@@ -1,0 +1,617 @@
+// runtime.cpp -- context, weight residency, dispatch and the extern "C" ABI of
+// libprism_hip.so (declared in include/prism_hip.h).
+//
+// The executor semantics follow the reference's projection boundary
+// (src/kernels/projection.rs): eligibility is decided from geometry before any
+// launch, outputs are complete and finite or the call fails with the output
+// zero-filled, nothing is replayed elsewhere, and a device fault latches the
+// context as unsupported (tools/adreno-vulkan/src/executor.rs:1507-1530).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/prism_hip.h"
+#include "kernels.hpp"
+
+using namespace prism;
+
+namespace {
+
+struct Weight {
+    uint64_t key = 0;
+    uint32_t kind = 0;
+    uint64_t cols = 0, rows = 0, row_bytes = 0, bytes = 0;
+    void *dev = nullptr;
+    bool owned = false;
+};
+
+// Grow-only device scratch buffer.
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+bool layout(uint32_t kind, uint64_t *group, uint64_t *block) {
+    switch (kind) {
+    case PRISM_KIND_Q8_0: *group = 32; *block = 34; return true;
+    case PRISM_KIND_Q2_K: *group = 256; *block = 84; return true;
+    case PRISM_KIND_PQ2: *group = 128; *block = 34; return true;
+    case PRISM_KIND_PTQ1: *group = 128; *block = 28; return true;
+    default: return false;
+    }
+}
+
+// ActivationContract::for_tensor (src/kernels.rs:1663-1673): 0 = Q8_K, 1 = Q8_0, 2 = pinned PTQ1 Q8_0.
+int contract_for(uint32_t kind, uint64_t cols, int pinned) {
+    if (kind == PRISM_KIND_PTQ1 && pinned) return 2;
+    if (kind == PRISM_KIND_Q2_K) return 0;
+    if (kind == PRISM_KIND_PQ2 && cols % 256 == 0) return 0;
+    return 1;
+}
+
+}  // namespace
+
+struct prism_hip_ctx {
+    int device = 0;
+    uint64_t max_resident = 0, resident = 0;
+    hipStream_t stream = nullptr;
+    std::string identity, last_error;
+    bool faulted = false;
+    std::map<int64_t, Weight> weights;
+    std::map<uint64_t, int64_t> by_key;
+    int64_t next_id = 1;
+    int *err = nullptr;  // device error flag
+    DevBuf x, act, act2, out, gate, up, h, res;
+};
+
+namespace {
+
+int fail(prism_hip_ctx *c, int code, const std::string &msg) {
+    if (c) c->last_error = msg;
+    return code;
+}
+
+// Maps a HIP failure to the latched device-fault state.
+int hip_fail(prism_hip_ctx *c, hipError_t e, const char *what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return fail(c, PRISM_ERR_RESOURCE, m);
+    c->faulted = true;
+    return fail(c, PRISM_ERR_DEVICE_FAULT, m);
+}
+
+#define HIP_OR_FAIL(ctx, call)                                 \
+    do {                                                       \
+        hipError_t e_ = (call);                                \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+    } while (0)
+
+int ensure(prism_hip_ctx *c, DevBuf &b, size_t bytes) {
+    if (bytes <= b.cap) return PRISM_OK;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    size_t n = bytes < 4096 ? 4096 : bytes;
+    hipError_t e = hipMalloc(&b.p, n);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(scratch)");
+    b.cap = n;
+    return PRISM_OK;
+}
+
+int check_ready(prism_hip_ctx *c) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
+    return PRISM_OK;
+}
+
+const Weight *find(prism_hip_ctx *c, prism_weight_id w) {
+    auto it = c->weights.find(w);
+    return it == c->weights.end() ? nullptr : &it->second;
+}
+
+// Reads and clears the device error flag after the stream drained.
+int drain(prism_hip_ctx *c, hipStream_t s) {
+    HIP_OR_FAIL(c, hipStreamSynchronize(s));
+    int flag = 0;
+    HIP_OR_FAIL(c, hipMemcpy(&flag, c->err, sizeof(int), hipMemcpyDeviceToHost));
+    if (flag) {
+        if (launch_fill_i32(c->err, 0, 1, s)) return hip_fail(c, hipGetLastError(), "reset error flag");
+        HIP_OR_FAIL(c, hipStreamSynchronize(s));
+        if (flag & kErrInput) return fail(c, PRISM_ERR_NONFINITE, "non-finite activation input");
+        if (flag & kErrQuantRange) return fail(c, PRISM_ERR_NONFINITE, "activation quantization scale overflow");
+        return fail(c, PRISM_ERR_NONFINITE, "non-finite value in projection output");
+    }
+    return PRISM_OK;
+}
+
+int quantize(prism_hip_ctx *c, int contract, const float *x, uint64_t cols, uint32_t tokens, int pinned, void *out,
+             hipStream_t s) {
+    int rc = contract == 0 ? launch_quantize_q8k(x, cols, tokens, pinned, out, c->err, s)
+                           : launch_quantize_q8_0(x, cols, tokens, contract == 2 ? PRISM_Q8_PINNED_NATIVE
+                                                                                : (pinned ? PRISM_Q8_PINNED
+                                                                                          : PRISM_Q8_SOURCE),
+                                                  out, c->err, s);
+    if (rc) return hip_fail(c, hipGetLastError(), "quantize launch");
+    return PRISM_OK;
+}
+
+size_t act_bytes(int contract, uint64_t cols, uint32_t tokens) {
+    return contract == 0 ? sizeof(prism_q8k_block) * ((cols + 255) / 256) * tokens
+                         : sizeof(prism_q8_block) * (cols / 32) * tokens;
+}
+
+int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
+           float *out, hipStream_t s) {
+    MatvecArgs a;
+    a.kind = w.kind;
+    a.cols = w.cols;
+    a.rows = w.rows;
+    a.row_bytes = w.row_bytes;
+    a.w = static_cast<const uint8_t *>(w.dev);
+    a.act = act;
+    a.act_format = act_format;
+    a.tokens = tokens;
+    a.pinned = pinned;
+    a.out = out;
+    a.err = c->err;
+    a.stream = s;
+    int rc = launch_matvec(a);
+    if (rc == -2) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported matvec geometry");
+    if (rc) return hip_fail(c, hipGetLastError(), "matvec launch");
+    return PRISM_OK;
+}
+
+// Quantize device floats with the contract matvec_into would use, then project.
+int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
+                    DevBuf &scratch, hipStream_t s) {
+    const int contract = contract_for(w.kind, w.cols, pinned);
+    int rc = ensure(c, scratch, act_bytes(contract, w.cols, tokens));
+    if (rc) return rc;
+    rc = quantize(c, contract, x, w.cols, tokens, pinned, scratch.p, s);
+    if (rc) return rc;
+    return matvec(c, w, contract == 0 ? kActQ8K : kActQ8, scratch.p, tokens, pinned, out, s);
+}
+
+bool eligible(uint32_t kind, uint64_t cols, uint64_t rows, int path) {
+    uint64_t g, b;
+    if (!layout(kind, &g, &b) || cols == 0 || rows == 0 || cols % g) return false;
+    if (rows > 0xffffffffull || cols > 0xffffffffull) return false;
+    switch (path) {
+    case PRISM_PATH_Q8K:
+        if (kind == PRISM_KIND_PQ2) return cols % 256 == 0;
+        return kind == PRISM_KIND_Q2_K || kind == PRISM_KIND_PTQ1;
+    case PRISM_PATH_Q8: return kind == PRISM_KIND_PTQ1 || kind == PRISM_KIND_PQ2 || kind == PRISM_KIND_Q8_0;
+    case PRISM_PATH_F32: return true;
+    default: return false;
+    }
+}
+
+void zero(float *p, size_t n) {
+    if (p) std::memset(p, 0, sizeof(float) * n);
+}
+
+// Shared front half of the synchronous host-pointer projections.
+int prepare_weight(prism_hip_ctx *c, prism_weight_id wid, int path, const Weight **out) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    const Weight *w = find(c, wid);
+    if (!w) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
+    if (!eligible(w->kind, w->cols, w->rows, path))
+        return fail(c, PRISM_ERR_UNSUPPORTED, "projection not supported for this tensor");
+    *out = w;
+    return PRISM_OK;
+}
+
+int finish(prism_hip_ctx *c, float *host_out, const float *dev_out, size_t n) {
+    hipError_t e = hipMemcpyAsync(host_out, dev_out, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "copy output");
+    return drain(c, c->stream);
+}
+
+int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Weight *d, const float *x,
+                   const float *residual, int pinned, float *out, float *h, hipStream_t s) {
+    // Shapes: gate/up [ffn][hidden], down [hidden][ffn] (projection.rs:571-597).
+    if (g.cols != u.cols || g.rows != u.rows || g.kind != u.kind)
+        return fail(c, PRISM_ERR_INVALID_INPUT, "gate/up geometry differs");
+    if (d && (d->cols != g.rows || d->rows != g.cols))
+        return fail(c, PRISM_ERR_INVALID_INPUT, "down geometry does not match gate/up");
+    int rc = ensure(c, c->gate, sizeof(float) * g.rows);
+    if (!rc) rc = ensure(c, c->up, sizeof(float) * g.rows);
+    if (rc) return rc;
+    const int contract = contract_for(g.kind, g.cols, pinned);
+    rc = ensure(c, c->act, act_bytes(contract, g.cols, 1));
+    if (!rc) rc = quantize(c, contract, x, g.cols, 1, pinned, c->act.p, s);
+    if (!rc) rc = matvec(c, g, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->gate.p), s);
+    if (!rc) rc = matvec(c, u, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->up.p), s);
+    if (rc) return rc;
+    float *hv = h;
+    if (!hv) {
+        rc = ensure(c, c->h, sizeof(float) * g.rows);
+        if (rc) return rc;
+        hv = static_cast<float *>(c->h.p);
+    }
+    if (launch_swiglu(static_cast<float *>(c->gate.p), static_cast<float *>(c->up.p), hv, g.rows, 1, pinned, c->err, s))
+        return hip_fail(c, hipGetLastError(), "swiglu launch");
+    if (!d) return PRISM_OK;
+    rc = project_f32_dev(c, *d, hv, 1, pinned, out, c->act2, s);
+    if (rc) return rc;
+    if (residual && launch_add_residual(out, residual, d->rows, c->err, s))
+        return hip_fail(c, hipGetLastError(), "residual launch");
+    return PRISM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+prism_hip_ctx *prism_hip_create(int device, uint64_t max_resident_bytes, uint32_t flags) {
+    if (flags != 0) return nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return nullptr;
+    if (hipSetDevice(device) != hipSuccess) return nullptr;
+    auto *c = new prism_hip_ctx();
+    c->device = device;
+    c->max_resident = max_resident_bytes;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess || hipStreamCreate(&c->stream) != hipSuccess ||
+        hipMalloc(&c->err, sizeof(int)) != hipSuccess || hipMemset(c->err, 0, sizeof(int)) != hipSuccess) {
+        delete c;
+        return nullptr;
+    }
+    char buf[256];
+    std::snprintf(buf, sizeof buf, "prism-hip/%s/%d-cu/exact-scalar-order", prop.gcnArchName, prop.multiProcessorCount);
+    c->identity = buf;
+    return c;
+}
+
+void prism_hip_destroy(prism_hip_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    prism_hip_weight_release_all(c);
+    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res})
+        if (b->p) (void)hipFree(b->p);
+    if (c->err) (void)hipFree(c->err);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char *prism_hip_identity(const prism_hip_ctx *c) { return c ? c->identity.c_str() : ""; }
+const char *prism_hip_last_error(const prism_hip_ctx *c) { return c ? c->last_error.c_str() : "null context"; }
+int prism_hip_faulted(const prism_hip_ctx *c) { return c ? (c->faulted ? 1 : 0) : 1; }
+uint64_t prism_hip_operation_capacity(const prism_hip_ctx *c) { return (!c || c->faulted) ? 0 : UINT64_MAX; }
+
+int64_t prism_hip_operation_count(const prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows) {
+    if (!c || c->faulted) return -1;
+    if (!eligible(kind, cols, rows, PRISM_PATH_F32)) return -1;
+    return static_cast<int64_t>(cols * rows);
+}
+
+int prism_hip_supports(const prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows, int path) {
+    if (!c || c->faulted) return 0;
+    return eligible(kind, cols, rows, path) ? 1 : 0;
+}
+
+static prism_weight_id add_weight(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
+                                  uint64_t bytes, bool owned, void *dev) {
+    Weight w;
+    w.key = key;
+    w.kind = kind;
+    w.cols = cols;
+    w.rows = rows;
+    uint64_t g, b;
+    layout(kind, &g, &b);
+    w.row_bytes = cols / g * b;
+    w.bytes = bytes;
+    w.dev = dev;
+    w.owned = owned;
+    const int64_t id = c->next_id++;
+    c->weights[id] = w;
+    if (owned) {
+        c->resident += bytes;
+        c->by_key[key] = id;
+    }
+    return id;
+}
+
+static int check_geometry(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows, uint64_t bytes) {
+    uint64_t g, b;
+    if (!layout(kind, &g, &b)) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported tensor kind");
+    if (cols == 0 || rows == 0 || cols % g) return fail(c, PRISM_ERR_INVALID_INPUT, "incomplete blocks");
+    if (rows > 0xffffffffull || cols > 0xffffffffull) return fail(c, PRISM_ERR_INVALID_INPUT, "extent overflow");
+    if (cols / g * b * rows != bytes) return fail(c, PRISM_ERR_INVALID_INPUT, "byte extent mismatch");
+    return PRISM_OK;
+}
+
+prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
+                                         const void *host, uint64_t bytes) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!host) return fail(c, PRISM_ERR_INVALID_INPUT, "null weight bytes");
+    rc = check_geometry(c, kind, cols, rows, bytes);
+    if (rc) return rc;
+    auto k = c->by_key.find(key);
+    if (k != c->by_key.end()) {
+        const Weight *w = find(c, k->second);
+        if (w && w->kind == kind && w->cols == cols && w->rows == rows) return k->second;
+        return fail(c, PRISM_ERR_INVALID_INPUT, "key already bound to a different tensor");
+    }
+    if (c->max_resident && c->resident + bytes > c->max_resident)
+        return fail(c, PRISM_ERR_RESOURCE, "resident weight budget exceeded");
+    void *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, bytes);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(weights)");
+    e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(c, e, "upload weights");
+    }
+    return add_weight(c, key, kind, cols, rows, bytes, true, dev);
+}
+
+prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,
+                                             const void *dev, uint64_t bytes) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!dev) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    rc = check_geometry(c, kind, cols, rows, bytes);
+    if (rc) return rc;
+    return add_weight(c, 0, kind, cols, rows, bytes, false, const_cast<void *>(dev));
+}
+
+int prism_hip_weight_release(prism_hip_ctx *c, prism_weight_id id) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    auto it = c->weights.find(id);
+    if (it == c->weights.end()) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
+    if (it->second.owned) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(it->second.dev);
+        c->resident -= it->second.bytes;
+        c->by_key.erase(it->second.key);
+    }
+    c->weights.erase(it);
+    return PRISM_OK;
+}
+
+int prism_hip_weight_release_all(prism_hip_ctx *c) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    (void)hipStreamSynchronize(c->stream);
+    for (auto &kv : c->weights)
+        if (kv.second.owned) (void)hipFree(kv.second.dev);
+    c->weights.clear();
+    c->by_key.clear();
+    c->resident = 0;
+    return PRISM_OK;
+}
+
+uint64_t prism_hip_resident_bytes(const prism_hip_ctx *c) { return c ? c->resident : 0; }
+
+int prism_hip_project_q8k(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k_block *act, uint64_t nblocks,
+                          uint32_t tokens, int fused, float *out) {
+    const Weight *w = nullptr;
+    int rc = prepare_weight(c, wid, PRISM_PATH_Q8K, &w);
+    if (rc) {
+        if (c && w) zero(out, w->rows * tokens);
+        return rc;
+    }
+    const size_t n = w->rows * tokens;
+    if (!act || !out || tokens == 0 || nblocks != (w->cols + 255) / 256 * tokens) {
+        zero(out, n);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_K activation extent mismatch");
+    }
+    const size_t ab = sizeof(prism_q8k_block) * nblocks;
+    rc = ensure(c, c->act, ab);
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * n);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(c->act.p, act, ab, hipMemcpyHostToDevice, c->stream);
+        rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
+    }
+    if (!rc) rc = matvec(c, *w, kActQ8K, c->act.p, tokens, fused, static_cast<float *>(c->out.p), c->stream);
+    if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), n);
+    if (rc) zero(out, n);
+    return rc;
+}
+
+int prism_hip_project_q8(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_block *act, uint64_t nblocks,
+                         uint32_t tokens, int pinned, float *out) {
+    const Weight *w = nullptr;
+    int rc = prepare_weight(c, wid, PRISM_PATH_Q8, &w);
+    if (rc) return rc;
+    const size_t n = w->rows * tokens;
+    if (!act || !out || tokens == 0 || nblocks != w->cols / 32 * tokens) {
+        zero(out, n);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_0 activation extent mismatch");
+    }
+    const size_t ab = sizeof(prism_q8_block) * nblocks;
+    rc = ensure(c, c->act, ab);
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * n);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(c->act.p, act, ab, hipMemcpyHostToDevice, c->stream);
+        rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
+    }
+    if (!rc) rc = matvec(c, *w, kActQ8, c->act.p, tokens, pinned, static_cast<float *>(c->out.p), c->stream);
+    if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), n);
+    if (rc) zero(out, n);
+    return rc;
+}
+
+static int project_f32_host(prism_hip_ctx *c, prism_weight_id wid, const float *x, uint32_t tokens, int pinned,
+                            float *out) {
+    const Weight *w = nullptr;
+    int rc = prepare_weight(c, wid, PRISM_PATH_F32, &w);
+    if (rc) return rc;
+    const size_t n = w->rows * tokens;
+    if (!x || !out || tokens == 0) {
+        zero(out, n);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
+    }
+    rc = ensure(c, c->x, sizeof(float) * w->cols * tokens);
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * n);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * w->cols * tokens, hipMemcpyHostToDevice, c->stream);
+        rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
+    }
+    if (!rc)
+        rc = project_f32_dev(c, *w, static_cast<float *>(c->x.p), tokens, pinned, static_cast<float *>(c->out.p),
+                             c->act, c->stream);
+    if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), n);
+    if (rc) zero(out, n);
+    return rc;
+}
+
+int prism_hip_project_f32(prism_hip_ctx *c, prism_weight_id w, const float *x, uint32_t tokens, int pinned,
+                          float *out) {
+    return project_f32_host(c, w, x, tokens, pinned, out);
+}
+
+int prism_hip_prefill(prism_hip_ctx *c, prism_weight_id w, const float *x, uint32_t tokens, int pinned, float *out) {
+    return project_f32_host(c, w, x, tokens, pinned, out);
+}
+
+int prism_hip_mul_mat(prism_hip_ctx *c, prism_weight_id a, const float *b, uint32_t ncols, float *out) {
+    return project_f32_host(c, a, b, ncols, 0, out);
+}
+
+int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, int pinned,
+                                float *const *outs) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!ws || !outs || !x || n == 0 || n > 8) return fail(c, PRISM_ERR_INVALID_INPUT, "bad projection group");
+    const Weight *w[8];
+    for (uint32_t i = 0; i < n; ++i) {
+        w[i] = find(c, ws[i]);
+        if (!w[i] || !outs[i]) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id in group");
+        if (w[i]->cols != w[0]->cols ||
+            contract_for(w[i]->kind, w[i]->cols, pinned) != contract_for(w[0]->kind, w[0]->cols, pinned))
+            return fail(c, PRISM_ERR_INVALID_INPUT, "group members do not share an activation contract");
+    }
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n; ++i) total += w[i]->rows;
+    const int contract = contract_for(w[0]->kind, w[0]->cols, pinned);
+    rc = ensure(c, c->x, sizeof(float) * w[0]->cols);
+    if (!rc) rc = ensure(c, c->act, act_bytes(contract, w[0]->cols, 1));
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * total);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * w[0]->cols, hipMemcpyHostToDevice, c->stream);
+        rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
+    }
+    if (!rc) rc = quantize(c, contract, static_cast<float *>(c->x.p), w[0]->cols, 1, pinned, c->act.p, c->stream);
+    uint64_t off = 0;
+    for (uint32_t i = 0; i < n && !rc; ++i) {
+        rc = matvec(c, *w[i], contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned,
+                    static_cast<float *>(c->out.p) + off, c->stream);
+        off += w[i]->rows;
+    }
+    off = 0;
+    for (uint32_t i = 0; i < n && !rc; ++i) {
+        hipError_t e = hipMemcpyAsync(outs[i], static_cast<float *>(c->out.p) + off, sizeof(float) * w[i]->rows,
+                                      hipMemcpyDeviceToHost, c->stream);
+        if (e != hipSuccess) rc = hip_fail(c, e, "copy group output");
+        off += w[i]->rows;
+    }
+    if (!rc) rc = drain(c, c->stream);
+    if (rc)
+        for (uint32_t i = 0; i < n; ++i)
+            if (w[i]) zero(outs[i], w[i]->rows);
+    return rc;
+}
+
+static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did, const float *x,
+                    const float *residual, int pinned, float *out) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
+    if (!g || !u || (did && !d)) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
+    const uint64_t nout = d ? d->rows : g->rows;
+    if (!x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
+    const bool kind_ok = (g->kind == PRISM_KIND_PQ2 || g->kind == PRISM_KIND_Q2_K || g->kind == PRISM_KIND_PTQ1 ||
+                          g->kind == PRISM_KIND_Q8_0) &&
+                         (!d || d->kind == g->kind);
+    if (!kind_ok) {
+        zero(out, nout);
+        return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind for gate, up and down");
+    }
+    rc = ensure(c, c->x, sizeof(float) * g->cols);
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * nout);
+    if (!rc && residual) rc = ensure(c, c->res, sizeof(float) * nout);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * g->cols, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess && residual)
+            e = hipMemcpyAsync(c->res.p, residual, sizeof(float) * nout, hipMemcpyHostToDevice, c->stream);
+        rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
+    }
+    if (!rc) {
+        float *o = static_cast<float *>(c->out.p);
+        rc = ffn_chain_impl(c, *g, *u, d, static_cast<float *>(c->x.p), residual ? static_cast<float *>(c->res.p) : nullptr,
+                            pinned, d ? o : nullptr, d ? nullptr : o, c->stream);
+    }
+    if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), nout);
+    if (rc) zero(out, nout);
+    return rc;
+}
+
+int prism_hip_ffn_swiglu(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
+                         float *out) {
+    return ffn_host(c, gate, up, 0, x, nullptr, pinned, out);
+}
+
+int prism_hip_ffn_chain(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                        const float *x, const float *residual, int pinned, float *out) {
+    if (down == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "down projection required");
+    return ffn_host(c, gate, up, down, x, residual, pinned, out);
+}
+
+int prism_hip_quantize_q8k_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int pinned,
+                                  prism_q8k_block *out, void *stream) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!x || !out || cols == 0 || cols % 256) return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_K needs cols % 256 == 0");
+    return quantize(c, 0, x, cols, tokens, pinned, out, stream ? static_cast<hipStream_t>(stream) : c->stream);
+}
+
+int prism_hip_quantize_q8_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int contract,
+                                 prism_q8_block *out, void *stream) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!x || !out || cols == 0 || cols % 32 || contract < 0 || contract > 2)
+        return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_0 needs cols % 32 == 0 and a known contract");
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    if (launch_quantize_q8_0(x, cols, tokens, contract, out, c->err, s)) return hip_fail(c, hipGetLastError(), "quantize");
+    return PRISM_OK;
+}
+
+int prism_hip_project_device(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act, uint32_t tokens,
+                             int pinned, float *out, void *stream) {
+    const Weight *w = nullptr;
+    int rc = prepare_weight(c, wid, path, &w);
+    if (rc) return rc;
+    if (!act || !out || tokens == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    if (path == PRISM_PATH_F32)
+        return project_f32_dev(c, *w, static_cast<const float *>(act), tokens, pinned, out, c->act, s);
+    return matvec(c, *w, path == PRISM_PATH_Q8K ? kActQ8K : kActQ8, act, tokens, pinned, out, s);
+}
+
+int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
+                               const float *x, const float *residual, int pinned, float *out, float *h,
+                               void *stream) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    const Weight *g = find(c, gid), *u = find(c, uid), *d = find(c, did);
+    if (!g || !u || !d || !x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
+    if (d->kind != g->kind) return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind");
+    return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, stream ? static_cast<hipStream_t>(stream) : c->stream);
+}
+
+int prism_hip_sync(prism_hip_ctx *c, void *stream) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
+    return drain(c, stream ? static_cast<hipStream_t>(stream) : c->stream);
+}
+
+void *prism_hip_stream(prism_hip_ctx *c) { return c ? static_cast<void *>(c->stream) : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,273 @@
+"""ctypes binding of libprism_hip.so (include/prism_hip.h).
+
+The library is the product; this module only marshals numpy arrays and torch
+device tensors across its C ABI.  Importing it never falls back to anything: if
+the shared library is missing or fails to load, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import itertools
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libprism_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "prism_hip.h")
+
+KIND_Q8_0 = 8
+KIND_Q2_K = 10
+KIND_PQ2 = 142
+KIND_PTQ1 = 143
+LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28)}
+
+OK = 0
+ERR_INVALID_INPUT = -1
+ERR_RESOURCE = -2
+ERR_NONFINITE = -3
+ERR_DEVICE_FAULT = -4
+ERR_UNSUPPORTED = -5
+
+PATH_Q8K = 0
+PATH_Q8 = 1
+PATH_F32 = 2
+
+Q8_SOURCE = 0
+Q8_PINNED = 1
+Q8_PINNED_NATIVE = 2
+
+Q8K_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (256,)), ("sums", "<i2", (16,))])
+Q8_DTYPE = np.dtype([("scale", "<f4"), ("sum", "<f4"), ("values", "i1", (32,))])
+
+
+class PrismError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"prism_hip error {code}: {message}")
+        self.code = code
+
+
+def header_symbols() -> list[str]:
+    """Every prism_hip_* function declared in include/prism_hip.h."""
+    with open(HEADER) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(prism_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+_lib = None
+# Keys for weights registered without an explicit tensor identity: never reused.
+_fresh_keys = itertools.count(1 << 62)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with prism-inference_amd/build.py")
+    L = ctypes.CDLL(LIB_PATH)
+    P, U64, U32, I, I64 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_int64
+    sig = {
+        "prism_hip_create": (P, [I, U64, U32]),
+        "prism_hip_destroy": (None, [P]),
+        "prism_hip_identity": (ctypes.c_char_p, [P]),
+        "prism_hip_last_error": (ctypes.c_char_p, [P]),
+        "prism_hip_faulted": (I, [P]),
+        "prism_hip_operation_capacity": (U64, [P]),
+        "prism_hip_operation_count": (I64, [P, U32, U64, U64]),
+        "prism_hip_supports": (I, [P, U32, U64, U64, I]),
+        "prism_hip_weight_acquire": (I64, [P, U64, U32, U64, U64, P, U64]),
+        "prism_hip_weight_wrap_device": (I64, [P, U32, U64, U64, P, U64]),
+        "prism_hip_weight_release": (I, [P, I64]),
+        "prism_hip_weight_release_all": (I, [P]),
+        "prism_hip_resident_bytes": (U64, [P]),
+        "prism_hip_project_q8k": (I, [P, I64, P, U64, U32, I, P]),
+        "prism_hip_project_q8": (I, [P, I64, P, U64, U32, I, P]),
+        "prism_hip_project_f32": (I, [P, I64, P, U32, I, P]),
+        "prism_hip_project_f32_group": (I, [P, P, U32, P, I, P]),
+        "prism_hip_ffn_swiglu": (I, [P, I64, I64, P, I, P]),
+        "prism_hip_ffn_chain": (I, [P, I64, I64, I64, P, P, I, P]),
+        "prism_hip_prefill": (I, [P, I64, P, U32, I, P]),
+        "prism_hip_mul_mat": (I, [P, I64, P, U32, P]),
+        "prism_hip_quantize_q8k_device": (I, [P, P, U64, U32, I, P, P]),
+        "prism_hip_quantize_q8_device": (I, [P, P, U64, U32, I, P, P]),
+        "prism_hip_project_device": (I, [P, I64, I, P, U32, I, P, P]),
+        "prism_hip_ffn_chain_device": (I, [P, I64, I64, I64, P, P, I, P, P, P]),
+        "prism_hip_sync": (I, [P, P]),
+        "prism_hip_stream": (P, [P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):  # torch tensor
+        return ctypes.c_void_p(a.data_ptr())
+    assert a.flags["C_CONTIGUOUS"], "arrays must be C contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Context:
+    """One prism_hip context (one per host thread), mirroring an installed executor."""
+
+    def __init__(self, device: int = 0, max_resident_bytes: int = 0):
+        self._h = lib().prism_hip_create(device, max_resident_bytes, 0)
+        if not self._h:
+            raise RuntimeError(f"prism_hip_create({device}) failed")
+
+    def close(self):
+        if self._h:
+            lib().prism_hip_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- plumbing --
+    def _check(self, rc: int):
+        if rc != OK:
+            raise PrismError(rc, lib().prism_hip_last_error(self._h).decode())
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def identity(self) -> str:
+        return lib().prism_hip_identity(self._h).decode()
+
+    @property
+    def last_error(self) -> str:
+        return lib().prism_hip_last_error(self._h).decode()
+
+    @property
+    def faulted(self) -> bool:
+        return bool(lib().prism_hip_faulted(self._h))
+
+    def operation_capacity(self) -> int:
+        return lib().prism_hip_operation_capacity(self._h)
+
+    def operation_count(self, kind: int, cols: int, rows: int) -> int:
+        return lib().prism_hip_operation_count(self._h, kind, cols, rows)
+
+    def supports(self, kind: int, cols: int, rows: int, path: int) -> bool:
+        return bool(lib().prism_hip_supports(self._h, kind, cols, rows, path))
+
+    def stream(self) -> int:
+        return lib().prism_hip_stream(self._h)
+
+    # -- weights --
+    def weight(self, kind: int, cols: int, rows: int, data, key: int | None = None) -> int:
+        buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data,
+                                   dtype=np.uint8)
+        key = next(_fresh_keys) if key is None else key
+        wid = lib().prism_hip_weight_acquire(self._h, key & 0xFFFFFFFFFFFFFFFF, kind, cols, rows, _ptr(buf), buf.size)
+        if wid < 0:
+            self._check(int(wid))
+        return int(wid)
+
+    def weight_device(self, kind: int, cols: int, rows: int, tensor) -> int:
+        nbytes = tensor.numel() * tensor.element_size()
+        wid = lib().prism_hip_weight_wrap_device(self._h, kind, cols, rows, _ptr(tensor), nbytes)
+        if wid < 0:
+            self._check(int(wid))
+        return int(wid)
+
+    def release(self, wid: int):
+        self._check(lib().prism_hip_weight_release(self._h, wid))
+
+    def release_all(self):
+        self._check(lib().prism_hip_weight_release_all(self._h))
+
+    def resident_bytes(self) -> int:
+        return lib().prism_hip_resident_bytes(self._h)
+
+    # -- synchronous host projections; return (code, out) when check=False --
+    def _run(self, rc: int, out, check: bool):
+        if check:
+            self._check(rc)
+            return out
+        return rc, out
+
+    def project_q8k(self, wid: int, rows: int, act: np.ndarray, tokens: int = 1, fused: bool = False, check=True):
+        out = np.full(rows * tokens, 7.0, np.float32)
+        rc = lib().prism_hip_project_q8k(self._h, wid, _ptr(act), act.size, tokens, int(fused), _ptr(out))
+        return self._run(rc, out.reshape(tokens, rows) if tokens > 1 else out, check)
+
+    def project_q8(self, wid: int, rows: int, act: np.ndarray, tokens: int = 1, pinned: bool = False, check=True):
+        out = np.full(rows * tokens, 7.0, np.float32)
+        rc = lib().prism_hip_project_q8(self._h, wid, _ptr(act), act.size, tokens, int(pinned), _ptr(out))
+        return self._run(rc, out.reshape(tokens, rows) if tokens > 1 else out, check)
+
+    def project_f32(self, wid: int, rows: int, x, tokens: int = 1, pinned: bool = False, check=True):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.full(rows * tokens, 7.0, np.float32)
+        rc = lib().prism_hip_project_f32(self._h, wid, _ptr(x), tokens, int(pinned), _ptr(out))
+        return self._run(rc, out.reshape(tokens, rows) if tokens > 1 else out, check)
+
+    def prefill(self, wid: int, rows: int, X, pinned: bool = False, check=True):
+        X = np.ascontiguousarray(X, np.float32)
+        out = np.full(X.shape[0] * rows, 7.0, np.float32)
+        rc = lib().prism_hip_prefill(self._h, wid, _ptr(X), X.shape[0], int(pinned), _ptr(out))
+        return self._run(rc, out.reshape(X.shape[0], rows), check)
+
+    def mul_mat(self, wid: int, rows: int, B, check=True):
+        B = np.ascontiguousarray(B, np.float32)
+        out = np.full(B.shape[0] * rows, 7.0, np.float32)
+        rc = lib().prism_hip_mul_mat(self._h, wid, _ptr(B), B.shape[0], _ptr(out))
+        return self._run(rc, out.reshape(B.shape[0], rows), check)
+
+    def project_f32_group(self, wids, rows_list, x, pinned: bool = False, check=True):
+        x = np.ascontiguousarray(x, np.float32)
+        outs = [np.full(r, 7.0, np.float32) for r in rows_list]
+        ids = np.array(wids, np.int64)
+        ptrs = (ctypes.c_void_p * len(outs))(*[o.ctypes.data for o in outs])
+        rc = lib().prism_hip_project_f32_group(self._h, _ptr(ids), len(outs), _ptr(x), int(pinned), ptrs)
+        return self._run(rc, outs, check)
+
+    def ffn_swiglu(self, g: int, u: int, ffn: int, x, pinned: bool = False, check=True):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.full(ffn, 7.0, np.float32)
+        rc = lib().prism_hip_ffn_swiglu(self._h, g, u, _ptr(x), int(pinned), _ptr(out))
+        return self._run(rc, out, check)
+
+    def ffn_chain(self, g: int, u: int, d: int, hidden: int, x, residual=None, pinned: bool = False, check=True):
+        x = np.ascontiguousarray(x, np.float32)
+        res = np.ascontiguousarray(residual, np.float32) if residual is not None else None
+        out = np.full(hidden, 7.0, np.float32)
+        rc = lib().prism_hip_ffn_chain(self._h, g, u, d, _ptr(x), _ptr(res), int(pinned), _ptr(out))
+        return self._run(rc, out, check)
+
+    # -- device-pointer dispatch (torch tensors) --
+    def quantize_q8k_device(self, x, cols: int, tokens: int, pinned: bool, out, stream=None):
+        self._check(lib().prism_hip_quantize_q8k_device(self._h, _ptr(x), cols, tokens, int(pinned), _ptr(out), stream))
+
+    def quantize_q8_device(self, x, cols: int, tokens: int, contract: int, out, stream=None):
+        self._check(lib().prism_hip_quantize_q8_device(self._h, _ptr(x), cols, tokens, contract, _ptr(out), stream))
+
+    def project_device(self, wid: int, path: int, act, tokens: int, pinned: bool, out, stream=None):
+        self._check(lib().prism_hip_project_device(self._h, wid, path, _ptr(act), tokens, int(pinned), _ptr(out), stream))
+
+    def ffn_chain_device(self, g, u, d, x, residual, pinned, out, h=None, stream=None):
+        self._check(lib().prism_hip_ffn_chain_device(self._h, g, u, d, _ptr(x), _ptr(residual), int(pinned), _ptr(out),
+                                                     _ptr(h), stream))
+
+    def sync(self, stream=None) -> int:
+        return lib().prism_hip_sync(self._h, stream)

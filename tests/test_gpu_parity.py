@@ -1,0 +1,377 @@
+"""GPU parity: every HIP path through the C ABI against the oracle, bit-exact.
+
+The reference's native captures (PQ2 fused/unfused KAT, PTQ1 pinned/source dot
+bits, Q2_K generic dots, the closed-form matvec KATs) are replayed through the
+GPU; random shapes and the benchmark configurations are compared with the CPU
+oracle on identical seeded inputs.  Tolerance: 0 ULP for every integer-dot /
+binary32-chain output; the source-order SwiGLU (device libm exp) is compared
+with max |diff| <= 1e-3 * max |ref|.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+import fixtures_util as fx
+import prism_hip as ph
+import synth
+from hiprt import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ph.Context(0)
+    yield c
+    c.close()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def assert_bits_equal(got, ref, what=""):
+    g, r = bits(got), bits(ref)
+    if not np.array_equal(g, r):
+        idx = np.nonzero(g != r)[0]
+        i = idx[0]
+        raise AssertionError(f"{what}: {idx.size} mismatches, first at {i}: gpu={np.float32(got.flat[i])!r} "
+                             f"oracle={np.float32(ref.flat[i])!r}")
+
+
+# ---- native captures through the GPU -------------------------------------------------
+
+def test_gpu_pinned_pq2_accumulation_matches_native_capture(ctx):
+    w = bytearray([0xAA] * 68)
+    w[0:2] = (0x3C01).to_bytes(2, "little")
+    w[34:36] = (0x3787).to_bytes(2, "little")
+    act = np.zeros(1, ph.Q8K_DTYPE)
+    act["scale"] = np.uint32(0x3DA00001).view(np.float32)
+    act["values"][0, :128] = 3
+    act["values"][0, 128:] = -13
+    act["sums"][0, :8] = 48
+    act["sums"][0, 8:] = -208
+    wid = ctx.weight(ph.KIND_PQ2, 256, 1, bytes(w))
+    assert int(bits(ctx.project_q8k(wid, 1, act, fused=True))[0]) == 0xC1F90B01
+    assert int(bits(ctx.project_q8k(wid, 1, act, fused=False))[0]) == 0xC1F90B02
+    ctx.release(wid)
+
+
+def test_gpu_ptq1_dot_matches_native_pinned_and_source_bits(ctx):
+    blob = fx.read("swift-ptq1-dot-parity.bin")
+    meta = fx.load_json("swift-ptq1-dot-parity.json")
+    cur = 0
+    for case in range(2):
+        width = int.from_bytes(blob[cur:cur + 4], "little")
+        expected = int.from_bytes(blob[cur + 4:cur + 8], "little")
+        wb = width // 128 * 28
+        weights = blob[cur + 8:cur + 8 + wb]
+        acts = blob[cur + 8 + wb:cur + 8 + wb + width // 32 * 34]
+        cur += 8 + wb + width // 32 * 34
+        q8 = np.zeros(width // 32, ph.Q8_DTYPE)
+        for i in range(width // 32):
+            q8[i]["scale"] = np.uint16(int.from_bytes(acts[34 * i:34 * i + 2], "little")).view(np.float16)
+            q8[i]["values"] = np.frombuffer(acts[34 * i + 2:34 * i + 34], np.int8)
+        wid = ctx.weight(ph.KIND_PTQ1, width, 1, weights)
+        assert int(bits(ctx.project_q8(wid, 1, q8, pinned=True))[0]) == expected
+        assert int(bits(ctx.project_q8(wid, 1, q8, pinned=False))[0]) == meta["fixtures"][case]["source_bits"]
+        ctx.release(wid)
+
+
+def test_gpu_q2k_generic_dot_matches_native_records(ctx):
+    for case in fx.load_json("upstream-kquants-q2k.json")["Cases"]:
+        count = case["Count"]
+        w = fx.hexbytes(case["OutputHex"])
+        act = np.frombuffer(fx.hexbytes(case["ActivationsHex"]), ph.Q8K_DTYPE).copy()
+        wid = ctx.weight(ph.KIND_Q2_K, count, 1, w)
+        got = ctx.project_q8k(wid, 1, act)
+        assert got.tobytes() == fx.hexbytes(case["GenericDotHex"]), case["Name"]
+        ctx.release(wid)
+
+
+def test_gpu_closed_form_matvec_kats(ctx):
+    import oracle
+
+    cases = []
+    first = fx.pq2_block(0x3C00, [(1, 2), (2, 2), (3, 2)])
+    second = fx.pq2_block(0x3800, [(0, 0)])
+    x = np.zeros(256, np.float32)
+    x[[0, 1, 2, 3, 128, 255]] = [127.0, 0.5, 1.5, 2.5, -1.5, -127.0]
+    cases.append((ph.KIND_PQ2, 256, first + second, x, 5.0))
+    w = fx.pq2_block(0x3C00, [(0, 3)]) + fx.pq2_block(0, [(0, 3)])
+    x = np.zeros(256, np.float32)
+    x[0] = -127.0
+    cases.append((ph.KIND_PQ2, 256, w, x, -254.0))
+    cases.append((ph.KIND_PQ2, 256, w, np.zeros(256, np.float32), 0.0))
+    blk = oracle.pack_ptq(fx.pq2_block(0x4000, [(1, 2), (2, 2), (33, 2)]))
+    x = np.zeros(128, np.float32)
+    x[[0, 1, 2, 32, 33]] = [127.0, 0.5, 1.5, 63.5, 0.25]
+    cases.append((ph.KIND_PTQ1, 128, blk, x, 7.0))
+    blk = oracle.pack_ptq(fx.pq2_block(0x3C00, [(0, 2)]))
+    x = np.zeros(128, np.float32)
+    x[0] = 1.0
+    cases.append((ph.KIND_PTQ1, 128, blk, x, np.float32(0.99993896)))
+    f1 = fx.pq2_block(0x4000, [(1, 2), (2, 3), (33, 2)])
+    x = np.zeros(128, np.float32)
+    x[[0, 1, 2, 32, 33]] = [127.0, 0.5, 1.5, 63.5, 0.25]
+    cases.append((ph.KIND_PQ2, 128, f1, x, 11.0))
+    f2 = fx.pq2_block(0x3800, [(1, 2), (2, 3), (33, 2)])
+    f3 = fx.pq2_block(0x3C00, [(1, 2), (2, 3), (33, 2)])
+    cases.append((ph.KIND_PQ2, 384, f1 + f2 + f3, np.concatenate([x, x, x]), 19.25))
+    for kind, cols, w, x, expected in cases:
+        wid = ctx.weight(kind, cols, 1, w)
+        got = ctx.project_f32(wid, 1, x)
+        assert got[0] == np.float32(expected), (kind, cols, got[0], expected)
+        ctx.release(wid)
+
+
+# ---- quantizers ------------------------------------------------------------------------
+
+def _quant_inputs():
+    rng = np.random.default_rng(21)
+    xs = [rng.standard_normal(4096).astype(np.float32),
+          (rng.standard_normal(2048) * np.exp2(rng.integers(-30, 30, 2048))).astype(np.float32),
+          np.zeros(512, np.float32)]
+    ties = np.zeros(256, np.float32)
+    ties[5], ties[9], ties[100] = -3.0, 3.0, 1.5
+    xs.append(ties)
+    for case in fx.load_json("swift-q8-parity.json")["cases"]:
+        xs.append(np.tile(fx.f32_from_hex_words(case["input_bits"]), 8))
+    for word in (0xBE010F7E, 0x3E010F7E):
+        x = np.zeros(256, np.float32)
+        x[0] = np.uint32(0x3E653D88).view(np.float32)
+        x[1] = np.uint32(word).view(np.float32)
+        xs.append(x)
+    for case in fx.load_json("swift-ptq1-q8-scale-parity.json")["cases"]:
+        xs.append(np.tile(np.array(case["input_bits"], np.uint32).view(np.float32), 8))
+    for case in fx.load_json("row-quantizers-path.json")["Cases"]:
+        if case["TypeId"] in (8, 15):
+            xs.append(np.frombuffer(fx.hexbytes(case["InputHex"]), "<f4").copy())
+    return xs
+
+
+def test_gpu_quantizers_match_oracle_bytes(ctx):
+    import oracle
+
+    def expect(quant, args, dev_out, what):
+        # Same bytes when the reference quantizer succeeds, an error when it rejects the
+        # input (e.g. a binary16 scale overflow for |x| > 65504*127).
+        try:
+            ref = quant(*args)
+        except oracle.OracleError:
+            assert ctx.sync() == ph.ERR_NONFINITE, what
+            return
+        assert ctx.sync() == 0, what
+        assert dev_out.to_numpy(np.uint8).tobytes() == ref.tobytes(), what
+
+    for i, x in enumerate(_quant_inputs()):
+        n = x.size - x.size % 256
+        if n:
+            xd = DeviceBuffer.from_numpy(x[:n])
+            for pinned in (False, True):
+                out = DeviceBuffer(n // 256 * 292)
+                ctx.quantize_q8k_device(xd, n, 1, pinned, out)
+                expect(oracle.quantize_q8k, (x[:n], pinned), out, ("q8k", i, pinned))
+        n = x.size - x.size % 32
+        xd = DeviceBuffer.from_numpy(x[:n])
+        for contract in (0, 1, 2):
+            out = DeviceBuffer(n // 32 * 40)
+            ctx.quantize_q8_device(xd, n, 1, contract, out)
+            expect(oracle.quantize_q8_0, (x[:n], contract), out, ("q8_0", i, contract))
+
+
+def test_gpu_quantizer_rejects_nonfinite_and_overflow(ctx):
+    x = np.ones(256, np.float32)
+    x[17] = np.nan
+    out = DeviceBuffer(292)
+    ctx.quantize_q8k_device(DeviceBuffer.from_numpy(x), 256, 1, False, out)
+    assert ctx.sync() == ph.ERR_NONFINITE
+    tiny = np.zeros(256, np.float32)
+    tiny[0] = np.uint32(1).view(np.float32)
+    ctx.quantize_q8k_device(DeviceBuffer.from_numpy(tiny), 256, 1, False, out)
+    assert ctx.sync() == ph.ERR_NONFINITE
+    assert ctx.sync() == 0  # flag cleared
+
+
+# ---- random shapes, every kind and contract -------------------------------------------
+
+SHAPES = [
+    (ph.KIND_PTQ1, 37, 256), (ph.KIND_PTQ1, 64, 2048), (ph.KIND_PTQ1, 50, 384), (ph.KIND_PTQ1, 33, 6144),
+    (ph.KIND_PTQ1, 9, 8192), (ph.KIND_PTQ1, 21, 16384),
+    (ph.KIND_PQ2, 37, 256), (ph.KIND_PQ2, 64, 2048), (ph.KIND_PQ2, 40, 384), (ph.KIND_PQ2, 33, 6144),
+    (ph.KIND_PQ2, 19, 12288), (ph.KIND_PQ2, 17, 128),
+    (ph.KIND_Q2_K, 37, 256), (ph.KIND_Q2_K, 64, 2048), (ph.KIND_Q2_K, 33, 6144), (ph.KIND_Q2_K, 21, 16384),
+    (ph.KIND_Q8_0, 37, 128), (ph.KIND_Q8_0, 64, 2048), (ph.KIND_Q8_0, 50, 2080), (ph.KIND_Q8_0, 33, 4096),
+    (ph.KIND_Q8_0, 9, 8192),
+]
+
+
+@pytest.mark.parametrize("kind,rows,cols", SHAPES)
+def test_gpu_project_f32_matches_oracle_matvec(ctx, kind, rows, cols):
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=rows * 7 + cols) if kind != ph.KIND_PQ2 else \
+        synth.pq2_weights(rows, cols, seed=rows + cols, levels=4)
+    x = synth.activations(cols, seed=cols + 1)
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, x, pinned, threads=THREADS)
+        got = ctx.project_f32(wid, rows, x, pinned=pinned)
+        assert_bits_equal(got, ref, f"kind={kind} {rows}x{cols} pinned={pinned}")
+    ctx.release(wid)
+
+
+@pytest.mark.parametrize("kind,rows,cols", [s for s in SHAPES if s[0] != ph.KIND_Q8_0 and s[2] % 256 == 0])
+def test_gpu_project_q8k_prepared_codes(ctx, kind, rows, cols):
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=11 + rows)
+    x = synth.activations(cols, seed=cols + 2)
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        act = oracle.quantize_q8k(x, pinned)
+        if kind == ph.KIND_PTQ1:
+            ref = np.array([oracle.dot_ptq1_q8k(w[r * (cols // 128) * 28:(r + 1) * (cols // 128) * 28], act)
+                            for r in range(rows)], np.float32)
+        else:
+            ref = oracle.project_q8k(kind, cols, rows, w, act, pinned, threads=THREADS)
+        got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), fused=pinned)
+        assert_bits_equal(got, ref, f"q8k kind={kind} pinned={pinned}")
+    ctx.release(wid)
+
+
+@pytest.mark.parametrize("kind,rows,cols", [(ph.KIND_PTQ1, 37, 2048), (ph.KIND_PQ2, 40, 384),
+                                            (ph.KIND_PQ2, 40, 2048), (ph.KIND_Q8_0, 37, 2048)])
+def test_gpu_project_q8_prepared_codes(ctx, kind, rows, cols):
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=5 + rows)
+    x = synth.activations(cols, seed=cols + 3)
+    wid = ctx.weight(kind, cols, rows, w)
+    for contract in (0, 1, 2):
+        act = oracle.quantize_q8_0(x, contract)
+        for pinned in (False, True):
+            ref = oracle.project_q8(kind, cols, rows, w, act, pinned, threads=THREADS)
+            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=pinned)
+            assert_bits_equal(got, ref, f"q8 kind={kind} contract={contract} pinned={pinned}")
+    ctx.release(wid)
+
+
+# ---- multi-token, groups, backend op -------------------------------------------------
+
+def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
+    import oracle
+
+    rows, cols, M = 96, 2048, 9
+    for kind in (ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0):
+        w = synth.weights(kind, rows, cols, seed=kind)
+        X = synth.activations(cols, seed=4, tokens=M)
+        wid = ctx.weight(kind, cols, rows, w)
+        for pinned in (False, True):
+            ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+            assert_bits_equal(ctx.prefill(wid, rows, X, pinned=pinned), ref, f"prefill kind={kind}")
+        assert_bits_equal(ctx.mul_mat(wid, rows, X), oracle.prefill(kind, cols, rows, w, X, False, THREADS), "mul_mat")
+        ctx.release(wid)
+
+
+def test_gpu_project_f32_group_siblings(ctx):
+    import oracle
+
+    cols = 2048
+    ws = [synth.ptq1_weights(r, cols, seed=r) for r in (64, 48, 80)]
+    ids = [ctx.weight(ph.KIND_PTQ1, cols, r, w) for r, w in zip((64, 48, 80), ws)]
+    x = synth.activations(cols, seed=9)
+    for pinned in (False, True):
+        outs = ctx.project_f32_group(ids, [64, 48, 80], x, pinned=pinned)
+        for r, w, o in zip((64, 48, 80), ws, outs):
+            assert_bits_equal(o, oracle.matvec(ph.KIND_PTQ1, cols, r, w, x, pinned), "group")
+    for i in ids:
+        ctx.release(i)
+
+
+# ---- FFN ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_PTQ1])
+def test_gpu_ffn_chain(ctx, kind):
+    import oracle
+
+    hidden, ffn = 2048, 6144
+    wg = synth.weights(kind, ffn, hidden, seed=1)
+    wu = synth.weights(kind, ffn, hidden, seed=2)
+    wd = synth.weights(kind, hidden, ffn, seed=3)
+    x = synth.activations(hidden, seed=4)
+    res = synth.activations(hidden, seed=5)
+    g, u, d = (ctx.weight(kind, hidden, ffn, wg), ctx.weight(kind, hidden, ffn, wu), ctx.weight(kind, ffn, hidden, wd))
+    # pinned: ggml vector exp + correctly rounded division -> bit-exact end to end
+    ref, h = oracle.ffn(kind, hidden, ffn, wg, wu, wd, x, res, pinned=True, threads=THREADS)
+    assert_bits_equal(ctx.ffn_swiglu(g, u, ffn, x, pinned=True), h, "swiglu pinned")
+    assert_bits_equal(ctx.ffn_chain(g, u, d, hidden, x, res, pinned=True), ref, "ffn pinned")
+    # source: libm exp on each side; compare with the tolerance stated in the module docstring
+    ref, h = oracle.ffn(kind, hidden, ffn, wg, wu, wd, x, None, pinned=False, threads=THREADS)
+    got_h = ctx.ffn_swiglu(g, u, ffn, x, pinned=False)
+    assert np.max(np.abs(got_h - h)) <= 1e-6 * np.max(np.abs(h))
+    got = ctx.ffn_chain(g, u, d, hidden, x, None, pinned=False)
+    assert np.max(np.abs(got - ref)) <= 1e-3 * np.max(np.abs(ref))
+    for i in (g, u, d):
+        ctx.release(i)
+
+
+# ---- errors ---------------------------------------------------------------------------
+
+def test_gpu_errors_clear_output_and_do_not_latch(ctx):
+    rows, cols = 8, 256
+    w = bytearray(synth.ptq1_weights(rows, cols, seed=1).tobytes())
+    w[28 * 5 + 26:28 * 5 + 28] = (0x7C00).to_bytes(2, "little")  # +inf scale in row 2
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, bytes(w))
+    rc, out = ctx.project_f32(wid, rows, synth.activations(cols, 1), check=False)
+    assert rc == ph.ERR_NONFINITE and not out.any()
+    x = synth.activations(cols, 2)
+    x[3] = np.inf
+    good = ctx.weight(ph.KIND_PTQ1, cols, rows, synth.ptq1_weights(rows, cols, seed=2))
+    rc, out = ctx.project_f32(good, rows, x, check=False)
+    assert rc == ph.ERR_NONFINITE and not out.any()
+    rc, out = ctx.project_q8(good, rows, np.zeros(3, ph.Q8_DTYPE), check=False)
+    assert rc == ph.ERR_INVALID_INPUT and not out.any()
+    assert not ctx.supports(ph.KIND_Q2_K, 256, 4, ph.PATH_Q8)
+    assert not ctx.supports(ph.KIND_PQ2, 384, 4, ph.PATH_Q8K)
+    assert ctx.supports(ph.KIND_PQ2, 384, 4, ph.PATH_Q8)
+    assert not ctx.faulted and ctx.operation_capacity() > 0
+    assert ctx.operation_count(ph.KIND_PTQ1, 2048, 16) == 2048 * 16
+    ok = ctx.project_f32(good, rows, synth.activations(cols, 3))
+    assert np.isfinite(ok).all()
+    ctx.release(wid)
+    ctx.release(good)
+
+
+def test_gpu_weight_cache_by_key_and_budget():
+    with ph.Context(0, max_resident_bytes=4096) as c:
+        w = synth.ptq1_weights(16, 256, seed=1)
+        a = c.weight(ph.KIND_PTQ1, 256, 16, w, key=42)
+        b = c.weight(ph.KIND_PTQ1, 256, 16, w, key=42)
+        assert a == b and c.resident_bytes() == w.size
+        with pytest.raises(ph.PrismError) as e:
+            c.weight(ph.KIND_PTQ1, 256, 256, synth.ptq1_weights(256, 256, seed=2), key=43)
+        assert e.value.code == ph.ERR_RESOURCE
+
+
+# ---- device-pointer path and determinism ----------------------------------------------
+
+def test_gpu_device_pointer_path_matches_host_path(ctx):
+    rows, cols = 300, 4096
+    for kind in (ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_Q8_0, ph.KIND_PQ2):
+        w = synth.weights(kind, rows, cols, seed=kind + 1)
+        x = synth.activations(cols, seed=12)
+        wd = DeviceBuffer.from_numpy(w)
+        wid = ctx.weight_device(kind, cols, rows, wd)
+        out = DeviceBuffer(rows * 4)
+        ctx.project_device(wid, ph.PATH_F32, DeviceBuffer.from_numpy(x), 1, False, out)
+        assert ctx.sync() == 0
+        host = ctx.project_f32(wid, rows, x)
+        assert_bits_equal(out.to_numpy(np.float32), host, f"device path kind={kind}")
+        again = ctx.project_f32(wid, rows, x)
+        assert_bits_equal(again, host, "repeat")
+        ctx.release(wid)
