@@ -48,30 +48,19 @@ def chunk_for(k: int) -> int:
 
 
 class Rotation:
-    """`copies` device copies of one packed tensor (identical bytes, distinct addresses)."""
+    """`copies` context-owned device copies of one packed tensor (identical bytes, distinct
+    addresses), each stored in the library's tiled layout."""
 
     def __init__(self, ctx: ph.Context, kind: int, rows: int, cols: int, data: np.ndarray, copies: int):
         self.nbytes = data.size
-        self.buf = hiprt.DeviceBuffer(self.nbytes * copies)
-        self.buf.upload(data)
-        for i in range(1, copies):
-            hiprt.copy_d2d(self.buf.ptr + i * self.nbytes, self.buf.ptr, self.nbytes)
-        self.ids = [ctx.weight_device(kind, cols, rows, _View(self.buf.ptr + i * self.nbytes, self.nbytes))
-                    for i in range(copies)]
+        src = hiprt.DeviceBuffer.from_numpy(data)
+        self.ids = [ctx.weight_from_device(kind, cols, rows, src) for _ in range(copies)]
+        src.free()
 
-
-class _View:
-    def __init__(self, ptr: int, nbytes: int):
-        self.ptr, self.nbytes = ptr, nbytes
-
-    def data_ptr(self):
-        return self.ptr
-
-    def numel(self):
-        return self.nbytes
-
-    def element_size(self):
-        return 1
+    def release(self, ctx: ph.Context):
+        for wid in self.ids:
+            ctx.release(wid)
+        self.ids = []
 
 
 def ffn_step_bytes() -> int:
@@ -145,28 +134,23 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
     for i in range(min(copies, 8)):
         ctx.project_device(rot.ids[i], path, act, 1, False, out, stream)
     assert ctx.sync() == 0
-    evs = [hiprt.Event() for _ in range(2 * launches)]
+    e0, e1 = hiprt.Event(), hiprt.Event()
+    e0.record(stream)
     for i in range(launches):
-        evs[2 * i].record(stream)
         ctx.project_device(rot.ids[i % copies], path, act, 1, False, out, stream)
-        evs[2 * i + 1].record(stream)
-    evs[-1].synchronize()
+    e1.record(stream)
+    e1.synchronize()
     assert ctx.sync() == 0
-    durs = np.array([evs[2 * i].elapsed_ms(evs[2 * i + 1]) for i in range(launches)])
+    t = e0.elapsed_ms(e1) / launches * 1e-3
     nbytes = w.size + act_bytes + 4 * rows
-    t = float(np.median(durs)) * 1e-3
-    for wid in rot.ids:
-        ctx.release(wid)
-    rot.buf.free()
-    return {"kind": kind, "rows": rows, "cols": cols, "bytes_per_launch": int(nbytes),
-            "avg_us": float(durs.mean()) * 1e3, "median_us": t * 1e6, "GBps": nbytes / t / 1e9,
-            "frac_hbm": nbytes / t / PEAK_HBM}
+    rot.release(ctx)
+    return {"kind": kind, "rows": rows, "cols": cols, "bytes_per_launch": int(nbytes), "copies": copies,
+            "avg_us": t * 1e6, "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM}
 
 
 def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 3):
     w = synth.ptq1_weights(rows, cols, seed=9)
-    wbuf = hiprt.DeviceBuffer.from_numpy(w)
-    wid = ctx.weight_device(ph.KIND_PTQ1, cols, rows, _View(wbuf.ptr, w.size))
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
     X = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=10, tokens=M))
     out = hiprt.DeviceBuffer(4 * rows * M)
     stream = ctx.stream()
@@ -228,7 +212,7 @@ def main() -> int:
     value = nbytes / (ms * 1e-3) / 1e9
     log(f"ffn step: {ms * 1e3:.2f} us/step (wall {wall_ms * 1e3:.2f}), {value:.1f} GB/s")
     kern = bench_matvec_kernel(ctx, ph.KIND_Q2_K, FFN, HIDDEN)
-    log(f"q2k matvec {FFN}x{HIDDEN}: {kern['median_us']:.2f} us, {kern['GBps']:.1f} GB/s")
+    log(f"q2k matvec {FFN}x{HIDDEN}: {kern['avg_us']:.2f} us, {kern['GBps']:.1f} GB/s")
     extras = {}
     if not args.no_extras:
         extras["matvec"] = []
@@ -237,7 +221,7 @@ def main() -> int:
                                  (ph.KIND_PTQ1, 151936, 4096), (ph.KIND_Q2_K, 151936, 4096),
                                  (ph.KIND_Q8_0, 151936, 4096)]:
             r = bench_matvec_kernel(ctx, kind, rows, cols, launches=100)
-            log(f"matvec kind={kind} {rows}x{cols}: {r['median_us']:.2f} us, {r['GBps']:.1f} GB/s")
+            log(f"matvec kind={kind} {rows}x{cols}: {r['avg_us']:.2f} us, {r['GBps']:.1f} GB/s")
             extras["matvec"].append(r)
         extras["prefill_ptq1_6144x2048"] = []
         for M in (128, 512):
@@ -268,7 +252,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(kern["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(kern["frac_hbm"], 4), "traffic": None,
                      "kernel": f"Q2_K x Q8_K matvec {FFN}x{HIDDEN}", "bytes_per_launch": kern["bytes_per_launch"],
-                     "avg_launch_us": round(kern["median_us"], 3)},
+                     "avg_launch_us": round(kern["avg_us"], 3)},
         "cpu_baseline": cpu,
     }
     if extras:

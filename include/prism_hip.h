@@ -108,6 +108,10 @@ int prism_hip_supports(const prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, u
  * same geometry returns its id without copying. */
 prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *ctx, uint64_t key, uint32_t kind, uint64_t cols,
                                          uint64_t rows, const void *host, uint64_t bytes);
+/* As prism_hip_weight_acquire, from native bytes already in device memory (read
+ * only during the call; the context keeps its own copy). */
+prism_weight_id prism_hip_weight_acquire_device(prism_hip_ctx *ctx, uint64_t key, uint32_t kind, uint64_t cols,
+                                                uint64_t rows, const void *device_ptr, uint64_t bytes);
 /* Registers caller-owned device memory holding the packed tensor (no copy).  The
  * caller keeps it alive until release. */
 prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows,

@@ -35,7 +35,14 @@ struct MatvecArgs {
 };
 
 // Returns 0 on success, -1 when the launch failed, -2 when the shape is unsupported.
+// launch_matvec reads weights in the native row-major layout, launch_matvec_tiled in
+// the 64-row tiled layout of tiled.hpp.
 int launch_matvec(const MatvecArgs &a);
+int launch_matvec_tiled(const MatvecArgs &a);
+// Whether (kind, cols, rows) can be stored tiled, and the native -> tiled repack
+// (the destination must hold tiled_bytes() and be zero-filled beforehand).
+bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows);
+int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols, uint64_t rows, hipStream_t s);
 int launch_quantize_q8k(const float *x, uint64_t cols, uint32_t tokens, int pinned, void *out, int *err,
                         hipStream_t s);
 int launch_quantize_q8_0(const float *x, uint64_t cols, uint32_t tokens, int contract, void *out, int *err,

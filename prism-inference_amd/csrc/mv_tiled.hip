@@ -1,0 +1,511 @@
+// mv_tiled.hip -- batch-1 packed matvec over the 64-row tiled weight layout (gfx950).
+//
+// Lane r of a wavefront owns row r of a 64-row tile and walks the row's units
+// (128 weights; a 256-weight super-block for Q2_K) in order, so the reference's
+// binary32 chain out = ((0 + t0) + t1) + ... is evaluated serially in the lane
+// that owns the row, with no cross-lane float reduction at all.  Every weight load
+// is one contiguous 16/8/4/2-byte-per-lane buffer load (the tiled layout puts the
+// same piece of 64 rows side by side), and out-of-range lanes read the buffer's
+// zero padding.  All lanes of a wavefront process the same unit at the same time,
+// so the prepared activation is wave-uniform: it is fetched with scalar loads and
+// fed to v_dot4 as a scalar operand, costing no LDS or vector bandwidth.
+//
+// Small matrices split K across the KS wavefronts of a workgroup: each wavefront
+// computes the per-unit terms of its K range, the terms meet in LDS, and wavefront
+// 0 folds them in unit order -- the same serial chain, only computed later.
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "tiled.hpp"
+
+namespace prism {
+
+namespace {
+
+enum class Op : int { PTQ1_SRC, PTQ1_PINNED, PTQ1_Q8K, PQ2_UNFUSED, PQ2_FUSED, PQ2_Q8, Q2K, Q8_0 };
+
+template <Op O>
+constexpr uint32_t kind_of() {
+    return O == Op::Q2K    ? kQ2_K
+           : O == Op::Q8_0 ? kQ8_0
+           : (O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED || O == Op::PQ2_Q8) ? kPQ2
+                                                                              : kPTQ1;
+}
+// Native bytes per unit.
+template <Op O>
+constexpr uint32_t unit_bytes() {
+    return kind_of<O>() == kPTQ1 ? 28 : kind_of<O>() == kPQ2 ? 34 : kind_of<O>() == kQ2_K ? 84 : 136;
+}
+// binary32 terms per unit handed to the fold when K is split across wavefronts.
+template <Op O>
+constexpr int terms_per_unit() {
+    return O == Op::PTQ1_PINNED ? 9 : O == Op::PQ2_FUSED ? 2 : O == Op::Q8_0 ? 4 : 1;
+}
+
+constexpr uint32_t sel(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+// Sum of the four signed bytes of a dword.
+__device__ __forceinline__ int bsum4(uint32_t a, int c) { return sdot4(a, 0x01010101u, c); }
+
+// ---- PTQ1 trit decode ---------------------------------------------------------------
+// Byte x carries trits t_k = ((x*3^k mod 256)*3) >> 8 (tools/ternary/src/lib.rs:202-250).
+// Two bytes travel in the 16-bit lanes of a dword: x*3 never carries across lanes,
+// the digit lands in each lane's high byte and the low byte is the next remainder.
+// One v_perm gathers the four digits (0..2) of bytes 4w..4w+3 into a dword for v_dot4
+// against the activation codes they multiply; sum (t-1)a = sum t*a - sum a.
+// Element map: byte b<16 digit k -> 16k+b; byte 16+b (b<8) digit k -> 80+8k+b;
+// byte 24+b (b<2) digit k<4 -> 120+2k+b.  acc(q) receives quad q (elements 4q..4q+3).
+template <typename Act, typename Acc>
+__device__ __forceinline__ void ptq1_dots(const uint32_t x[7], const Act &a, Acc &&acc) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t L = x[w] & 0x00ff00ffu, H = (x[w] >> 8) & 0x00ff00ffu;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const uint32_t mL = L * 3u, mH = H * 3u;
+            int &r = acc(4 * k + w);
+            r = sdot4(perm(mH, mL, sel(1, 5, 3, 7)), a(4 * k + w), r);
+            L = mL & 0x00ff00ffu;
+            H = mH & 0x00ff00ffu;
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        uint32_t L = x[4 + w] & 0x00ff00ffu, H = (x[4 + w] >> 8) & 0x00ff00ffu;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const uint32_t mL = L * 3u, mH = H * 3u;
+            int &r = acc(20 + 2 * k + w);
+            r = sdot4(perm(mH, mL, sel(1, 5, 3, 7)), a(20 + 2 * k + w), r);
+            L = mL & 0x00ff00ffu;
+            H = mH & 0x00ff00ffu;
+        }
+    }
+    uint32_t T = (x[6] & 0xffu) | ((x[6] & 0xff00u) << 8);
+    const uint32_t m0 = T * 3u;
+    T = m0 & 0x00ff00ffu;
+    const uint32_t m1 = T * 3u;
+    T = m1 & 0x00ff00ffu;
+    const uint32_t m2 = T * 3u;
+    T = m2 & 0x00ff00ffu;
+    const uint32_t m3 = T * 3u;
+    int &r30 = acc(30);
+    r30 = sdot4(perm(m1, m0, sel(1, 3, 5, 7)), a(30), r30);
+    int &r31 = acc(31);
+    r31 = sdot4(perm(m3, m2, sel(1, 3, 5, 7)), a(31), r31);
+}
+
+// PQ2 code dword i holds elements 16i..16i+15, element 16i+4q+p in byte q, bits 2p.
+// Given the 16 activation codes of those elements (natural order, dwords q0..q3),
+// accumulates sum c*a into a0 + a1/4 + a2/16 (the masks leave field p scaled by 4^p)
+// and the code sum into s.  The activation quad paired with field p is
+// (a[p], a[4+p], a[8+p], a[12+p]): a 4x4 byte transpose.
+__device__ __forceinline__ void pq2_dword(uint32_t c, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, int &a0,
+                                          int &a1, int &a2, int &s) {
+    s = bsum4(q3, bsum4(q2, bsum4(q1, bsum4(q0, s))));
+    const uint32_t t0 = perm(q1, q0, sel(0, 4, 1, 5)), t1 = perm(q3, q2, sel(0, 4, 1, 5));
+    const uint32_t t2 = perm(q1, q0, sel(2, 6, 3, 7)), t3 = perm(q3, q2, sel(2, 6, 3, 7));
+    a0 = sdot4(c & 0x03030303u, perm(t1, t0, sel(0, 1, 4, 5)), a0);
+    a1 = sdot4(c & 0x0c0c0c0cu, perm(t1, t0, sel(2, 3, 6, 7)), a1);
+    a2 = sdot4(c & 0x30303030u, perm(t3, t2, sel(0, 1, 4, 5)), a2);
+    a2 = sdot4((c >> 2) & 0x30303030u, perm(t3, t2, sel(2, 3, 6, 7)), a2);
+}
+
+// ---- per-unit raw weight data ---------------------------------------------------------
+template <Op O>
+struct Raw;
+template <>
+struct Raw<Op::PTQ1_SRC> {
+    uint32_t x[7];
+};
+template <>
+struct Raw<Op::PTQ1_PINNED> : Raw<Op::PTQ1_SRC> {};
+template <>
+struct Raw<Op::PTQ1_Q8K> : Raw<Op::PTQ1_SRC> {};
+template <>
+struct Raw<Op::PQ2_UNFUSED> {
+    uint32_t c[8];
+    uint32_t d;
+};
+template <>
+struct Raw<Op::PQ2_FUSED> : Raw<Op::PQ2_UNFUSED> {};
+template <>
+struct Raw<Op::PQ2_Q8> : Raw<Op::PQ2_UNFUSED> {};
+template <>
+struct Raw<Op::Q2K> {
+    uint32_t q[16];
+    uint32_t sc[4];
+    uint32_t dm;
+};
+template <>
+struct Raw<Op::Q8_0> {
+    uint32_t c[32];
+    uint32_t s[2];
+};
+
+// Loads unit `seg` (byte offset of the unit's segment in the tile) for tile-row `r`.
+template <Op O>
+__device__ __forceinline__ void load_unit(Raw<O> &w, __amdgpu_buffer_rsrc_t rs, uint32_t seg, uint32_t trp,
+                                          uint32_t r) {
+    if constexpr (kind_of<O>() == kPTQ1) {
+        const u32x4 a = bload4(rs, seg + 16u * r);
+        const u32x2 b = bload2(rs, seg + 16u * trp + 8u * r);
+        const uint32_t c = bload1(rs, seg + 24u * trp + 4u * r);
+        w.x[0] = a.x; w.x[1] = a.y; w.x[2] = a.z; w.x[3] = a.w;
+        w.x[4] = b.x; w.x[5] = b.y; w.x[6] = c;
+    } else if constexpr (kind_of<O>() == kPQ2) {
+        const u32x4 a = bload4(rs, seg + 16u * r);
+        const u32x4 b = bload4(rs, seg + 16u * trp + 16u * r);
+        w.c[0] = a.x; w.c[1] = a.y; w.c[2] = a.z; w.c[3] = a.w;
+        w.c[4] = b.x; w.c[5] = b.y; w.c[6] = b.z; w.c[7] = b.w;
+        w.d = __builtin_amdgcn_raw_buffer_load_b16(rs, static_cast<int>(seg + 32u * trp + 2u * r), 0, 0);
+    } else if constexpr (kind_of<O>() == kQ2_K) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32x4 a = bload4(rs, seg + 16u * p * trp + 16u * r);
+            w.q[4 * p] = a.x; w.q[4 * p + 1] = a.y; w.q[4 * p + 2] = a.z; w.q[4 * p + 3] = a.w;
+        }
+        const u32x4 s = bload4(rs, seg + 64u * trp + 16u * r);
+        w.sc[0] = s.x; w.sc[1] = s.y; w.sc[2] = s.z; w.sc[3] = s.w;
+        w.dm = bload1(rs, seg + 80u * trp + 4u * r);
+    } else {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const u32x4 a = bload4(rs, seg + 16u * p * trp + 16u * r);
+            w.c[4 * p] = a.x; w.c[4 * p + 1] = a.y; w.c[4 * p + 2] = a.z; w.c[4 * p + 3] = a.w;
+        }
+        const u32x2 s = bload2(rs, seg + 128u * trp + 8u * r);
+        w.s[0] = s.x;
+        w.s[1] = s.y;
+    }
+}
+
+// ---- per-unit arithmetic ------------------------------------------------------------
+// `act` is the token's prepared activation; every index into it is wave-uniform.
+// Terms go to t[] in the order the reference's chain consumes them.
+template <Op O>
+__device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restrict__ act, uint32_t u, float *t) {
+    if constexpr (O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED) {
+        const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
+        const uint32_t *av[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) av[g] = reinterpret_cast<const uint32_t *>(b[g].values);
+        auto a = [&](int q) -> uint32_t { return av[q >> 3][q & 7]; };
+        const float d = h2f(w.x[6] >> 16);
+        if constexpr (O == Op::PTQ1_SRC) {
+            int acc[4] = {0, 0, 0, 0};
+            ptq1_dots(w.x, a, [&](int q) -> int & { return acc[q >> 3]; });
+            // dot_q8_groups, src/kernels.rs:1043-1064
+            float tt = 0.0f;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                int s = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s = bsum4(av[g][i], s);
+                tt = tt + b[g].scale * static_cast<float>(acc[g] - s);
+            }
+            t[0] = d * tt;
+        } else {
+            // q8_native_lanes (src/kernels.rs:1066-1076): lane l of group g owns positions
+            // 4l..4l+3 and 16+4l..16+4l+3, i.e. quads l and l+4 of the group.
+            int acc[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = 0;
+            ptq1_dots(w.x, a, [&](int q) -> int & { return acc[4 * (q >> 3) + (q & 3)]; });
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int g0 = i >> 1, l0 = 2 * (i & 1);
+                const int s0 = bsum4(av[g0][l0 + 4], bsum4(av[g0][l0], 0));
+                const int s1 = bsum4(av[g0][l0 + 5], bsum4(av[g0][l0 + 1], 0));
+                const int lo = acc[2 * i] - s0, hi = acc[2 * i + 1] - s1;
+                t[i] = __uint_as_float((static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16));
+            }
+            t[8] = d;
+        }
+    } else if constexpr (O == Op::PTQ1_Q8K) {
+        const Q8KBlock *b = static_cast<const Q8KBlock *>(act) + (u >> 1);
+        const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values) + 32 * (u & 1);
+        auto a = [&](int q) -> uint32_t { return av[q]; };
+        int acc = 0;
+        ptq1_dots(w.x, a, [&](int) -> int & { return acc; });
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s = bsum4(av[i], s);
+        // dot_ptq1_q8k, src/kernels.rs:1026-1034
+        t[0] = (h2f(w.x[6] >> 16) * b->scale) * static_cast<float>(acc - s);
+    } else if constexpr (O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED) {
+        const Q8KBlock *b = static_cast<const Q8KBlock *>(act) + (u >> 1);
+        const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values) + 32 * (u & 1);
+        int a0 = 0, a1 = 0, a2 = 0, s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            pq2_dword(w.c[i], av[4 * i], av[4 * i + 1], av[4 * i + 2], av[4 * i + 3], a0, a1, a2, s);
+        const int I = a0 + (a1 >> 2) + (a2 >> 4) - s;  // sum (c-1)*a, exact
+        // dot_pq2::<FUSED>, src/kernels.rs:941-955
+        const float dd = h2f(w.d) * b->scale;
+        const float sf = static_cast<float>(I);
+        if constexpr (O == Op::PQ2_UNFUSED) {
+            t[0] = dd * sf;
+        } else {
+            t[0] = dd;
+            t[1] = sf;
+        }
+    } else if constexpr (O == Op::PQ2_Q8) {
+        // dot_q8_groups for an odd-group PQ2 row (src/kernels.rs:1043-1064); the pinned
+        // contract keeps this order for PQ2 (:1109-1121).
+        const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
+        float tt = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t *av = reinterpret_cast<const uint32_t *>(b[g].values);
+            int a0 = 0, a1 = 0, a2 = 0, s = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pq2_dword(w.c[2 * g + h], av[4 * h], av[4 * h + 1], av[4 * h + 2], av[4 * h + 3], a0, a1, a2, s);
+            tt = tt + b[g].scale * static_cast<float>(a0 + (a1 >> 2) + (a2 >> 4) - s);
+        }
+        t[0] = h2f(w.d) * tt;
+    } else if constexpr (O == Op::Q2K) {
+        const Q8KBlock *b = static_cast<const Q8KBlock *>(act) + u;
+        const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values);
+        // Code dword w: half h = w/8, bytes 4(w%8).. ; field p -> elements 128h+32p+4(w%8)..+3,
+        // sub-block g = 8h + 2p + (w%8 >= 4).  Masking in place scales field p by 4^p; the
+        // top field is shifted down first so every code byte stays below 128 (v_dot4 reads
+        // signed bytes), leaving fields 2 and 3 both scaled by 16.
+        int sb[16];
+#pragma unroll
+        for (int g = 0; g < 16; ++g) sb[g] = 0;
+#pragma unroll
+        for (int wd = 0; wd < 16; ++wd) {
+            const int h = wd >> 3, wh = wd & 7;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int g = 8 * h + 2 * p + (wh >> 2);
+                const uint32_t m = p < 3 ? w.q[wd] & (0x03030303u << (2 * p)) : (w.q[wd] >> 2) & 0x30303030u;
+                sb[g] = sdot4(m, av[32 * h + 8 * p + wh], sb[g]);
+            }
+        }
+        int isum = 0, msum = 0;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const uint32_t byte = (w.sc[g >> 2] >> (8 * (g & 3))) & 0xffu;
+            const int p = (g & 7) >> 1;
+            const int shift = p < 3 ? 2 * p : 4;
+            isum += static_cast<int>(byte & 15u) * (sb[g] >> shift);
+            msum += static_cast<int>(b->sums[g]) * static_cast<int>(byte >> 4);
+        }
+        // dot_q2_k_block, src/kernels/kquants.rs:193-196
+        const float as = b->scale;
+        t[0] = (as * h2f(w.dm & 0xffffu)) * static_cast<float>(isum) -
+               (as * h2f(w.dm >> 16)) * static_cast<float>(msum);
+    } else {
+        const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t *av = reinterpret_cast<const uint32_t *>(b[j].values);
+            int I = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) I = sdot4(w.c[8 * j + i], av[i], I);
+            const uint32_t sbits = (w.s[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            // dot_legacy, src/kernels.rs:1241-1244
+            t[j] = (h2f(sbits) * b[j].scale) * static_cast<float>(I);
+        }
+    }
+}
+
+// Running state of one row's chain.
+template <Op O>
+struct Chain {
+    float o = 0.0f;
+    float L[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // pinned PTQ1 lanes
+
+    __device__ __forceinline__ void fold(const float *t, const void *__restrict__ act, uint32_t u) {
+        if constexpr (O == Op::PQ2_FUSED) {
+            o = __builtin_fmaf(t[0], t[1], o);
+        } else if constexpr (O == Op::PTQ1_PINNED) {
+            // dot_q8_groups_pinned, src/kernels.rs:1134-1146
+            const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float dd = t[8] * b[g].scale;
+                const uint32_t p0 = __float_as_uint(t[2 * g]), p1 = __float_as_uint(t[2 * g + 1]);
+                L[0] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p0 & 0xffffu)), dd, L[0]);
+                L[1] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p0 >> 16)), dd, L[1]);
+                L[2] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p1 & 0xffffu)), dd, L[2]);
+                L[3] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p1 >> 16)), dd, L[3]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < terms_per_unit<O>(); ++j) o = o + t[j];
+        }
+    }
+    __device__ __forceinline__ float result() const {
+        if constexpr (O == Op::PTQ1_PINNED) return (L[0] + L[1]) + (L[2] + L[3]);
+        return o;
+    }
+};
+
+template <Op O, int KS>
+__global__ __launch_bounds__(64 * KS) void k_mv(const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu,
+                                                 const void *__restrict__ act, float *__restrict__ out,
+                                                 int *__restrict__ err) {
+    extern __shared__ float lds[];
+    constexpr uint32_t UB = unit_bytes<O>();
+    constexpr int TPU = terms_per_unit<O>();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tile = blockIdx.x;
+    const uint32_t row_bytes = nu * UB;
+    const uint32_t left = rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(W + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    const uint32_t u0 = wave * nu / KS, u1 = (wave + 1) * nu / KS;
+
+    Chain<O> ch;
+    const uint32_t stride = nu * TPU + 1;
+    Raw<O> cur;
+    if (u0 < u1) load_unit<O>(cur, rs, u0 * trp * UB, trp, lane);
+    for (uint32_t u = u0; u < u1; ++u) {
+        Raw<O> nxt;
+        if (u + 1 < u1) load_unit<O>(nxt, rs, (u + 1) * trp * UB, trp, lane);
+        float t[TPU];
+        unit_terms<O>(cur, act, u, t);
+        if constexpr (KS == 1) {
+            ch.fold(t, act, u);
+        } else {
+#pragma unroll
+            for (int j = 0; j < TPU; ++j) lds[lane * stride + u * TPU + j] = t[j];
+        }
+        cur = nxt;
+    }
+    if constexpr (KS > 1) {
+        __syncthreads();
+        if (wave != 0) return;
+        const float *tr = lds + lane * stride;
+        for (uint32_t u = 0; u < nu; ++u) {
+            float t[TPU];
+#pragma unroll
+            for (int j = 0; j < TPU; ++j) t[j] = tr[u * TPU + j];
+            ch.fold(t, act, u);
+        }
+    }
+    if (lane < trows) {
+        const float o = ch.result();
+        out[static_cast<size_t>(tile) * kTile + lane] = o;
+        if (!finite(o)) raise_error(err, kErrNonfinite);
+    }
+}
+
+// ---- native -> tiled repack ------------------------------------------------------------
+// One thread per (row, unit).  Byte copies: this runs once per uploaded tensor.
+__global__ void k_repack(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, uint32_t kind, uint64_t rows,
+                         uint32_t nu) {
+    TiledFormat f;
+    tiled_format(kind, &f);
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= rows * nu) return;
+    const uint64_t r = idx / nu;
+    const uint32_t u = static_cast<uint32_t>(idx % nu);
+    const uint64_t row_bytes = static_cast<uint64_t>(nu) * f.unit_bytes;
+    const uint64_t tile = r / kTile;
+    const uint32_t lr = static_cast<uint32_t>(r % kTile);
+    const uint32_t trp = tile_rows_padded(rows, tile);
+    const uint8_t *s = src + r * row_bytes + static_cast<uint64_t>(u) * f.unit_bytes;
+    uint8_t *seg = dst + tile * kTile * row_bytes + static_cast<uint64_t>(u) * trp * f.unit_bytes;
+    for (uint32_t p = 0; p < f.npieces; ++p) {
+        uint8_t *d = seg + static_cast<uint64_t>(f.poff[p]) * trp + static_cast<uint64_t>(lr) * f.psize[p];
+        if (kind == kQ8_0 && p == 8) {
+            for (int j = 0; j < 4; ++j) {
+                d[2 * j] = s[34 * j];
+                d[2 * j + 1] = s[34 * j + 1];
+            }
+        } else {
+            for (uint32_t i = 0; i < f.psize[p]; ++i) d[i] = s[f.nsrc[p] + i];
+        }
+    }
+}
+
+template <Op O, int KS>
+int launch_ks(const MatvecArgs &a, const void *act, float *out, uint32_t nu) {
+    const uint32_t tiles = static_cast<uint32_t>((a.rows + kTile - 1) / kTile);
+    const size_t lds = KS > 1 ? sizeof(float) * kTile * (nu * terms_per_unit<O>() + 1) : 0;
+    hipLaunchKernelGGL((k_mv<O, KS>), dim3(tiles), dim3(64 * KS), lds, a.stream, a.w, static_cast<uint32_t>(a.rows),
+                       nu, act, out, a.err);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+constexpr size_t kFoldLds = 64 * 1024;
+
+// K is split across up to 16 wavefronts when the matrix has too few tiles to keep
+// every CU busy (aiming at ~8 resident wavefronts per CU), provided the fold's
+// term array fits in LDS.
+template <Op O>
+int launch_op(const MatvecArgs &a, const void *act, float *out) {
+    const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    uint32_t ks = 1;
+    while (ks < 16 && tiles * ks < 2048 && ks * 2 <= nu &&
+           sizeof(float) * kTile * (nu * terms_per_unit<O>() + 1) <= kFoldLds)
+        ks *= 2;
+    switch (ks) {
+    case 1: return launch_ks<O, 1>(a, act, out, nu);
+    case 2: return launch_ks<O, 2>(a, act, out, nu);
+    case 4: return launch_ks<O, 4>(a, act, out, nu);
+    case 8: return launch_ks<O, 8>(a, act, out, nu);
+    default: return launch_ks<O, 16>(a, act, out, nu);
+    }
+}
+
+}  // namespace
+
+bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows) {
+    if (rows == 0 || rows > 0xffffffffull) return false;
+    TiledFormat f;
+    if (!tiled_format(kind, &f) || cols % f.unit_weights) return false;
+    const uint64_t row_bytes = cols / f.unit_weights * f.unit_bytes;
+    return row_bytes * kTile < (1ull << 31);  // 32-bit in-tile offsets
+}
+
+int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols, uint64_t rows, hipStream_t s) {
+    TiledFormat f;
+    if (!tiled_format(kind, &f)) return -2;
+    const uint32_t nu = static_cast<uint32_t>(cols / f.unit_weights);
+    const uint64_t n = rows * nu;
+    hipLaunchKernelGGL(k_repack, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(native), static_cast<uint8_t *>(tiled), kind, rows, nu);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_matvec_tiled(const MatvecArgs &a) {
+    const size_t act_stride = a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
+                                                      : sizeof(Q8Block) * (a.cols / 32);
+    for (uint32_t tok = 0; tok < a.tokens; ++tok) {
+        const void *act = static_cast<const uint8_t *>(a.act) + act_stride * tok;
+        float *out = a.out + a.rows * tok;
+        int rc;
+        if (a.kind == kPTQ1) {
+            if (a.act_format == kActQ8K)
+                rc = launch_op<Op::PTQ1_Q8K>(a, act, out);
+            else
+                rc = a.pinned ? launch_op<Op::PTQ1_PINNED>(a, act, out) : launch_op<Op::PTQ1_SRC>(a, act, out);
+        } else if (a.kind == kPQ2) {
+            if (a.act_format != kActQ8K)
+                rc = launch_op<Op::PQ2_Q8>(a, act, out);
+            else
+                rc = a.pinned ? launch_op<Op::PQ2_FUSED>(a, act, out) : launch_op<Op::PQ2_UNFUSED>(a, act, out);
+        } else if (a.kind == kQ2_K) {
+            rc = launch_op<Op::Q2K>(a, act, out);
+        } else if (a.kind == kQ8_0) {
+            rc = launch_op<Op::Q8_0>(a, act, out);
+        } else {
+            return -2;
+        }
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+}  // namespace prism

@@ -16,6 +16,7 @@
 
 #include "../../include/prism_hip.h"
 #include "kernels.hpp"
+#include "tiled.hpp"
 
 using namespace prism;
 
@@ -27,6 +28,7 @@ struct Weight {
     uint64_t cols = 0, rows = 0, row_bytes = 0, bytes = 0;
     void *dev = nullptr;
     bool owned = false;
+    bool tiled = false;  // 64-row tiled device layout (tiled.hpp) instead of native rows
 };
 
 // Grow-only device scratch buffer.
@@ -158,7 +160,7 @@ int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, u
     a.out = out;
     a.err = c->err;
     a.stream = s;
-    int rc = launch_matvec(a);
+    int rc = w.tiled ? launch_matvec_tiled(a) : launch_matvec(a);
     if (rc == -2) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported matvec geometry");
     if (rc) return hip_fail(c, hipGetLastError(), "matvec launch");
     return PRISM_OK;
@@ -326,6 +328,34 @@ static int check_geometry(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64
     return PRISM_OK;
 }
 
+// Copies native device bytes into a context-owned buffer, repacked into the tiled
+// layout when the geometry allows it (the native copy serves every other shape).
+static prism_weight_id store_weight(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
+                                    const void *native, uint64_t bytes) {
+    const bool tiled = tiled_supported(kind, cols, rows);
+    const uint64_t row_bytes = bytes / rows;
+    const uint64_t dev_bytes = tiled ? tiled_bytes(rows, row_bytes) : bytes;
+    void *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, dev_bytes);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(weights)");
+    if (tiled) {
+        e = hipMemsetAsync(dev, 0, dev_bytes, c->stream);
+        if (e == hipSuccess && launch_repack(native, dev, kind, cols, rows, c->stream)) e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    } else {
+        e = hipMemcpy(dev, native, bytes, hipMemcpyDeviceToDevice);
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(c, e, "store weights");
+    }
+    const prism_weight_id id = add_weight(c, key, kind, cols, rows, bytes, true, dev);
+    c->weights[id].tiled = tiled;
+    c->resident += dev_bytes - bytes;
+    c->weights[id].bytes = dev_bytes;
+    return id;
+}
+
 prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
                                          const void *host, uint64_t bytes) {
     int rc = check_ready(c);
@@ -341,15 +371,32 @@ prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *c, uint64_t key, uint32_
     }
     if (c->max_resident && c->resident + bytes > c->max_resident)
         return fail(c, PRISM_ERR_RESOURCE, "resident weight budget exceeded");
-    void *dev = nullptr;
-    hipError_t e = hipMalloc(&dev, bytes);
-    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(weights)");
-    e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-        (void)hipFree(dev);
-        return hip_fail(c, e, "upload weights");
+    void *staging = nullptr;
+    hipError_t e = hipMalloc(&staging, bytes);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(weight staging)");
+    e = hipMemcpy(staging, host, bytes, hipMemcpyHostToDevice);
+    prism_weight_id id = e == hipSuccess ? store_weight(c, key, kind, cols, rows, staging, bytes)
+                                         : hip_fail(c, e, "upload weights");
+    (void)hipFree(staging);
+    return id;
+}
+
+prism_weight_id prism_hip_weight_acquire_device(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols,
+                                                uint64_t rows, const void *device_ptr, uint64_t bytes) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!device_ptr) return fail(c, PRISM_ERR_INVALID_INPUT, "null weight bytes");
+    rc = check_geometry(c, kind, cols, rows, bytes);
+    if (rc) return rc;
+    auto k = c->by_key.find(key);
+    if (k != c->by_key.end()) {
+        const Weight *w = find(c, k->second);
+        if (w && w->kind == kind && w->cols == cols && w->rows == rows) return k->second;
+        return fail(c, PRISM_ERR_INVALID_INPUT, "key already bound to a different tensor");
     }
-    return add_weight(c, key, kind, cols, rows, bytes, true, dev);
+    if (c->max_resident && c->resident + bytes > c->max_resident)
+        return fail(c, PRISM_ERR_RESOURCE, "resident weight budget exceeded");
+    return store_weight(c, key, kind, cols, rows, device_ptr, bytes);
 }
 
 prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,

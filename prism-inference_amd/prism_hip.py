@@ -79,6 +79,7 @@ def lib() -> ctypes.CDLL:
         "prism_hip_operation_count": (I64, [P, U32, U64, U64]),
         "prism_hip_supports": (I, [P, U32, U64, U64, I]),
         "prism_hip_weight_acquire": (I64, [P, U64, U32, U64, U64, P, U64]),
+        "prism_hip_weight_acquire_device": (I64, [P, U64, U32, U64, U64, P, U64]),
         "prism_hip_weight_wrap_device": (I64, [P, U32, U64, U64, P, U64]),
         "prism_hip_weight_release": (I, [P, I64]),
         "prism_hip_weight_release_all": (I, [P]),
@@ -179,6 +180,16 @@ class Context:
                                    dtype=np.uint8)
         key = next(_fresh_keys) if key is None else key
         wid = lib().prism_hip_weight_acquire(self._h, key & 0xFFFFFFFFFFFFFFFF, kind, cols, rows, _ptr(buf), buf.size)
+        if wid < 0:
+            self._check(int(wid))
+        return int(wid)
+
+    def weight_from_device(self, kind: int, cols: int, rows: int, tensor, key: int | None = None) -> int:
+        """Context-owned copy (tiled where supported) of native bytes in device memory."""
+        nbytes = tensor.numel() * tensor.element_size()
+        key = next(_fresh_keys) if key is None else key
+        wid = lib().prism_hip_weight_acquire_device(self._h, key & 0xFFFFFFFFFFFFFFFF, kind, cols, rows, _ptr(tensor),
+                                                    nbytes)
         if wid < 0:
             self._check(int(wid))
         return int(wid)
