@@ -26,7 +26,7 @@ SOURCES = ["quantize.hip", "matvec.hip", "mv_tiled.hip", "ffn.hip", "runtime.cpp
 FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-ffp-contract=off",
     "-fno-fast-math",

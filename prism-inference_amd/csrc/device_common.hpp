@@ -72,6 +72,42 @@ __device__ __forceinline__ uint32_t bload1(__amdgpu_buffer_rsrc_t r, uint32_t of
     return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
 }
 
+// ggml's vectorised expf polynomial, a published method restated by the reference at
+// src/kernels/pinned_activations.rs:26-62, with the same explicit fused multiply-adds.
+__device__ __forceinline__ float vector_exp(float value) {
+    const float z = __builtin_fmaf(value, __uint_as_float(0x3fb8aa3bu), 12582912.0f);
+    const float n = z - 12582912.0f;
+    float r = __builtin_fmaf(-n, __uint_as_float(0x3f317200u), value);
+    r = __builtin_fmaf(-n, __uint_as_float(0x35bfbe8eu), r);
+    const uint32_t e = __float_as_uint(z) << 23;
+    const float k = __uint_as_float(e + __float_as_uint(1.0f));
+    const float sq = r * r;
+    const float inner = __builtin_fmaf(__builtin_fmaf(__uint_as_float(0x3c072010u), r, __uint_as_float(0x3d2b9f17u)), sq,
+                                       __builtin_fmaf(__uint_as_float(0x3e2aaf33u), r, __uint_as_float(0x3efffedbu)));
+    const float poly = __builtin_fmaf(inner, sq, __uint_as_float(0x3f7ffff6u) * r);
+    if (fabsf(n) > 126.0f) {
+        const uint32_t shift = n <= 0.0f ? 0x82000000u : 0u;
+        const float s1 = __uint_as_float(shift + 0x7f000000u);
+        if (fabsf(n) > 192.0f) return s1 * s1;
+        const float s2 = __uint_as_float(e - shift);
+        return __builtin_fmaf(s2, poly, s2) * s1;
+    }
+    return __builtin_fmaf(poly, k, k);
+}
+
+// One SwiGLU element, h = up * silu(gate).  Source order (src/graph.rs:121-131,
+// src/kernels.rs:3365-3368): up * (g / (1 + exp(-g))).  Pinned order
+// (src/kernels/pinned_activations.rs:141-178): (g * up) / (1 + vexp(0 - g)) for the
+// first n/4*4 elements of the vector and (g * up) / (1 + exp(-g)) for the tail.
+__device__ __forceinline__ float swiglu_one(float gate, float up, uint64_t i, uint64_t n, int pinned) {
+    if (pinned) {
+        const float den = 1.0f + (i < n / 4 * 4 ? vector_exp(0.0f - gate) : expf(-gate));
+        return (gate * up) / den;
+    }
+    const float silu = gate / (1.0f + expf(-gate));
+    return up * silu;
+}
+
 __device__ __forceinline__ void raise_error(int *flag, int bits) {
     if (flag) __hip_atomic_fetch_or(flag, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -14,42 +14,13 @@
 
 namespace prism {
 
-__device__ float vector_exp(float value) {
-    const float z = __builtin_fmaf(value, __uint_as_float(0x3fb8aa3bu), 12582912.0f);
-    const float n = z - 12582912.0f;
-    float r = __builtin_fmaf(-n, __uint_as_float(0x3f317200u), value);
-    r = __builtin_fmaf(-n, __uint_as_float(0x35bfbe8eu), r);
-    const uint32_t e = __float_as_uint(z) << 23;
-    const float k = __uint_as_float(e + __float_as_uint(1.0f));
-    const float sq = r * r;
-    const float inner = __builtin_fmaf(__builtin_fmaf(__uint_as_float(0x3c072010u), r, __uint_as_float(0x3d2b9f17u)), sq,
-                                       __builtin_fmaf(__uint_as_float(0x3e2aaf33u), r, __uint_as_float(0x3efffedbu)));
-    const float poly = __builtin_fmaf(inner, sq, __uint_as_float(0x3f7ffff6u) * r);
-    if (fabsf(n) > 126.0f) {
-        const uint32_t shift = n <= 0.0f ? 0x82000000u : 0u;
-        const float s1 = __uint_as_float(shift + 0x7f000000u);
-        if (fabsf(n) > 192.0f) return s1 * s1;
-        const float s2 = __uint_as_float(e - shift);
-        return __builtin_fmaf(s2, poly, s2) * s1;
-    }
-    return __builtin_fmaf(poly, k, k);
-}
-
 __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ g, const float *__restrict__ u,
                                                 float *__restrict__ h, uint64_t n, uint64_t total, int pinned,
                                                 int *__restrict__ err) {
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= total) return;
     const uint64_t i = idx % n;
-    const float gate = g[idx], up = u[idx];
-    float r;
-    if (pinned) {
-        const float den = 1.0f + (i < n / 4 * 4 ? vector_exp(0.0f - gate) : expf(-gate));
-        r = (gate * up) / den;
-    } else {
-        const float silu = gate / (1.0f + expf(-gate));
-        r = up * silu;
-    }
+    const float r = swiglu_one(g[idx], u[idx], i, n, pinned);
     h[idx] = r;
     if (!finite(r)) raise_error(err, kErrNonfinite);
 }

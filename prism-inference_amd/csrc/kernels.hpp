@@ -11,8 +11,9 @@ constexpr int kErrNonfinite = 1;   // non-finite output / scale (PRISM_ERR_NONFI
 constexpr int kErrQuantRange = 2;  // activation quantizer overflow (PRISM_ERR_NONFINITE)
 constexpr int kErrInput = 4;       // non-finite activation input (PRISM_ERR_NONFINITE)
 
-// Activation-side formats consumed by the matvec kernels.
-enum ActFormat : int { kActQ8K = 0, kActQ8 = 1 };
+// Activation-side formats consumed by the matvec kernels.  kActF32: f32 input the
+// tiled kernels quantize in their prologue (contract in MatvecArgs::qcontract).
+enum ActFormat : int { kActQ8K = 0, kActQ8 = 1, kActF32 = 2 };
 
 // Which binary32 order a projection follows.
 //   kind PTQ1 + Q8   : src (dot_q8_groups) or pinned (dot_q8_groups_pinned)
@@ -22,16 +23,21 @@ enum ActFormat : int { kActQ8K = 0, kActQ8 = 1 };
 //   kind Q2_K + Q8K  : kquants::dot
 //   kind Q8_0 + Q8   : dot_legacy
 struct MatvecArgs {
-    uint32_t kind;
-    uint64_t cols, rows, row_bytes;
-    const uint8_t *w;  // device, rows*row_bytes
-    const void *act;   // device, token-major prepared blocks
-    int act_format;    // ActFormat
-    uint32_t tokens;
-    int pinned;        // pinned Q8 order (PTQ1) or fused FMA (PQ2 + Q8K)
-    float *out;        // device, [tokens][rows]
-    int *err;          // device error flag
-    hipStream_t stream;
+    uint32_t kind = 0;
+    uint64_t cols = 0, rows = 0, row_bytes = 0;
+    const uint8_t *w = nullptr;   // device, rows*row_bytes
+    const uint8_t *w2 = nullptr;  // tiled only: FFN up matrix; out then receives SwiGLU(gate, up)
+    const void *act = nullptr;    // device, token-major prepared blocks (or f32 rows)
+    int act_format = kActQ8K;     // ActFormat
+    int qcontract = 0;            // kActF32: Q8_K pinned flag, or Q8_0 contract (PRISM_Q8_*)
+    bool qcontract_is_q8k = false;  // kActF32: the prologue quantizes to Q8_K
+    uint32_t tokens = 1;
+    int pinned = 0;               // pinned Q8 order (PTQ1) or fused FMA (PQ2 + Q8K); SwiGLU order
+    float *out = nullptr;         // device, [tokens][rows]
+    const float *residual = nullptr;  // tiled only: added to every output row
+    int *err = nullptr;           // device error flag
+    hipStream_t stream = nullptr;
+    uint32_t cus = 256;           // compute units of the device
 };
 
 // Returns 0 on success, -1 when the launch failed, -2 when the shape is unsupported.
@@ -39,6 +45,9 @@ struct MatvecArgs {
 // the 64-row tiled layout of tiled.hpp.
 int launch_matvec(const MatvecArgs &a);
 int launch_matvec_tiled(const MatvecArgs &a);
+// Whether a kActF32 tiled call must be given prepared blocks instead (large matrices
+// run a separate quantize kernel; the prologue would repeat it per workgroup).
+bool tiled_needs_prepared(const MatvecArgs &a);
 // Whether (kind, cols, rows) can be stored tiled, and the native -> tiled repack
 // (the destination must hold tiled_bytes() and be zero-filled beforehand).
 bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows);

@@ -15,6 +15,7 @@
 // 0 folds them in unit order -- the same serial chain, only computed later.
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "quant_dev.hpp"
 #include "tiled.hpp"
 
 namespace prism {
@@ -346,56 +347,187 @@ struct Chain {
     }
 };
 
-template <Op O, int KS>
-__global__ __launch_bounds__(64 * KS) void k_mv(const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu,
-                                                 const void *__restrict__ act, float *__restrict__ out,
-                                                 int *__restrict__ err) {
-    extern __shared__ float lds[];
+// Kernel parameters (passed by value).
+struct MvParams {
+    const uint8_t *w[2];  // tiled weights; w[1] is the FFN up matrix when NMAT == 2
+    uint32_t rows, nu, cols;
+    const void *act;      // prepared blocks, or f32 input when the prologue quantizes
+    int qcontract;        // prologue quantizer: Q8_K pinned flag / Q8_0 contract
+    int pinned;           // SwiGLU order (NMAT == 2)
+    uint32_t ks, lpr;     // split mode: wavefronts per matrix, lanes per row
+    float *out;
+    const float *residual;
+    int *err;
+};
+
+template <Op O>
+constexpr bool act_is_q8k() {
+    return O == Op::PTQ1_Q8K || O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED || O == Op::Q2K;
+}
+
+// Prepared-activation bytes for `cols` inputs (one token).
+template <Op O>
+__host__ __device__ constexpr uint32_t act_bytes_for(uint32_t cols) {
+    return act_is_q8k<O>() ? cols / 256 * static_cast<uint32_t>(sizeof(Q8KBlock))
+                           : cols / 32 * static_cast<uint32_t>(sizeof(Q8Block));
+}
+
+__host__ __device__ constexpr uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
+
+// Big matrices: one wavefront per 64-row tile walks the whole row; the prepared
+// activation (global, wave-uniform) arrives through scalar loads and the chain
+// stays in registers.
+template <Op O>
+__global__ __launch_bounds__(64) void k_mv_rows(MvParams p) {
+    constexpr uint32_t UB = unit_bytes<O>();
+    const uint32_t lane = threadIdx.x;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t nu = p.nu, row_bytes = nu * UB;
+    const uint32_t left = p.rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    const void *act = p.act;
+    Chain<O> ch;
+    auto step = [&](const Raw<O> &w, uint32_t u) {
+        float t[terms_per_unit<O>()];
+        unit_terms<O>(w, act, u, t);
+        ch.fold(t, act, u);
+    };
+    // Two register buffers in ping-pong: the next unit's loads are in flight while the
+    // current one is decoded, and no buffer is copied (a copy would wait for the loads).
+    Raw<O> A, B;
+    uint32_t u = 0;
+    load_unit<O>(A, rs, 0, trp, lane);
+    while (u + 1 < nu) {
+        load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
+        step(A, u);
+        if (u + 2 < nu) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+        step(B, u + 1);
+        u += 2;
+    }
+    if (u < nu) step(A, u);
+    if (lane < trows) {
+        const size_t row = static_cast<size_t>(tile) * kTile + lane;
+        float o = ch.result();
+        if (p.residual) o = o + p.residual[row];
+        p.out[row] = o;
+        if (!finite(o)) raise_error(p.err, kErrNonfinite);
+    }
+}
+
+// Small matrices: a workgroup owns rw = 64/lpr rows of a tile; its ks wavefronts
+// (per matrix) and the lpr lane groups of each wavefront split the row's units
+// (lane group c of wavefront w takes units w*lpr+c, +ks*lpr, ...).  Each unit's
+// terms land in LDS and wavefront 0 folds them in unit order.  The activation is
+// staged in LDS by the prologue: either the prepared blocks are copied (COPY), or
+// the f32 input is quantized with the contract matvec_into uses (QUANT), which
+// makes the whole projection one launch.  NMAT == 2: gate (wavefronts 0..ks-1) and
+// up (ks..2ks-1) share the activation and the epilogue writes SwiGLU(gate, up).
+// The first unit's weight loads are issued before the prologue so that their
+// latency overlaps it.
+template <Op O, bool QUANT, int NMAT>
+__global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr uint32_t UB = unit_bytes<O>();
     constexpr int TPU = terms_per_unit<O>();
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t tile = blockIdx.x;
-    const uint32_t row_bytes = nu * UB;
-    const uint32_t left = rows - tile * kTile;
+    const uint32_t nwaves = blockDim.x >> 6;
+    const uint32_t ks = p.ks, lpr = p.lpr, rw = kTile / lpr;
+    const uint32_t mat = (NMAT == 2 && wave >= ks) ? 1u : 0u;
+    const uint32_t mw = wave - mat * ks;
+    const uint32_t tile = blockIdx.x / lpr, sub = blockIdx.x % lpr;
+    const uint32_t c = lane / rw, r = lane % rw;
+    const uint32_t kt = ks * lpr, kk = mw * lpr + c;
+    const uint32_t nu = p.nu, row_bytes = nu * UB;
+    const uint32_t left = p.rows - tile * kTile;
     const uint32_t trows = left < kTile ? left : kTile;
     const uint32_t trp = (trows + 7u) & ~7u;
-    const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc(W + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
-    const uint32_t u0 = wave * nu / KS, u1 = (wave + 1) * nu / KS;
+    const uint32_t tr = sub * rw + r;  // row within the tile
 
-    Chain<O> ch;
+    const uint32_t abytes = align16(act_bytes_for<O>(p.cols));
+    const uint32_t xbytes = QUANT ? 4u * p.cols : 0u;
     const uint32_t stride = nu * TPU + 1;
-    Raw<O> cur;
-    if (u0 < u1) load_unit<O>(cur, rs, u0 * trp * UB, trp, lane);
-    for (uint32_t u = u0; u < u1; ++u) {
-        Raw<O> nxt;
-        if (u + 1 < u1) load_unit<O>(nxt, rs, (u + 1) * trp * UB, trp, lane);
-        float t[TPU];
-        unit_terms<O>(cur, act, u, t);
-        if constexpr (KS == 1) {
-            ch.fold(t, act, u);
-        } else {
-#pragma unroll
-            for (int j = 0; j < TPU; ++j) lds[lane * stride + u * TPU + j] = t[j];
-        }
-        cur = nxt;
-    }
-    if constexpr (KS > 1) {
+    float *terms = reinterpret_cast<float *>(smem + abytes + xbytes) + mat * rw * stride;
+    float *res = reinterpret_cast<float *>(smem + abytes + xbytes) + NMAT * rw * stride;
+
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    Raw<O> A, B;
+    uint32_t u = kk;
+    if (u < nu) load_unit<O>(A, rs, u * trp * UB, trp, tr);
+
+    // ---- prologue: stage the activation in LDS -------------------------------------
+    if constexpr (QUANT) {
+        float *xs = reinterpret_cast<float *>(smem + abytes);
+        const float4 *src = static_cast<const float4 *>(p.act);
+        for (uint32_t i = threadIdx.x; i < p.cols / 4; i += blockDim.x) reinterpret_cast<float4 *>(xs)[i] = src[i];
         __syncthreads();
-        if (wave != 0) return;
-        const float *tr = lds + lane * stride;
-        for (uint32_t u = 0; u < nu; ++u) {
-            float t[TPU];
-#pragma unroll
-            for (int j = 0; j < TPU; ++j) t[j] = tr[u * TPU + j];
-            ch.fold(t, act, u);
+        int e = 0;
+        if constexpr (act_is_q8k<O>()) {
+            Q8KBlock *o = reinterpret_cast<Q8KBlock *>(smem);
+            const uint32_t nb = p.cols / 256;
+            for (uint32_t b = 4 * wave; b < nb; b += 4 * nwaves)
+                e |= q8k_blocks_wave(xs + 256 * b, nb - b < 4 ? nb - b : 4u, p.qcontract, o + b, lane);
+        } else {
+            Q8Block *o = reinterpret_cast<Q8Block *>(smem);
+            const uint32_t nb = p.cols / 32;
+            for (uint32_t b = 32 * wave; b < nb; b += 32 * nwaves)
+                e |= q8_0_blocks_wave(xs + 32 * b, nb - b < 32 ? nb - b : 32u, p.qcontract, o + b, lane);
         }
+        // Every workgroup sees the same input; the first one reports its errors.
+        if (e && lane == 0 && blockIdx.x == 0) raise_error(p.err, e);
+    } else {
+        const uint32_t *src = static_cast<const uint32_t *>(p.act);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(smem);
+        for (uint32_t i = threadIdx.x; i < act_bytes_for<O>(p.cols) / 4; i += blockDim.x) dst[i] = src[i];
     }
-    if (lane < trows) {
-        const float o = ch.result();
-        out[static_cast<size_t>(tile) * kTile + lane] = o;
-        if (!finite(o)) raise_error(err, kErrNonfinite);
+    __syncthreads();
+    const void *act = smem;
+
+    // ---- main loop: ping-pong over this lane's units --------------------------------
+    auto step = [&](const Raw<O> &w, uint32_t v) {
+        float t[TPU];
+        unit_terms<O>(w, act, v, t);
+#pragma unroll
+        for (int j = 0; j < TPU; ++j) terms[r * stride + v * TPU + j] = t[j];
+    };
+    while (u + kt < nu) {
+        load_unit<O>(B, rs, (u + kt) * trp * UB, trp, tr);
+        step(A, u);
+        if (u + 2 * kt < nu) load_unit<O>(A, rs, (u + 2 * kt) * trp * UB, trp, tr);
+        step(B, u + kt);
+        u += 2 * kt;
+    }
+    if (u < nu) step(A, u);
+    __syncthreads();
+
+    // ---- fold in unit order and epilogue ---------------------------------------------
+    const bool folder = mw == 0 && lane < rw;
+    const bool valid = tr < trows;
+    const size_t row = static_cast<size_t>(tile) * kTile + tr;
+    float o = 0.0f;
+    if (folder) {
+        Chain<O> ch;
+        const float *t = terms + lane * stride;
+        for (uint32_t v = 0; v < nu; ++v) ch.fold(t + v * TPU, act, v);
+        o = ch.result();
+    }
+    if constexpr (NMAT == 1) {
+        if (folder && valid) {
+            if (p.residual) o = o + p.residual[row];
+            p.out[row] = o;
+            if (!finite(o)) raise_error(p.err, kErrNonfinite);
+        }
+    } else {
+        if (folder) res[mat * rw + lane] = o;
+        __syncthreads();
+        if (wave == 0 && lane < rw && valid) {
+            const float h = swiglu_one(res[lane], res[rw + lane], row, p.rows, p.pinned);
+            p.out[row] = h;
+            if (!finite(h)) raise_error(p.err, kErrNonfinite);
+        }
     }
 }
 
@@ -428,35 +560,102 @@ __global__ void k_repack(const uint8_t *__restrict__ src, uint8_t *__restrict__ 
     }
 }
 
-template <Op O, int KS>
-int launch_ks(const MatvecArgs &a, const void *act, float *out, uint32_t nu) {
-    const uint32_t tiles = static_cast<uint32_t>((a.rows + kTile - 1) / kTile);
-    const size_t lds = KS > 1 ? sizeof(float) * kTile * (nu * terms_per_unit<O>() + 1) : 0;
-    hipLaunchKernelGGL((k_mv<O, KS>), dim3(tiles), dim3(64 * KS), lds, a.stream, a.w, static_cast<uint32_t>(a.rows),
-                       nu, act, out, a.err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+constexpr size_t kSplitLds = 64 * 1024;
+
+struct SplitPlan {
+    uint32_t ks, lpr;
+    size_t lds;
+};
+
+// Split-mode geometry: enough lane groups per row that the tiles cover every CU,
+// then enough wavefronts per workgroup for ~8 resident wavefronts per CU, never
+// more K-split ways than the row has units.
+template <Op O>
+bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t nmat, uint32_t cus, SplitPlan *pl) {
+    const uint64_t tiles = (rows + kTile - 1) / kTile;
+    uint32_t lpr = 1;
+    while (lpr < 8 && tiles * lpr < cus && lpr * 2 <= nu) lpr *= 2;
+    uint32_t ks = 1;
+    while (ks * 2 * nmat <= 16 && ks * 2 * lpr <= nu && tiles * lpr * ks * 2 * nmat <= 8ull * cus) ks *= 2;
+    // A quantizing prologue wants several wavefronts per workgroup: trade lane groups
+    // for wavefronts while the workgroup has fewer than four.
+    while (quant && ks * nmat < 4 && lpr > 1 && ks * 2 * nmat <= 16) {
+        lpr /= 2;
+        ks *= 2;
+    }
+    const uint32_t rw = kTile / lpr;
+    pl->ks = ks;
+    pl->lpr = lpr;
+    pl->lds = align16(act_bytes_for<O>(cols)) + (quant ? 4ull * cols : 0) +
+              sizeof(float) * nmat * rw * (nu * terms_per_unit<O>() + 1) + (nmat == 2 ? sizeof(float) * 2 * rw : 0);
+    return pl->lds <= kSplitLds;
 }
 
-constexpr size_t kFoldLds = 64 * 1024;
-
-// K is split across up to 16 wavefronts when the matrix has too few tiles to keep
-// every CU busy (aiming at ~8 resident wavefronts per CU), provided the fold's
-// term array fits in LDS.
 template <Op O>
 int launch_op(const MatvecArgs &a, const void *act, float *out) {
     const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
-    uint32_t ks = 1;
-    while (ks < 16 && tiles * ks < 2048 && ks * 2 <= nu &&
-           sizeof(float) * kTile * (nu * terms_per_unit<O>() + 1) <= kFoldLds)
-        ks *= 2;
-    switch (ks) {
-    case 1: return launch_ks<O, 1>(a, act, out, nu);
-    case 2: return launch_ks<O, 2>(a, act, out, nu);
-    case 4: return launch_ks<O, 4>(a, act, out, nu);
-    case 8: return launch_ks<O, 8>(a, act, out, nu);
-    default: return launch_ks<O, 16>(a, act, out, nu);
+    const bool quant = a.act_format == kActF32;
+    const uint32_t nmat = a.w2 ? 2u : 1u;
+    MvParams p{};
+    p.w[0] = a.w;
+    p.w[1] = a.w2 ? a.w2 : a.w;
+    p.rows = static_cast<uint32_t>(a.rows);
+    p.nu = nu;
+    p.cols = static_cast<uint32_t>(a.cols);
+    p.act = act;
+    p.qcontract = a.qcontract;
+    p.pinned = a.pinned;
+    p.out = out;
+    p.residual = a.residual;
+    p.err = a.err;
+    if (!quant && nmat == 1 && tiles >= a.cus) {
+        hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
     }
+    SplitPlan pl;
+    if (!plan_split<O>(a.rows, nu, p.cols, quant, nmat, a.cus, &pl)) return -2;
+    p.ks = pl.ks;
+    p.lpr = pl.lpr;
+    const dim3 grid(static_cast<uint32_t>(tiles * pl.lpr)), block(64 * pl.ks * nmat);
+    if (nmat == 2) {
+        if (!quant) return -2;
+        hipLaunchKernelGGL((k_mv_split<O, true, 2>), grid, block, pl.lds, a.stream, p);
+    } else if (quant) {
+        hipLaunchKernelGGL((k_mv_split<O, true, 1>), grid, block, pl.lds, a.stream, p);
+    } else {
+        hipLaunchKernelGGL((k_mv_split<O, false, 1>), grid, block, pl.lds, a.stream, p);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <Op O>
+bool op_needs_prepared(const MatvecArgs &a) {
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    if (a.w2) return false;
+    if (tiles >= a.cus) return true;
+    SplitPlan pl;
+    const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    return !plan_split<O>(a.rows, nu, static_cast<uint32_t>(a.cols), true, 1, a.cus, &pl);
+}
+
+// Selects the arithmetic order from (kind, activation format, pinned): the orders of
+// dot_q8_groups / dot_q8_groups_pinned / dot_ptq1_q8k / dot_pq2::<FUSED> /
+// kquants::dot / dot_legacy (src/kernels.rs:941-1248, src/kernels/kquants.rs:346-430).
+template <typename F>
+int dispatch(const MatvecArgs &a, F &&f) {
+    const bool q8k = a.act_format == kActQ8K || (a.act_format == kActF32 && a.qcontract_is_q8k);
+    if (a.kind == kPTQ1) {
+        if (q8k) return f.template operator()<Op::PTQ1_Q8K>();
+        return a.pinned ? f.template operator()<Op::PTQ1_PINNED>() : f.template operator()<Op::PTQ1_SRC>();
+    }
+    if (a.kind == kPQ2) {
+        if (!q8k) return f.template operator()<Op::PQ2_Q8>();
+        return a.pinned ? f.template operator()<Op::PQ2_FUSED>() : f.template operator()<Op::PQ2_UNFUSED>();
+    }
+    if (a.kind == kQ2_K) return f.template operator()<Op::Q2K>();
+    if (a.kind == kQ8_0) return f.template operator()<Op::Q8_0>();
+    return -2;
 }
 
 }  // namespace
@@ -480,32 +679,20 @@ int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols,
 }
 
 int launch_matvec_tiled(const MatvecArgs &a) {
-    const size_t act_stride = a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
-                                                      : sizeof(Q8Block) * (a.cols / 32);
+    const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
+                             : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
+                                                       : sizeof(Q8Block) * (a.cols / 32);
     for (uint32_t tok = 0; tok < a.tokens; ++tok) {
-        const void *act = static_cast<const uint8_t *>(a.act) + act_stride * tok;
+        const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;
         float *out = a.out + a.rows * tok;
-        int rc;
-        if (a.kind == kPTQ1) {
-            if (a.act_format == kActQ8K)
-                rc = launch_op<Op::PTQ1_Q8K>(a, act, out);
-            else
-                rc = a.pinned ? launch_op<Op::PTQ1_PINNED>(a, act, out) : launch_op<Op::PTQ1_SRC>(a, act, out);
-        } else if (a.kind == kPQ2) {
-            if (a.act_format != kActQ8K)
-                rc = launch_op<Op::PQ2_Q8>(a, act, out);
-            else
-                rc = a.pinned ? launch_op<Op::PQ2_FUSED>(a, act, out) : launch_op<Op::PQ2_UNFUSED>(a, act, out);
-        } else if (a.kind == kQ2_K) {
-            rc = launch_op<Op::Q2K>(a, act, out);
-        } else if (a.kind == kQ8_0) {
-            rc = launch_op<Op::Q8_0>(a, act, out);
-        } else {
-            return -2;
-        }
+        const int rc = dispatch(a, [&]<Op O>() { return launch_op<O>(a, act, out); });
         if (rc) return rc;
     }
     return 0;
+}
+
+bool tiled_needs_prepared(const MatvecArgs &a) {
+    return dispatch(a, [&]<Op O>() { return op_needs_prepared<O>(a) ? 1 : 0; }) == 1;
 }
 
 }  // namespace prism

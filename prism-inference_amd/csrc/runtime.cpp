@@ -59,6 +59,7 @@ int contract_for(uint32_t kind, uint64_t cols, int pinned) {
 
 struct prism_hip_ctx {
     int device = 0;
+    uint32_t cus = 256;
     uint64_t max_resident = 0, resident = 0;
     hipStream_t stream = nullptr;
     std::string identity, last_error;
@@ -145,8 +146,8 @@ size_t act_bytes(int contract, uint64_t cols, uint32_t tokens) {
                          : sizeof(prism_q8_block) * (cols / 32) * tokens;
 }
 
-int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
-           float *out, hipStream_t s) {
+MatvecArgs matvec_args(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
+                       float *out, hipStream_t s) {
     MatvecArgs a;
     a.kind = w.kind;
     a.cols = w.cols;
@@ -160,21 +161,52 @@ int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, u
     a.out = out;
     a.err = c->err;
     a.stream = s;
-    int rc = w.tiled ? launch_matvec_tiled(a) : launch_matvec(a);
+    a.cus = c->cus;
+    return a;
+}
+
+int run_matvec(prism_hip_ctx *c, const MatvecArgs &a, bool tiled) {
+    int rc = tiled ? launch_matvec_tiled(a) : launch_matvec(a);
     if (rc == -2) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported matvec geometry");
     if (rc) return hip_fail(c, hipGetLastError(), "matvec launch");
     return PRISM_OK;
 }
 
+int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
+           float *out, hipStream_t s) {
+    return run_matvec(c, matvec_args(c, w, act_format, act, tokens, pinned, out, s), w.tiled);
+}
+
+// f32 input for a tiled weight, quantized in the kernel prologue with the contract
+// matvec_into would use; `residual` is added to every output row.
+MatvecArgs f32_args(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
+                    const float *residual, hipStream_t s) {
+    MatvecArgs a = matvec_args(c, w, kActF32, x, tokens, pinned, out, s);
+    const int contract = contract_for(w.kind, w.cols, pinned);
+    a.qcontract_is_q8k = contract == 0;
+    a.qcontract = contract == 0 ? pinned : contract == 2 ? PRISM_Q8_PINNED_NATIVE : (pinned ? PRISM_Q8_PINNED : PRISM_Q8_SOURCE);
+    a.residual = residual;
+    return a;
+}
+
 // Quantize device floats with the contract matvec_into would use, then project.
 int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
-                    DevBuf &scratch, hipStream_t s) {
+                    DevBuf &scratch, hipStream_t s, const float *residual = nullptr) {
+    if (w.tiled) {
+        MatvecArgs a = f32_args(c, w, x, tokens, pinned, out, residual, s);
+        if (!tiled_needs_prepared(a)) return run_matvec(c, a, true);
+    }
     const int contract = contract_for(w.kind, w.cols, pinned);
     int rc = ensure(c, scratch, act_bytes(contract, w.cols, tokens));
     if (rc) return rc;
     rc = quantize(c, contract, x, w.cols, tokens, pinned, scratch.p, s);
     if (rc) return rc;
-    return matvec(c, w, contract == 0 ? kActQ8K : kActQ8, scratch.p, tokens, pinned, out, s);
+    MatvecArgs a = matvec_args(c, w, contract == 0 ? kActQ8K : kActQ8, scratch.p, tokens, pinned, out, s);
+    if (w.tiled) a.residual = residual;
+    rc = run_matvec(c, a, w.tiled);
+    if (!rc && residual && !w.tiled && launch_add_residual(out, residual, w.rows * tokens, c->err, s))
+        return hip_fail(c, hipGetLastError(), "residual launch");
+    return rc;
 }
 
 bool eligible(uint32_t kind, uint64_t cols, uint64_t rows, int path) {
@@ -220,29 +252,42 @@ int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Wei
         return fail(c, PRISM_ERR_INVALID_INPUT, "gate/up geometry differs");
     if (d && (d->cols != g.rows || d->rows != g.cols))
         return fail(c, PRISM_ERR_INVALID_INPUT, "down geometry does not match gate/up");
-    int rc = ensure(c, c->gate, sizeof(float) * g.rows);
-    if (!rc) rc = ensure(c, c->up, sizeof(float) * g.rows);
-    if (rc) return rc;
-    const int contract = contract_for(g.kind, g.cols, pinned);
-    rc = ensure(c, c->act, act_bytes(contract, g.cols, 1));
-    if (!rc) rc = quantize(c, contract, x, g.cols, 1, pinned, c->act.p, s);
-    if (!rc) rc = matvec(c, g, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->gate.p), s);
-    if (!rc) rc = matvec(c, u, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->up.p), s);
-    if (rc) return rc;
     float *hv = h;
+    int rc = PRISM_OK;
     if (!hv) {
         rc = ensure(c, c->h, sizeof(float) * g.rows);
         if (rc) return rc;
         hv = static_cast<float *>(c->h.p);
     }
-    if (launch_swiglu(static_cast<float *>(c->gate.p), static_cast<float *>(c->up.p), hv, g.rows, 1, pinned, c->err, s))
-        return hip_fail(c, hipGetLastError(), "swiglu launch");
+    bool fused = false;
+    if (g.tiled && u.tiled) {
+        // gate, up and SwiGLU in one launch, x quantized in the prologue.
+        MatvecArgs a = f32_args(c, g, x, 1, pinned, hv, nullptr, s);
+        a.w2 = static_cast<const uint8_t *>(u.dev);
+        if (!tiled_needs_prepared(a)) {
+            rc = run_matvec(c, a, true);
+            if (rc) return rc;
+            fused = true;
+        }
+    }
+    if (!fused) {
+        rc = ensure(c, c->gate, sizeof(float) * g.rows);
+        if (!rc) rc = ensure(c, c->up, sizeof(float) * g.rows);
+        if (rc) return rc;
+        const int contract = contract_for(g.kind, g.cols, pinned);
+        rc = ensure(c, c->act, act_bytes(contract, g.cols, 1));
+        if (!rc) rc = quantize(c, contract, x, g.cols, 1, pinned, c->act.p, s);
+        if (!rc)
+            rc = matvec(c, g, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->gate.p), s);
+        if (!rc)
+            rc = matvec(c, u, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->up.p), s);
+        if (rc) return rc;
+        if (launch_swiglu(static_cast<float *>(c->gate.p), static_cast<float *>(c->up.p), hv, g.rows, 1, pinned, c->err,
+                          s))
+            return hip_fail(c, hipGetLastError(), "swiglu launch");
+    }
     if (!d) return PRISM_OK;
-    rc = project_f32_dev(c, *d, hv, 1, pinned, out, c->act2, s);
-    if (rc) return rc;
-    if (residual && launch_add_residual(out, residual, d->rows, c->err, s))
-        return hip_fail(c, hipGetLastError(), "residual launch");
-    return PRISM_OK;
+    return project_f32_dev(c, *d, hv, 1, pinned, out, c->act2, s, residual);
 }
 
 }  // namespace
@@ -263,6 +308,7 @@ prism_hip_ctx *prism_hip_create(int device, uint64_t max_resident_bytes, uint32_
         delete c;
         return nullptr;
     }
+    c->cus = static_cast<uint32_t>(prop.multiProcessorCount);
     char buf[256];
     std::snprintf(buf, sizeof buf, "prism-hip/%s/%d-cu/exact-scalar-order", prop.gcnArchName, prop.multiProcessorCount);
     c->identity = buf;

@@ -261,6 +261,31 @@ def test_gpu_project_q8_prepared_codes(ctx, kind, rows, cols):
     ctx.release(wid)
 
 
+# ---- large matrices: one wavefront per 64-row tile (>= one tile per CU) ----------------
+
+@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 256), (ph.KIND_PQ2, 256), (ph.KIND_PQ2, 384),
+                                       (ph.KIND_Q2_K, 256), (ph.KIND_Q8_0, 256)])
+def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
+    """rows spans more 64-row tiles than the device has CUs (the one-wavefront-per-tile
+    kernel with scalar activation loads), with a partial last tile."""
+    import oracle
+
+    import hiprt
+
+    rows = 64 * hiprt.cu_count(0) + 37
+    w = synth.weights(kind, rows, cols, seed=17) if kind != ph.KIND_PQ2 else synth.pq2_weights(rows, cols, 17, 4)
+    x = synth.activations(cols, seed=18)
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, x, pinned, threads=THREADS)
+        assert_bits_equal(ctx.project_f32(wid, rows, x, pinned=pinned), ref, f"rows kind={kind} pinned={pinned}")
+    if kind in (ph.KIND_PTQ1, ph.KIND_Q8_0) or (kind == ph.KIND_PQ2 and cols % 256):
+        act = oracle.quantize_q8_0(x, 1)
+        ref = oracle.project_q8(kind, cols, rows, w, act, True, threads=THREADS)
+        assert_bits_equal(ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=True), ref, "rows q8")
+    ctx.release(wid)
+
+
 # ---- multi-token, groups, backend op -------------------------------------------------
 
 def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
