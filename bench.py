@@ -148,7 +148,7 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
             "avg_us": t * 1e6, "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM}
 
 
-def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 3):
+def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 20):
     w = synth.ptq1_weights(rows, cols, seed=9)
     wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
     X = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=10, tokens=M))
@@ -224,7 +224,7 @@ def main() -> int:
             log(f"matvec kind={kind} {rows}x{cols}: {r['avg_us']:.2f} us, {r['GBps']:.1f} GB/s")
             extras["matvec"].append(r)
         extras["prefill_ptq1_6144x2048"] = []
-        for M in (128, 512):
+        for M in (128, 512, 2048):
             r = bench_prefill(ctx, M)
             log(f"prefill M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
             extras["prefill_ptq1_6144x2048"].append(r)

@@ -68,7 +68,7 @@ struct prism_hip_ctx {
     std::map<uint64_t, int64_t> by_key;
     int64_t next_id = 1;
     int *err = nullptr;  // device error flag
-    DevBuf x, act, act2, out, gate, up, h, res;
+    DevBuf x, act, act2, out, gate, up, h, res, pre;
 };
 
 namespace {
@@ -189,9 +189,20 @@ MatvecArgs f32_args(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t 
     return a;
 }
 
+// Token count from which f32 projections of PTQ1 weights (source contract) run as one
+// tiled-prefill GEMM instead of one matvec per token.
+constexpr uint32_t kPrefillMinTokens = 16;
+
 // Quantize device floats with the contract matvec_into would use, then project.
 int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
                     DevBuf &scratch, hipStream_t s, const float *residual = nullptr) {
+    if (w.tiled && tokens >= kPrefillMinTokens && !residual && prefill_supported(w.kind, w.cols, w.rows, pinned)) {
+        int rc = ensure(c, c->pre, prefill_scratch_bytes(w.cols, tokens));
+        if (rc) return rc;
+        if (launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, c->pre.p, c->err, s))
+            return hip_fail(c, hipGetLastError(), "prefill launch");
+        return PRISM_OK;
+    }
     if (w.tiled) {
         MatvecArgs a = f32_args(c, w, x, tokens, pinned, out, residual, s);
         if (!tiled_needs_prepared(a)) return run_matvec(c, a, true);
@@ -320,7 +331,7 @@ void prism_hip_destroy(prism_hip_ctx *c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     prism_hip_weight_release_all(c);
-    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res})
+    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res, &c->pre})
         if (b->p) (void)hipFree(b->p);
     if (c->err) (void)hipFree(c->err);
     if (c->stream) (void)hipStreamDestroy(c->stream);

@@ -303,6 +303,23 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
         ctx.release(wid)
 
 
+@pytest.mark.parametrize("rows,cols,M", [(200, 2048, 16), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128)])
+def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
+    """PTQ1 source-contract prefill runs as one f16-MFMA GEMM from 16 tokens on; every
+    token row must equal the reference's per-token matvec bit for bit (partial row
+    tiles, partial token tiles, several token workgroups)."""
+    import oracle
+
+    w = synth.ptq1_weights(rows, cols, seed=rows + M)
+    X = synth.activations(cols, seed=M, tokens=M)
+    X[3] *= 1e-3  # a token with small scales
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
+    ref = oracle.prefill(ph.KIND_PTQ1, cols, rows, w, X, False, threads=THREADS)
+    assert_bits_equal(ctx.prefill(wid, rows, X, pinned=False), ref, f"prefill gemm {rows}x{cols} M={M}")
+    assert_bits_equal(ctx.mul_mat(wid, rows, X), ref, "mul_mat gemm")
+    ctx.release(wid)
+
+
 def test_gpu_project_f32_group_siblings(ctx):
     import oracle
 
