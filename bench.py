@@ -4,9 +4,14 @@
 Headline workload (one "step"): the Qwen35-shaped dense FFN decode step at batch 1
 with Q2_K weights -- quantize x (f32 -> Q8_K), gate and up matvecs 2048->6144,
 SwiGLU, quantize h, down matvec 6144->2048 -- in the public (source) arithmetic
-contract.  Weights are rotated over >= 1 GiB of distinct device copies so every
-step streams them from HBM; steps are captured in HIP graphs on the library's
-stream and timed with HIP events on that stream.
+contract.  It runs as two kernels (gate+up+SwiGLU, down).  Weights are rotated over
+>= 1 GiB of distinct device copies so every step streams them from HBM; steps are
+captured in HIP graphs on the library's stream and timed with HIP events there.
+
+The roofline entry is the step's dominant kernel, the fused gate+up+SwiGLU launch,
+timed with HIP events around back-to-back launches on the same stream.  Its HBM
+traffic comes from the rocprof FETCH_SIZE / WRITE_SIZE summaries committed under
+profiles/ (scaled by a plain device copy of known size; --calibrate-copy runs it).
 
 Prints ONE JSON line on rank 0 (the only rank: this build runs on one GPU).
 """
@@ -65,9 +70,15 @@ class Rotation:
 
 def ffn_step_bytes() -> int:
     """Algorithmic HBM bytes of one FFN step: packed weights at native block size, the f32
-    input, gate/up/down f32 outputs and the f32 SwiGLU vector read by its quantizer."""
+    input, the f32 SwiGLU vector (written by the first kernel, read by the second) and
+    the f32 output."""
     w = 3 * FFN * HIDDEN // 256 * 84
-    return w + 4 * HIDDEN + 2 * 4 * FFN + 4 * FFN + 4 * HIDDEN
+    return w + 4 * HIDDEN + 2 * 4 * FFN + 4 * HIDDEN
+
+
+def gateup_bytes() -> int:
+    """Algorithmic bytes of the gate+up+SwiGLU kernel: both weight matrices, x, and h."""
+    return 2 * FFN * HIDDEN // 256 * 84 + 4 * HIDDEN + 4 * FFN
 
 
 def bench_ffn(ctx: ph.Context, steps: int, warmup: int):
@@ -110,7 +121,71 @@ def bench_ffn(ctx: ph.Context, steps: int, warmup: int):
     y = out.to_numpy(np.float32)
     assert np.isfinite(y).all()
     ms = e0.elapsed_ms(e1) / steps
+    del graphs
+    for r in (g, u, d):
+        r.release(ctx)
     return ms, wall / steps * 1e3, copies
+
+
+def bench_gateup_kernel(ctx: ph.Context, launches: int = 400):
+    """The FFN step's dominant kernel alone: gate+up+SwiGLU (x quantized in its prologue),
+    back-to-back launches over rotated weight copies, HIP events on the library stream."""
+    per_copy = 2 * FFN * HIDDEN // 256 * 84
+    copies = math.ceil(ROTATE_BYTES / per_copy)
+    g = Rotation(ctx, ph.KIND_Q2_K, FFN, HIDDEN, synth.q2k_weights(FFN, HIDDEN, seed=111), copies)
+    u = Rotation(ctx, ph.KIND_Q2_K, FFN, HIDDEN, synth.q2k_weights(FFN, HIDDEN, seed=112), copies)
+    x = hiprt.DeviceBuffer.from_numpy(synth.activations(HIDDEN, seed=113))
+    h = hiprt.DeviceBuffer(4 * FFN)
+    stream = ctx.stream()
+    for i in range(min(copies, 16)):
+        ctx.ffn_chain_device(g.ids[i], u.ids[i], 0, x, None, False, h, None, stream)
+    assert ctx.sync() == 0
+    e0, e1 = hiprt.Event(), hiprt.Event()
+    e0.record(stream)
+    for i in range(launches):
+        ctx.ffn_chain_device(g.ids[i % copies], u.ids[i % copies], 0, x, None, False, h, None, stream)
+    e1.record(stream)
+    e1.synchronize()
+    assert ctx.sync() == 0
+    t = e0.elapsed_ms(e1) / launches * 1e-3
+    g.release(ctx)
+    u.release(ctx)
+    return {"avg_us": t * 1e6, "bytes_per_launch": gateup_bytes(), "GBps": gateup_bytes() / t / 1e9,
+            "copies": copies}
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch of a kernel from a committed rocprof summary
+    (profiles/<name>): lines 'fetch_kib_per_dispatch: X', 'write_kib_per_dispatch: Y',
+    'copy_fetch_scale: A', 'copy_write_scale: B' (counter KiB -> bytes of a plain copy).
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if ":" in line:
+                k, v = line.split(":", 1)
+                try:
+                    vals[k.strip().strip("-* `")] = float(v.strip().strip("`"))
+                except ValueError:
+                    pass
+    need = ("fetch_kib_per_dispatch", "write_kib_per_dispatch", "copy_fetch_scale", "copy_write_scale")
+    if not all(k in vals for k in need):
+        return None
+    return vals["fetch_kib_per_dispatch"] * vals["copy_fetch_scale"] + \
+        vals["write_kib_per_dispatch"] * vals["copy_write_scale"]
+
+
+def calibrate_copy(nbytes: int = 256 << 20, reps: int = 10) -> int:
+    """A plain device-to-device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE."""
+    a, b = hiprt.DeviceBuffer(nbytes), hiprt.DeviceBuffer(nbytes)
+    for _ in range(reps):
+        hiprt.copy_d2d(b.ptr, a.ptr, nbytes)
+    hiprt.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": nbytes, "reps": reps}), flush=True)
+    return 0
 
 
 def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launches: int = 200):
@@ -197,6 +272,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--prefill-only", default="", help="comma-separated token counts: time only the prefill GEMM")
+    ap.add_argument("--matvec-only", default="", help="comma-separated kind:rows:cols: time only these matvecs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -205,14 +283,24 @@ def main() -> int:
     if hiprt.device_count() < 1:
         print("bench.py: no HIP device", file=sys.stderr)
         return 1
+    if args.calibrate_copy:
+        return calibrate_copy()
     ctx = ph.Context(0)
     log(ctx.identity)
+    if args.prefill_only or args.matvec_only:
+        for M in filter(None, args.prefill_only.split(",")):
+            print(json.dumps(bench_prefill(ctx, int(M))), flush=True)
+        for spec in filter(None, args.matvec_only.split(",")):
+            kind, rows, cols = (int(v) for v in spec.split(":"))
+            print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols)), flush=True)
+        ctx.close()
+        return 0
     ms, wall_ms, copies = bench_ffn(ctx, args.steps, args.warmup)
     nbytes = ffn_step_bytes()
     value = nbytes / (ms * 1e-3) / 1e9
     log(f"ffn step: {ms * 1e3:.2f} us/step (wall {wall_ms * 1e3:.2f}), {value:.1f} GB/s")
-    kern = bench_matvec_kernel(ctx, ph.KIND_Q2_K, FFN, HIDDEN)
-    log(f"q2k matvec {FFN}x{HIDDEN}: {kern['avg_us']:.2f} us, {kern['GBps']:.1f} GB/s")
+    kern = bench_gateup_kernel(ctx)
+    log(f"gate+up+SwiGLU kernel: {kern['avg_us']:.2f} us, {kern['GBps']:.1f} GB/s")
     extras = {}
     if not args.no_extras:
         extras["matvec"] = []
@@ -250,9 +338,10 @@ def main() -> int:
                    "bytes_per_step": nbytes, "frac_hbm_peak": round(value * 1e9 / PEAK_HBM, 4),
                    "tokens_per_s": round(1e3 / ms, 1)},
         "roofline": {"bound": "hbm", "achieved": round(kern["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": round(kern["frac_hbm"], 4), "traffic": None,
-                     "kernel": f"Q2_K x Q8_K matvec {FFN}x{HIDDEN}", "bytes_per_launch": kern["bytes_per_launch"],
-                     "avg_launch_us": round(kern["avg_us"], 3)},
+                     "frac": round(kern["GBps"] * 1e9 / PEAK_HBM, 4),
+                     "traffic": measured_traffic("ffn_gateup_traffic.md"),
+                     "kernel": "k_mv_split<Q2K, quantizing prologue, gate+up> (FFN gate+up+SwiGLU, 2x 6144x2048 Q2_K)",
+                     "bytes_per_launch": kern["bytes_per_launch"], "avg_launch_us": round(kern["avg_us"], 3)},
         "cpu_baseline": cpu,
     }
     if extras:

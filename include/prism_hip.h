@@ -173,7 +173,8 @@ int prism_hip_quantize_q8_device(prism_hip_ctx *ctx, const float *x, uint64_t co
  * PRISM_PATH_F32 floats quantized on the fly) into device out[tokens][rows]. */
 int prism_hip_project_device(prism_hip_ctx *ctx, prism_weight_id w, int path, const void *act, uint32_t tokens,
                              int pinned, float *out, void *stream);
-/* FFN chain on device pointers (h may be NULL; when set it receives the SwiGLU vector). */
+/* FFN chain on device pointers (h may be NULL; when set it receives the SwiGLU vector).
+ * down == 0 is project_f32_ffn_swiglu: out receives the SwiGLU vector (ffn floats). */
 int prism_hip_ffn_chain_device(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                                const float *x, const float *residual, int pinned, float *out, float *h,
                                void *stream);

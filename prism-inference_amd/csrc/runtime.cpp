@@ -704,10 +704,13 @@ int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weig
                                void *stream) {
     int rc = check_ready(c);
     if (rc) return rc;
-    const Weight *g = find(c, gid), *u = find(c, uid), *d = find(c, did);
-    if (!g || !u || !d || !x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
-    if (d->kind != g->kind) return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind");
-    return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, stream ? static_cast<hipStream_t>(stream) : c->stream);
+    const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
+    if (!g || !u || (did && !d) || !x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
+    if (d && d->kind != g->kind) return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind");
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    // Without a down projection the call is project_f32_ffn_swiglu: out receives h.
+    if (!d) return ffn_chain_impl(c, *g, *u, nullptr, x, nullptr, pinned, nullptr, out, s);
+    return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, s);
 }
 
 int prism_hip_sync(prism_hip_ctx *c, void *stream) {
