@@ -13,6 +13,8 @@
 // Small matrices split K across the KS wavefronts of a workgroup: each wavefront
 // computes the per-unit terms of its K range, the terms meet in LDS, and wavefront
 // 0 folds them in unit order -- the same serial chain, only computed later.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "quant_dev.hpp"
@@ -374,6 +376,11 @@ __host__ __device__ constexpr uint32_t act_bytes_for(uint32_t cols) {
 
 __host__ __device__ constexpr uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
+template <Op O>
+struct ActBlock {
+    using type = typename std::conditional<act_is_q8k<O>(), Q8KBlock, Q8Block>::type;
+};
+
 // Big matrices: one wavefront per 64-row tile walks the whole row; the prepared
 // activation (global, wave-uniform) arrives through scalar loads and the chain
 // stays in registers.
@@ -447,10 +454,9 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
     const uint32_t tr = sub * rw + r;  // row within the tile
 
     const uint32_t abytes = align16(act_bytes_for<O>(p.cols));
-    const uint32_t xbytes = QUANT ? 4u * p.cols : 0u;
     const uint32_t stride = nu * TPU + 1;
-    float *terms = reinterpret_cast<float *>(smem + abytes + xbytes) + mat * rw * stride;
-    float *res = reinterpret_cast<float *>(smem + abytes + xbytes) + NMAT * rw * stride;
+    float *terms = reinterpret_cast<float *>(smem + abytes) + mat * rw * stride;
+    float *res = reinterpret_cast<float *>(smem + abytes) + NMAT * rw * stride;
 
     const __amdgpu_buffer_rsrc_t rs =
         make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
@@ -460,28 +466,29 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
 
     // ---- prologue: stage the activation in LDS -------------------------------------
     if constexpr (QUANT) {
-        float *xs = reinterpret_cast<float *>(smem + abytes);
-        const float4 *src = static_cast<const float4 *>(p.act);
-        for (uint32_t i = threadIdx.x; i < p.cols / 4; i += blockDim.x) reinterpret_cast<float4 *>(xs)[i] = src[i];
-        __syncthreads();
-        int e = 0;
-        if constexpr (act_is_q8k<O>()) {
-            Q8KBlock *o = reinterpret_cast<Q8KBlock *>(smem);
-            const uint32_t nb = p.cols / 256;
-            for (uint32_t b = 4 * wave; b < nb; b += 4 * nwaves)
-                e |= q8k_blocks_wave(xs + 256 * b, nb - b < 4 ? nb - b : 4u, p.qcontract, o + b, lane);
-        } else {
-            Q8Block *o = reinterpret_cast<Q8Block *>(smem);
-            const uint32_t nb = p.cols / 32;
-            for (uint32_t b = 32 * wave; b < nb; b += 32 * nwaves)
-                e |= q8_0_blocks_wave(xs + 32 * b, nb - b < 32 ? nb - b : 32u, p.qcontract, o + b, lane);
-        }
+        const int e = quantize_prologue<act_is_q8k<O>()>(static_cast<const float *>(p.act), p.cols, p.qcontract,
+                                                         reinterpret_cast<typename ActBlock<O>::type *>(smem), wave,
+                                                         nwaves, lane);
         // Every workgroup sees the same input; the first one reports its errors.
         if (e && lane == 0 && blockIdx.x == 0) raise_error(p.err, e);
     } else {
+        // Copy the prepared blocks: 16 loads per thread in flight before any store.
         const uint32_t *src = static_cast<const uint32_t *>(p.act);
         uint32_t *dst = reinterpret_cast<uint32_t *>(smem);
-        for (uint32_t i = threadIdx.x; i < act_bytes_for<O>(p.cols) / 4; i += blockDim.x) dst[i] = src[i];
+        const uint32_t n = act_bytes_for<O>(p.cols) / 4;
+        for (uint32_t base = 0; base < n; base += 16 * blockDim.x) {
+            uint32_t tmp[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t i = base + j * blockDim.x + threadIdx.x;
+                tmp[j] = i < n ? src[i] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t i = base + j * blockDim.x + threadIdx.x;
+                if (i < n) dst[i] = tmp[j];
+            }
+        }
     }
     __syncthreads();
     const void *act = smem;
@@ -586,8 +593,8 @@ bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t 
     const uint32_t rw = kTile / lpr;
     pl->ks = ks;
     pl->lpr = lpr;
-    pl->lds = align16(act_bytes_for<O>(cols)) + (quant ? 4ull * cols : 0) +
-              sizeof(float) * nmat * rw * (nu * terms_per_unit<O>() + 1) + (nmat == 2 ? sizeof(float) * 2 * rw : 0);
+    pl->lds = align16(act_bytes_for<O>(cols)) + sizeof(float) * nmat * rw * (nu * terms_per_unit<O>() + 1) +
+              (nmat == 2 ? sizeof(float) * 2 * rw : 0);
     return pl->lds <= kSplitLds;
 }
 

@@ -8,7 +8,7 @@
 // wave-uniform arguments and returns the error bits it found (wave-uniform).
 // Blocks are spread wide over the lanes (16 lanes per Q8_K block, 2 per Q8_0
 // block) so that most of the work is in-lane and the cross-lane reductions are
-// only 4 (Q8_K) or 1 (Q8_0) shuffle steps deep.
+// only 4 (Q8_K) or 1 (Q8_0) DPP steps deep.
 #pragma once
 
 #include "device_common.hpp"
@@ -16,24 +16,54 @@
 
 namespace prism {
 
+// DPP lane exchanges within rows of 16 lanes (register speed, no LDS round trip).
+// XOR masks 15, 7, 3 and 1 (row mirror, half-row mirror, two quad permutes) span
+// the four lane-index bits, so a butterfly over them combines all 16 lanes.
+constexpr int kDppRowMirror = 0x140, kDppHalfMirror = 0x141, kDppQuadRev = 0x1B, kDppQuadSwap = 0xB1;
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+// One butterfly step of the (|x|, index, x) maximum: the lower index wins ties.
+template <int CTRL>
+__device__ __forceinline__ void max_step(float &best, int &bidx, float &bval) {
+    const float ob = dpp_f<CTRL>(best), ov = dpp_f<CTRL>(bval);
+    const int oi = dpp_i<CTRL>(bidx);
+    const bool take = ob > best || (ob == best && oi < bidx);
+    best = take ? ob : best;
+    bidx = take ? oi : bidx;
+    bval = take ? ov : bval;
+}
+
 // Up to four Q8_K blocks (256 values each): block lane/16; lane s of a block owns
 // elements 16s..16s+15, which is exactly bsums group s.  The block maximum is the
 // FIRST element with the strictly greatest |x|, sign kept (src/kernels.rs:484-492),
 // found by an (|x|, index) reduction with a lowest-index tie-break.
-template <typename XPtr, typename OutPtr>
-__device__ __forceinline__ int q8k_blocks_wave(XPtr x, uint32_t nblocks, int pinned, OutPtr o, uint32_t lane) {
+// This lane's 16 inputs of a four-block Q8_K set (zeros past nblocks).
+template <typename XPtr>
+__device__ __forceinline__ void q8k_load(XPtr x, uint32_t nblocks, uint32_t lane, float (&v)[16]) {
     const uint32_t b = lane >> 4, s = lane & 15;
-    const bool active = b < nblocks;
-    float v[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (active) q = reinterpret_cast<const float4 *>(x + 256 * b + 16 * s)[i];
+        if (b < nblocks) q = reinterpret_cast<const float4 *>(x + 256 * b + 16 * s)[i];
         v[4 * i] = q.x;
         v[4 * i + 1] = q.y;
         v[4 * i + 2] = q.z;
         v[4 * i + 3] = q.w;
     }
+}
+
+template <typename OutPtr>
+__device__ __forceinline__ int q8k_process(const float (&v)[16], uint32_t nblocks, int pinned, OutPtr o,
+                                           uint32_t lane) {
+    const uint32_t b = lane >> 4, s = lane & 15;
+    const bool active = b < nblocks;
     bool bad = false;
     float best = 0.0f, bval = 0.0f;
     int bidx = 0x7fffffff;
@@ -41,42 +71,35 @@ __device__ __forceinline__ int q8k_blocks_wave(XPtr x, uint32_t nblocks, int pin
     for (int i = 0; i < 16; ++i) {
         bad |= !finite(v[i]);
         const float a = fabsf(v[i]);
-        if (a > best) {
-            best = a;
-            bidx = static_cast<int>(16 * s + i);
-            bval = v[i];
-        }
+        const bool take = a > best;
+        best = take ? a : best;
+        bidx = take ? static_cast<int>(16 * s + i) : bidx;
+        bval = take ? v[i] : bval;
     }
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) {
-        const float ob = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bidx, off, 64);
-        const float ov = __shfl_xor(bval, off, 64);
-        if (ob > best || (ob == best && oi < bidx)) {
-            best = ob;
-            bidx = oi;
-            bval = ov;
-        }
-    }
+    max_step<kDppRowMirror>(best, bidx, bval);
+    max_step<kDppHalfMirror>(best, bidx, bval);
+    max_step<kDppQuadRev>(best, bidx, bval);
+    max_step<kDppQuadSwap>(best, bidx, bval);
     if (__any(bad)) return kErrInput;
     const float inv = best != 0.0f ? -127.0f / bval : 0.0f;
     if (__any(active && !finite(inv))) return kErrQuantRange;
     const float scale = best != 0.0f ? 1.0f / inv : 0.0f;
     uint32_t packed[4] = {0, 0, 0, 0};
-    if (best != 0.0f) {
+    // inv == 0 (an all-zero block) yields all-zero codes in both contracts.
+    if (pinned) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            int q;
-            if (pinned) {
-                const float r = __builtin_fmaf(inv, v[i], 12582912.0f);
-                q = static_cast<int>(__float_as_uint(r) & 0x7fffffu) - 0x400000;
-                q = q > 127 ? 127 : q;
-            } else {
-                float r = __builtin_rintf(v[i] * inv);
-                r = r > 127.0f ? 127.0f : r;
-                q = static_cast<int>(r);
-            }
+            const float r = __builtin_fmaf(inv, v[i], 12582912.0f);
+            int q = static_cast<int>(__float_as_uint(r) & 0x7fffffu) - 0x400000;
+            q = q > 127 ? 127 : q;
             packed[i >> 2] |= (static_cast<uint32_t>(q) & 0xffu) << (8 * (i & 3));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float r = __builtin_rintf(v[i] * inv);
+            r = r > 127.0f ? 127.0f : r;
+            packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xffu) << (8 * (i & 3));
         }
     }
     if (active) {
@@ -93,21 +116,33 @@ __device__ __forceinline__ int q8k_blocks_wave(XPtr x, uint32_t nblocks, int pin
     return 0;
 }
 
-// Up to 32 Q8_0 blocks (32 values each): block lane/2, 16 values per lane.
 template <typename XPtr, typename OutPtr>
-__device__ __forceinline__ int q8_0_blocks_wave(XPtr x, uint32_t nblocks, int contract, OutPtr o, uint32_t lane) {
-    const uint32_t b = lane >> 1, h = lane & 1;
-    const bool active = b < nblocks;
+__device__ __forceinline__ int q8k_blocks_wave(XPtr x, uint32_t nblocks, int pinned, OutPtr o, uint32_t lane) {
     float v[16];
+    q8k_load(x, nblocks, lane, v);
+    return q8k_process(v, nblocks, pinned, o, lane);
+}
+
+// Up to 32 Q8_0 blocks (32 values each): block lane/2, 16 values per lane.
+template <typename XPtr>
+__device__ __forceinline__ void q8_0_load(XPtr x, uint32_t nblocks, uint32_t lane, float (&v)[16]) {
+    const uint32_t b = lane >> 1, h = lane & 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (active) q = reinterpret_cast<const float4 *>(x + 32 * b + 16 * h)[i];
+        if (b < nblocks) q = reinterpret_cast<const float4 *>(x + 32 * b + 16 * h)[i];
         v[4 * i] = q.x;
         v[4 * i + 1] = q.y;
         v[4 * i + 2] = q.z;
         v[4 * i + 3] = q.w;
     }
+}
+
+template <typename OutPtr>
+__device__ __forceinline__ int q8_0_process(const float (&v)[16], uint32_t nblocks, int contract, OutPtr o,
+                                            uint32_t lane) {
+    const uint32_t b = lane >> 1, h = lane & 1;
+    const bool active = b < nblocks;
     bool bad = false;
     float m = 0.0f;
 #pragma unroll
@@ -115,7 +150,7 @@ __device__ __forceinline__ int q8_0_blocks_wave(XPtr x, uint32_t nblocks, int co
         bad |= !finite(v[i]);
         m = fmaxf(m, fabsf(v[i]));
     }
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, dpp_f<kDppQuadSwap>(m));
     if (__any(bad)) return kErrInput;
     const bool pinned = contract != 0, native = contract == 2;
     const float d = native ? m * __uint_as_float(0x3c010204u) : m / 127.0f;
@@ -132,7 +167,7 @@ __device__ __forceinline__ int q8_0_blocks_wave(XPtr x, uint32_t nblocks, int co
         qsum += q;
         packed[i >> 2] |= (static_cast<uint32_t>(q) & 0xffu) << (8 * (i & 3));
     }
-    qsum += __shfl_xor(qsum, 1, 64);
+    qsum += dpp_i<kDppQuadSwap>(qsum);
     const float scale = round_f16(d);
     if (__any(active && (range || !finite(scale)))) return kErrQuantRange;
     if (active) {
@@ -145,6 +180,51 @@ __device__ __forceinline__ int q8_0_blocks_wave(XPtr x, uint32_t nblocks, int co
         }
     }
     return 0;
+}
+
+template <typename XPtr, typename OutPtr>
+__device__ __forceinline__ int q8_0_blocks_wave(XPtr x, uint32_t nblocks, int contract, OutPtr o, uint32_t lane) {
+    float v[16];
+    q8_0_load(x, nblocks, lane, v);
+    return q8_0_process(v, nblocks, contract, o, lane);
+}
+
+// A workgroup's prologue: quantizes the f32 vector x (cols values, global memory)
+// into blocks `o` (LDS).  Wavefront w takes block sets w, w + nwaves, ...; the next
+// set's loads are issued before the current one is processed, so the global reads
+// cost one round trip, not one per set.  Returns the error bits seen.
+template <bool Q8K, typename OutPtr>
+__device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, uint32_t cols, int contract, OutPtr o,
+                                                 uint32_t wave, uint32_t nwaves, uint32_t lane) {
+    constexpr uint32_t per_set = Q8K ? 4 : 32, blk = Q8K ? 256 : 32;
+    const uint32_t nb = cols / blk;
+    uint32_t b = per_set * wave;
+    if (b >= nb) return 0;
+    int e = 0;
+    float v[16];
+    auto load = [&](uint32_t at, float (&dst)[16]) {
+        const uint32_t n = nb - at < per_set ? nb - at : per_set;
+        if constexpr (Q8K)
+            q8k_load(x + static_cast<size_t>(blk) * at, n, lane, dst);
+        else
+            q8_0_load(x + static_cast<size_t>(blk) * at, n, lane, dst);
+    };
+    load(b, v);
+    while (true) {
+        const uint32_t nxt = b + per_set * nwaves;
+        float vn[16];
+        if (nxt < nb) load(nxt, vn);
+        const uint32_t n = nb - b < per_set ? nb - b : per_set;
+        if constexpr (Q8K)
+            e |= q8k_process(v, n, contract, o + b, lane);
+        else
+            e |= q8_0_process(v, n, contract, o + b, lane);
+        if (nxt >= nb) break;
+        b = nxt;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = vn[i];
+    }
+    return e;
 }
 
 }  // namespace prism
