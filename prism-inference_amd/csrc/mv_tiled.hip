@@ -99,6 +99,71 @@ __device__ __forceinline__ void ptq1_dots(const uint32_t x[7], const Act &a, Acc
     r31 = sdot4(perm(m3, m2, sel(1, 3, 5, 7)), a(31), r31);
 }
 
+// ---- PTQ1 decode table (LDS) ----------------------------------------------------------
+// Entry e (a code byte) holds its trits minus one as signed bytes: lo = (t0-1, t1-1,
+// t2-1, t3-1), hi = (t4-1, 0, 0, 0).  Looking a byte up costs one v_perm (address) and
+// one ds_read_b64 instead of the ~7.5 VALU instructions per byte of the SWAR form, and
+// the signed trits need no activation-sum correction.  The table is replicated 32
+// times, entry-major (copy c of entry e at byte 256e + 8c), and lane l reads copy l%32:
+// the 32 lanes of each half-wavefront then hit 32 distinct bank pairs whatever the
+// codes, and a lane's address is the code byte in bits 8..15 over its copy offset.
+constexpr uint32_t kLutCopies = 32;
+__shared__ __attribute__((aligned(16))) uint2 g_ptq1_lut[256 * kLutCopies];
+
+__device__ __forceinline__ void ptq1_lut_fill(uint32_t tid, uint32_t nthreads) {
+    for (uint32_t i = tid; i < 256 * kLutCopies; i += nthreads) {
+        uint32_t r = i / kLutCopies, lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const uint32_t m = r * 3u;
+            const uint32_t t = ((m >> 8) - 1u) & 0xffu;  // trit_k - 1 as a byte
+            r = m & 0xffu;
+            if (k < 4)
+                lo |= t << (8 * k);
+            else
+                hi = t;
+        }
+        g_ptq1_lut[i] = make_uint2(lo, hi);
+    }
+}
+
+// Table entry of byte b of code dword x; `lbase` = 8 * (lane % 32).
+__device__ __forceinline__ uint2 lut_at(uint32_t x, uint32_t lbase, uint32_t b) {
+    const uint32_t addr = perm(x, lbase, sel(0, 4 + b, 12, 12));
+    return *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(g_ptq1_lut) + addr);
+}
+
+// Same contract as ptq1_dots, but acc(q) receives sum (t-1)*a directly.  The four
+// entries of a code dword are transposed (8 v_perm) into the natural quads
+// (digit k of bytes 4w..4w+3), so the activation keeps its natural order.
+template <typename Act, typename Acc>
+__device__ __forceinline__ void ptq1_dots_lut(const uint32_t x[7], uint32_t lbase, const Act &a, Acc &&acc) {
+#pragma unroll
+    for (int w = 0; w < 6; ++w) {
+        const uint2 e0 = lut_at(x[w], lbase, 0), e1 = lut_at(x[w], lbase, 1);
+        const uint2 e2 = lut_at(x[w], lbase, 2), e3 = lut_at(x[w], lbase, 3);
+        const uint32_t l01 = perm(e1.x, e0.x, sel(0, 4, 1, 5)), h01 = perm(e1.x, e0.x, sel(2, 6, 3, 7));
+        const uint32_t l23 = perm(e3.x, e2.x, sel(0, 4, 1, 5)), h23 = perm(e3.x, e2.x, sel(2, 6, 3, 7));
+        uint32_t T[5];
+        T[0] = perm(l23, l01, sel(0, 1, 4, 5));
+        T[1] = perm(l23, l01, sel(2, 3, 6, 7));
+        T[2] = perm(h23, h01, sel(0, 1, 4, 5));
+        T[3] = perm(h23, h01, sel(2, 3, 6, 7));
+        T[4] = perm(e1.y, e0.y, sel(0, 4, 12, 12)) | perm(e3.y, e2.y, sel(12, 12, 0, 4));
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const int q = w < 4 ? 4 * k + w : 20 + 2 * k + (w - 4);
+            int &r = acc(q);
+            r = sdot4(T[k], a(q), r);
+        }
+    }
+    const uint2 e0 = lut_at(x[6], lbase, 0), e1 = lut_at(x[6], lbase, 1);
+    int &r30 = acc(30);
+    r30 = sdot4(perm(e1.x, e0.x, sel(0, 4, 1, 5)), a(30), r30);
+    int &r31 = acc(31);
+    r31 = sdot4(perm(e1.x, e0.x, sel(2, 6, 3, 7)), a(31), r31);
+}
+
 // PQ2 code dword i holds elements 16i..16i+15, element 16i+4q+p in byte q, bits 2p.
 // Given the 16 activation codes of those elements (natural order, dwords q0..q3),
 // accumulates sum c*a into a0 + a1/4 + a2/16 (the masks leave field p scaled by 4^p)
@@ -187,8 +252,18 @@ __device__ __forceinline__ void load_unit(Raw<O> &w, __amdgpu_buffer_rsrc_t rs, 
 // ---- per-unit arithmetic ------------------------------------------------------------
 // `act` is the token's prepared activation; every index into it is wave-uniform.
 // Terms go to t[] in the order the reference's chain consumes them.
-template <Op O>
-__device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restrict__ act, uint32_t u, float *t) {
+// LUT selects the PTQ1 decoder: the SWAR digit extraction (trits 0..2, corrected by
+// the activation sums) or the LDS table (trits already minus one); `lbase` is the
+// lane's table-copy offset.
+template <Op O, bool LUT = false>
+__device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restrict__ act, uint32_t u, float *t,
+                                           uint32_t lbase = 0) {
+    auto trits = [&](const auto &raw, const auto &a, auto &&acc) {
+        if constexpr (LUT)
+            ptq1_dots_lut(raw.x, lbase, a, acc);
+        else
+            ptq1_dots(raw.x, a, acc);
+    };
     if constexpr (O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED) {
         const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
         const uint32_t *av[4];
@@ -198,14 +273,16 @@ __device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restri
         const float d = h2f(w.x[6] >> 16);
         if constexpr (O == Op::PTQ1_SRC) {
             int acc[4] = {0, 0, 0, 0};
-            ptq1_dots(w.x, a, [&](int q) -> int & { return acc[q >> 3]; });
+            trits(w, a, [&](int q) -> int & { return acc[q >> 3]; });
             // dot_q8_groups, src/kernels.rs:1043-1064
             float tt = 0.0f;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 int s = 0;
+                if constexpr (!LUT) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) s = bsum4(av[g][i], s);
+                    for (int i = 0; i < 8; ++i) s = bsum4(av[g][i], s);
+                }
                 tt = tt + b[g].scale * static_cast<float>(acc[g] - s);
             }
             t[0] = d * tt;
@@ -215,12 +292,15 @@ __device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restri
             int acc[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = 0;
-            ptq1_dots(w.x, a, [&](int q) -> int & { return acc[4 * (q >> 3) + (q & 3)]; });
+            trits(w, a, [&](int q) -> int & { return acc[4 * (q >> 3) + (q & 3)]; });
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int g0 = i >> 1, l0 = 2 * (i & 1);
-                const int s0 = bsum4(av[g0][l0 + 4], bsum4(av[g0][l0], 0));
-                const int s1 = bsum4(av[g0][l0 + 5], bsum4(av[g0][l0 + 1], 0));
+                int s0 = 0, s1 = 0;
+                if constexpr (!LUT) {
+                    s0 = bsum4(av[g0][l0 + 4], bsum4(av[g0][l0], 0));
+                    s1 = bsum4(av[g0][l0 + 5], bsum4(av[g0][l0 + 1], 0));
+                }
                 const int lo = acc[2 * i] - s0, hi = acc[2 * i + 1] - s1;
                 t[i] = __uint_as_float((static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16));
             }
@@ -231,10 +311,12 @@ __device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restri
         const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values) + 32 * (u & 1);
         auto a = [&](int q) -> uint32_t { return av[q]; };
         int acc = 0;
-        ptq1_dots(w.x, a, [&](int) -> int & { return acc; });
+        trits(w, a, [&](int) -> int & { return acc; });
         int s = 0;
+        if constexpr (!LUT) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) s = bsum4(av[i], s);
+            for (int i = 0; i < 32; ++i) s = bsum4(av[i], s);
+        }
         // dot_ptq1_q8k, src/kernels.rs:1026-1034
         t[0] = (h2f(w.x[6] >> 16) * b->scale) * static_cast<float>(acc - s);
     } else if constexpr (O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED) {
@@ -384,21 +466,19 @@ struct ActBlock {
 // Big matrices: one wavefront per 64-row tile walks the whole row; the prepared
 // activation (global, wave-uniform) arrives through scalar loads and the chain
 // stays in registers.
-template <Op O>
-__global__ __launch_bounds__(64) void k_mv_rows(MvParams p) {
+template <Op O, bool LUT>
+__device__ __forceinline__ void rows_tile(const MvParams &p, const void *__restrict__ act, uint32_t tile, uint32_t lane,
+                                          uint32_t lbase) {
     constexpr uint32_t UB = unit_bytes<O>();
-    const uint32_t lane = threadIdx.x;
-    const uint32_t tile = blockIdx.x;
     const uint32_t nu = p.nu, row_bytes = nu * UB;
     const uint32_t left = p.rows - tile * kTile;
     const uint32_t trows = left < kTile ? left : kTile;
     const uint32_t trp = (trows + 7u) & ~7u;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
-    const void *act = p.act;
     Chain<O> ch;
     auto step = [&](const Raw<O> &w, uint32_t u) {
         float t[terms_per_unit<O>()];
-        unit_terms<O>(w, act, u, t);
+        unit_terms<O, LUT>(w, act, u, t, lbase);
         ch.fold(t, act, u);
     };
     // Two register buffers in ping-pong: the next unit's loads are in flight while the
@@ -421,6 +501,29 @@ __global__ __launch_bounds__(64) void k_mv_rows(MvParams p) {
         p.out[row] = o;
         if (!finite(o)) raise_error(p.err, kErrNonfinite);
     }
+}
+
+template <Op O>
+__global__ __launch_bounds__(64) void k_mv_rows(MvParams p) {
+    rows_tile<O, false>(p, p.act, blockIdx.x, threadIdx.x, 0);
+}
+
+// PTQ1 with the LDS decode table: one workgroup per CU builds the 64 KiB table once and
+// its wavefronts take tiles round-robin over the grid (tile = wave * grid + block, ...),
+// which spreads the tiles evenly over the CUs.  The activation comes as its own
+// __restrict__ argument: the row stores of one tile then provably leave it intact for
+// the next, and its loads stay scalar.
+constexpr uint32_t kLutThreads = 1024;
+template <Op O>
+__global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const void *__restrict__ act) {
+    ptq1_lut_fill(threadIdx.x, blockDim.x);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tiles = (p.rows + kTile - 1) / kTile;
+    const uint32_t step = gridDim.x * (blockDim.x >> 6);
+    for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += step)
+        rows_tile<O, true>(p, act, tile, lane, 8u * (lane & 31u));
 }
 
 // Small matrices: a workgroup owns rw = 64/lpr rows of a tile; its ks wavefronts
@@ -617,6 +720,10 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.residual = a.residual;
     p.err = a.err;
     if (!quant && nmat == 1 && tiles >= a.cus) {
+        if constexpr (kind_of<O>() == kPTQ1) {
+            hipLaunchKernelGGL(k_mv_rows_lut<O>, dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
         hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }

@@ -221,7 +221,6 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
             e |= q8_0_process(v, n, contract, o + b, lane);
         if (nxt >= nb) break;
         b = nxt;
-#pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = vn[i];
     }
     return e;

@@ -286,6 +286,39 @@ def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("cols", [384, 1024])
+def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols):
+    """PTQ1 on the row-tile path decodes trits through the LDS table, one workgroup per
+    CU taking tiles round-robin: enough tiles that some wavefronts take two, an odd and
+    an even unit count, a partial last tile, and all three activation contracts."""
+    import oracle
+
+    import hiprt
+
+    kind = ph.KIND_PTQ1
+    cus = hiprt.cu_count(0)
+    rows = 64 * (16 * cus + 3) + 37
+    w = synth.weights(kind, rows, cols, seed=29 + cols)
+    x = synth.activations(cols, seed=30)
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, x, pinned, threads=THREADS)
+        assert_bits_equal(ctx.project_f32(wid, rows, x, pinned=pinned), ref, f"table f32 pinned={pinned}")
+    for contract in (0, 2):
+        act = oracle.quantize_q8_0(x, contract)
+        for pinned in (False, True):
+            ref = oracle.project_q8(kind, cols, rows, w, act, pinned, threads=THREADS)
+            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=pinned)
+            assert_bits_equal(got, ref, f"table q8 contract={contract} pinned={pinned}")
+    if cols % 256 == 0:
+        act = oracle.quantize_q8k(x, False)
+        nb = cols // 128 * 28
+        ref = np.array([oracle.dot_ptq1_q8k(w[r * nb:(r + 1) * nb], act) for r in range(0, rows, 997)], np.float32)
+        got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE))
+        assert_bits_equal(got[::997], ref, "table q8k")
+    ctx.release(wid)
+
+
 # ---- multi-token, groups, backend op -------------------------------------------------
 
 def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
