@@ -185,6 +185,49 @@ int prism_hip_sync(prism_hip_ctx *ctx, void *stream);
 /* The context's internal stream (a hipStream_t), for ordering caller work. */
 void *prism_hip_stream(prism_hip_ctx *ctx);
 
+/* ---- full-attention decode step ---------------------------------------------------
+ * A resident decoder over a context: the layer loop of the reference's Qwen35 graph
+ * for full-attention layers (src/graph.rs:3870-3995) in the source arithmetic, with
+ * every linear layer PTQ1 on the packed-matvec kernels and a tied Q8_0 LM head /
+ * token embedding.  Per layer: RMSNorm fused into the q/k/v projection (one PTQ1
+ * matrix of (heads + 2*kv_heads)*head_dim rows), per-head q/k RMSNorm + RoPE +
+ * binary16 rounding, binary16 KV cache append, attention (f16 dots and value sums
+ * in binary64, softmax_round_f16), o projection + residual, post-norm fused into the
+ * gate/up/SwiGLU launch, down + residual; then the final norm, the LM head and the
+ * greedy choice, whose embedding feeds the next step.  The geometry has no attention
+ * output gate (the query projection is heads*head_dim wide).  No counterpart C API
+ * exists in the reference: this is the reference's own graph code, restated around
+ * the executor entry points above. */
+typedef struct prism_hip_decoder prism_hip_decoder;
+typedef struct {
+    uint64_t hidden, ffn, heads, kv_heads, head_dim, rope, vocab, layers, max_tokens;
+    uint64_t rope_sections[4]; /* M-RoPE sections; text positions use sectors 0..2 */
+    float rope_base, eps;
+} prism_decoder_geometry;
+
+/* head_dim must be 128; hidden, ffn multiples of 128; max_tokens <= 8192.  max_steps bounds one
+ * generate(). */
+prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *ctx, const prism_decoder_geometry *g, uint32_t max_steps);
+void prism_hip_decoder_destroy(prism_hip_decoder *d);
+/* Host tensors of layer l, native layouts: qkv PTQ1 [(heads+2kv)*head_dim][hidden]
+ * (q rows, then k, then v), o PTQ1 [hidden][heads*head_dim], gate/up PTQ1
+ * [ffn][hidden], down PTQ1 [hidden][ffn]; norm/post_norm [hidden], q_norm/k_norm
+ * [head_dim] f32. */
+int prism_hip_decoder_set_layer(prism_hip_decoder *d, uint32_t layer, const uint8_t *qkv, const uint8_t *o,
+                                const uint8_t *gate, const uint8_t *up, const uint8_t *down, const float *norm,
+                                const float *post_norm, const float *q_norm, const float *k_norm);
+/* Binary16 cache rows [tokens][kv_heads*head_dim] of layer l (positions 0..tokens-1). */
+int prism_hip_decoder_set_cache(prism_hip_decoder *d, uint32_t layer, const uint16_t *k, const uint16_t *v,
+                                uint64_t tokens);
+/* Tied LM head / embedding, Q8_0 [vocab][hidden] native rows, and the final norm. */
+int prism_hip_decoder_set_head(prism_hip_decoder *d, const uint8_t *lm_head, const float *output_norm);
+/* Runs `steps` greedy decode steps from `token` at position `pos`: tokens_out[steps]
+ * receives the chosen tokens, logits_out (NULL or steps*vocab floats) every step's
+ * logits, seconds (NULL allowed) the device time of the steps.  use_graph replays
+ * one captured HIP graph per step. */
+int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t pos, uint32_t steps, int use_graph,
+                               uint32_t *tokens_out, float *logits_out, double *seconds);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,6 +92,13 @@ def lib():
             "po_vector_exp": (ctypes.c_float, [ctypes.c_float]),
             "po_swiglu": (None, [P, P, S, I]),
             "po_ffn": (I, [U, S, S, P, P, P, P, P, I, P, P, I]),
+            "po_rms_norm": (I, [P, P, S, ctypes.c_float, P]),
+            "po_rope_frequencies": (None, [S, P, P, ctypes.c_float, P, P]),
+            "po_norm_rope_f16": (I, [P, P, S, S, P, P, ctypes.c_float]),
+            "po_softmax_round_f16": (I, [P, S]),
+            "po_attention_head": (I, [P, P, P, S, S, S, P, P, S, P, P]),
+            "po_decoder_step": (I, [P, P, P, P, U, S, P, I]),
+            "po_argmax": (S, [P, S]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -283,3 +290,102 @@ def prefill(kind: int, cols: int, rows: int, w, X, pinned: bool = False, threads
     """Tiled prefill semantics: each token row equals its own matvec (src/kernels/prefill.rs:829-887)."""
     X = _f32(X)
     return np.stack([matvec(kind, cols, rows, w, X[m], pinned, threads) for m in range(X.shape[0])])
+
+
+# ---- full-attention decode step (decoder_oracle.c) ---------------------------------
+
+class DecoderGeometry(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "rope", "vocab",
+                                                "layers", "max_tokens")] + [
+        ("rope_sections", ctypes.c_size_t * 4), ("rope_base", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+class DecoderLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("qkv", "o", "gate", "up", "down", "norm", "post_norm", "q_norm",
+                                                "k_norm", "kcache", "vcache")]
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    out = np.zeros_like(x)
+    _check(lib().po_rms_norm(_p(x), _p(w), x.size, eps, _p(out)), "rms_norm")
+    return out
+
+
+def rope_frequencies(rope: int, sections, positions, base: float):
+    sec = (ctypes.c_size_t * 4)(*sections)
+    pos = (ctypes.c_size_t * 4)(*positions)
+    c = np.zeros(rope // 2, np.float32)
+    s = np.zeros(rope // 2, np.float32)
+    lib().po_rope_frequencies(rope, sec, pos, base, _p(c), _p(s))
+    return c, s
+
+
+def norm_rope_f16(v, w, rope: int, cosines, sines, eps: float) -> np.ndarray:
+    v = _f32(v).copy()
+    w, c, s = _f32(w), _f32(cosines), _f32(sines)
+    _check(lib().po_norm_rope_f16(_p(v), _p(w), v.size, rope, _p(c), _p(s), eps), "norm_rope_f16")
+    return v
+
+
+def softmax_round_f16(v) -> np.ndarray:
+    v = _f32(v).copy()
+    _check(lib().po_softmax_round_f16(_p(v), v.size), "softmax_round_f16")
+    return v
+
+
+def attention_head(q, kc, vc, stride: int, offset: int, past: int, kcur, vcur) -> np.ndarray:
+    q, kcur, vcur = _f32(q), _f32(kcur), _f32(vcur)
+    kc = np.ascontiguousarray(kc, np.uint16)
+    vc = np.ascontiguousarray(vc, np.uint16)
+    scores = np.zeros(past + 1, np.float32)
+    out = np.zeros(q.size, np.float32)
+    _check(lib().po_attention_head(_p(q), _p(kc), _p(vc), stride, offset, past, _p(kcur), _p(vcur), q.size,
+                                   _p(scores), _p(out)), "attention_head")
+    return out
+
+
+def argmax(v) -> int:
+    v = _f32(v)
+    return int(lib().po_argmax(_p(v), v.size))
+
+
+class Decoder:
+    """The decode step over a model dict (see prism_hip.synth decoder models): holds its
+    own binary16 KV caches, which every step appends to."""
+
+    def __init__(self, model: dict, threads: int = 1):
+        g = model["geometry"]
+        self.model = model
+        self.threads = threads
+        self.g = DecoderGeometry(g["hidden"], g["ffn"], g["heads"], g["kv_heads"], g["head_dim"], g["rope"],
+                                 g["vocab"], g["layers"], g["max_tokens"], (ctypes.c_size_t * 4)(*g["rope_sections"]),
+                                 g["rope_base"], g["eps"])
+        kw = g["kv_heads"] * g["head_dim"]
+        self.kcache, self.vcache = [], []
+        keep = []
+        layers = (DecoderLayer * g["layers"])()
+        for i, L in enumerate(model["layers"]):
+            k = np.zeros((g["max_tokens"], kw), np.uint16)
+            v = np.zeros((g["max_tokens"], kw), np.uint16)
+            n = L["kv_prefill"]
+            k[:n] = L["k_prefill"]
+            v[:n] = L["v_prefill"]
+            self.kcache.append(k)
+            self.vcache.append(v)
+            arrs = {name: np.ascontiguousarray(L[name]) for name in ("qkv", "o", "gate", "up", "down", "norm",
+                                                                       "post_norm", "q_norm", "k_norm")}
+            keep.append(arrs)
+            layers[i] = DecoderLayer(*(_p(arrs[n]) for n in ("qkv", "o", "gate", "up", "down", "norm", "post_norm",
+                                                              "q_norm", "k_norm")), _p(k), _p(v))
+        self.layers = layers
+        self._keep = keep
+        self.lm_head = np.ascontiguousarray(model["lm_head"])
+        self.output_norm = _f32(model["output_norm"])
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        logits = np.zeros(self.g.vocab, np.float32)
+        rc = lib().po_decoder_step(ctypes.byref(self.g), self.layers, _p(self.lm_head), _p(self.output_norm),
+                                   token, pos, _p(logits), self.threads)
+        _check(rc, "decoder_step")
+        return logits

@@ -113,6 +113,37 @@ int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const ui
            const uint8_t *wd, const float *x, const float *residual, int pinned, float *out,
            float *h_out, int threads);
 
+/* ---- full-attention decode step, source order (decoder_oracle.c) ---- */
+typedef struct {
+    size_t hidden, ffn, heads, kv_heads, head_dim, rope, vocab, layers, max_tokens;
+    size_t rope_sections[4];
+    float rope_base, eps;
+} po_decoder_geometry;
+
+typedef struct {
+    const uint8_t *qkv;   /* PTQ1 [(heads + 2 kv_heads) * head_dim][hidden]: q, k, v rows */
+    const uint8_t *o;     /* PTQ1 [hidden][heads * head_dim] */
+    const uint8_t *gate;  /* PTQ1 [ffn][hidden] */
+    const uint8_t *up;    /* PTQ1 [ffn][hidden] */
+    const uint8_t *down;  /* PTQ1 [hidden][ffn] */
+    const float *norm, *post_norm, *q_norm, *k_norm;
+    uint16_t *kcache, *vcache; /* binary16 [max_tokens][kv_heads * head_dim] */
+} po_decoder_layer;
+
+int po_rms_norm(const float *x, const float *w, size_t n, float eps, float *out); /* kernels.rs:3389-3418,3823-3878 */
+void po_rope_frequencies(size_t rope, const size_t sections[4], const size_t positions[4], float base,
+                         float *cosines, float *sines);                           /* graph.rs:6406-6431 */
+int po_norm_rope_f16(float *v, const float *w, size_t head, size_t rope, const float *cosines,
+                     const float *sines, float eps);                              /* kernels.rs:3679-3733 */
+int po_softmax_round_f16(float *v, size_t n);                                     /* kernels.rs:4431-4462 */
+int po_attention_head(const float *q, const uint16_t *kc, const uint16_t *vc, size_t stride, size_t offset,
+                      size_t past, const float *kcur, const float *vcur, size_t head, float *scores,
+                      float *out);                                                /* graph.rs:4884-4911 */
+int po_decoder_step(const po_decoder_geometry *g, const po_decoder_layer *layers, const uint8_t *lm_head,
+                    const float *output_norm, uint32_t token, size_t pos, float *logits,
+                    int threads);                                                 /* graph.rs:3870-3995 */
+size_t po_argmax(const float *v, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,7 +21,8 @@ OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libprism_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["quantize.hip", "matvec.hip", "mv_tiled.hip", "prefill.hip", "ffn.hip", "runtime.cpp"]
+SOURCES = ["quantize.hip", "matvec.hip", "mv_tiled.hip", "prefill.hip", "ffn.hip", "decode.hip", "runtime.cpp",
+           "decoder.cpp"]
 
 FLAGS = [
     "--offload-arch=gfx950",

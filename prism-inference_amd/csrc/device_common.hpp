@@ -42,7 +42,14 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
 // binary32 -> binary16 -> binary32 with ties to even (src/kernels.rs:2824-2830).
-__device__ __forceinline__ float round_f16(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+// The empty asm materializes the binary32 value first: otherwise the compiler folds a
+// preceding binary32 multiply into the conversion (v_fma_mixlo_f16), which rounds the
+// exact product once instead of rounding the binary32 product, and differs whenever
+// that product lands exactly on a binary16 midpoint.
+__device__ __forceinline__ float round_f16(float v) {
+    asm volatile("" : "+v"(v));
+    return static_cast<float>(static_cast<_Float16>(v));
+}
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
@@ -95,16 +102,25 @@ __device__ __forceinline__ float vector_exp(float value) {
     return __builtin_fmaf(poly, k, k);
 }
 
+// binary32 exp / cos / sin evaluated in binary64 and rounded once.  That is the
+// correctly rounded result except when the exact value lies within the binary64
+// error of a binary32 rounding boundary, so it agrees with the reference's libm
+// (Rust's f32::exp / cos / sin, themselves within about half an ulp) far more often
+// than the device's single-precision routines, which are within about one ulp.
+__device__ __forceinline__ float exp_f32(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+__device__ __forceinline__ float cos_f32(float x) { return static_cast<float>(cos(static_cast<double>(x))); }
+__device__ __forceinline__ float sin_f32(float x) { return static_cast<float>(sin(static_cast<double>(x))); }
+
 // One SwiGLU element, h = up * silu(gate).  Source order (src/graph.rs:121-131,
 // src/kernels.rs:3365-3368): up * (g / (1 + exp(-g))).  Pinned order
 // (src/kernels/pinned_activations.rs:141-178): (g * up) / (1 + vexp(0 - g)) for the
 // first n/4*4 elements of the vector and (g * up) / (1 + exp(-g)) for the tail.
 __device__ __forceinline__ float swiglu_one(float gate, float up, uint64_t i, uint64_t n, int pinned) {
     if (pinned) {
-        const float den = 1.0f + (i < n / 4 * 4 ? vector_exp(0.0f - gate) : expf(-gate));
+        const float den = 1.0f + (i < n / 4 * 4 ? vector_exp(0.0f - gate) : exp_f32(-gate));
         return (gate * up) / den;
     }
-    const float silu = gate / (1.0f + expf(-gate));
+    const float silu = gate / (1.0f + exp_f32(-gate));
     return up * silu;
 }
 

@@ -35,6 +35,8 @@ struct MatvecArgs {
     int pinned = 0;               // pinned Q8 order (PTQ1) or fused FMA (PQ2 + Q8K); SwiGLU order
     float *out = nullptr;         // device, [tokens][rows]
     const float *residual = nullptr;  // tiled only: added to every output row
+    const float *norm_w = nullptr;    // tiled kActF32 only: RMSNorm weights applied before quantizing
+    float eps = 0.0f;                 // RMSNorm epsilon
     int *err = nullptr;           // device error flag
     hipStream_t stream = nullptr;
     uint32_t cus = 256;           // compute units of the device
@@ -70,5 +72,36 @@ int launch_swiglu(const float *gate, const float *up, float *h, uint64_t n, uint
 int launch_add_residual(float *out, const float *residual, uint64_t n, int *err, hipStream_t s);
 // p[0..n) = v with a kernel (safe inside captured graphs, unlike a memset node).
 int launch_fill_i32(int *p, int v, uint32_t n, hipStream_t s);
+
+// ---- decode step (decode.hip) ----
+// Device-resident position / token / step counter of a decoder; the last kernel of a
+// step advances it, so one captured graph serves every step.
+struct DecodeState {
+    uint32_t pos, token, step, pad;
+};
+struct AttnArgs {
+    const float *qkv;            // this token's projections: q [heads*D] | k [kv*D] | v [kv*D]
+    const float *q_norm, *k_norm;  // per-head RMSNorm weights [D]
+    uint16_t *kcache, *vcache;   // binary16 [max_tokens][kv*D]
+    float *scores;               // [heads][max_tokens]
+    float *out;                  // attended [heads*D]
+    const DecodeState *state;
+    uint32_t heads, kv_heads, head_dim, rope, max_tokens;
+    uint32_t sections[4];        // M-RoPE sections (src/graph.rs:6406-6431)
+    float theta_scale, eps;      // rope_base^(-2/rope) as binary32 powf, RMSNorm epsilon
+    int *err;
+    hipStream_t stream;
+};
+// q/k norm + RoPE + KV append + scores, then softmax + values: two launches.
+int launch_attention(const AttnArgs &a);
+// Final RMSNorm + Q8_0 (source) quantization of n values into q8_out.
+int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *q8_out, int *err, hipStream_t s);
+// out = dequantized row state->token of the tiled Q8_0 matrix [rows][cols].
+int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, const DecodeState *st, float *out,
+                 hipStream_t s);
+// Greedy token from logits[vocab], recorded and advanced in the state, and its
+// embedding (row of the tiled Q8_0 matrix [vocab][cols]) written to out.
+int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
+                        uint32_t *tokens, uint32_t max_steps, float *out, hipStream_t s);
 
 }  // namespace prism

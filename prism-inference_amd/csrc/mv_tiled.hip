@@ -442,6 +442,8 @@ struct MvParams {
     float *out;
     const float *residual;
     int *err;
+    const float *norm_w;  // QUANT prologue: RMSNorm weights applied before quantizing (or null)
+    float eps;            // RMSNorm epsilon
 };
 
 template <Op O>
@@ -560,6 +562,7 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
     const uint32_t stride = nu * TPU + 1;
     float *terms = reinterpret_cast<float *>(smem + abytes) + mat * rw * stride;
     float *res = reinterpret_cast<float *>(smem + abytes) + NMAT * rw * stride;
+    double *red = reinterpret_cast<double *>(smem + abytes + align16(4u * (NMAT * rw * stride + 2 * rw)));
 
     const __amdgpu_buffer_rsrc_t rs =
         make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
@@ -569,9 +572,19 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
 
     // ---- prologue: stage the activation in LDS -------------------------------------
     if constexpr (QUANT) {
-        const int e = quantize_prologue<act_is_q8k<O>()>(static_cast<const float *>(p.act), p.cols, p.qcontract,
-                                                         reinterpret_cast<typename ActBlock<O>::type *>(smem), wave,
-                                                         nwaves, lane);
+        const float *x = static_cast<const float *>(p.act);
+        auto *blocks = reinterpret_cast<typename ActBlock<O>::type *>(smem);
+        int e;
+        if (p.norm_w) {
+            // RMSNorm fused ahead of the quantizer: every workgroup normalizes the whole
+            // input itself, so the projection stays one launch.
+            const float scale = rms_scale_wg(x, p.cols, p.eps, red);
+            e = scale == 0.0f ? kErrNonfinite
+                              : quantize_prologue<act_is_q8k<O>()>(x, p.cols, p.qcontract, blocks, wave, nwaves, lane,
+                                                                   NormPre{p.norm_w, scale});
+        } else {
+            e = quantize_prologue<act_is_q8k<O>()>(x, p.cols, p.qcontract, blocks, wave, nwaves, lane);
+        }
         // Every workgroup sees the same input; the first one reports its errors.
         if (e && lane == 0 && blockIdx.x == 0) raise_error(p.err, e);
     } else {
@@ -696,8 +709,10 @@ bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t 
     const uint32_t rw = kTile / lpr;
     pl->ks = ks;
     pl->lpr = lpr;
-    pl->lds = align16(act_bytes_for<O>(cols)) + sizeof(float) * nmat * rw * (nu * terms_per_unit<O>() + 1) +
-              (nmat == 2 ? sizeof(float) * 2 * rw : 0);
+    // activation blocks | terms (| SwiGLU inputs) | 16 doubles for the RMSNorm reduction
+    pl->lds = align16(act_bytes_for<O>(cols)) +
+              align16(static_cast<uint32_t>(sizeof(float) * (nmat * rw * (nu * terms_per_unit<O>() + 1) + 2 * rw))) +
+              16 * sizeof(double);
     return pl->lds <= kSplitLds;
 }
 
@@ -719,6 +734,8 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.out = out;
     p.residual = a.residual;
     p.err = a.err;
+    p.norm_w = a.norm_w;
+    p.eps = a.eps;
     if (!quant && nmat == 1 && tiles >= a.cus) {
         if constexpr (kind_of<O>() == kPTQ1) {
             hipLaunchKernelGGL(k_mv_rows_lut<O>, dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);

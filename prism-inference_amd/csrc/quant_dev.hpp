@@ -189,13 +189,37 @@ __device__ __forceinline__ int q8_0_blocks_wave(XPtr x, uint32_t nblocks, int co
     return q8_0_process(v, nblocks, contract, o, lane);
 }
 
+// Element transforms applied to a lane's 16 consecutive inputs (first element index
+// `first`) before they are quantized; `active` is false for lanes past the last block,
+// which hold zeros and must not read the transform's own data.
+struct NoPre {
+    __device__ __forceinline__ void operator()(float (&)[16], uint32_t, bool) const {}
+};
+// RMSNorm in the reference's source order, (x * scale) * w (src/kernels.rs:3389-3418).
+struct NormPre {
+    const float *w;
+    float scale;
+    __device__ __forceinline__ void operator()(float (&v)[16], uint32_t first, bool active) const {
+        if (!active) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 q = reinterpret_cast<const float4 *>(w + first)[i];
+            v[4 * i] = (v[4 * i] * scale) * q.x;
+            v[4 * i + 1] = (v[4 * i + 1] * scale) * q.y;
+            v[4 * i + 2] = (v[4 * i + 2] * scale) * q.z;
+            v[4 * i + 3] = (v[4 * i + 3] * scale) * q.w;
+        }
+    }
+};
+
 // A workgroup's prologue: quantizes the f32 vector x (cols values, global memory)
 // into blocks `o` (LDS).  Wavefront w takes block sets w, w + nwaves, ...; the next
 // set's loads are issued before the current one is processed, so the global reads
-// cost one round trip, not one per set.  Returns the error bits seen.
-template <bool Q8K, typename OutPtr>
+// cost one round trip, not one per set.  `pre` transforms the inputs first.
+// Returns the error bits seen.
+template <bool Q8K, typename OutPtr, typename Pre = NoPre>
 __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, uint32_t cols, int contract, OutPtr o,
-                                                 uint32_t wave, uint32_t nwaves, uint32_t lane) {
+                                                 uint32_t wave, uint32_t nwaves, uint32_t lane, const Pre &pre = Pre{}) {
     constexpr uint32_t per_set = Q8K ? 4 : 32, blk = Q8K ? 256 : 32;
     const uint32_t nb = cols / blk;
     uint32_t b = per_set * wave;
@@ -209,12 +233,16 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
         else
             q8_0_load(x + static_cast<size_t>(blk) * at, n, lane, dst);
     };
+    // This lane's block within a set and the index of its first input.
+    const uint32_t lb = Q8K ? lane >> 4 : lane >> 1;
+    const uint32_t lo = Q8K ? 16u * (lane & 15u) : 16u * (lane & 1u);
     load(b, v);
     while (true) {
         const uint32_t nxt = b + per_set * nwaves;
         float vn[16];
         if (nxt < nb) load(nxt, vn);
         const uint32_t n = nb - b < per_set ? nb - b : per_set;
+        pre(v, blk * (b + lb) + lo, lb < n);
         if constexpr (Q8K)
             e |= q8k_process(v, n, contract, o + b, lane);
         else
@@ -224,6 +252,32 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
         for (int i = 0; i < 16; ++i) v[i] = vn[i];
     }
     return e;
+}
+
+// RMSNorm scale of x[0..n) over a whole workgroup (rms_norm_scale_inner,
+// src/kernels.rs:3823-3878): binary64 sum of the binary32 squares, mean rounded to
+// binary32, 1 / sqrt(mean + eps).  Threads sum strided elements, wavefronts reduce
+// with cross-lane shuffles and wavefront 0 folds the wavefront sums in order, so
+// only the order of the binary64 additions differs from the reference's sequential
+// sum.  `red` is LDS scratch for 16 doubles.  Returns a non-positive or non-finite
+// scale as 0 (the caller raises the error); every thread gets the same value.
+__device__ __forceinline__ float rms_scale_wg(const float *__restrict__ x, uint32_t n, float eps, double *red) {
+    double s = 0.0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        s += static_cast<double>(v * v);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    const uint32_t wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63u) == 0) red[wave] = s;
+    __syncthreads();
+    double t = 0.0;
+    for (uint32_t w = 0; w < nw; ++w) t += red[w];
+    __syncthreads();
+    const float mean = static_cast<float>(t / static_cast<double>(n));
+    const float scale = 1.0f / __builtin_sqrtf(mean + eps);
+    return (finite(scale) && scale > 0.0f) ? scale : 0.0f;
 }
 
 }  // namespace prism

@@ -1,0 +1,186 @@
+// runtime_internal.hpp -- state and helpers shared by the translation units that
+// implement the extern "C" ABI of libprism_hip.so (runtime.cpp, decoder.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/prism_hip.h"
+#include "kernels.hpp"
+#include "tiled.hpp"
+
+namespace prism::rt {
+
+struct Weight {
+    uint64_t key = 0;
+    uint32_t kind = 0;
+    uint64_t cols = 0, rows = 0, row_bytes = 0, bytes = 0;
+    void *dev = nullptr;
+    bool owned = false;
+    bool tiled = false;  // 64-row tiled device layout (tiled.hpp) instead of native rows
+};
+
+// Grow-only device scratch buffer.
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+inline bool layout(uint32_t kind, uint64_t *group, uint64_t *block) {
+    switch (kind) {
+    case PRISM_KIND_Q8_0: *group = 32; *block = 34; return true;
+    case PRISM_KIND_Q2_K: *group = 256; *block = 84; return true;
+    case PRISM_KIND_PQ2: *group = 128; *block = 34; return true;
+    case PRISM_KIND_PTQ1: *group = 128; *block = 28; return true;
+    default: return false;
+    }
+}
+
+// ActivationContract::for_tensor (src/kernels.rs:1663-1673): 0 = Q8_K, 1 = Q8_0, 2 = pinned PTQ1 Q8_0.
+inline int contract_for(uint32_t kind, uint64_t cols, int pinned) {
+    if (kind == PRISM_KIND_PTQ1 && pinned) return 2;
+    if (kind == PRISM_KIND_Q2_K) return 0;
+    if (kind == PRISM_KIND_PQ2 && cols % 256 == 0) return 0;
+    return 1;
+}
+
+}  // namespace prism::rt
+
+struct prism_hip_ctx {
+    int device = 0;
+    uint32_t cus = 256;
+    uint64_t max_resident = 0, resident = 0;
+    hipStream_t stream = nullptr;
+    std::string identity, last_error;
+    bool faulted = false;
+    std::map<int64_t, prism::rt::Weight> weights;
+    std::map<uint64_t, int64_t> by_key;
+    int64_t next_id = 1;
+    int *err = nullptr;  // device error flag
+    prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre;
+};
+
+namespace prism::rt {
+
+inline int fail(prism_hip_ctx *c, int code, const std::string &msg) {
+    if (c) c->last_error = msg;
+    return code;
+}
+
+// Maps a HIP failure to the latched device-fault state.
+inline int hip_fail(prism_hip_ctx *c, hipError_t e, const char *what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return fail(c, PRISM_ERR_RESOURCE, m);
+    c->faulted = true;
+    return fail(c, PRISM_ERR_DEVICE_FAULT, m);
+}
+
+#define HIP_OR_FAIL(ctx, call)                                 \
+    do {                                                       \
+        hipError_t e_ = (call);                                \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+    } while (0)
+
+inline int ensure(prism_hip_ctx *c, DevBuf &b, size_t bytes) {
+    if (bytes <= b.cap) return PRISM_OK;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    size_t n = bytes < 4096 ? 4096 : bytes;
+    hipError_t e = hipMalloc(&b.p, n);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(scratch)");
+    b.cap = n;
+    return PRISM_OK;
+}
+
+inline int check_ready(prism_hip_ctx *c) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
+    return PRISM_OK;
+}
+
+inline const Weight *find(prism_hip_ctx *c, prism_weight_id w) {
+    auto it = c->weights.find(w);
+    return it == c->weights.end() ? nullptr : &it->second;
+}
+
+// Reads and clears the device error flag after the stream drained.
+inline int drain(prism_hip_ctx *c, hipStream_t s) {
+    HIP_OR_FAIL(c, hipStreamSynchronize(s));
+    int flag = 0;
+    HIP_OR_FAIL(c, hipMemcpy(&flag, c->err, sizeof(int), hipMemcpyDeviceToHost));
+    if (flag) {
+        if (launch_fill_i32(c->err, 0, 1, s)) return hip_fail(c, hipGetLastError(), "reset error flag");
+        HIP_OR_FAIL(c, hipStreamSynchronize(s));
+        if (flag & kErrInput) return fail(c, PRISM_ERR_NONFINITE, "non-finite activation input");
+        if (flag & kErrQuantRange) return fail(c, PRISM_ERR_NONFINITE, "activation quantization scale overflow");
+        return fail(c, PRISM_ERR_NONFINITE, "non-finite value in projection output");
+    }
+    return PRISM_OK;
+}
+
+inline int quantize(prism_hip_ctx *c, int contract, const float *x, uint64_t cols, uint32_t tokens, int pinned, void *out,
+             hipStream_t s) {
+    int rc = contract == 0 ? launch_quantize_q8k(x, cols, tokens, pinned, out, c->err, s)
+                           : launch_quantize_q8_0(x, cols, tokens, contract == 2 ? PRISM_Q8_PINNED_NATIVE
+                                                                                : (pinned ? PRISM_Q8_PINNED
+                                                                                          : PRISM_Q8_SOURCE),
+                                                  out, c->err, s);
+    if (rc) return hip_fail(c, hipGetLastError(), "quantize launch");
+    return PRISM_OK;
+}
+
+inline size_t act_bytes(int contract, uint64_t cols, uint32_t tokens) {
+    return contract == 0 ? sizeof(prism_q8k_block) * ((cols + 255) / 256) * tokens
+                         : sizeof(prism_q8_block) * (cols / 32) * tokens;
+}
+
+inline MatvecArgs matvec_args(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
+                       float *out, hipStream_t s) {
+    MatvecArgs a;
+    a.kind = w.kind;
+    a.cols = w.cols;
+    a.rows = w.rows;
+    a.row_bytes = w.row_bytes;
+    a.w = static_cast<const uint8_t *>(w.dev);
+    a.act = act;
+    a.act_format = act_format;
+    a.tokens = tokens;
+    a.pinned = pinned;
+    a.out = out;
+    a.err = c->err;
+    a.stream = s;
+    a.cus = c->cus;
+    return a;
+}
+
+inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &a, bool tiled) {
+    int rc = tiled ? launch_matvec_tiled(a) : launch_matvec(a);
+    if (rc == -2) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported matvec geometry");
+    if (rc) return hip_fail(c, hipGetLastError(), "matvec launch");
+    return PRISM_OK;
+}
+
+inline int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
+           float *out, hipStream_t s) {
+    return run_matvec(c, matvec_args(c, w, act_format, act, tokens, pinned, out, s), w.tiled);
+}
+
+// f32 input for a tiled weight, quantized in the kernel prologue with the contract
+// matvec_into would use; `residual` is added to every output row.
+inline MatvecArgs f32_args(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
+                    const float *residual, hipStream_t s) {
+    MatvecArgs a = matvec_args(c, w, kActF32, x, tokens, pinned, out, s);
+    const int contract = contract_for(w.kind, w.cols, pinned);
+    a.qcontract_is_q8k = contract == 0;
+    a.qcontract = contract == 0 ? pinned : contract == 2 ? PRISM_Q8_PINNED_NATIVE : (pinned ? PRISM_Q8_PINNED : PRISM_Q8_SOURCE);
+    a.residual = residual;
+    return a;
+}
+
+}  // namespace prism::rt

@@ -98,6 +98,12 @@ def lib() -> ctypes.CDLL:
         "prism_hip_ffn_chain_device": (I, [P, I64, I64, I64, P, P, I, P, P, P]),
         "prism_hip_sync": (I, [P, P]),
         "prism_hip_stream": (P, [P]),
+        "prism_hip_decoder_create": (P, [P, P, U32]),
+        "prism_hip_decoder_destroy": (None, [P]),
+        "prism_hip_decoder_set_layer": (I, [P, U32, P, P, P, P, P, P, P, P, P]),
+        "prism_hip_decoder_set_cache": (I, [P, U32, P, P, U64]),
+        "prism_hip_decoder_set_head": (I, [P, P, P]),
+        "prism_hip_decoder_generate": (I, [P, U32, U64, U32, I, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -282,3 +288,64 @@ class Context:
 
     def sync(self, stream=None) -> int:
         return lib().prism_hip_sync(self._h, stream)
+
+
+class DecoderGeometry(ctypes.Structure):
+    """prism_decoder_geometry."""
+    _fields_ = [(n, ctypes.c_uint64) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "rope", "vocab",
+                                                "layers", "max_tokens")] + [
+        ("rope_sections", ctypes.c_uint64 * 4), ("rope_base", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+class Decoder:
+    """A resident full-attention decoder (prism_hip_decoder_*) built from a model dict
+    (synth.decoder_model): weights uploaded and repacked once, KV caches prefilled."""
+
+    def __init__(self, ctx: Context, model: dict, max_steps: int = 128):
+        g = model["geometry"]
+        self.ctx = ctx
+        self.g = g
+        geo = DecoderGeometry(g["hidden"], g["ffn"], g["heads"], g["kv_heads"], g["head_dim"], g["rope"], g["vocab"],
+                              g["layers"], g["max_tokens"], (ctypes.c_uint64 * 4)(*g["rope_sections"]),
+                              g["rope_base"], g["eps"])
+        self._h = lib().prism_hip_decoder_create(ctx._h, ctypes.byref(geo), max_steps)
+        if not self._h:
+            raise PrismError(ERR_INVALID_INPUT, lib().prism_hip_last_error(ctx._h).decode())
+        try:
+            for i, L in enumerate(model["layers"]):
+                arrs = [np.ascontiguousarray(L[n]) for n in ("qkv", "o", "gate", "up", "down")]
+                norms = [np.ascontiguousarray(L[n], np.float32) for n in ("norm", "post_norm", "q_norm", "k_norm")]
+                self._check(lib().prism_hip_decoder_set_layer(self._h, i, *(_ptr(a) for a in arrs + norms)))
+                k = np.ascontiguousarray(L["k_prefill"], np.uint16)
+                v = np.ascontiguousarray(L["v_prefill"], np.uint16)
+                self._check(lib().prism_hip_decoder_set_cache(self._h, i, _ptr(k), _ptr(v), L["kv_prefill"]))
+            lm = np.ascontiguousarray(model["lm_head"])
+            on = np.ascontiguousarray(model["output_norm"], np.float32)
+            self._check(lib().prism_hip_decoder_set_head(self._h, _ptr(lm), _ptr(on)))
+        except Exception:
+            self.close()
+            raise
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise PrismError(rc, lib().prism_hip_last_error(self.ctx._h).decode())
+
+    def generate(self, token: int, pos: int, steps: int, graph: bool = True, logits: bool = False):
+        """Greedy decode: returns (tokens[steps], logits[steps][vocab] or None, device seconds)."""
+        toks = np.zeros(steps, np.uint32)
+        lg = np.zeros((steps, self.g["vocab"]), np.float32) if logits else None
+        secs = ctypes.c_double(0.0)
+        self._check(lib().prism_hip_decoder_generate(self._h, token, pos, steps, int(graph), _ptr(toks),
+                                                     _ptr(lg) if logits else None, ctypes.byref(secs)))
+        return toks, lg, secs.value
+
+    def close(self) -> None:
+        if self._h:
+            lib().prism_hip_decoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -124,3 +124,57 @@ def activations(n: int, seed: int, tokens: int = 1) -> np.ndarray:
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((tokens, n)).astype(np.float32)
     return x[0] if tokens == 1 else x
+
+
+# ---- full-attention decode step ------------------------------------------------------
+
+# The 28-layer decode workload: hidden 2048, 16 query / 4 KV heads of 128, FFN 6144,
+# tied 151936-token Q8_0 LM head, binary16 KV cache prefilled to 1024 tokens with room
+# for 128 more.  RoPE on 64 of each head's 128 dimensions with base 1e7 and M-RoPE
+# sections (11, 11, 10, 0), the reference's Qwen35 test geometry (src/graph.rs:7321-7322).
+DECODE_GEOMETRY = {
+    "hidden": 2048, "ffn": 6144, "heads": 16, "kv_heads": 4, "head_dim": 128, "rope": 64,
+    "rope_sections": (11, 11, 10, 0), "rope_base": 10_000_000.0, "eps": 1e-6,
+    "vocab": 151936, "layers": 28, "max_tokens": 1024 + 128,
+}
+
+
+def _norm_weights(rng, n: int) -> np.ndarray:
+    """RMSNorm weights 1 + 0.1 N(0,1) (binary32)."""
+    return (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+
+
+def decoder_model(seed: int = 0, kv_prefill: int = 1024, **overrides) -> dict:
+    """Seeded synthetic decoder: every linear layer PTQ1 (the ternary distribution
+    above), q/k/v stacked into one matrix of (heads + 2 kv_heads) * head_dim rows, a
+    Q8_0 LM head from N(0,0.02) floats that doubles as the token embedding, RMSNorm
+    weights around 1, and binary16 KV caches prefilled with N(0,1) values."""
+    g = dict(DECODE_GEOMETRY)
+    g.update(overrides)
+    H, F, D = g["hidden"], g["ffn"], g["head_dim"]
+    QW, KW = g["heads"] * D, g["kv_heads"] * D
+    assert kv_prefill <= g["max_tokens"]
+    rng = np.random.default_rng(seed)
+    layers = []
+    for layer in range(g["layers"]):
+        s = 1_000_003 * seed + 16 * layer
+        layers.append({
+            "qkv": ptq1_weights(QW + 2 * KW, H, s + 1),
+            "o": ptq1_weights(H, QW, s + 2),
+            "gate": ptq1_weights(F, H, s + 3),
+            "up": ptq1_weights(F, H, s + 4),
+            "down": ptq1_weights(H, F, s + 5),
+            "norm": _norm_weights(rng, H),
+            "post_norm": _norm_weights(rng, H),
+            "q_norm": _norm_weights(rng, D),
+            "k_norm": _norm_weights(rng, D),
+            "kv_prefill": kv_prefill,
+            "k_prefill": rng.standard_normal((kv_prefill, KW)).astype(np.float16).view(np.uint16),
+            "v_prefill": rng.standard_normal((kv_prefill, KW)).astype(np.float16).view(np.uint16),
+        })
+    return {
+        "geometry": g,
+        "layers": layers,
+        "lm_head": q8_0_weights(g["vocab"], H, 1_000_003 * seed + 999_983),
+        "output_norm": _norm_weights(rng, H),
+    }

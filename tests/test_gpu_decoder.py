@@ -1,0 +1,112 @@
+"""The resident full-attention decoder (prism_hip_decoder_*) against the oracle's
+decode step, with teacher forcing: the oracle replays the tokens the GPU chose.
+
+Parity bar for the full step (logits after 2..28 layers): max |gpu - oracle| over
+a step's logits <= 1e-3 * max |oracle logit| (source SiLU, softmax exp and RoPE
+cos/sin come from different libms; every projection and quantizer is bit-exact),
+and every greedy token equal to the oracle's argmax unless the oracle's two logits
+are within that tolerance of each other.
+"""
+
+import numpy as np
+import pytest
+
+import prism_hip as ph
+import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+THREADS = 16
+
+SMALL = dict(hidden=512, ffn=1024, heads=4, kv_heads=2, vocab=2048, layers=2, max_tokens=96)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ph.Context(0)
+    yield c
+    c.close()
+
+
+def check_against_oracle(model, pos, first, toks, logits):
+    import oracle
+
+    od = oracle.Decoder(model, threads=THREADS)
+    tok = first
+    for i in range(len(toks)):
+        ref = od.step(tok, pos + i)
+        scale = float(np.abs(ref).max())
+        err = float(np.abs(logits[i] - ref).max())
+        assert err <= TOL * scale, f"step {i}: max |gpu - oracle| = {err} > {TOL} * {scale}"
+        want = oracle.argmax(ref)
+        if int(toks[i]) != want:
+            gap = abs(float(ref[want]) - float(ref[int(toks[i])]))
+            assert gap <= TOL * scale, f"step {i}: token {toks[i]} vs oracle {want} (gap {gap})"
+        tok = int(toks[i])
+
+
+@pytest.mark.parametrize("seed,prefill", [(1, 40), (2, 0), (3, 1)])
+def test_gpu_decoder_small_matches_oracle(ctx, seed, prefill):
+    """Two layers, small widths: every step's logits and greedy token; the first
+    position in a cache (prefill 0) and a single cached token included."""
+    model = synth.decoder_model(seed, kv_prefill=prefill, **SMALL)
+    dec = ph.Decoder(ctx, model, max_steps=16)
+    try:
+        toks, logits, _ = dec.generate(7, prefill, 12, graph=False, logits=True)
+    finally:
+        dec.close()
+    check_against_oracle(model, prefill, 7, toks, logits)
+
+
+def test_gpu_decoder_graph_replay_equals_eager(ctx):
+    """The captured graph (position and token read from device memory) gives the same
+    bits as launching every kernel each step, on a second generate as well."""
+    model = synth.decoder_model(4, kv_prefill=33, **SMALL)
+    outs = []
+    for graph in (False, True, True):
+        dec = ph.Decoder(ctx, model, max_steps=16)
+        try:
+            toks, logits, _ = dec.generate(11, 33, 9, graph=graph, logits=True)
+            if graph:  # a second call replays the same graph from a fresh start
+                toks2, logits2, _ = dec.generate(11, 33, 9, graph=True, logits=True)
+                assert np.array_equal(toks, toks2)
+                assert np.array_equal(logits.view(np.uint32), logits2.view(np.uint32))
+        finally:
+            dec.close()
+        outs.append((toks, logits))
+    for toks, logits in outs[1:]:
+        assert np.array_equal(toks, outs[0][0])
+        assert np.array_equal(logits.view(np.uint32), outs[0][1].view(np.uint32))
+
+
+def test_gpu_decoder_full_width_matches_oracle(ctx):
+    """The workload's widths (hidden 2048, 16/4 heads, FFN 6144, 151936-token LM head
+    on the row-tile kernel) with two layers and a 1024-token cache."""
+    model = synth.decoder_model(5, kv_prefill=1024, layers=2)
+    dec = ph.Decoder(ctx, model, max_steps=4)
+    try:
+        toks, logits, _ = dec.generate(1, 1024, 3, graph=True, logits=True)
+    finally:
+        dec.close()
+    check_against_oracle(model, 1024, 1, toks, logits)
+
+
+def test_gpu_decoder_rejects_bad_arguments(ctx):
+    model = synth.decoder_model(6, kv_prefill=8, **SMALL)
+    dec = ph.Decoder(ctx, model, max_steps=4)
+    try:
+        with pytest.raises(ph.PrismError):
+            dec.generate(model["geometry"]["vocab"], 8, 2)  # token out of range
+        with pytest.raises(ph.PrismError):
+            dec.generate(1, SMALL["max_tokens"] - 1, 2)  # past the cache
+        with pytest.raises(ph.PrismError):
+            dec.generate(1, 8, 5)  # more steps than max_steps
+        toks, _, _ = dec.generate(1, 8, 2)  # still usable
+        assert toks.shape == (2,)
+    finally:
+        dec.close()
+    bad = synth.decoder_model(6, kv_prefill=0, **dict(SMALL, layers=1))
+    bad["geometry"]["head_dim"] = 64
+    with pytest.raises(ph.PrismError):
+        ph.Decoder(ctx, bad)
