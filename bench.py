@@ -244,6 +244,58 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
     return {"M": M, "ms": t * 1e3, "TOPS": ops / t / 1e12, "frac_int8_peak": ops / t / PEAK_I8}
 
 
+def decode_token_bytes(g: dict, pos: int) -> int:
+    """Algorithmic bytes of one decode step at position `pos`: every packed weight at
+    its native size once (PTQ1 linears, the Q8_0 LM head), the binary16 K and V rows
+    attention reads (pos + 1 tokens per layer), and the embedding row."""
+    H, F, D = g["hidden"], g["ffn"], g["head_dim"]
+    QW, KW = g["heads"] * D, g["kv_heads"] * D
+
+    def ptq1(rows, cols):
+        return rows * cols // 128 * 28
+
+    layer = ptq1(QW + 2 * KW, H) + ptq1(H, QW) + 2 * ptq1(F, H) + ptq1(H, F)
+    kv = 2 * (pos + 1) * KW * 2
+    return g["layers"] * (layer + kv) + g["vocab"] * H // 32 * 34 + H // 32 * 34
+
+
+def bench_decode(ctx: ph.Context, steps: int = 128, cpu_steps: int = 2, graph: bool = True):
+    """The 28-layer synthetic decode step: greedy generation of `steps` tokens from
+    position 1024 (KV caches prefilled with 1024 tokens), one captured HIP graph per
+    step, timed with HIP events on the library stream; the oracle's step timed beside
+    it on the host for `cpu_steps` tokens."""
+    t0 = time.perf_counter()
+    model = synth.decoder_model(0)
+    g = model["geometry"]
+    log(f"decode model generated in {time.perf_counter() - t0:.1f} s")
+    dec = ph.Decoder(ctx, model, max_steps=steps)
+    dec.generate(1, 1024, 8, graph=graph)  # capture and warm
+    toks, _, secs = dec.generate(1, 1024, steps, graph=graph)
+    dec.close()
+    nbytes = sum(decode_token_bytes(g, 1024 + i) for i in range(steps))
+    out = {"workload": "28-layer synthetic decode, hidden 2048, 16/4 heads x 128, FFN 6144, PTQ1 linears, "
+                       "tied Q8_0 LM head 151936, f16 KV prefilled to 1024, greedy",
+           "steps": steps, "graph": graph, "tokens_per_s": steps / secs, "ms_per_token": secs / steps * 1e3,
+           "bytes_per_token": nbytes // steps, "GBps": nbytes / secs / 1e9, "frac_hbm": nbytes / secs / PEAK_HBM,
+           "first_tokens": [int(t) for t in toks[:8]]}
+    if cpu_steps:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+
+        threads = min(16, os.cpu_count() or 1)
+        od = oracle.Decoder(model, threads=threads)
+        tok, cpu_toks, t0 = 1, [], time.perf_counter()
+        for i in range(cpu_steps):
+            tok = oracle.argmax(od.step(tok, 1024 + i))
+            cpu_toks.append(tok)
+        dt = (time.perf_counter() - t0) / cpu_steps
+        out["cpu_baseline"] = {"tokens_per_s": 1.0 / dt, "cores": threads, "kind": "port",
+                               "sample": f"{cpu_steps} decode steps of the scalar C restatement, rows split over "
+                                         f"{threads} threads",
+                               "same_tokens": cpu_toks == [int(t) for t in toks[:cpu_steps]]}
+    return out
+
+
 def cpu_baseline(budget_s: float = 12.0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -275,6 +327,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="", help="comma-separated token counts: time only the prefill GEMM")
     ap.add_argument("--matvec-only", default="", help="comma-separated kind:rows:cols: time only these matvecs")
+    ap.add_argument("--decode-only", action="store_true", help="time only the 28-layer decode step")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="with --decode-only: launch every kernel each step instead of replaying a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -287,6 +342,10 @@ def main() -> int:
         return calibrate_copy()
     ctx = ph.Context(0)
     log(ctx.identity)
+    if args.decode_only:
+        print(json.dumps(bench_decode(ctx, cpu_steps=0, graph=not args.decode_eager)), flush=True)
+        ctx.close()
+        return 0
     if args.prefill_only or args.matvec_only:
         for M in filter(None, args.prefill_only.split(",")):
             print(json.dumps(bench_prefill(ctx, int(M))), flush=True)
@@ -316,6 +375,9 @@ def main() -> int:
             r = bench_prefill(ctx, M)
             log(f"prefill M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
             extras["prefill_ptq1_6144x2048"].append(r)
+        r = bench_decode(ctx)
+        log(f"decode: {r['ms_per_token']:.3f} ms/token, {r['tokens_per_s']:.1f} tok/s, {r['GBps']:.1f} GB/s")
+        extras["decode_28_layer"] = r
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
         log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")

@@ -24,7 +24,9 @@ namespace {
 
 constexpr uint32_t kHead = 128;        // head dimension the attention kernels are built for
 constexpr uint32_t kScoreChunk = 256;  // positions per score workgroup
-constexpr uint32_t kValueGroups = 8;   // position groups per value workgroup (x 128 dims)
+constexpr uint32_t kValueDims = 32;     // dimensions per value workgroup
+constexpr uint32_t kValueGroups = 128;  // position groups per value workgroup (x kValueDims/4 threads)
+constexpr uint32_t kMaxTokens = 8192;   // KV cache positions the value kernel's LDS allows
 
 __device__ __forceinline__ uint16_t f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
@@ -123,18 +125,22 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
     if (e && tid == 0) raise_error(p.err, e);
 }
 
-// Grid (heads), 1024 threads, dynamic LDS = max_tokens floats.  softmax_round_f16
-// (src/kernels.rs:4431-4462) of the head's pos+1 scores, then source_value_tile
-// (src/kernels.rs:2971-3011): out[d] = sum_t p_t * v_t[d] in binary64, rounded to
-// binary32; thread (g, d) sums positions g, g+8, ... and the eight partial sums are
-// added in order.
+// Grid (heads, kHead / kValueDims), 1024 threads.  softmax_round_f16 (src/kernels.rs:
+// 4431-4462) of the head's pos+1 scores -- every workgroup recomputes it -- then
+// source_value_tile (src/kernels.rs:2971-3011) for this workgroup's kValueDims
+// dimensions: out[d] = sum_t p_t v_t[d] in binary64.  Each term is a binary16 x
+// binary16 product, exact in binary32, and a binary64 sum of such terms is exact
+// unless they span more than 53 bits of magnitude (probabilities below 2^-24 are
+// binary16 zeros), so summing the positions in 128 interleaved groups and then the
+// groups does not change the result.
 __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
-    extern __shared__ float prob[];
     __shared__ float redf[16];
     __shared__ double redd[16];
-    __shared__ double part[kValueGroups][kHead];
+    __shared__ float prob[kMaxTokens];
+    __shared__ double acc[16][kValueDims];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
-    const uint32_t h = blockIdx.x, kh = h / (p.heads / p.kv_heads), kw = p.kv_heads * kHead;
+    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kValueDims;
+    const uint32_t kh = h / (p.heads / p.kv_heads), kw = p.kv_heads * kHead;
     const uint32_t pos = p.state->pos;
     if (pos >= p.max_tokens) return;  // reported by the score kernel
     const uint32_t n = pos + 1;
@@ -153,14 +159,14 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     m = redf[0];
     for (uint32_t w = 1; w < nw; ++w) m = fmaxf(m, redf[w]);
     if (__syncthreads_or(bad) || !finite(m)) {
-        if (tid == 0) raise_error(p.err, kErrNonfinite);
+        if (tid == 0 && blockIdx.y == 0) raise_error(p.err, kErrNonfinite);
         return;
     }
     double tot = 0.0;
     for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const float v = exp_f32(sc[i] - m);
-        prob[i] = v;
-        tot += static_cast<double>(v);
+        const float e = exp_f32(sc[i] - m);
+        prob[i] = e;
+        tot += static_cast<double>(e);
     }
 #pragma unroll
     for (int k = 32; k >= 1; k >>= 1) tot += __shfl_xor(tot, k);
@@ -171,20 +177,44 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     const float inv = static_cast<float>(1.0 / tot);
     for (uint32_t i = tid; i < n; i += blockDim.x) prob[i] = round_f16(prob[i] * inv);
     __syncthreads();
-    const uint32_t g = tid / kHead, d = tid % kHead;
-    if (g < kValueGroups) {
-        double s = 0.0;
-        const uint16_t *v = p.vcache + kh * kHead + d;
-        for (uint32_t i = g; i < n; i += kValueGroups)
-            s += static_cast<double>(prob[i] * h2f(v[static_cast<size_t>(i) * kw]));
-        part[g][d] = s;
+    // Thread (g, q): positions g, g+128, ... of dimensions d0+4q .. d0+4q+3, eight rows
+    // loaded per batch before any is used.
+    const uint32_t g = tid / (kValueDims / 4), q = tid % (kValueDims / 4);
+    double a[4] = {0.0, 0.0, 0.0, 0.0};
+    const uint16_t *vb = p.vcache + kh * kHead + d0 + 4 * q;
+    for (uint32_t i0 = g; i0 < n; i0 += 8 * kValueGroups) {
+        uint2 w[8];
+        float pr[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t i = i0 + k * kValueGroups;
+            const bool in = i < n;
+            w[k] = in ? *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i) * kw) : make_uint2(0, 0);
+            pr[k] = in ? prob[i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            a[0] += static_cast<double>(pr[k] * h2f(w[k].x & 0xffffu));
+            a[1] += static_cast<double>(pr[k] * h2f(w[k].x >> 16));
+            a[2] += static_cast<double>(pr[k] * h2f(w[k].y & 0xffffu));
+            a[3] += static_cast<double>(pr[k] * h2f(w[k].y >> 16));
+        }
     }
+    // A wavefront holds eight groups of the same eight quads (lane = 8 * group + quad):
+    // fold them with lane shuffles, then the wavefronts through LDS.
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int k = 8; k <= 32; k <<= 1) a[j] += __shfl_xor(a[j], k);
+    if (lane < kValueDims / 4)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[wave][4 * q + j] = a[j];
     __syncthreads();
-    if (tid < kHead) {
-        double s = part[0][tid];
-        for (uint32_t k = 1; k < kValueGroups; ++k) s += part[k][tid];
-        const float o = static_cast<float>(s);
-        p.out[h * kHead + tid] = o;
+    if (tid < kValueDims) {
+        double t = acc[0][tid];
+        for (uint32_t w = 1; w < nw; ++w) t += acc[w][tid];
+        const float o = static_cast<float>(t);
+        p.out[h * kHead + d0 + tid] = o;
         if (!finite(o)) raise_error(p.err, kErrNonfinite);
     }
 }
@@ -227,31 +257,25 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t *__restrict__ emb, 
     for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = q8_0_tiled_at(emb, rows, cols, token, i);
 }
 
-// One workgroup: greedy choice (the first index of the largest logit), recorded in
-// the state and the token history, position advanced, and the chosen token's
-// embedding (the tied LM head row) written as the next step's hidden state.
-__global__ __launch_bounds__(1024) void k_argmax_embed(const float *__restrict__ logits, uint32_t vocab,
-                                                       const uint8_t *__restrict__ emb, uint32_t cols,
-                                                       DecodeState *__restrict__ st, uint32_t *__restrict__ tokens,
-                                                       uint32_t max_steps, float *__restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ uint32_t bi[16];
-    __shared__ uint32_t chosen;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
-    float best = -__builtin_inff();
-    uint32_t idx = 0xffffffffu;
-    for (uint32_t i = tid; i < vocab; i += blockDim.x) {
-        const float v = logits[i];
-        if (v > best || idx == 0xffffffffu) {
-            best = v;
-            idx = i;
-        }
-    }
+// Greedy choice: the first index of the largest logit.  k_argmax_slices reduces
+// contiguous slices to their (largest value, first index); k_argmax_embed reduces the
+// slices in order, records the token in the state and the token history, advances
+// the position, and writes the chosen token's embedding (the tied LM head row) as the
+// next step's hidden state.
+constexpr uint32_t kArgmaxGroups = 128;
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+    return bi == 0xffffffffu || (i != 0xffffffffu && (v > bv || (v == bv && i < bi)));
+}
+
+// Workgroup-wide (value, index) reduction; every thread returns the winner.
+__device__ void reduce_best(float &best, uint32_t &idx, float *bv, uint32_t *bi) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
 #pragma unroll
     for (int k = 32; k >= 1; k >>= 1) {
         const float ov = __shfl_xor(best, k);
         const uint32_t oi = __shfl_xor(idx, k);
-        if (ov > best || (ov == best && oi < idx)) {
+        if (better(ov, oi, best, idx)) {
             best = ov;
             idx = oi;
         }
@@ -261,33 +285,84 @@ __global__ __launch_bounds__(1024) void k_argmax_embed(const float *__restrict__
         bi[wave] = idx;
     }
     __syncthreads();
-    if (tid == 0) {
-        float b = bv[0];
-        uint32_t t = bi[0];
-        for (uint32_t w = 1; w < nw; ++w)
-            if (bv[w] > b || (bv[w] == b && bi[w] < t)) {
-                b = bv[w];
-                t = bi[w];
+    best = bv[0];
+    idx = bi[0];
+    for (uint32_t w = 1; w < nw; ++w)
+        if (better(bv[w], bi[w], best, idx)) {
+            best = bv[w];
+            idx = bi[w];
+        }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_slices(const float *__restrict__ logits, uint32_t vocab,
+                                                       float *__restrict__ pval, uint32_t *__restrict__ pidx) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t span = (vocab + gridDim.x - 1) / gridDim.x;
+    const uint32_t lo = blockIdx.x * span, hi = lo + span < vocab ? lo + span : vocab;
+    float best = -__builtin_inff();
+    uint32_t idx = 0xffffffffu;
+    for (uint32_t i0 = lo + tid; i0 < hi; i0 += 8 * blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t i = i0 + k * blockDim.x;
+            v[k] = i < hi ? logits[i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t i = i0 + k * blockDim.x;
+            if (i < hi && better(v[k], i, best, idx)) {
+                best = v[k];
+                idx = i;
             }
-        chosen = t;
+        }
+    }
+    reduce_best(best, idx, bv, bi);
+    if (tid == 0) {
+        pval[blockIdx.x] = best;
+        pidx[blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ pval, const uint32_t *__restrict__ pidx,
+                                                      uint32_t vocab, const uint8_t *__restrict__ emb, uint32_t cols,
+                                                      DecodeState *__restrict__ st, uint32_t *__restrict__ tokens,
+                                                      uint32_t max_steps, float *__restrict__ out) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const uint32_t tid = threadIdx.x;
+    float best = -__builtin_inff();
+    uint32_t idx = 0xffffffffu;
+    for (uint32_t g = tid; g < kArgmaxGroups; g += blockDim.x)
+        if (better(pval[g], pidx[g], best, idx)) {
+            best = pval[g];
+            idx = pidx[g];
+        }
+    reduce_best(best, idx, bv, bi);
+    const uint32_t token = idx < vocab ? idx : 0;  // a slice always holds a valid index
+    if (tid == 0) {
         const uint32_t step = st->step;
-        if (step < max_steps) tokens[step] = t;
-        st->token = t;
+        if (step < max_steps) tokens[step] = token;
+        st->token = token;
         st->step = step + 1;
         st->pos = st->pos + 1;
     }
-    __syncthreads();
-    const uint32_t token = chosen;
     for (uint32_t i = tid; i < cols; i += blockDim.x) out[i] = q8_0_tiled_at(emb, vocab, cols, token, i);
 }
 
 }  // namespace
 
+size_t argmax_scratch_bytes() { return (sizeof(float) + sizeof(uint32_t)) * kArgmaxGroups; }
+
 int launch_attention(const AttnArgs &a) {
-    if (a.head_dim != kHead || a.rope > kHead || a.rope % 2 || a.kv_heads == 0 || a.heads % a.kv_heads) return -2;
+    if (a.head_dim != kHead || a.rope > kHead || a.rope % 2 || a.kv_heads == 0 || a.heads % a.kv_heads ||
+        a.max_tokens > kMaxTokens)
+        return -2;
     const dim3 sg(a.heads, (a.max_tokens + kScoreChunk - 1) / kScoreChunk);
     hipLaunchKernelGGL(k_attn_scores, sg, dim3(256), 0, a.stream, a);
-    hipLaunchKernelGGL(k_attn_values, dim3(a.heads), dim3(1024), sizeof(float) * a.max_tokens, a.stream, a);
+    hipLaunchKernelGGL(k_attn_values, dim3(a.heads, kHead / kValueDims), dim3(1024), 0, a.stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -304,8 +379,11 @@ int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, const Deco
 }
 
 int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
-                        uint32_t *tokens, uint32_t max_steps, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(1024), 0, s, logits, vocab,
+                        uint32_t *tokens, uint32_t max_steps, float *out, void *scratch, hipStream_t s) {
+    float *pval = static_cast<float *>(scratch);
+    uint32_t *pidx = reinterpret_cast<uint32_t *>(pval + kArgmaxGroups);
+    hipLaunchKernelGGL(k_argmax_slices, dim3(kArgmaxGroups), dim3(256), 0, s, logits, vocab, pval, pidx);
+    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(256), 0, s, pval, pidx, vocab,
                        static_cast<const uint8_t *>(emb_tiled), cols, st, tokens, max_steps, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -36,6 +36,7 @@ struct prism_hip_decoder {
     float *logits_all = nullptr;
     size_t logits_all_steps = 0;
     void *lm_act = nullptr;
+    void *argmax_scratch = nullptr;  // zero-filled at creation
     DecodeState *state = nullptr;
     uint32_t *tokens = nullptr;
     std::vector<void *> owned;  // device allocations freed on destroy
@@ -134,7 +135,7 @@ int enqueue_step(prism_hip_decoder *d) {
     int rc = matvec(c, *lm, kActQ8, d->lm_act, 1, 0, d->logits, s);
     if (rc) return rc;
     if (launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), lm->dev, static_cast<uint32_t>(g.hidden),
-                            d->state, d->tokens, d->max_steps, h0, s))
+                            d->state, d->tokens, d->max_steps, h0, d->argmax_scratch, s))
         return hip_fail(c, hipGetLastError(), "argmax launch");
     return PRISM_OK;
 }
@@ -194,6 +195,10 @@ prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decode
     if (!rc) rc = dalloc(d, &d->lm_act, sizeof(prism_q8_block) * (H / 32));
     if (!rc) rc = dalloc(d, &d->state, sizeof(DecodeState));
     if (!rc) rc = dalloc(d, &d->tokens, sizeof(uint32_t) * max_steps);
+    const size_t gs = argmax_scratch_bytes();
+    if (!rc) rc = dalloc(d, &d->argmax_scratch, gs);
+    if (!rc && hipMemset(d->argmax_scratch, 0, gs) != hipSuccess)
+        rc = hip_fail(c, hipGetLastError(), "decoder scratch reset");
     if (rc) {
         prism_hip_decoder_destroy(d);
         return nullptr;

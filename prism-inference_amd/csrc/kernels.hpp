@@ -100,8 +100,11 @@ int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *
 int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, const DecodeState *st, float *out,
                  hipStream_t s);
 // Greedy token from logits[vocab], recorded and advanced in the state, and its
-// embedding (row of the tiled Q8_0 matrix [vocab][cols]) written to out.
+// embedding (row of the tiled Q8_0 matrix [vocab][cols]) written to out; two launches.
+// scratch: argmax_scratch_bytes() of device memory.
+size_t argmax_scratch_bytes();
 int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
-                        uint32_t *tokens, uint32_t max_steps, float *out, hipStream_t s);
+                        uint32_t *tokens, uint32_t max_steps, float *out, void *scratch, hipStream_t s);
+
 
 }  // namespace prism
