@@ -32,6 +32,18 @@ __device__ __forceinline__ uint16_t f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
+// rope_frequencies_mrope (src/graph.rs:6406-6431) for text positions [pos, pos, pos, 0]:
+// index i rotates by theta_sector * scale^i, the products rounded one by one; thread
+// i < rope/2 writes pair i.
+__device__ __forceinline__ void rope_freqs(DecodeState *st, uint32_t pos, const RopeArgs &r) {
+    const uint32_t i = threadIdx.x;
+    if (i >= r.rope / 2) return;
+    float angle = i < 3 * r.sections[i % 3] ? static_cast<float>(pos) : 0.0f;
+    for (uint32_t k = 0; k < i; ++k) angle = angle * r.theta_scale;
+    st->cs[i] = cos_f32(angle);
+    st->sn[i] = sin_f32(angle);
+}
+
 // rms_norm_rope_round_f16_into::<false> (src/kernels.rs:3679-3733) of one head
 // (kHead values at src) into dst (LDS): (x * scale) * w, rotate the first `rope`
 // dimensions (index i with i + rope/2), round to binary16.  Every thread of the
@@ -71,7 +83,6 @@ __device__ int norm_rope_head(const float *__restrict__ src, const float *__rest
 // caches, and thread t scores position chunk*256 + t <= pos:
 // f16_dot(q, k) * (1/sqrt(head)) with the current key taken from registers.
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
-    __shared__ float cs[kHead / 2], sn[kHead / 2];
     __shared__ float qv[kHead], kv[kHead], tmp[kHead];
     __shared__ double red[16];
     const uint32_t tid = threadIdx.x, h = blockIdx.x, chunk = blockIdx.y;
@@ -82,16 +93,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
         if (tid == 0 && h == 0 && chunk == 0) raise_error(p.err, kErrInput);
         return;
     }
-    // rope_frequencies_mrope (src/graph.rs:6406-6431) for text positions [pos, pos, pos, 0]:
-    // index i rotates by theta_sector * scale^i, the products rounded one by one.
-    if (tid < p.rope / 2) {
-        const uint32_t sector = tid % 3;
-        float angle = tid < 3 * p.sections[sector] ? static_cast<float>(pos) : 0.0f;
-        for (uint32_t i = 0; i < tid; ++i) angle = angle * p.theta_scale;
-        cs[tid] = cos_f32(angle);
-        sn[tid] = sin_f32(angle);
-    }
-    __syncthreads();
+    const float *cs = p.state->cs, *sn = p.state->sn;
     int e = norm_rope_head(p.qkv + h * kHead, p.q_norm, qv, tmp, red, cs, sn, p.rope, p.eps);
     e |= norm_rope_head(p.qkv + qw + kh * kHead, p.k_norm, kv, tmp, red, cs, sn, p.rope, p.eps);
     if (h % group == 0 && chunk == 0 && tid < kHead) {
@@ -104,23 +106,30 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHead));
     const uint32_t t = chunk * kScoreChunk + tid;
     if (t <= pos) {
-        double s = 0.0;
+        // Four binary64 partial sums shorten the dependent chain; the terms are binary16
+        // x binary16 products (exact in binary32) whose binary64 sums are exact, so the
+        // split changes no bit of f16_dot's sequential sum.
+        double s[4] = {0.0, 0.0, 0.0, 0.0};
         if (t == pos) {
-            for (uint32_t d = 0; d < kHead; ++d) s += static_cast<double>(qv[d] * kv[d]);
+            for (uint32_t d = 0; d < kHead; d += 4)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[j] += static_cast<double>(qv[d + j] * kv[d + j]);
         } else {
             const uint4 *k = reinterpret_cast<const uint4 *>(p.kcache + static_cast<size_t>(t) * kw + kh * kHead);
-#pragma unroll 4
+            uint4 w[kHead / 8];
+#pragma unroll
+            for (uint32_t c = 0; c < kHead / 8; ++c) w[c] = k[c];
+#pragma unroll
             for (uint32_t c = 0; c < kHead / 8; ++c) {
-                const uint4 q = k[c];
-                const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+                const uint32_t w4[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    s += static_cast<double>(qv[8 * c + 2 * j] * h2f(w4[j] & 0xffffu));
-                    s += static_cast<double>(qv[8 * c + 2 * j + 1] * h2f(w4[j] >> 16));
+                    s[j] += static_cast<double>(qv[8 * c + 2 * j] * h2f(w4[j] & 0xffffu));
+                    s[j] += static_cast<double>(qv[8 * c + 2 * j + 1] * h2f(w4[j] >> 16));
                 }
             }
         }
-        p.scores[static_cast<size_t>(h) * p.max_tokens + t] = static_cast<float>(s) * scale;
+        p.scores[static_cast<size_t>(h) * p.max_tokens + t] = static_cast<float>((s[0] + s[1]) + (s[2] + s[3])) * scale;
     }
     if (e && tid == 0) raise_error(p.err, e);
 }
@@ -252,8 +261,9 @@ __device__ __forceinline__ float q8_0_tiled_at(const uint8_t *__restrict__ w, ui
 }
 
 __global__ __launch_bounds__(256) void k_embed(const uint8_t *__restrict__ emb, uint64_t rows, uint32_t cols,
-                                               const DecodeState *__restrict__ st, float *__restrict__ out) {
+                                               DecodeState *__restrict__ st, RopeArgs rope, float *__restrict__ out) {
     const uint32_t token = st->token;
+    rope_freqs(st, st->pos, rope);
     for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = q8_0_tiled_at(emb, rows, cols, token, i);
 }
 
@@ -328,11 +338,13 @@ __global__ __launch_bounds__(256) void k_argmax_slices(const float *__restrict__
 
 __global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ pval, const uint32_t *__restrict__ pidx,
                                                       uint32_t vocab, const uint8_t *__restrict__ emb, uint32_t cols,
-                                                      DecodeState *__restrict__ st, uint32_t *__restrict__ tokens,
-                                                      uint32_t max_steps, float *__restrict__ out) {
+                                                      DecodeState *__restrict__ st, RopeArgs rope,
+                                                      uint32_t *__restrict__ tokens, uint32_t max_steps,
+                                                      float *__restrict__ out) {
     __shared__ float bv[4];
     __shared__ uint32_t bi[4];
     const uint32_t tid = threadIdx.x;
+    const uint32_t pos = st->pos;  // read before thread 0 advances it
     float best = -__builtin_inff();
     uint32_t idx = 0xffffffffu;
     for (uint32_t g = tid; g < kArgmaxGroups; g += blockDim.x)
@@ -347,8 +359,9 @@ __global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ 
         if (step < max_steps) tokens[step] = token;
         st->token = token;
         st->step = step + 1;
-        st->pos = st->pos + 1;
+        st->pos = pos + 1;
     }
+    rope_freqs(st, pos + 1, rope);
     for (uint32_t i = tid; i < cols; i += blockDim.x) out[i] = q8_0_tiled_at(emb, vocab, cols, token, i);
 }
 
@@ -372,19 +385,23 @@ int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, const DecodeState *st, float *out,
-                 hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, static_cast<const uint8_t *>(emb_tiled), rows, cols, st, out);
+int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, DecodeState *st, const RopeArgs &rope,
+                 float *out, hipStream_t s) {
+    if (rope.rope > 2 * 64) return -2;
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, static_cast<const uint8_t *>(emb_tiled), rows, cols, st,
+                       rope, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
-                        uint32_t *tokens, uint32_t max_steps, float *out, void *scratch, hipStream_t s) {
+                        const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, void *scratch,
+                        hipStream_t s) {
+    if (rope.rope > 2 * 64) return -2;
     float *pval = static_cast<float *>(scratch);
     uint32_t *pidx = reinterpret_cast<uint32_t *>(pval + kArgmaxGroups);
     hipLaunchKernelGGL(k_argmax_slices, dim3(kArgmaxGroups), dim3(256), 0, s, logits, vocab, pval, pidx);
     hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(256), 0, s, pval, pidx, vocab,
-                       static_cast<const uint8_t *>(emb_tiled), cols, st, tokens, max_steps, out);
+                       static_cast<const uint8_t *>(emb_tiled), cols, st, rope, tokens, max_steps, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -94,6 +94,15 @@ int project(prism_hip_decoder *d, prism_weight_id wid, const float *x, float *ou
     return run_matvec(c, a, true);
 }
 
+// rope_frequencies_mrope (src/graph.rs:6406-6431): theta_scale = rope_base.powf(-2 / rope).
+RopeArgs rope_args(const prism_decoder_geometry &g) {
+    RopeArgs r{};
+    r.rope = static_cast<uint32_t>(g.rope);
+    for (int i = 0; i < 4; ++i) r.sections[i] = static_cast<uint32_t>(g.rope_sections[i]);
+    r.theta_scale = ::powf(g.rope_base, -2.0f / static_cast<float>(g.rope));
+    return r;
+}
+
 // Enqueues one decode step on the context stream (also used under graph capture).
 int enqueue_step(prism_hip_decoder *d) {
     prism_hip_ctx *c = d->ctx;
@@ -110,9 +119,6 @@ int enqueue_step(prism_hip_decoder *d) {
     at.head_dim = static_cast<uint32_t>(g.head_dim);
     at.rope = static_cast<uint32_t>(g.rope);
     at.max_tokens = static_cast<uint32_t>(g.max_tokens);
-    for (int i = 0; i < 4; ++i) at.sections[i] = static_cast<uint32_t>(g.rope_sections[i]);
-    // rope_frequencies_mrope (src/graph.rs:6411): theta_scale = rope_base.powf(-2 / rope).
-    at.theta_scale = ::powf(g.rope_base, -2.0f / static_cast<float>(g.rope));
     at.eps = g.eps;
     at.err = c->err;
     at.stream = s;
@@ -135,7 +141,7 @@ int enqueue_step(prism_hip_decoder *d) {
     int rc = matvec(c, *lm, kActQ8, d->lm_act, 1, 0, d->logits, s);
     if (rc) return rc;
     if (launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), lm->dev, static_cast<uint32_t>(g.hidden),
-                            d->state, d->tokens, d->max_steps, h0, d->argmax_scratch, s))
+                            d->state, rope_args(g), d->tokens, d->max_steps, h0, d->argmax_scratch, s))
         return hip_fail(c, hipGetLastError(), "argmax launch");
     return PRISM_OK;
 }
@@ -292,7 +298,8 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
     HIP_OR_FAIL(c, hipMemcpyAsync(d->state, &init, sizeof(init), hipMemcpyHostToDevice, s));
     HIP_OR_FAIL(c, hipStreamSynchronize(s));
     const Weight *lm = find(c, d->lm_head);
-    if (launch_embed(lm->dev, d->g.vocab, static_cast<uint32_t>(d->g.hidden), d->state, d->hidden[0], s))
+    if (launch_embed(lm->dev, d->g.vocab, static_cast<uint32_t>(d->g.hidden), d->state, rope_args(d->g), d->hidden[0],
+                     s))
         return hip_fail(c, hipGetLastError(), "embed launch");
     if (use_graph && !d->exec) {
         HIP_OR_FAIL(c, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));

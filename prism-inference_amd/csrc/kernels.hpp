@@ -78,6 +78,14 @@ int launch_fill_i32(int *p, int v, uint32_t n, hipStream_t s);
 // step advances it, so one captured graph serves every step.
 struct DecodeState {
     uint32_t pos, token, step, pad;
+    float cs[64], sn[64];  // RoPE cosines / sines of `pos` (rope_frequencies_mrope)
+};
+// RoPE geometry (src/graph.rs:6406-6431): rotated dimensions, M-RoPE sections and
+// theta_scale = rope_base^(-2/rope) as binary32 powf.
+struct RopeArgs {
+    uint32_t rope;
+    uint32_t sections[4];
+    float theta_scale;
 };
 struct AttnArgs {
     const float *qkv;            // this token's projections: q [heads*D] | k [kv*D] | v [kv*D]
@@ -87,8 +95,7 @@ struct AttnArgs {
     float *out;                  // attended [heads*D]
     const DecodeState *state;
     uint32_t heads, kv_heads, head_dim, rope, max_tokens;
-    uint32_t sections[4];        // M-RoPE sections (src/graph.rs:6406-6431)
-    float theta_scale, eps;      // rope_base^(-2/rope) as binary32 powf, RMSNorm epsilon
+    float eps;                   // RMSNorm epsilon
     int *err;
     hipStream_t stream;
 };
@@ -96,15 +103,17 @@ struct AttnArgs {
 int launch_attention(const AttnArgs &a);
 // Final RMSNorm + Q8_0 (source) quantization of n values into q8_out.
 int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *q8_out, int *err, hipStream_t s);
-// out = dequantized row state->token of the tiled Q8_0 matrix [rows][cols].
-int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, const DecodeState *st, float *out,
-                 hipStream_t s);
-// Greedy token from logits[vocab], recorded and advanced in the state, and its
-// embedding (row of the tiled Q8_0 matrix [vocab][cols]) written to out; two launches.
+// out = dequantized row state->token of the tiled Q8_0 matrix [rows][cols]; the state's
+// RoPE frequencies are set for state->pos.
+int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, DecodeState *st, const RopeArgs &rope,
+                 float *out, hipStream_t s);
+// Greedy token from logits[vocab], recorded and advanced in the state (with the RoPE
+// frequencies of the new position), and its embedding (row of the tiled Q8_0 matrix [vocab][cols]) written to out; two launches.
 // scratch: argmax_scratch_bytes() of device memory.
 size_t argmax_scratch_bytes();
 int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
-                        uint32_t *tokens, uint32_t max_steps, float *out, void *scratch, hipStream_t s);
+                        const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, void *scratch,
+                        hipStream_t s);
 
 
 }  // namespace prism
