@@ -188,39 +188,41 @@ def calibrate_copy(nbytes: int = 256 << 20, reps: int = 10) -> int:
     return 0
 
 
-def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launches: int = 200):
-    """Per-launch duration of one matvec kernel (prepared Q8_K/Q8_0 activation already in HBM),
-    bracketed by HIP events on the library stream, weights rotated over >= 1 GiB."""
+def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launches: int = 200, tokens: int = 1):
+    """Per-launch duration of one matvec kernel (prepared Q8_K/Q8_0 activations of `tokens`
+    tokens already in HBM), bracketed by HIP events on the library stream, weights rotated
+    over >= 1 GiB.  tokens > 1 is the skinny batch: each weight byte is read once per launch."""
     w = synth.weights(kind, rows, cols, seed=7)
     copies = max(2, math.ceil(ROTATE_BYTES / w.size))
     rot = Rotation(ctx, kind, rows, cols, w, copies)
     contract = 0 if kind in (ph.KIND_Q2_K,) or (kind == ph.KIND_PQ2 and cols % 256 == 0) else 1
-    x = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=8))
+    x = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=8, tokens=tokens))
     if contract == 0:
-        act = hiprt.DeviceBuffer(cols // 256 * 292)
-        ctx.quantize_q8k_device(x, cols, 1, False, act)
+        act = hiprt.DeviceBuffer(cols // 256 * 292 * tokens)
+        ctx.quantize_q8k_device(x, cols, tokens, False, act)
         path, act_bytes = ph.PATH_Q8K, cols // 256 * 292
     else:
-        act = hiprt.DeviceBuffer(cols // 32 * 40)
-        ctx.quantize_q8_device(x, cols, 1, ph.Q8_SOURCE, act)
+        act = hiprt.DeviceBuffer(cols // 32 * 40 * tokens)
+        ctx.quantize_q8_device(x, cols, tokens, ph.Q8_SOURCE, act)
         path, act_bytes = ph.PATH_Q8, cols // 32 * 34
-    out = hiprt.DeviceBuffer(4 * rows)
+    out = hiprt.DeviceBuffer(4 * rows * tokens)
     stream = ctx.stream()
     for i in range(min(copies, 8)):
-        ctx.project_device(rot.ids[i], path, act, 1, False, out, stream)
+        ctx.project_device(rot.ids[i], path, act, tokens, False, out, stream)
     assert ctx.sync() == 0
     e0, e1 = hiprt.Event(), hiprt.Event()
     e0.record(stream)
     for i in range(launches):
-        ctx.project_device(rot.ids[i % copies], path, act, 1, False, out, stream)
+        ctx.project_device(rot.ids[i % copies], path, act, tokens, False, out, stream)
     e1.record(stream)
     e1.synchronize()
     assert ctx.sync() == 0
     t = e0.elapsed_ms(e1) / launches * 1e-3
-    nbytes = w.size + act_bytes + 4 * rows
+    nbytes = w.size + (act_bytes + 4 * rows) * tokens
     rot.release(ctx)
-    return {"kind": kind, "rows": rows, "cols": cols, "bytes_per_launch": int(nbytes), "copies": copies,
-            "avg_us": t * 1e6, "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM}
+    return {"kind": kind, "rows": rows, "cols": cols, "tokens": tokens, "bytes_per_launch": int(nbytes),
+            "copies": copies, "avg_us": t * 1e6, "us_per_token": t * 1e6 / tokens, "GBps": nbytes / t / 1e9,
+            "frac_hbm": nbytes / t / PEAK_HBM}
 
 
 def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 20):
@@ -326,7 +328,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="", help="comma-separated token counts: time only the prefill GEMM")
-    ap.add_argument("--matvec-only", default="", help="comma-separated kind:rows:cols: time only these matvecs")
+    ap.add_argument("--matvec-only", default="",
+                    help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--decode-only", action="store_true", help="time only the 28-layer decode step")
     ap.add_argument("--decode-eager", action="store_true",
                     help="with --decode-only: launch every kernel each step instead of replaying a HIP graph")
@@ -350,8 +353,8 @@ def main() -> int:
         for M in filter(None, args.prefill_only.split(",")):
             print(json.dumps(bench_prefill(ctx, int(M))), flush=True)
         for spec in filter(None, args.matvec_only.split(",")):
-            kind, rows, cols = (int(v) for v in spec.split(":"))
-            print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols)), flush=True)
+            kind, rows, cols, *tok = (int(v) for v in spec.split(":"))
+            print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols, tokens=tok[0] if tok else 1)), flush=True)
         ctx.close()
         return 0
     ms, wall_ms, copies = bench_ffn(ctx, args.steps, args.warmup)
@@ -370,6 +373,15 @@ def main() -> int:
             r = bench_matvec_kernel(ctx, kind, rows, cols, launches=100)
             log(f"matvec kind={kind} {rows}x{cols}: {r['avg_us']:.2f} us, {r['GBps']:.1f} GB/s")
             extras["matvec"].append(r)
+        extras["skinny_batch"] = []
+        for kind, rows, cols in [(ph.KIND_PTQ1, 12288, 4096), (ph.KIND_Q2_K, 12288, 4096), (ph.KIND_Q8_0, 12288, 4096),
+                                 (ph.KIND_PTQ1, 151936, 4096), (ph.KIND_Q2_K, 151936, 4096),
+                                 (ph.KIND_Q8_0, 151936, 4096)]:
+            for B in (4, 16):
+                r = bench_matvec_kernel(ctx, kind, rows, cols, launches=50, tokens=B)
+                log(f"skinny kind={kind} {rows}x{cols} B={B}: {r['avg_us']:.2f} us "
+                    f"({r['us_per_token']:.2f} us/token), {r['GBps']:.1f} GB/s")
+                extras["skinny_batch"].append(r)
         extras["prefill_ptq1_6144x2048"] = []
         for M in (128, 512, 2048):
             r = bench_prefill(ctx, M)

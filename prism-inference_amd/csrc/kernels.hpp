@@ -34,7 +34,7 @@ struct MatvecArgs {
     uint32_t tokens = 1;
     int pinned = 0;               // pinned Q8 order (PTQ1) or fused FMA (PQ2 + Q8K); SwiGLU order
     float *out = nullptr;         // device, [tokens][rows]
-    const float *residual = nullptr;  // tiled only: added to every output row
+    const float *residual = nullptr;  // tiled only: [tokens][rows], added to the outputs
     const float *norm_w = nullptr;    // tiled kActF32 only: RMSNorm weights applied before quantizing
     float eps = 0.0f;                 // RMSNorm epsilon
     int *err = nullptr;           // device error flag

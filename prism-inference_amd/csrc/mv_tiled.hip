@@ -528,6 +528,65 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
         rows_tile<O, true>(p, act, tile, lane, 8u * (lane & 31u));
 }
 
+// Skinny batches (2..NB tokens, the matvec-to-matmul transition): one wavefront per
+// 64-row tile loads each unit of weights once and folds it into one chain per token,
+// every chain in its own token's unit order.  Token t's prepared activation sits at
+// act + t * act_stride bytes and its output row block at out + t * rows (residual
+// likewise).  The per-token chain and arithmetic are exactly the batch-1 ones.
+template <Op O, int NB>
+__global__ __launch_bounds__(64) void k_mv_rows_batch(MvParams p, const void *__restrict__ act, uint32_t ntok,
+                                                      uint32_t act_stride) {
+    constexpr uint32_t UB = unit_bytes<O>();
+    const uint32_t lane = threadIdx.x, tile = blockIdx.x;
+    const uint32_t nu = p.nu, row_bytes = nu * UB;
+    const uint32_t left = p.rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    Chain<O> ch[NB];
+    auto step = [&](const Raw<O> &w, uint32_t u) {
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            if (t < static_cast<int>(ntok)) {
+                const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
+                float tt[terms_per_unit<O>()];
+                unit_terms<O>(w, a, u, tt);
+                ch[t].fold(tt, a, u);
+            }
+        }
+    };
+    Raw<O> A, B;
+    uint32_t u = 0;
+    load_unit<O>(A, rs, 0, trp, lane);
+    while (u + 1 < nu) {
+        load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
+        step(A, u);
+        if (u + 2 < nu) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+        step(B, u + 1);
+        u += 2;
+    }
+    if (u < nu) step(A, u);
+    if (lane < trows) {
+        const size_t row = static_cast<size_t>(tile) * kTile + lane;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            if (t < static_cast<int>(ntok)) {
+                const size_t at = static_cast<size_t>(t) * p.rows + row;
+                float o = ch[t].result();
+                if (p.residual) o = o + p.residual[at];
+                p.out[at] = o;
+                if (!finite(o)) raise_error(p.err, kErrNonfinite);
+            }
+        }
+    }
+}
+
+// Row count from which a skinny batch runs weights-once: one wavefront per tile needs
+// several tiles per SIMD before the per-token chains stop dominating (measured: at
+// 12288 rows token-by-token launches are faster, at 151936 weights-once is 1.5-4x).
+constexpr uint64_t kBatchMinRows = 65536;
+constexpr uint32_t kBatchMax = 16;
+
 // Small matrices: a workgroup owns rw = 64/lpr rows of a tile; its ks wavefronts
 // (per matrix) and the lpr lane groups of each wavefront split the row's units
 // (lane group c of wavefront w takes units w*lpr+c, +ks*lpr, ...).  Each unit's
@@ -809,20 +868,61 @@ int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols,
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+template <Op O>
+int launch_batch(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t act_stride, float *out,
+                 const float *residual) {
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    MvParams p{};
+    p.w[0] = p.w[1] = a.w;
+    p.rows = static_cast<uint32_t>(a.rows);
+    p.nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    p.cols = static_cast<uint32_t>(a.cols);
+    p.pinned = a.pinned;
+    p.out = out;
+    p.residual = residual;
+    p.err = a.err;
+    const dim3 grid(static_cast<uint32_t>(tiles)), block(64);
+    if (ntok <= 4)
+        hipLaunchKernelGGL((k_mv_rows_batch<O, 4>), grid, block, 0, a.stream, p, act, ntok, act_stride);
+    else if (ntok <= 8)
+        hipLaunchKernelGGL((k_mv_rows_batch<O, 8>), grid, block, 0, a.stream, p, act, ntok, act_stride);
+    else
+        hipLaunchKernelGGL((k_mv_rows_batch<O, 16>), grid, block, 0, a.stream, p, act, ntok, act_stride);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+bool batch_eligible(const MatvecArgs &a) { return a.tokens >= 2 && !a.w2 && a.rows >= kBatchMinRows; }
+
 int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
+    if (a.act_format != kActF32 && batch_eligible(a)) {
+        for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
+            const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
+            const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;
+            float *out = a.out + a.rows * tok;
+            const float *res = a.residual ? a.residual + a.rows * tok : nullptr;
+            const int rc = dispatch(a, [&]<Op O>() {
+                return launch_batch<O>(a, act, n, static_cast<uint32_t>(in_stride), out, res);
+            });
+            if (rc) return rc;
+        }
+        return 0;
+    }
     for (uint32_t tok = 0; tok < a.tokens; ++tok) {
         const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;
         float *out = a.out + a.rows * tok;
-        const int rc = dispatch(a, [&]<Op O>() { return launch_op<O>(a, act, out); });
+        MatvecArgs at = a;
+        if (at.residual) at.residual += a.rows * tok;
+        const int rc = dispatch(a, [&]<Op O>() { return launch_op<O>(at, act, out); });
         if (rc) return rc;
     }
     return 0;
 }
 
 bool tiled_needs_prepared(const MatvecArgs &a) {
+    if (batch_eligible(a)) return true;
     return dispatch(a, [&]<Op O>() { return op_needs_prepared<O>(a) ? 1 : 0; }) == 1;
 }
 

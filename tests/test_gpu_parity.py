@@ -319,6 +319,38 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 384), (ph.KIND_PQ2, 512), (ph.KIND_PQ2, 384),
+                                       (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256)])
+def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols):
+    """2..17 tokens on a matrix of >= 8192 rows run weights-once (one wavefront per tile
+    folds every token's chain); each token's row must equal its own matvec, in every
+    contract, with partial chunks of the 16-token batch and a partial last tile."""
+    import oracle
+
+    rows = 65536 + 37
+    w = synth.weights(kind, rows, cols, seed=41) if kind != ph.KIND_PQ2 else synth.pq2_weights(rows, cols, 41, 4)
+    wid = ctx.weight(kind, cols, rows, w)
+    for tokens in (2, 5, 17):
+        X = synth.activations(cols, seed=42 + tokens, tokens=tokens)
+        for pinned in (False, True):
+            ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+            got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
+            assert_bits_equal(got, ref, f"batch f32 kind={kind} tokens={tokens} pinned={pinned}")
+        if kind in (ph.KIND_PTQ1, ph.KIND_Q8_0) or (kind == ph.KIND_PQ2 and cols % 256):
+            act = np.concatenate([oracle.quantize_q8_0(X[t], 2 if kind == ph.KIND_PTQ1 else 1) for t in range(tokens)])
+            ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * (cols // 32):(t + 1) * (cols // 32)], True,
+                                              threads=THREADS) for t in range(tokens)])
+            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens, pinned=True)
+            assert_bits_equal(got, ref, f"batch q8 kind={kind} tokens={tokens}")
+        else:
+            act = np.concatenate([oracle.quantize_q8k(X[t], True) for t in range(tokens)])
+            ref = np.stack([oracle.project_q8k(kind, cols, rows, w, act[t * (cols // 256):(t + 1) * (cols // 256)], True,
+                                               threads=THREADS) for t in range(tokens)])
+            got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens, fused=True)
+            assert_bits_equal(got, ref, f"batch q8k kind={kind} tokens={tokens}")
+    ctx.release(wid)
+
+
 # ---- multi-token, groups, backend op -------------------------------------------------
 
 def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
