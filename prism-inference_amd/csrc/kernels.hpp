@@ -40,6 +40,8 @@ struct MatvecArgs {
     int *err = nullptr;           // device error flag
     hipStream_t stream = nullptr;
     uint32_t cus = 256;           // compute units of the device
+    void *scratch = nullptr;      // tiled only: tiled_scratch_bytes() of device memory
+    size_t scratch_bytes = 0;
 };
 
 // Returns 0 on success, -1 when the launch failed, -2 when the shape is unsupported.
@@ -50,6 +52,8 @@ int launch_matvec_tiled(const MatvecArgs &a);
 // Whether a kActF32 tiled call must be given prepared blocks instead (large matrices
 // run a separate quantize kernel; the prologue would repeat it per workgroup).
 bool tiled_needs_prepared(const MatvecArgs &a);
+// Device scratch a tiled call needs (the lane-ordered activations of a skinny batch).
+size_t tiled_scratch_bytes(const MatvecArgs &a);
 // Whether (kind, cols, rows) can be stored tiled, and the native -> tiled repack
 // (the destination must hold tiled_bytes() and be zero-filled beforehand).
 bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows);

@@ -587,6 +587,581 @@ __global__ __launch_bounds__(64) void k_mv_rows_batch(MvParams p, const void *__
 constexpr uint64_t kBatchMinRows = 65536;
 constexpr uint32_t kBatchMax = 16;
 
+// ---- skinny batches on the int8 matrix cores ------------------------------------------
+// 2..16 tokens.  A wavefront owns 16 rows (a quarter of a 64-row tile) and every token,
+// and computes the exact integer dot of each (row, token, group) with one
+// v_mfma_i32_16x16x32_i8 (a 32-element group) or v_mfma_i32_16x16x64_i8: rows on the M
+// side (lane l supplies row l%16), tokens on the N side (lane l supplies token l%16),
+// and the group's elements spread over the four lane groups s = l/16 in any order, as
+// long as a lane's weight and activation bytes pair the same elements -- the integer
+// dot is exact in every order.  Lane l receives rows 4s..4s+3 of token l%16 and runs
+// those four rows' binary32 chains for that token in unit order, with the batch-1
+// arithmetic, so every output equals its own matvec bit for bit.  The weights of the
+// 16 rows are decoded once for all tokens, straight into the operand layout (no LDS).
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+struct SkParams {
+    const uint8_t *w;   // tiled weights
+    const uint8_t *sw;  // lane-ordered activations (k_sk_prep), or the prepared blocks
+    float *out;         // [ntok][rows]
+    const float *residual;
+    int *err;
+    uint32_t rows, nu, ntok;
+    uint32_t act_stride;  // prepared blocks: bytes per token
+};
+
+template <Op O>
+constexpr bool skinny_supported() {
+    return O != Op::PTQ1_PINNED;
+}
+
+// Per-lane geometry: the tile's buffer, the lane's A row and first output row.
+struct SkLane {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t trp, ra, rc, s, lane, tok;
+    const uint8_t *sw, *scales;  // lane-ordered activation operands and token scales
+};
+
+__device__ __forceinline__ v4i mfma32(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, v4i c) {
+    const long a = static_cast<long>((static_cast<uint64_t>(a1) << 32) | a0);
+    const long b = static_cast<long>((static_cast<uint64_t>(b1) << 32) | b0);
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4i mfma64(const u32x4 &a, const u32x4 &b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a), __builtin_bit_cast(v4i, b), c, 0, 0, 0);
+}
+// Four signed bytes from four small codes: byte value c becomes map's byte c.
+__device__ __forceinline__ uint32_t code_map(uint32_t codes, uint32_t map) { return perm(0u, map, codes); }
+// Bytes x*m (two 16-bit lanes, each byte times m, products below 256).
+__device__ __forceinline__ uint32_t bytes_times(uint32_t x, uint32_t m) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, x) * u16x2{static_cast<uint16_t>(m),
+                                                                               static_cast<uint16_t>(m)});
+}
+// PTQ1 digits of the four bytes of x: byte j gets digit k_j, selected by the per-16-bit
+// lane multipliers pl (bytes 0, 2) and ph (bytes 1, 3), each 3^k (mod-256 remainder
+// then times 3, the digit in the high byte), as signed trits t-1.
+__device__ __forceinline__ uint32_t trit_quad(uint32_t x, uint32_t pl, uint32_t ph) {
+    const uint32_t L = x & 0x00ff00ffu, H = (x >> 8) & 0x00ff00ffu;
+    const uint32_t mL = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, L) * __builtin_bit_cast(u16x2, pl)) &
+                        0x00ff00ffu;
+    const uint32_t mH = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, H) * __builtin_bit_cast(u16x2, ph)) &
+                        0x00ff00ffu;
+    return code_map(perm(mH * 3u, mL * 3u, sel(1, 5, 3, 7)), 0x000100ffu);
+}
+
+// Activation operand bytes per lane and unit in the lane-ordered copy (k_sk_prep).
+template <Op O>
+constexpr uint32_t sk_lane_bytes() {
+    return O == Op::Q2K ? 64 : 32;
+}
+
+template <Op O>
+struct SkFrag;
+template <>
+struct SkFrag<Op::Q8_0> {
+    u32x2 a[4];
+    u32x4 sc0, sc1;  // binary16 block scales of the lane's four output rows
+    u32x4 b[2];      // block j's eight activation bytes in dwords 2j, 2j+1
+    u32x4 as;        // the token's block scales
+};
+template <>
+struct SkFrag<Op::Q2K> {
+    u32x4 q;   // code bytes 16s..16s+15 of the A row
+    u32x2 sc;  // its scale bytes 8(s/2)..+7
+    u32x4 dm;  // d | dmin << 16 of the four output rows
+    u32x4 b[4];
+    u32x4 as;
+};
+template <>
+struct SkFrag<Op::PTQ1_SRC> {
+    uint32_t a, b0, b1, tl;  // A-piece dword s, B piece, tail dword of the A row
+    u32x4 dd;                // tail dwords (scale in the high half) of the four output rows
+    u32x4 b[2];              // activation quads paired with the eight digit quads
+    u32x4 as;
+};
+template <>
+struct SkFrag<Op::PTQ1_Q8K> : SkFrag<Op::PTQ1_SRC> {};
+template <>
+struct SkFrag<Op::PQ2_UNFUSED> {
+    u32x4 ca, cb;  // code dwords 0..3 and 4..7 of the A row
+    u32x2 dd;      // binary16 scales of the four output rows
+    u32x4 b[2];    // group g's activation bytes (gathered at stride 4) in dwords 2g, 2g+1
+    u32x4 as;
+};
+template <>
+struct SkFrag<Op::PQ2_FUSED> : SkFrag<Op::PQ2_UNFUSED> {};
+template <>
+struct SkFrag<Op::PQ2_Q8> : SkFrag<Op::PQ2_UNFUSED> {};
+
+// PTQ1 lane plan.  Unit element map (tools/ternary/src/lib.rs:202-250): A-piece byte b
+// digit k -> 16k+b, B-piece byte b digit k -> 80+8k+b, tail byte b digit k<4 -> 120+2k+b.
+// Lane group s takes, as (dword, digit) quads of natural consecutive elements:
+//   group 0: (A_s, 0) (A_s, 1)        -> 4s, 16+4s
+//   group 1: (A_s, 2) (A_s, 3)        -> 32+4s, 48+4s
+//   group 2: (A_s, 4) (B_{s/2}, s%2)  -> 64+4s, 80+8(s%2)+4(s/2)
+//   group 3: s<3: (B_0, 2+s) (B_1, 2+s) -> 96+8s, 100+8s;  s=3: the tail bytes
+//            repeated (b24 b25 b24 b25) with digits (0,0,1,1) and (2,2,3,3) -> 120, 124
+struct Ptq1Plan {
+    uint32_t off[8];  // element offsets of the eight quads within the unit
+    uint32_t p2h, p3l_l, p3l_h, p3h_l, p3h_h;
+};
+__device__ __forceinline__ Ptq1Plan ptq1_plan(uint32_t s) {
+    Ptq1Plan q;
+    q.off[0] = 4 * s;
+    q.off[1] = 16 + 4 * s;
+    q.off[2] = 32 + 4 * s;
+    q.off[3] = 48 + 4 * s;
+    q.off[4] = 64 + 4 * s;
+    q.off[5] = 80 + 8 * (s & 1) + 4 * (s >> 1);
+    q.off[6] = s < 3 ? 96 + 8 * s : 120;
+    q.off[7] = s < 3 ? 100 + 8 * s : 124;
+    q.p2h = (s & 1) ? 0x00030003u : 0x00010001u;
+    const uint32_t p3 = s == 0 ? 9u : s == 1 ? 27u : 81u;
+    q.p3l_l = q.p3l_h = s < 3 ? p3 * 0x00010001u : (1u | (3u << 16));
+    q.p3h_l = q.p3h_h = s < 3 ? p3 * 0x00010001u : (9u | (27u << 16));
+    return q;
+}
+
+// First activation element (within the unit) of dword k of lane group s's operand
+// bytes, and the element stride of its four bytes.
+template <Op O>
+__device__ __forceinline__ uint32_t sk_elem(uint32_t s, uint32_t k, uint32_t &stride) {
+    stride = 1;
+    if constexpr (O == Op::Q8_0) {
+        return 32u * (k >> 1) + 8u * s + 4u * (k & 1u);
+    } else if constexpr (O == Op::Q2K) {
+        return 128u * (s >> 1) + 32u * (k >> 2) + 16u * (s & 1u) + 4u * (k & 3u);
+    } else if constexpr (kind_of<O>() == kPTQ1) {
+        return ptq1_plan(s).off[k];
+    } else {
+        stride = 4;
+        return 16u * (2u * (k >> 1) + (s >> 1)) + 2u * (s & 1u) + (k & 1u);
+    }
+}
+template <Op O>
+constexpr bool sk_q8_groups() {
+    return O == Op::Q8_0 || O == Op::PTQ1_SRC || O == Op::PQ2_Q8;
+}
+// Byte of activation element e of unit u in a token's prepared blocks.
+template <Op O>
+__device__ __forceinline__ const int8_t *sk_value(const uint8_t *a, uint32_t u, uint32_t e) {
+    if constexpr (sk_q8_groups<O>())
+        return reinterpret_cast<const Q8Block *>(a)[4u * u + (e >> 5)].values + (e & 31u);
+    else if constexpr (O == Op::Q2K)
+        return reinterpret_cast<const Q8KBlock *>(a)[u].values + e;
+    else
+        return reinterpret_cast<const Q8KBlock *>(a)[u >> 1].values + 128u * (u & 1u) + e;
+}
+
+// Lane-ordered copy of a skinny batch's activations: for unit u and lane l (token l%16,
+// clamped to the batch; lane group s = l/16) the sk_lane_bytes the lane feeds the
+// matrix cores, at sw + (u*64 + l) * sk_lane_bytes, then the scales [u][16 tokens][4]
+// (group scales, or the block scale repeated).  Every skinny wavefront then reads its
+// activation operands with contiguous loads.
+template <Op O>
+__global__ __launch_bounds__(256) void k_sk_prep(const uint8_t *__restrict__ act, uint32_t act_stride, uint32_t ntok,
+                                                 uint32_t nu, uint32_t *__restrict__ sw) {
+    constexpr uint32_t LD = sk_lane_bytes<O>() / 4;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx < nu * 64u * LD) {
+        const uint32_t k = idx % LD, lane = (idx / LD) & 63u, u = idx / (LD * 64u);
+        const uint32_t i = lane & 15u, tok = i < ntok ? i : ntok - 1u;
+        uint32_t stride;
+        const uint32_t e = sk_elem<O>(lane >> 4, k, stride);
+        const int8_t *src = sk_value<O>(act + static_cast<size_t>(tok) * act_stride, u, e);
+        uint32_t v;
+        if (stride == 1)
+            v = *reinterpret_cast<const uint32_t *>(src);
+        else
+            v = static_cast<uint8_t>(src[0]) | (static_cast<uint32_t>(static_cast<uint8_t>(src[4])) << 8) |
+                (static_cast<uint32_t>(static_cast<uint8_t>(src[8])) << 16) |
+                (static_cast<uint32_t>(static_cast<uint8_t>(src[12])) << 24);
+        sw[idx] = v;
+    }
+    if (idx < nu * 64u) {
+        const uint32_t g = idx & 3u, i = (idx >> 2) & 15u, u = idx >> 6;
+        const uint8_t *a = act + static_cast<size_t>(i < ntok ? i : ntok - 1u) * act_stride;
+        float sc;
+        if constexpr (sk_q8_groups<O>())
+            sc = reinterpret_cast<const Q8Block *>(a)[4u * u + g].scale;
+        else if constexpr (O == Op::Q2K)
+            sc = reinterpret_cast<const Q8KBlock *>(a)[u].scale;
+        else
+            sc = reinterpret_cast<const Q8KBlock *>(a)[u >> 1].scale;
+        reinterpret_cast<float *>(sw + nu * 64u * LD)[idx] = sc;
+    }
+}
+
+// The same operand dwords and scales straight from the token's prepared blocks (no
+// lane-ordered copy): scattered loads, cheaper than a second launch on small matrices.
+template <Op O>
+__device__ __forceinline__ void sk_load_act_raw(SkFrag<O> &f, const uint8_t *a, uint32_t u, uint32_t s,
+                                                const Ptq1Plan &pp) {
+    if constexpr (O == Op::Q8_0) {
+        const Q8Block *blk = reinterpret_cast<const Q8Block *>(a) + 4u * u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x2 lo = *reinterpret_cast<const u32x2 *>(blk[2 * h].values + 8u * s);
+            const u32x2 hi = *reinterpret_cast<const u32x2 *>(blk[2 * h + 1].values + 8u * s);
+            f.b[h] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+        f.as = u32x4{__float_as_uint(blk[0].scale), __float_as_uint(blk[1].scale), __float_as_uint(blk[2].scale),
+                     __float_as_uint(blk[3].scale)};
+    } else if constexpr (O == Op::Q2K) {
+        const Q8KBlock *blk = reinterpret_cast<const Q8KBlock *>(a) + u;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            f.b[p] = *reinterpret_cast<const u32x4a *>(blk->values + 128u * (s >> 1) + 32u * p + 16u * (s & 1u));
+        f.as.x = __float_as_uint(blk->scale);
+    } else if constexpr (kind_of<O>() == kPTQ1) {
+        uint32_t x[8];
+        if constexpr (O == Op::PTQ1_SRC) {
+            const Q8Block *blk = reinterpret_cast<const Q8Block *>(a) + 4u * u;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                x[k] = *reinterpret_cast<const uint32_t *>(blk[k >> 1].values + (pp.off[k] - 32u * (k >> 1)));
+            f.as = u32x4{__float_as_uint(blk[0].scale), __float_as_uint(blk[1].scale), __float_as_uint(blk[2].scale),
+                         __float_as_uint(blk[3].scale)};
+        } else {
+            const Q8KBlock *blk = reinterpret_cast<const Q8KBlock *>(a) + (u >> 1);
+            const int8_t *v = blk->values + 128u * (u & 1u);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] = *reinterpret_cast<const uint32_t *>(v + pp.off[k]);
+            f.as.x = __float_as_uint(blk->scale);
+        }
+        f.b[0] = u32x4{x[0], x[1], x[2], x[3]};
+        f.b[1] = u32x4{x[4], x[5], x[6], x[7]};
+    } else {
+        // Natural bytes 16m..16m+15 (m = 2g + s/2), transposed to stride-4 gathers.
+        const uint32_t p0 = 2u * (s & 1u);
+        const uint32_t gsel = p0 | ((4u + p0) << 8) | ((p0 + 1u) << 16) | ((5u + p0) << 24);
+        uint32_t x[8];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            u32x4 q;
+            if constexpr (O == Op::PQ2_Q8)
+                q = *reinterpret_cast<const u32x4a *>(reinterpret_cast<const Q8Block *>(a)[4u * u + g].values +
+                                                      16u * (s >> 1));
+            else
+                q = *reinterpret_cast<const u32x4a *>(reinterpret_cast<const Q8KBlock *>(a)[u >> 1].values +
+                                                      128u * (u & 1u) + 16u * (2u * g + (s >> 1)));
+            const uint32_t t01 = perm(q.y, q.x, gsel), t23 = perm(q.w, q.z, gsel);
+            x[2 * g] = perm(t23, t01, sel(0, 1, 4, 5));
+            x[2 * g + 1] = perm(t23, t01, sel(2, 3, 6, 7));
+        }
+        f.b[0] = u32x4{x[0], x[1], x[2], x[3]};
+        f.b[1] = u32x4{x[4], x[5], x[6], x[7]};
+        if constexpr (O == Op::PQ2_Q8) {
+            const Q8Block *blk = reinterpret_cast<const Q8Block *>(a) + 4u * u;
+            f.as = u32x4{__float_as_uint(blk[0].scale), __float_as_uint(blk[1].scale), __float_as_uint(blk[2].scale),
+                         __float_as_uint(blk[3].scale)};
+        } else {
+            f.as.x = __float_as_uint(reinterpret_cast<const Q8KBlock *>(a)[u >> 1].scale);
+        }
+    }
+}
+
+template <Op O, bool SW>
+__device__ __forceinline__ void sk_load(SkFrag<O> &f, const SkLane &L, uint32_t u, const Ptq1Plan &pp) {
+    constexpr uint32_t UB = unit_bytes<O>(), LB = sk_lane_bytes<O>();
+    const uint32_t seg = u * L.trp * UB, s = L.s;
+    if constexpr (SW) {
+        const u32x4 *b = reinterpret_cast<const u32x4 *>(L.sw + (static_cast<size_t>(u) * 64u + L.lane) * LB);
+#pragma unroll
+        for (uint32_t k = 0; k < LB / 16; ++k) f.b[k] = b[k];
+        f.as = *reinterpret_cast<const u32x4 *>(L.scales + (u * 16u + L.tok) * 16u);
+    } else {
+        sk_load_act_raw<O>(f, L.sw, u, s, pp);
+    }
+    if constexpr (O == Op::Q8_0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            f.a[j] = bload2(L.rs, seg + (2u * j + (s >> 1)) * 16u * L.trp + 16u * L.ra + 8u * (s & 1u));
+        f.sc0 = bload4(L.rs, seg + 128u * L.trp + 8u * L.rc);
+        f.sc1 = bload4(L.rs, seg + 128u * L.trp + 8u * L.rc + 16u);
+    } else if constexpr (O == Op::Q2K) {
+        f.q = bload4(L.rs, seg + 16u * s * L.trp + 16u * L.ra);
+        f.sc = bload2(L.rs, seg + 64u * L.trp + 16u * L.ra + 8u * (s >> 1));
+        f.dm = bload4(L.rs, seg + 80u * L.trp + 4u * L.rc);
+    } else if constexpr (kind_of<O>() == kPTQ1) {
+        f.a = bload1(L.rs, seg + 16u * L.ra + 4u * s);
+        const u32x2 bb = bload2(L.rs, seg + 16u * L.trp + 8u * L.ra);
+        f.b0 = bb.x;
+        f.b1 = bb.y;
+        f.tl = bload1(L.rs, seg + 24u * L.trp + 4u * L.ra);
+        f.dd = bload4(L.rs, seg + 24u * L.trp + 4u * L.rc);
+    } else {
+        f.ca = bload4(L.rs, seg + 16u * L.ra);
+        f.cb = bload4(L.rs, seg + 16u * L.trp + 16u * L.ra);
+        f.dd = bload2(L.rs, seg + 32u * L.trp + 2u * L.rc);
+    }
+}
+
+// One unit's binary32 terms tv[v][...] of the lane's four chains (rows rc+v, this lane's
+// token), in the order Chain<O>::fold consumes them.
+template <Op O>
+__device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, const Ptq1Plan &pp,
+                                         float tv[4][terms_per_unit<O>()]) {
+    const uint32_t s = L.s;
+    const v4i zero = {0, 0, 0, 0};
+    if constexpr (O == Op::Q8_0) {
+        v4i acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[j] = mfma32(f.a[j].x, f.a[j].y, f.b[j >> 1][2 * (j & 1)], f.b[j >> 1][2 * (j & 1) + 1], zero);
+        const float as[4] = {__uint_as_float(f.as.x), __uint_as_float(f.as.y), __uint_as_float(f.as.z),
+                             __uint_as_float(f.as.w)};
+        const uint32_t sw[8] = {f.sc0.x, f.sc0.y, f.sc0.z, f.sc0.w, f.sc1.x, f.sc1.y, f.sc1.z, f.sc1.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t bits = (sw[2 * v + (j >> 1)] >> (16 * (j & 1))) & 0xffffu;
+                // dot_legacy, src/kernels.rs:1241-1244
+                tv[v][j] = (h2f(bits) * as[j]) * static_cast<float>(acc[j][v]);
+            }
+        }
+    } else if constexpr (O == Op::Q2K) {
+        // Lane group s holds code bytes 16s..16s+15: half h = s/2, elements
+        // 128h + 32p + 16(s%2) + e of sub-block g = 8h + 2p + s%2 in field p.  The
+        // weight operand carries scale_g * q (at most 45, still a byte), so one dot
+        // gives sum_g scale_g * dot_g; a second one with min_g repeated gives
+        // sum_g min_g * bsum_g: both exact integers of kquants::dot.
+        v4i isum = zero, msum = zero;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t byte = (f.sc[p >> 1] >> (16u * (p & 1) + 8u * (s & 1u))) & 0xffu;
+            const uint32_t scale = byte & 15u, mn = byte >> 4;
+            u32x4 a1;
+            a1.x = bytes_times((f.q.x >> (2 * p)) & 0x03030303u, scale);
+            a1.y = bytes_times((f.q.y >> (2 * p)) & 0x03030303u, scale);
+            a1.z = bytes_times((f.q.z >> (2 * p)) & 0x03030303u, scale);
+            a1.w = bytes_times((f.q.w >> (2 * p)) & 0x03030303u, scale);
+            const uint32_t m4 = mn * 0x01010101u;
+            const u32x4 a2 = {m4, m4, m4, m4};
+            isum = mfma64(a1, f.b[p], isum);
+            msum = mfma64(a2, f.b[p], msum);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            // dot_q2_k_block, src/kernels/kquants.rs:193-196
+            const float as = __uint_as_float(f.as.x);
+            tv[v][0] = (as * h2f(f.dm[v] & 0xffffu)) * static_cast<float>(isum[v]) -
+                       (as * h2f(f.dm[v] >> 16)) * static_cast<float>(msum[v]);
+        }
+    } else if constexpr (kind_of<O>() == kPTQ1) {
+        // A_s digits 0..4, sequentially (remainder times 3 per digit).
+        uint32_t q[8];
+        {
+            uint32_t Lw = f.a & 0x00ff00ffu, Hw = (f.a >> 8) & 0x00ff00ffu;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) {
+                const uint32_t mL = Lw * 3u, mH = Hw * 3u;
+                q[k] = code_map(perm(mH, mL, sel(1, 5, 3, 7)), 0x000100ffu);
+                Lw = mL & 0x00ff00ffu;
+                Hw = mH & 0x00ff00ffu;
+            }
+        }
+        const uint32_t trep = perm(f.tl, f.tl, sel(0, 1, 0, 1));
+        q[5] = trit_quad((s >> 1) ? f.b1 : f.b0, pp.p2h, pp.p2h);
+        q[6] = trit_quad(s < 3 ? f.b0 : trep, pp.p3l_l, pp.p3l_h);
+        q[7] = trit_quad(s < 3 ? f.b1 : trep, pp.p3h_l, pp.p3h_h);
+        // Quad order: group 0 = (q0, q1), group 1 = (q2, q3), group 2 = (q4, q5), group 3 = (q6, q7).
+        const float as[4] = {__uint_as_float(f.as.x), __uint_as_float(f.as.y), __uint_as_float(f.as.z),
+                             __uint_as_float(f.as.w)};
+        if constexpr (O == Op::PTQ1_SRC) {
+            v4i acc[4];
+            acc[0] = mfma32(q[0], q[1], f.b[0].x, f.b[0].y, zero);
+            acc[1] = mfma32(q[2], q[3], f.b[0].z, f.b[0].w, zero);
+            acc[2] = mfma32(q[4], q[5], f.b[1].x, f.b[1].y, zero);
+            acc[3] = mfma32(q[6], q[7], f.b[1].z, f.b[1].w, zero);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                // dot_q8_groups, src/kernels.rs:1043-1064
+                float tt = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) tt = tt + as[g] * static_cast<float>(acc[g][v]);
+                tv[v][0] = h2f(f.dd[v] >> 16) * tt;
+            }
+        } else {
+            v4i acc = mfma32(q[0], q[1], f.b[0].x, f.b[0].y, zero);
+            acc = mfma32(q[2], q[3], f.b[0].z, f.b[0].w, acc);
+            acc = mfma32(q[4], q[5], f.b[1].x, f.b[1].y, acc);
+            acc = mfma32(q[6], q[7], f.b[1].z, f.b[1].w, acc);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                // dot_ptq1_q8k, src/kernels.rs:1026-1034
+                tv[v][0] = (h2f(f.dd[v] >> 16) * as[0]) * static_cast<float>(acc[v]);
+            }
+        }
+    } else {
+        // PQ2: group g = code dwords 2g, 2g+1 (element 16i+4q+p in byte q, bits 2p).  Lane
+        // group s takes dword m = 2g + s/2, fields p0 = 2(s%2) and p0+1: elements
+        // 16m + 4q + p, paired with the activation bytes gathered at stride 4.
+        const uint32_t p0 = 2u * (s & 1u);
+        const uint32_t c[8] = {f.ca.x, f.ca.y, f.ca.z, f.ca.w, f.cb.x, f.cb.y, f.cb.z, f.cb.w};
+        const uint32_t ab[8] = {f.b[0].x, f.b[0].y, f.b[0].z, f.b[0].w, f.b[1].x, f.b[1].y, f.b[1].z, f.b[1].w};
+        const float as[4] = {__uint_as_float(f.as.x), __uint_as_float(f.as.y), __uint_as_float(f.as.z),
+                             __uint_as_float(f.as.w)};
+        v4i acc[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t x = (s >> 1) ? c[2 * g + 1] : c[2 * g];
+            const uint32_t wlo = code_map((x >> (2u * p0)) & 0x03030303u, 0x020100ffu);
+            const uint32_t whi = code_map((x >> (2u * p0 + 2u)) & 0x03030303u, 0x020100ffu);
+            const uint32_t alo = ab[2 * g], ahi = ab[2 * g + 1];
+            if constexpr (O == Op::PQ2_Q8)
+                acc[g] = mfma32(wlo, whi, alo, ahi, zero);
+            else
+                acc[0] = mfma32(wlo, whi, alo, ahi, g == 0 ? zero : acc[0]);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float d = h2f((f.dd[v >> 1] >> (16 * (v & 1))) & 0xffffu);
+            if constexpr (O == Op::PQ2_Q8) {
+                // dot_q8_groups for an odd-group PQ2 row, src/kernels.rs:1043-1064
+                float tt = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) tt = tt + as[g] * static_cast<float>(acc[g][v]);
+                tv[v][0] = d * tt;
+            } else {
+                // dot_pq2::<FUSED>, src/kernels.rs:941-955
+                const float dd = d * as[0];
+                const float sf = static_cast<float>(acc[0][v]);
+                if constexpr (O == Op::PQ2_UNFUSED) {
+                    tv[v][0] = dd * sf;
+                } else {
+                    tv[v][0] = dd;
+                    tv[v][1] = sf;
+                }
+            }
+        }
+    }
+}
+
+// KS == 1: one wavefront per 16-row block runs every unit and keeps the four chains in
+// registers.  KS > 1 (fewer blocks than the chip has SIMDs): the KS wavefronts of a
+// workgroup share one block and take its units in chunks of KS (wavefront w: unit
+// c*KS + w); each writes its unit's terms to LDS, and after a barrier every thread folds
+// one (row, token) element through the chunk's units in unit order -- the same serial
+// chain, computed by a different lane.  Chunk parity double-buffers the terms, so one
+// barrier per chunk suffices.
+template <Op O, bool SW, int KS>
+__global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
+    constexpr uint32_t UB = unit_bytes<O>();
+    constexpr int TPU = terms_per_unit<O>();
+    const uint32_t lane = threadIdx.x & 63u, i = lane & 15u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tile = blockIdx.x >> 2, quarter = blockIdx.x & 3u;
+    const uint32_t left = p.rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    if (16u * quarter >= trows) return;
+    SkLane L;
+    L.s = lane >> 4;
+    L.lane = lane;
+    L.tok = i;
+    L.trp = (trows + 7u) & ~7u;
+    L.rs = make_rsrc(p.w + static_cast<size_t>(tile) * kTile * p.nu * UB, L.trp * p.nu * UB);
+    L.ra = 16u * quarter + i;
+    L.rc = 16u * quarter + 4u * L.s;
+    if constexpr (SW) {
+        L.sw = p.sw;
+        L.scales = p.sw + static_cast<size_t>(p.nu) * 64u * sk_lane_bytes<O>();
+    } else {
+        L.sw = p.sw + static_cast<size_t>(i < p.ntok ? i : p.ntok - 1u) * p.act_stride;
+        L.scales = nullptr;
+    }
+    const Ptq1Plan pp = ptq1_plan(L.s);
+    const size_t obase = static_cast<size_t>(tile) * kTile + 16u * quarter;
+    auto store = [&](uint32_t tok, uint32_t r, float v) {  // r: row within the 16-row block
+        if (tok < p.ntok && 16u * quarter + r < trows) {
+            const size_t at = static_cast<size_t>(tok) * p.rows + obase + r;
+            if (p.residual) v = v + p.residual[at];
+            p.out[at] = v;
+            if (!finite(v)) raise_error(p.err, kErrNonfinite);
+        }
+    };
+    if constexpr (KS == 1) {
+        Chain<O> ch[4];
+        auto fold = [&](const SkFrag<O> &f) {
+            float tv[4][TPU];
+            sk_terms<O>(f, L, pp, tv);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ch[v].fold(tv[v], nullptr, 0);
+        };
+        // Two fragments in ping-pong: the next unit's loads are in flight during a fold.
+        SkFrag<O> A, B;
+        uint32_t u = 0;
+        sk_load<O, SW>(A, L, 0, pp);
+        while (u + 1 < p.nu) {
+            sk_load<O, SW>(B, L, u + 1, pp);
+            fold(A);
+            if (u + 2 < p.nu) sk_load<O, SW>(A, L, u + 2, pp);
+            fold(B);
+            u += 2;
+        }
+        if (u < p.nu) fold(A);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) store(i, 4u * L.s + v, ch[v].result());
+    } else {
+        // terms[parity][wave][term][element], element e = 4 * lane + v
+        __shared__ float terms[2][KS][TPU][256];
+        constexpr int EPT = KS <= 4 ? 4 / KS : 1;  // elements folded per thread: e = tid + 64 * KS * k
+        Chain<O> ch[EPT];
+        const uint32_t chunks = (p.nu + KS - 1) / KS;
+        auto produce = [&](const SkFrag<O> &f, uint32_t c) {
+            float tv[4][TPU];
+            sk_terms<O>(f, L, pp, tv);
+#pragma unroll
+            for (int j = 0; j < TPU; ++j)
+                *reinterpret_cast<float4 *>(&terms[c & 1u][wave][j][4u * lane]) =
+                    make_float4(tv[0][j], tv[1][j], tv[2][j], tv[3][j]);
+        };
+        auto consume = [&](uint32_t c) {
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < EPT; ++k) {
+                const uint32_t e = threadIdx.x + 64u * KS * k;
+                if (e >= 256u) break;
+#pragma unroll
+                for (int w = 0; w < KS; ++w) {
+                    if (c * KS + w < p.nu) {
+                        float t[TPU];
+#pragma unroll
+                        for (int j = 0; j < TPU; ++j) t[j] = terms[c & 1u][w][j][e];
+                        ch[k].fold(t, nullptr, 0);
+                    }
+                }
+            }
+        };
+        SkFrag<O> A, B;
+        uint32_t c = 0;
+        if (wave < p.nu) sk_load<O, SW>(A, L, wave, pp);
+        while (c + 1 < chunks) {
+            const uint32_t u1 = (c + 1) * KS + wave;
+            if (u1 < p.nu) sk_load<O, SW>(B, L, u1, pp);
+            if (c * KS + wave < p.nu) produce(A, c);
+            consume(c);
+            const uint32_t u2 = (c + 2) * KS + wave;
+            if (c + 2 < chunks && u2 < p.nu) sk_load<O, SW>(A, L, u2, pp);
+            if (u1 < p.nu) produce(B, c + 1);
+            consume(c + 1);
+            c += 2;
+        }
+        if (c < chunks) {
+            if (c * KS + wave < p.nu) produce(A, c);
+            consume(c);
+        }
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const uint32_t e = threadIdx.x + 64u * KS * k, src = e >> 2;
+            if (e < 256u) store(src & 15u, 4u * (src >> 4) + (e & 3u), ch[k].result());
+        }
+    }
+}
+
 // Small matrices: a workgroup owns rw = 64/lpr rows of a tile; its ks wavefronts
 // (per matrix) and the lpr lane groups of each wavefront split the row's units
 // (lane group c of wavefront w takes units w*lpr+c, +ks*lpr, ...).  Each unit's
@@ -893,10 +1468,92 @@ int launch_batch(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t a
 
 bool batch_eligible(const MatvecArgs &a) { return a.tokens >= 2 && !a.w2 && a.rows >= kBatchMinRows; }
 
+// Whether a skinny batch first copies its activations into lane order (one more launch,
+// then contiguous loads) instead of gathering them from the prepared blocks in every
+// wavefront.  Measured on 2048..151936 rows: the copy pays from 8192 rows or from 5
+// tokens; Q2_K's 256-element units halve its gathers, and the copy pays only from
+// 32768 rows.
+template <Op O>
+bool skinny_lane_ordered(uint64_t rows, uint32_t ntok) {
+    if constexpr (O == Op::Q2K) return rows >= 32768;
+    return rows >= 8192 || ntok > 4;
+}
+
+template <Op O>
+size_t skinny_scratch(const MatvecArgs &a) {
+    if (!skinny_lane_ordered<O>(a.rows, a.tokens < kBatchMax ? a.tokens : kBatchMax)) return 0;
+    const uint64_t nu = a.cols / (kind_of<O>() == kQ2_K ? 256 : 128);
+    return nu * 64u * (sk_lane_bytes<O>() + 4u);
+}
+
+template <Op O>
+int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t act_stride, float *out,
+                  const float *residual) {
+    const bool sw = skinny_lane_ordered<O>(a.rows, ntok);
+    if (sw && (!a.scratch || a.scratch_bytes < skinny_scratch<O>(a))) return -2;
+    const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    if (sw) {
+        const uint32_t nprep = nu * 64u * (sk_lane_bytes<O>() / 4u);
+        hipLaunchKernelGGL(k_sk_prep<O>, dim3((nprep + 255u) / 256u), dim3(256), 0, a.stream,
+                           static_cast<const uint8_t *>(act), act_stride, ntok, nu, static_cast<uint32_t *>(a.scratch));
+    }
+    SkParams p{};
+    p.w = a.w;
+    p.sw = static_cast<const uint8_t *>(sw ? a.scratch : act);
+    p.act_stride = act_stride;
+    p.out = out;
+    p.residual = residual;
+    p.err = a.err;
+    p.rows = static_cast<uint32_t>(a.rows);
+    p.nu = nu;
+    p.ntok = ntok;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    // Wavefronts per 16-row block: enough to give the chip about eight per SIMD.
+    const uint64_t blocks = tiles * 4;
+    const uint64_t want = 32ull * a.cus;
+    const int ks = blocks >= want ? 1 : blocks * 2 >= want ? 2 : blocks * 4 >= want ? 4 : 8;
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(64 * ks);
+    if (sw) {
+        if (ks == 1) hipLaunchKernelGGL((k_mv_skinny<O, true, 1>), grid, block, 0, a.stream, p);
+        else if (ks == 2) hipLaunchKernelGGL((k_mv_skinny<O, true, 2>), grid, block, 0, a.stream, p);
+        else if (ks == 4) hipLaunchKernelGGL((k_mv_skinny<O, true, 4>), grid, block, 0, a.stream, p);
+        else hipLaunchKernelGGL((k_mv_skinny<O, true, 8>), grid, block, 0, a.stream, p);
+    } else {
+        if (ks == 1) hipLaunchKernelGGL((k_mv_skinny<O, false, 1>), grid, block, 0, a.stream, p);
+        else if (ks == 2) hipLaunchKernelGGL((k_mv_skinny<O, false, 2>), grid, block, 0, a.stream, p);
+        else if (ks == 4) hipLaunchKernelGGL((k_mv_skinny<O, false, 4>), grid, block, 0, a.stream, p);
+        else hipLaunchKernelGGL((k_mv_skinny<O, false, 8>), grid, block, 0, a.stream, p);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Row count from which 2..16 tokens run on the matrix cores (16 rows per wavefront).
+constexpr uint64_t kSkinnyMinRows = 1024;
+bool skinny_eligible(const MatvecArgs &a) {
+    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows) return false;
+    return dispatch(a, [&]<Op O>() { return skinny_supported<O>() ? 1 : 0; }) == 1;
+}
+
 int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
+    if (a.act_format != kActF32 && skinny_eligible(a)) {
+        for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
+            const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
+            const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;
+            float *out = a.out + a.rows * tok;
+            const float *res = a.residual ? a.residual + a.rows * tok : nullptr;
+            const int rc = dispatch(a, [&]<Op O>() {
+                if constexpr (skinny_supported<O>())
+                    return launch_skinny<O>(a, act, n, static_cast<uint32_t>(in_stride), out, res);
+                else
+                    return -2;
+            });
+            if (rc) return rc;
+        }
+        return 0;
+    }
     if (a.act_format != kActF32 && batch_eligible(a)) {
         for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
             const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
@@ -921,8 +1578,18 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     return 0;
 }
 
+size_t tiled_scratch_bytes(const MatvecArgs &a) {
+    if (!skinny_eligible(a)) return 0;
+    return static_cast<size_t>(dispatch(a, [&]<Op O>() {
+        if constexpr (skinny_supported<O>())
+            return static_cast<int>(skinny_scratch<O>(a));
+        else
+            return 0;
+    }));
+}
+
 bool tiled_needs_prepared(const MatvecArgs &a) {
-    if (batch_eligible(a)) return true;
+    if (skinny_eligible(a) || batch_eligible(a)) return true;
     return dispatch(a, [&]<Op O>() { return op_needs_prepared<O>(a) ? 1 : 0; }) == 1;
 }
 

@@ -155,7 +155,7 @@ void prism_hip_destroy(prism_hip_ctx *c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     prism_hip_weight_release_all(c);
-    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res, &c->pre})
+    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res, &c->pre, &c->sk})
         if (b->p) (void)hipFree(b->p);
     if (c->err) (void)hipFree(c->err);
     if (c->stream) (void)hipStreamDestroy(c->stream);

@@ -62,7 +62,7 @@ struct prism_hip_ctx {
     std::map<uint64_t, int64_t> by_key;
     int64_t next_id = 1;
     int *err = nullptr;  // device error flag
-    prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre;
+    prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre, sk;
 };
 
 namespace prism::rt {
@@ -159,7 +159,17 @@ inline MatvecArgs matvec_args(prism_hip_ctx *c, const Weight &w, int act_format,
     return a;
 }
 
-inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &a, bool tiled) {
+inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &args, bool tiled) {
+    MatvecArgs a = args;
+    if (tiled) {
+        const size_t need = tiled_scratch_bytes(a);
+        if (need) {
+            const int e = ensure(c, c->sk, need);
+            if (e) return e;
+            a.scratch = c->sk.p;
+            a.scratch_bytes = c->sk.cap;
+        }
+    }
     int rc = tiled ? launch_matvec_tiled(a) : launch_matvec(a);
     if (rc == -2) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported matvec geometry");
     if (rc) return hip_fail(c, hipGetLastError(), "matvec launch");

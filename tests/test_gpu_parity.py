@@ -319,15 +319,19 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols):
     ctx.release(wid)
 
 
-@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 384), (ph.KIND_PQ2, 512), (ph.KIND_PQ2, 384),
-                                       (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256)])
-def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols):
-    """2..17 tokens on a matrix of >= 8192 rows run weights-once (one wavefront per tile
-    folds every token's chain); each token's row must equal its own matvec, in every
-    contract, with partial chunks of the 16-token batch and a partial last tile."""
+@pytest.mark.parametrize("rows", [1024 + 53, 20480 + 37, 40960 + 37, 65536 + 37, 131072 + 37])
+@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 384), (ph.KIND_PTQ1, 512), (ph.KIND_PQ2, 512),
+                                       (ph.KIND_PQ2, 384), (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256)])
+def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
+    """2..17 tokens run weights-once on the int8 matrix cores, 16 rows per block: the
+    row counts cover 8, 4, 2 and 1 wavefronts per block (K split over the workgroup,
+    terms folded through LDS), and rows x tokens cover both activation sources (prepared
+    blocks gathered directly, or a lane-ordered copy); the pinned PTQ1 order runs one
+    wavefront per tile from 65536 rows.  Each token's row must equal its own matvec, in
+    every contract, with partial chunks of the 16-token batch, a partial last tile and
+    16-row block."""
     import oracle
 
-    rows = 65536 + 37
     w = synth.weights(kind, rows, cols, seed=41) if kind != ph.KIND_PQ2 else synth.pq2_weights(rows, cols, 41, 4)
     wid = ctx.weight(kind, cols, rows, w)
     for tokens in (2, 5, 17):
@@ -336,18 +340,28 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols):
             ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
             got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
             assert_bits_equal(got, ref, f"batch f32 kind={kind} tokens={tokens} pinned={pinned}")
-        if kind in (ph.KIND_PTQ1, ph.KIND_Q8_0) or (kind == ph.KIND_PQ2 and cols % 256):
-            act = np.concatenate([oracle.quantize_q8_0(X[t], 2 if kind == ph.KIND_PTQ1 else 1) for t in range(tokens)])
-            ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * (cols // 32):(t + 1) * (cols // 32)], True,
-                                              threads=THREADS) for t in range(tokens)])
-            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens, pinned=True)
-            assert_bits_equal(got, ref, f"batch q8 kind={kind} tokens={tokens}")
-        else:
-            act = np.concatenate([oracle.quantize_q8k(X[t], True) for t in range(tokens)])
-            ref = np.stack([oracle.project_q8k(kind, cols, rows, w, act[t * (cols // 256):(t + 1) * (cols // 256)], True,
-                                               threads=THREADS) for t in range(tokens)])
-            got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens, fused=True)
-            assert_bits_equal(got, ref, f"batch q8k kind={kind} tokens={tokens}")
+        nq8, nq8k = cols // 32, cols // 256
+        if kind != ph.KIND_Q2_K:
+            for contract, pinned in ((0, False), (2, True)) if kind == ph.KIND_PTQ1 else ((1, False), (0, True)):
+                act = np.concatenate([oracle.quantize_q8_0(X[t], contract) for t in range(tokens)])
+                ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * nq8:(t + 1) * nq8], pinned,
+                                                  threads=THREADS) for t in range(tokens)])
+                got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens, pinned=pinned)
+                assert_bits_equal(got, ref, f"batch q8 kind={kind} tokens={tokens} pinned={pinned}")
+        if cols % 256 == 0 and kind != ph.KIND_Q8_0:
+            for fused in (False, True):
+                act = np.concatenate([oracle.quantize_q8k(X[t], fused) for t in range(tokens)])
+                got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens, fused=fused)
+                if kind == ph.KIND_PTQ1:
+                    nb = cols // 128 * 28
+                    sample = list(range(0, rows, 97)) + list(range(rows - 20, rows))
+                    ref = np.array([[oracle.dot_ptq1_q8k(w[r * nb:(r + 1) * nb], act[t * nq8k:(t + 1) * nq8k])
+                                     for r in sample] for t in range(tokens)], np.float32)
+                    got = got[:, sample]
+                else:
+                    ref = np.stack([oracle.project_q8k(kind, cols, rows, w, act[t * nq8k:(t + 1) * nq8k], fused,
+                                                       threads=THREADS) for t in range(tokens)])
+                assert_bits_equal(got, ref, f"batch q8k kind={kind} tokens={tokens} fused={fused}")
     ctx.release(wid)
 
 
