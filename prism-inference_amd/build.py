@@ -32,6 +32,9 @@ FLAGS = [
     "-ffp-contract=off",
     "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Matrix-core results in ordinary VGPRs: the binary32 chains read every MFMA result,
+    # and the accumulation-register form would add one v_accvgpr_read per value.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
     "-I", os.path.join(ROOT, "include"),
