@@ -36,6 +36,8 @@ extern "C" {
 /* Tensor kinds: GGML type ids (src/kernels.rs:75-87, src/backend.rs:99-141). */
 #define PRISM_KIND_Q8_0 8u
 #define PRISM_KIND_Q2_K 10u
+#define PRISM_KIND_TQ1_0 34u /* 256 ternary weights in 54 bytes (src/kernels/tquants.rs:17-23) */
+#define PRISM_KIND_TQ2_0 35u /* 256 ternary weights in 66 bytes */
 #define PRISM_KIND_PQ2 142u
 #define PRISM_KIND_PTQ1 143u
 

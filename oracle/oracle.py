@@ -21,6 +21,8 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 KIND_Q8_0 = 8
 KIND_Q2_K = 10
 KIND_Q8_K = 15
+KIND_TQ1_0 = 34
+KIND_TQ2_0 = 35
 KIND_PQ2 = 142
 KIND_PTQ1 = 143
 
@@ -34,7 +36,8 @@ ERR_RESOURCE = -2
 ERR_NONFINITE = -3
 ERR_UNSUPPORTED = -5
 
-LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_Q8_K: (256, 292), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28)}
+LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_Q8_K: (256, 292), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28),
+          KIND_TQ1_0: (256, 54), KIND_TQ2_0: (256, 66)}
 
 # numpy mirrors of the C structs (tools/ternary/src/lib.rs:27-39; src/kernels.rs:528-535)
 Q8K_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (256,)), ("sums", "<i2", (16,))])
@@ -99,6 +102,9 @@ def lib():
             "po_attention_head": (I, [P, P, P, S, S, S, P, P, S, P, P]),
             "po_decoder_step": (I, [P, P, P, P, U, S, P, I]),
             "po_argmax": (S, [P, S]),
+            "po_tq_codes": (None, [U, P, P]),
+            "po_dot_tq": (I, [U, P, S, P, P]),
+            "po_quantize_tq": (I, [U, P, S, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -215,6 +221,19 @@ def dot_q2k(row, act: np.ndarray) -> np.float32:
 def dot_q8_0(row, act: np.ndarray) -> np.float32:
     r = _u8(row)
     return _f(lib().po_dot_q8_0, _p(r), r.size // 34, _p(act))[0]
+
+
+def tq_codes(kind: int, block) -> np.ndarray:
+    """The 256 signed digits of one TQ1_0 / TQ2_0 block, in element order."""
+    b = _u8(block)
+    out = np.zeros(256, np.int16)
+    lib().po_tq_codes(kind, _p(b), _p(out))
+    return out
+
+
+def dot_tq(kind: int, row, act: np.ndarray) -> np.float32:
+    w = _u8(row)
+    return _f(lib().po_dot_tq, kind, _p(w), act.size, _p(act))[0]
 
 
 def dot_ptq1_q8k(row, act: np.ndarray) -> np.float32:

@@ -254,6 +254,8 @@ int po_layout(uint32_t kind, size_t *group, size_t *bytes) {
     case PO_KIND_Q8_K: *group = 256; *bytes = 292; return PO_OK;
     case PO_KIND_PQ2: *group = 128; *bytes = 34; return PO_OK;
     case PO_KIND_PTQ1: *group = 128; *bytes = 28; return PO_OK;
+    case PO_KIND_TQ1_0: *group = 256; *bytes = 54; return PO_OK; /* tquants.rs:17-23 */
+    case PO_KIND_TQ2_0: *group = 256; *bytes = 66; return PO_OK;
     default: return PO_ERR_UNSUPPORTED;
     }
 }
@@ -384,6 +386,10 @@ static int quantize_ternary(const float *x, uint8_t *blk) {
 int po_quantize_row(uint32_t kind, const float *x, size_t n, uint8_t *out, size_t out_len) {
     size_t group, bytes;
     if (po_layout(kind, &group, &bytes) || kind == PO_KIND_Q2_K) return PO_ERR_UNSUPPORTED;
+    if (kind == PO_KIND_TQ1_0 || kind == PO_KIND_TQ2_0) { /* kernels.rs:660, before the generic checks */
+        if (n % 256 == 0 && out_len != n / 256 * bytes) return PO_ERR_INVALID_INPUT;
+        return po_quantize_tq(kind, x, n, out);
+    }
     if (n == 0 || n % group) return PO_ERR_INVALID_INPUT;
     if (!all_finite(x, n)) return PO_ERR_NONFINITE;
     if (out_len != n / group * bytes) return PO_ERR_INVALID_INPUT;
@@ -474,6 +480,14 @@ int po_decode_row(uint32_t kind, size_t count, const uint8_t *bytes, float *out)
                 o[i] = v;
             }
             break;
+        case PO_KIND_TQ1_0:
+        case PO_KIND_TQ2_0: { /* tquants.rs:240-253 */
+            int16_t c[256];
+            if (scale_of(p + bb - 2, &d)) return PO_ERR_NONFINITE;
+            po_tq_codes(kind, p, c);
+            for (int i = 0; i < 256; i++) o[i] = (float)c[i] * d;
+            break;
+        }
         case PO_KIND_Q8_K: {
             float s;
             memcpy(&s, p, 4);
@@ -660,7 +674,7 @@ int po_packed_dot(uint32_t kind, size_t count, const uint8_t *w, size_t wlen, co
     if (kind == PO_KIND_Q8_K) return PO_ERR_INVALID_INPUT;
     if (po_layout(kind, &group, &bb)) return PO_ERR_UNSUPPORTED;
     if (count == 0 || count % group || count / group * bb != wlen) return PO_ERR_INVALID_INPUT;
-    if (kind == PO_KIND_PQ2 || kind == PO_KIND_Q2_K) {
+    if (kind == PO_KIND_PQ2 || kind == PO_KIND_Q2_K || kind == PO_KIND_TQ1_0 || kind == PO_KIND_TQ2_0) {
         if (count % 256 || count / 256 * 292 != alen) return PO_ERR_INVALID_INPUT;
         size_t na = count / 256;
         po_q8k_block *q = (po_q8k_block *)malloc(sizeof(po_q8k_block) * na);
@@ -670,7 +684,9 @@ int po_packed_dot(uint32_t kind, size_t count, const uint8_t *w, size_t wlen, co
         for (size_t i = 0; i < na; i++)
             if (!is_finite(q[i].scale)) rc = PO_ERR_NONFINITE;
         if (!rc)
-            rc = kind == PO_KIND_PQ2 ? po_dot_pq2(w, count / 128, q, 0, out) : po_dot_q2k(w, na, q, out);
+            rc = kind == PO_KIND_PQ2    ? po_dot_pq2(w, count / 128, q, 0, out)
+                 : kind == PO_KIND_Q2_K ? po_dot_q2k(w, na, q, out)
+                                        : po_dot_tq(kind, w, na, q, out);
         free(q);
         return rc;
     }
@@ -698,7 +714,7 @@ int po_packed_dot(uint32_t kind, size_t count, const uint8_t *w, size_t wlen, co
 /* src/kernels.rs:1663-1673 ActivationContract::for_tensor. */
 int po_activation_contract(uint32_t kind, size_t cols, int pinned) {
     if (kind == PO_KIND_PTQ1 && pinned) return 2;
-    if (kind == PO_KIND_Q2_K) return 0;
+    if (kind == PO_KIND_Q2_K || kind == PO_KIND_TQ1_0 || kind == PO_KIND_TQ2_0) return 0;
     if (kind == PO_KIND_PQ2 && cols % 256 == 0) return 0;
     return 1;
 }
@@ -719,6 +735,8 @@ static int row_dot(const job_t *j, size_t r, float *o) {
     const uint8_t *row = j->w + r * j->row_bytes;
     switch (j->kind) {
     case PO_KIND_Q2_K: return po_dot_q2k(row, j->cols / 256, j->q8k, o);
+    case PO_KIND_TQ1_0:
+    case PO_KIND_TQ2_0: return po_dot_tq(j->kind, row, j->cols / 256, j->q8k, o);
     case PO_KIND_Q8_0: return po_dot_q8_0(row, j->cols / 32, j->q8, o);
     case PO_KIND_PQ2:
         if (j->q8k) return po_dot_pq2(row, j->cols / 128, j->q8k, j->pinned, o);
@@ -771,7 +789,8 @@ static int run_rows(job_t *proto, int threads) {
 
 static int check_geometry(uint32_t kind, size_t cols, size_t rows, size_t *row_bytes) {
     size_t group, bb;
-    if (kind != PO_KIND_Q2_K && kind != PO_KIND_Q8_0 && kind != PO_KIND_PQ2 && kind != PO_KIND_PTQ1)
+    if (kind != PO_KIND_Q2_K && kind != PO_KIND_Q8_0 && kind != PO_KIND_PQ2 && kind != PO_KIND_PTQ1 &&
+        kind != PO_KIND_TQ1_0 && kind != PO_KIND_TQ2_0)
         return PO_ERR_UNSUPPORTED;
     po_layout(kind, &group, &bb);
     if (cols == 0 || rows == 0 || cols % group) return PO_ERR_INVALID_INPUT;
@@ -796,7 +815,7 @@ int po_project_q8(uint32_t kind, size_t cols, size_t rows, const uint8_t *w, con
                   int pinned, float *out, int threads) {
     job_t j = {0};
     int rc = check_geometry(kind, cols, rows, &j.row_bytes);
-    if (!rc && kind == PO_KIND_Q2_K) rc = PO_ERR_INVALID_INPUT;
+    if (!rc && po_activation_contract(kind, cols, 0) == 0 && kind != PO_KIND_PQ2) rc = PO_ERR_INVALID_INPUT;
     if (!rc) {
         j.kind = kind; j.cols = cols; j.rows = rows; j.w = w; j.q8 = act; j.pinned = pinned; j.out = out;
         rc = run_rows(&j, threads);

@@ -28,6 +28,8 @@ extern "C" {
 #define PO_KIND_Q8_0 8u
 #define PO_KIND_Q2_K 10u
 #define PO_KIND_Q8_K 15u
+#define PO_KIND_TQ1_0 34u
+#define PO_KIND_TQ2_0 35u
 #define PO_KIND_PQ2 142u
 #define PO_KIND_PTQ1 143u
 
@@ -65,6 +67,12 @@ float po_round_f16(float f);                                 /* kernels.rs:2824-
 void po_decode_ptq_trits(const uint8_t *blk, int16_t *out);  /* lib.rs:239-250 */
 int po_pack_ptq(const uint8_t *pq2, uint8_t *ptq);           /* lib.rs:163-189 */
 int po_unpack_ptq(const uint8_t *ptq, uint8_t *pq2);         /* lib.rs:260-290 */
+
+/* ---- TQ1_0 / TQ2_0 (src/kernels/tquants.rs, tquants_oracle.c) ---- */
+void po_tq_codes(uint32_t kind, const uint8_t *blk, int16_t *out);                  /* tquants.rs:145-190 */
+int po_dot_tq(uint32_t kind, const uint8_t *row, size_t nblocks, const po_q8k_block *act,
+              float *out);                                                            /* tquants.rs:255-273 */
+int po_quantize_tq(uint32_t kind, const float *x, size_t n, uint8_t *out);          /* tquants.rs:275-324 */
 
 /* ---- layout (src/kernels.rs:88-119) ---- */
 int po_layout(uint32_t kind, size_t *group, size_t *block_bytes);

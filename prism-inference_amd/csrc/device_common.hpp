@@ -14,8 +14,8 @@
 
 namespace prism {
 
-// Kinds (src/kernels.rs:75-87).
-constexpr uint32_t kQ8_0 = 8, kQ2_K = 10, kPQ2 = 142, kPTQ1 = 143;
+// Kinds (src/kernels.rs:75-87; TQ1_0 / TQ2_0 src/kernels/tquants.rs:17-23).
+constexpr uint32_t kQ8_0 = 8, kQ2_K = 10, kTQ1_0 = 34, kTQ2_0 = 35, kPQ2 = 142, kPTQ1 = 143;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));

@@ -436,6 +436,28 @@ __global__ void k_matvec_generic(uint32_t kind, int q8k, int pinned, const uint8
             o = o + ((as * h2f(ld16(p + 80))) * static_cast<float>(isum) -
                      (as * h2f(ld16(p + 82))) * static_cast<float>(msum));
         }
+    } else if (kind == kTQ1_0 || kind == kTQ2_0) {
+        // src/kernels/tquants.rs:255-273 (element maps :145-190)
+        const Q8KBlock *a = static_cast<const Q8KBlock *>(act);
+        const uint32_t bb = kind == kTQ1_0 ? 54 : 66;
+        for (uint32_t b = 0; b < cols / 256; ++b) {
+            const uint8_t *p = row + bb * b;
+            int I = 0;
+            for (int i = 0; i < 256; ++i) {
+                int wv;
+                if (kind == kTQ2_0) {
+                    wv = static_cast<int>((p[i / 128 * 32 + i % 32] >> (2 * (i % 128 / 32))) & 3) - 1;
+                } else if (i < 160) {
+                    wv = trit_of(p[i % 32], i / 32) - 1;
+                } else if (i < 240) {
+                    wv = trit_of(p[32 + (i - 160) % 16], (i - 160) / 16) - 1;
+                } else {
+                    wv = trit_of(p[48 + (i - 240) % 4], (i - 240) / 4) - 1;
+                }
+                I += wv * a[b].values[i];
+            }
+            o = o + static_cast<float>(I) * (h2f(ld16(p + bb - 2)) * a[b].scale);
+        }
     } else {
         const bool pq2 = kind == kPQ2;
         const uint32_t bb = pq2 ? 34 : 28;
@@ -532,6 +554,7 @@ static bool fits(const MatvecArgs &a) {
 }
 
 static bool fast_path(const MatvecArgs &a) {
+    if (a.kind == kTQ1_0 || a.kind == kTQ2_0) return false;  // native TQ rows: generic kernel only
     if (a.cols % 128 != 0 || a.cols / 128 > 256) return false;
     if (a.kind == kPTQ1 && a.act_format == kActQ8 && a.pinned && !fits<Op::PTQ1_PINNED>(a)) return false;
     if (a.kind == kQ8_0 && !fits<Op::Q8_0>(a)) return false;

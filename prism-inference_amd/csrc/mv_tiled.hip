@@ -24,19 +24,31 @@ namespace prism {
 
 namespace {
 
-enum class Op : int { PTQ1_SRC, PTQ1_PINNED, PTQ1_Q8K, PQ2_UNFUSED, PQ2_FUSED, PQ2_Q8, Q2K, Q8_0 };
+enum class Op : int { PTQ1_SRC, PTQ1_PINNED, PTQ1_Q8K, PQ2_UNFUSED, PQ2_FUSED, PQ2_Q8, Q2K, Q8_0, TQ1, TQ2 };
 
 template <Op O>
 constexpr uint32_t kind_of() {
     return O == Op::Q2K    ? kQ2_K
            : O == Op::Q8_0 ? kQ8_0
+           : O == Op::TQ1  ? kTQ1_0
+           : O == Op::TQ2  ? kTQ2_0
            : (O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED || O == Op::PQ2_Q8) ? kPQ2
                                                                               : kPTQ1;
 }
 // Native bytes per unit.
 template <Op O>
 constexpr uint32_t unit_bytes() {
-    return kind_of<O>() == kPTQ1 ? 28 : kind_of<O>() == kPQ2 ? 34 : kind_of<O>() == kQ2_K ? 84 : 136;
+    return kind_of<O>() == kPTQ1   ? 28
+           : kind_of<O>() == kPQ2  ? 34
+           : kind_of<O>() == kQ2_K ? 84
+           : O == Op::TQ1          ? 54
+           : O == Op::TQ2          ? 66
+                                   : 136;
+}
+// Weights per unit: a 256-element super-block (Q2_K, TQ1_0, TQ2_0) or 128.
+template <Op O>
+constexpr uint32_t unit_weights() {
+    return (O == Op::Q2K || O == Op::TQ1 || O == Op::TQ2) ? 256 : 128;
 }
 // binary32 terms per unit handed to the fold when K is split across wavefronts.
 template <Op O>
@@ -211,6 +223,16 @@ struct Raw<Op::Q8_0> {
     uint32_t c[32];
     uint32_t s[2];
 };
+template <>
+struct Raw<Op::TQ1> {
+    uint32_t q[13];  // code bytes 0..51
+    uint32_t d;      // binary16 scale
+};
+template <>
+struct Raw<Op::TQ2> {
+    uint32_t q[16];  // code bytes 0..63
+    uint32_t d;
+};
 
 // Loads unit `seg` (byte offset of the unit's segment in the tile) for tile-row `r`.
 template <Op O>
@@ -228,6 +250,16 @@ __device__ __forceinline__ void load_unit(Raw<O> &w, __amdgpu_buffer_rsrc_t rs, 
         w.c[0] = a.x; w.c[1] = a.y; w.c[2] = a.z; w.c[3] = a.w;
         w.c[4] = b.x; w.c[5] = b.y; w.c[6] = b.z; w.c[7] = b.w;
         w.d = __builtin_amdgcn_raw_buffer_load_b16(rs, static_cast<int>(seg + 32u * trp + 2u * r), 0, 0);
+    } else if constexpr (O == Op::TQ1 || O == Op::TQ2) {
+        constexpr int P = O == Op::TQ1 ? 3 : 4;  // 16-byte code pieces
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const u32x4 a = bload4(rs, seg + 16u * p * trp + 16u * r);
+            w.q[4 * p] = a.x; w.q[4 * p + 1] = a.y; w.q[4 * p + 2] = a.z; w.q[4 * p + 3] = a.w;
+        }
+        if constexpr (O == Op::TQ1) w.q[12] = bload1(rs, seg + 48u * trp + 4u * r);
+        constexpr uint32_t kScale = O == Op::TQ1 ? 52 : 64;  // scale piece offset (in TRP bytes)
+        w.d = __builtin_amdgcn_raw_buffer_load_b16(rs, static_cast<int>(seg + kScale * trp + 2u * r), 0, 0);
     } else if constexpr (kind_of<O>() == kQ2_K) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -384,6 +416,45 @@ __device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restri
         const float as = b->scale;
         t[0] = (as * h2f(w.dm & 0xffffu)) * static_cast<float>(isum) -
                (as * h2f(w.dm >> 16)) * static_cast<float>(msum);
+    } else if constexpr (O == Op::TQ1) {
+        // TQ1_0 (src/kernels/tquants.rs:192-215): byte b < 32 digit k -> element b + 32k,
+        // byte 32 + b digit k -> 160 + b + 16k, byte 48 + b digit k < 4 -> 240 + b + 4k, so
+        // the digit-k quad of a code dword pairs with one natural activation dword.  The
+        // digits (trit_k = ((x * 3^k mod 256) * 3) >> 8, as PTQ1) become signed bytes t - 1.
+        const Q8KBlock *b = static_cast<const Q8KBlock *>(act) + u;
+        const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values);
+        int I = 0;
+        auto digits = [&](uint32_t x, int nd, int a0, int astep) {
+            uint32_t L = x & 0x00ff00ffu, H = (x >> 8) & 0x00ff00ffu;
+            for (int k = 0; k < nd; ++k) {
+                const uint32_t mL = L * 3u, mH = H * 3u;
+                I = sdot4(perm(0u, 0x000100ffu, perm(mH, mL, sel(1, 5, 3, 7))), av[a0 + astep * k], I);
+                L = mL & 0x00ff00ffu;
+                H = mH & 0x00ff00ffu;
+            }
+        };
+#pragma unroll
+        for (int wd = 0; wd < 8; ++wd) digits(w.q[wd], 5, wd, 8);
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) digits(w.q[8 + wd], 5, 40 + wd, 4);
+        digits(w.q[12], 4, 60, 1);
+        // dot(), src/kernels/tquants.rs:264-270
+        t[0] = static_cast<float>(I) * (h2f(w.d) * b->scale);
+    } else if constexpr (O == Op::TQ2) {
+        // TQ2_0 (src/kernels/tquants.rs:217-238): byte 32h + b field k -> element
+        // 128h + 32k + b; fields become signed bytes c - 1.
+        const Q8KBlock *b = static_cast<const Q8KBlock *>(act) + u;
+        const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values);
+        int I = 0;
+#pragma unroll
+        for (int wd = 0; wd < 16; ++wd) {
+            const int h = wd >> 3, wh = wd & 7;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                I = sdot4(perm(0u, 0x020100ffu, (w.q[wd] >> (2 * k)) & 0x03030303u), av[32 * h + 8 * k + wh], I);
+        }
+        // dot(), src/kernels/tquants.rs:264-270
+        t[0] = static_cast<float>(I) * (h2f(w.d) * b->scale);
     } else {
         const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
 #pragma unroll
@@ -448,7 +519,8 @@ struct MvParams {
 
 template <Op O>
 constexpr bool act_is_q8k() {
-    return O == Op::PTQ1_Q8K || O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED || O == Op::Q2K;
+    return O == Op::PTQ1_Q8K || O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED || O == Op::Q2K || O == Op::TQ1 ||
+           O == Op::TQ2;
 }
 
 // Prepared-activation bytes for `cols` inputs (one token).
@@ -614,7 +686,7 @@ struct SkParams {
 
 template <Op O>
 constexpr bool skinny_supported() {
-    return O != Op::PTQ1_PINNED;
+    return O != Op::PTQ1_PINNED && O != Op::TQ1 && O != Op::TQ2;
 }
 
 // Per-lane geometry: the tile's buffer, the lane's A row and first output row.
@@ -1352,7 +1424,7 @@ bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t 
 
 template <Op O>
 int launch_op(const MatvecArgs &a, const void *act, float *out) {
-    const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
     const bool quant = a.act_format == kActF32;
     const uint32_t nmat = a.w2 ? 2u : 1u;
@@ -1400,7 +1472,7 @@ bool op_needs_prepared(const MatvecArgs &a) {
     if (a.w2) return false;
     if (tiles >= a.cus) return true;
     SplitPlan pl;
-    const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
     return !plan_split<O>(a.rows, nu, static_cast<uint32_t>(a.cols), true, 1, a.cus, &pl);
 }
 
@@ -1420,6 +1492,10 @@ int dispatch(const MatvecArgs &a, F &&f) {
     }
     if (a.kind == kQ2_K) return f.template operator()<Op::Q2K>();
     if (a.kind == kQ8_0) return f.template operator()<Op::Q8_0>();
+    // TQ1_0 / TQ2_0 take Q8_K activations only (ActivationContract::for_tensor,
+    // src/kernels.rs:1663-1673).
+    if (a.kind == kTQ1_0 && q8k) return f.template operator()<Op::TQ1>();
+    if (a.kind == kTQ2_0 && q8k) return f.template operator()<Op::TQ2>();
     return -2;
 }
 
@@ -1450,7 +1526,7 @@ int launch_batch(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t a
     MvParams p{};
     p.w[0] = p.w[1] = a.w;
     p.rows = static_cast<uint32_t>(a.rows);
-    p.nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    p.nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
     p.cols = static_cast<uint32_t>(a.cols);
     p.pinned = a.pinned;
     p.out = out;
@@ -1482,7 +1558,7 @@ bool skinny_lane_ordered(uint64_t rows, uint32_t ntok) {
 template <Op O>
 size_t skinny_scratch(const MatvecArgs &a) {
     if (!skinny_lane_ordered<O>(a.rows, a.tokens < kBatchMax ? a.tokens : kBatchMax)) return 0;
-    const uint64_t nu = a.cols / (kind_of<O>() == kQ2_K ? 256 : 128);
+    const uint64_t nu = a.cols / unit_weights<O>();
     return nu * 64u * (sk_lane_bytes<O>() + 4u);
 }
 
@@ -1491,7 +1567,7 @@ int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t 
                   const float *residual) {
     const bool sw = skinny_lane_ordered<O>(a.rows, ntok);
     if (sw && (!a.scratch || a.scratch_bytes < skinny_scratch<O>(a))) return -2;
-    const uint32_t nu = static_cast<uint32_t>(a.cols / (kind_of<O>() == kQ2_K ? 256 : 128));
+    const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
     if (sw) {
         const uint32_t nprep = nu * 64u * (sk_lane_bytes<O>() / 4u);
         hipLaunchKernelGGL(k_sk_prep<O>, dim3((nprep + 255u) / 256u), dim3(256), 0, a.stream,

@@ -51,7 +51,8 @@ bool eligible(uint32_t kind, uint64_t cols, uint64_t rows, int path) {
     switch (path) {
     case PRISM_PATH_Q8K:
         if (kind == PRISM_KIND_PQ2) return cols % 256 == 0;
-        return kind == PRISM_KIND_Q2_K || kind == PRISM_KIND_PTQ1;
+        return kind == PRISM_KIND_Q2_K || kind == PRISM_KIND_PTQ1 || kind == PRISM_KIND_TQ1_0 ||
+               kind == PRISM_KIND_TQ2_0;
     case PRISM_PATH_Q8: return kind == PRISM_KIND_PTQ1 || kind == PRISM_KIND_PQ2 || kind == PRISM_KIND_Q8_0;
     case PRISM_PATH_F32: return true;
     default: return false;
@@ -456,7 +457,7 @@ static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, 
     const uint64_t nout = d ? d->rows : g->rows;
     if (!x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
     const bool kind_ok = (g->kind == PRISM_KIND_PQ2 || g->kind == PRISM_KIND_Q2_K || g->kind == PRISM_KIND_PTQ1 ||
-                          g->kind == PRISM_KIND_Q8_0) &&
+                          g->kind == PRISM_KIND_Q8_0 || g->kind == PRISM_KIND_TQ1_0 || g->kind == PRISM_KIND_TQ2_0) &&
                          (!d || d->kind == g->kind);
     if (!kind_ok) {
         zero(out, nout);

@@ -37,6 +37,8 @@ inline bool layout(uint32_t kind, uint64_t *group, uint64_t *block) {
     case PRISM_KIND_Q2_K: *group = 256; *block = 84; return true;
     case PRISM_KIND_PQ2: *group = 128; *block = 34; return true;
     case PRISM_KIND_PTQ1: *group = 128; *block = 28; return true;
+    case PRISM_KIND_TQ1_0: *group = 256; *block = 54; return true;
+    case PRISM_KIND_TQ2_0: *group = 256; *block = 66; return true;
     default: return false;
     }
 }
@@ -44,7 +46,7 @@ inline bool layout(uint32_t kind, uint64_t *group, uint64_t *block) {
 // ActivationContract::for_tensor (src/kernels.rs:1663-1673): 0 = Q8_K, 1 = Q8_0, 2 = pinned PTQ1 Q8_0.
 inline int contract_for(uint32_t kind, uint64_t cols, int pinned) {
     if (kind == PRISM_KIND_PTQ1 && pinned) return 2;
-    if (kind == PRISM_KIND_Q2_K) return 0;
+    if (kind == PRISM_KIND_Q2_K || kind == PRISM_KIND_TQ1_0 || kind == PRISM_KIND_TQ2_0) return 0;
     if (kind == PRISM_KIND_PQ2 && cols % 256 == 0) return 0;
     return 1;
 }

@@ -36,6 +36,8 @@ struct TiledFormat {
 // Q2_K (10): codes 16..79 in four pieces | sub-block scales 0..15 | d, dmin 80..83.
 // Q8_0 (8), four 34-byte blocks per unit: codes of block j in pieces 2j, 2j+1
 //   (native 34j+2 .. 34j+33) | the four f16 scales, block j's at bytes 2j..2j+1.
+// TQ1_0 (34): codes 0..15 | 16..31 | 32..47 | 48..51 | f16 scale 52..53.
+// TQ2_0 (35): codes 0..63 in four pieces | f16 scale 64..65.
 __host__ __device__ inline bool tiled_format(uint32_t kind, TiledFormat *f) {
     switch (kind) {
     case 143:
@@ -46,6 +48,12 @@ __host__ __device__ inline bool tiled_format(uint32_t kind, TiledFormat *f) {
         return true;
     case 10:
         *f = {256, 84, 6, {16, 16, 16, 16, 16, 4}, {0, 16, 32, 48, 64, 80}, {16, 32, 48, 64, 0, 80}};
+        return true;
+    case 34:
+        *f = {256, 54, 5, {16, 16, 16, 4, 2}, {0, 16, 32, 48, 52}, {0, 16, 32, 48, 52}};
+        return true;
+    case 35:
+        *f = {256, 66, 5, {16, 16, 16, 16, 2}, {0, 16, 32, 48, 64}, {0, 16, 32, 48, 64}};
         return true;
     case 8:
         // The scale piece gathers four 2-byte fields; nsrc = 0 marks the gather.

@@ -20,9 +20,12 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "prism_hip.h")
 
 KIND_Q8_0 = 8
 KIND_Q2_K = 10
+KIND_TQ1_0 = 34
+KIND_TQ2_0 = 35
 KIND_PQ2 = 142
 KIND_PTQ1 = 143
-LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28)}
+LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28),
+          KIND_TQ1_0: (256, 54), KIND_TQ2_0: (256, 66)}
 
 OK = 0
 ERR_INVALID_INPUT = -1

@@ -14,9 +14,12 @@ import numpy as np
 
 KIND_Q8_0 = 8
 KIND_Q2_K = 10
+KIND_TQ1_0 = 34
+KIND_TQ2_0 = 35
 KIND_PQ2 = 142
 KIND_PTQ1 = 143
-LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28)}
+LAYOUT = {KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_PQ2: (128, 34), KIND_PTQ1: (128, 28),
+          KIND_TQ1_0: (256, 54), KIND_TQ2_0: (256, 66)}
 
 
 def row_bytes(kind: int, cols: int) -> int:
@@ -108,6 +111,17 @@ def q8_0_weights(rows: int, cols: int, seed: int) -> np.ndarray:
     return out.reshape(-1)
 
 
+def tq_weights(kind: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """TQ1_0 / TQ2_0 blocks: uniform code bytes (every byte is a valid code: TQ1_0 base-3
+    digits of any byte, TQ2_0 2-bit fields 0..3) and one binary16 scale |N(0,0.02)|."""
+    rng = np.random.default_rng(seed)
+    _, bb = LAYOUT[kind]
+    nb = rows * cols // 256
+    out = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+    out[:, bb - 2:] = _f16_bytes(np.abs(rng.normal(0.0, 0.02, nb)).astype(np.float32)).reshape(nb, 2)
+    return out.reshape(-1)
+
+
 def weights(kind: int, rows: int, cols: int, seed: int) -> np.ndarray:
     if kind == KIND_PTQ1:
         return ptq1_weights(rows, cols, seed)
@@ -117,6 +131,8 @@ def weights(kind: int, rows: int, cols: int, seed: int) -> np.ndarray:
         return q2k_weights(rows, cols, seed)
     if kind == KIND_Q8_0:
         return q8_0_weights(rows, cols, seed)
+    if kind in (KIND_TQ1_0, KIND_TQ2_0):
+        return tq_weights(kind, rows, cols, seed)
     raise ValueError(kind)
 
 

@@ -16,6 +16,7 @@ Sources (paths relative to the reference checkout):
   tests/fixtures/row-quantizers.json                  production row-quantizer records
   tests/fixtures/upstream-kquants.json                K-quant encode/decode/dot records
   tests/upstream_prism/pq2-inputs.bin                 15 upstream PQ2 row-shape inputs
+  tests/fixtures/upstream-tquants.json                TQ1_0/TQ2_0 encode/decode/dot records
 """
 
 import hashlib
@@ -38,6 +39,7 @@ COPY = [
     "tests/fixtures/swift-ptq1-dot-parity.bin",
     "tests/fixtures/swift-ptq1-dot-parity.json",
     "tests/upstream_prism/pq2-inputs.bin",
+    "tests/fixtures/upstream-tquants.json",
 ]
 
 

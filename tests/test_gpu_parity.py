@@ -207,6 +207,8 @@ SHAPES = [
     (ph.KIND_Q2_K, 37, 256), (ph.KIND_Q2_K, 64, 2048), (ph.KIND_Q2_K, 33, 6144), (ph.KIND_Q2_K, 21, 16384),
     (ph.KIND_Q8_0, 37, 128), (ph.KIND_Q8_0, 64, 2048), (ph.KIND_Q8_0, 50, 2080), (ph.KIND_Q8_0, 33, 4096),
     (ph.KIND_Q8_0, 9, 8192),
+    (ph.KIND_TQ1_0, 37, 256), (ph.KIND_TQ1_0, 64, 2048), (ph.KIND_TQ1_0, 33, 6144), (ph.KIND_TQ1_0, 21, 16384),
+    (ph.KIND_TQ2_0, 37, 256), (ph.KIND_TQ2_0, 64, 2048), (ph.KIND_TQ2_0, 33, 6144), (ph.KIND_TQ2_0, 19, 12288),
 ]
 
 
@@ -264,7 +266,8 @@ def test_gpu_project_q8_prepared_codes(ctx, kind, rows, cols):
 # ---- large matrices: one wavefront per 64-row tile (>= one tile per CU) ----------------
 
 @pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 256), (ph.KIND_PQ2, 256), (ph.KIND_PQ2, 384),
-                                       (ph.KIND_Q2_K, 256), (ph.KIND_Q8_0, 256)])
+                                       (ph.KIND_Q2_K, 256), (ph.KIND_Q8_0, 256), (ph.KIND_TQ1_0, 512),
+                                       (ph.KIND_TQ2_0, 512)])
 def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
     """rows spans more 64-row tiles than the device has CUs (the one-wavefront-per-tile
     kernel with scalar activation loads), with a partial last tile."""
@@ -321,7 +324,8 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols):
 
 @pytest.mark.parametrize("rows", [1024 + 53, 20480 + 37, 40960 + 37, 65536 + 37, 131072 + 37])
 @pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 384), (ph.KIND_PTQ1, 512), (ph.KIND_PQ2, 512),
-                                       (ph.KIND_PQ2, 384), (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256)])
+                                       (ph.KIND_PQ2, 384), (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256),
+                                       (ph.KIND_TQ1_0, 512), (ph.KIND_TQ2_0, 256)])
 def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     """2..17 tokens run weights-once on the int8 matrix cores, 16 rows per block: the
     row counts cover 8, 4, 2 and 1 wavefronts per block (K split over the workgroup,
@@ -341,7 +345,7 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
             got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
             assert_bits_equal(got, ref, f"batch f32 kind={kind} tokens={tokens} pinned={pinned}")
         nq8, nq8k = cols // 32, cols // 256
-        if kind != ph.KIND_Q2_K:
+        if kind not in (ph.KIND_Q2_K, ph.KIND_TQ1_0, ph.KIND_TQ2_0):
             for contract, pinned in ((0, False), (2, True)) if kind == ph.KIND_PTQ1 else ((1, False), (0, True)):
                 act = np.concatenate([oracle.quantize_q8_0(X[t], contract) for t in range(tokens)])
                 ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * nq8:(t + 1) * nq8], pinned,
@@ -418,7 +422,7 @@ def test_gpu_project_f32_group_siblings(ctx):
 
 # ---- FFN ------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_PTQ1])
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_PTQ1, ph.KIND_TQ1_0, ph.KIND_TQ2_0])
 def test_gpu_ffn_chain(ctx, kind):
     import oracle
 
@@ -498,3 +502,20 @@ def test_gpu_device_pointer_path_matches_host_path(ctx):
         again = ctx.project_f32(wid, rows, x)
         assert_bits_equal(again, host, "repeat")
         ctx.release(wid)
+
+
+@pytest.mark.parametrize("kind", [ph.KIND_TQ1_0, ph.KIND_TQ2_0])
+def test_gpu_wrapped_native_tq_rows_match_oracle(ctx, kind):
+    """A caller-owned device buffer in the native row-major layout (no tiled copy) runs
+    the reference-order row kernel; it must match the oracle like the tiled path."""
+    import oracle
+
+    rows, cols = 70, 1024
+    w = synth.weights(kind, rows, cols, seed=kind)
+    x = synth.activations(cols, seed=13)
+    wd = DeviceBuffer.from_numpy(w)
+    wid = ctx.weight_device(kind, cols, rows, wd)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, x, pinned, threads=THREADS)
+        assert_bits_equal(ctx.project_f32(wid, rows, x, pinned=pinned), ref, f"native kind={kind} pinned={pinned}")
+    ctx.release(wid)
