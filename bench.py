@@ -195,7 +195,7 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
     w = synth.weights(kind, rows, cols, seed=7)
     copies = max(2, math.ceil(ROTATE_BYTES / w.size))
     rot = Rotation(ctx, kind, rows, cols, w, copies)
-    contract = 0 if kind in (ph.KIND_Q2_K,) or (kind == ph.KIND_PQ2 and cols % 256 == 0) else 1
+    contract = 0 if kind in (ph.KIND_Q2_K, ph.KIND_TQ1_0, ph.KIND_TQ2_0) or (kind == ph.KIND_PQ2 and cols % 256 == 0) else 1
     x = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=8, tokens=tokens))
     if contract == 0:
         act = hiprt.DeviceBuffer(cols // 256 * 292 * tokens)
