@@ -230,6 +230,69 @@ int prism_hip_decoder_set_head(prism_hip_decoder *d, const uint8_t *lm_head, con
 int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t pos, uint32_t steps, int use_graph,
                                uint32_t *tokens_out, float *logits_out, double *seconds);
 
+/* ---- GGUF v3 weights (tools/gguf) --------------------------------------------------
+ * A bounded reader of the GGUF header, metadata table and tensor index: the checks of
+ * read_index (tools/gguf/src/stream.rs:349-657) -- magic, version, counts, unique keys
+ * and names, UTF-8 without interior NUL, a power-of-two general.alignment (default 32),
+ * 1..4 nonzero dimensions, known types (PQ2 142 / PTQ1 143 only in the Prism dialect),
+ * block-complete first dimensions, aligned offsets, in-file non-overlapping extents and
+ * the metadata budget.  Tensors and metadata keys enumerate in name order.  Host code:
+ * none of these functions touches the GPU except prism_hip_weight_from_gguf. */
+typedef struct prism_gguf prism_gguf;
+/* IndexPolicy (stream.rs:44-131); prism_gguf_default_policy fills IndexPolicy::new(). */
+typedef struct {
+    int allow_v2, allow_zero_tensors, allow_zero_metadata;
+    uint64_t max_file_bytes, max_tensors, max_metadata, metadata_budget;
+    uint64_t max_key_bytes, max_string_bytes, max_array_string_bytes;
+    uint64_t max_retained_string_array_bytes; /* 0 = unlimited */
+    uint64_t max_array_items, max_alignment;
+    int allow_positive_i32_alignment, reject_nonfinite_floats, reject_interior_nul_keys,
+        reject_interior_nul_strings;
+    uint64_t kv_overhead_bytes, string_overhead_bytes, tensor_overhead_bytes;
+    int charge_skipped_scalar_arrays;
+    int prism_dialect;        /* admit PQ2_0 (142) / PTQ1_0 (143) */
+    int retain_string_arrays; /* keep string-array elements (else validated and skipped) */
+    const uint32_t *allowed_types; /* optional allowlist of tensor type ids */
+    size_t allowed_type_count;
+} prism_gguf_policy;
+/* IndexedTensor (stream.rs:185-199). */
+typedef struct {
+    uint32_t type_id, ndims;
+    uint64_t dims[4]; /* GGML order: dims[0] is the packed (column) axis */
+    uint64_t relative_offset, offset, bytes, elements;
+} prism_gguf_tensor;
+
+void prism_gguf_default_policy(prism_gguf_policy *policy);
+/* policy NULL = defaults.  Errors: PRISM_ERR_INVALID_INPUT (message in prism_gguf_last_error). */
+int prism_gguf_open(const char *path, const prism_gguf_policy *policy, prism_gguf **out);
+void prism_gguf_close(prism_gguf *g);
+const char *prism_gguf_last_error(void); /* this thread's last GGUF failure */
+int prism_gguf_summary(const prism_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset,
+                       uint64_t *tensor_count, uint64_t *metadata_count, uint64_t *remaining_budget);
+int prism_gguf_tensor_at(const prism_gguf *g, uint64_t index, const char **name, prism_gguf_tensor *info);
+int prism_gguf_find_tensor(const prism_gguf *g, const char *name, prism_gguf_tensor *info);
+/* type_id: GGUF value type (8 string, 9 array); arrays report element type and count,
+ * and retained = 0 when their elements were validated and skipped. */
+int prism_gguf_metadata_at(const prism_gguf *g, uint64_t index, const char **key, uint32_t *type_id,
+                           uint32_t *element_type_id, uint64_t *count, int *retained);
+int prism_gguf_metadata_int(const prism_gguf *g, const char *key, int64_t *out);  /* any integer or bool scalar */
+int prism_gguf_metadata_float(const prism_gguf *g, const char *key, double *out); /* F32 / F64 scalar */
+/* A string scalar (element 0) or one element of a retained string array. */
+int prism_gguf_metadata_string(const prism_gguf *g, const char *key, uint64_t element, const char **text,
+                               uint64_t *len);
+/* Copies a tensor's payload (exactly info.bytes) from the file. */
+int prism_gguf_read_tensor(const prism_gguf *g, const char *name, void *dst, uint64_t dst_len);
+/* Uploads a tensor as a weight (dims[0] = cols, dims[1] = rows, higher dims 1), through
+ * prism_hip_weight_acquire with the given key (the residency cache's identity). */
+prism_weight_id prism_hip_weight_from_gguf(prism_hip_ctx *ctx, const prism_gguf *g, const char *name, uint64_t key);
+/* Lossless PQ2 -> PTQ1 export (tools/gguf/src/export.rs:130-318) into a new file (never
+ * overwrites): requires a UINT32 general.file_type 141 or 142 and at least one PQ2
+ * tensor; general.file_type becomes 143, PQ2 tensors become PTQ1 (each block packed and
+ * re-expanded to its exact source bytes), other payloads are copied verbatim, extents
+ * re-laid in offset order at the file's alignment.  receipt (optional) receives a JSON
+ * summary with the output's SHA-256. */
+int prism_gguf_export_ptq1(const char *src_path, const char *dst_path, char *receipt, size_t receipt_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,7 @@ LIB = os.path.join(HERE, "libprism_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["quantize.hip", "matvec.hip", "mv_tiled.hip", "prefill.hip", "ffn.hip", "decode.hip", "runtime.cpp",
-           "decoder.cpp"]
+           "decoder.cpp", "gguf.cpp"]
 
 FLAGS = [
     "--offload-arch=gfx950",

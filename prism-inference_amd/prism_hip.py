@@ -107,6 +107,20 @@ def lib() -> ctypes.CDLL:
         "prism_hip_decoder_set_cache": (I, [P, U32, P, P, U64]),
         "prism_hip_decoder_set_head": (I, [P, P, P]),
         "prism_hip_decoder_generate": (I, [P, U32, U64, U32, I, P, P, P]),
+        "prism_gguf_default_policy": (None, [P]),
+        "prism_gguf_open": (I, [ctypes.c_char_p, P, P]),
+        "prism_gguf_close": (None, [P]),
+        "prism_gguf_last_error": (ctypes.c_char_p, []),
+        "prism_gguf_summary": (I, [P, P, P, P, P, P, P]),
+        "prism_gguf_tensor_at": (I, [P, U64, P, P]),
+        "prism_gguf_find_tensor": (I, [P, ctypes.c_char_p, P]),
+        "prism_gguf_metadata_at": (I, [P, U64, P, P, P, P, P]),
+        "prism_gguf_metadata_int": (I, [P, ctypes.c_char_p, P]),
+        "prism_gguf_metadata_float": (I, [P, ctypes.c_char_p, P]),
+        "prism_gguf_metadata_string": (I, [P, ctypes.c_char_p, U64, P, P]),
+        "prism_gguf_read_tensor": (I, [P, ctypes.c_char_p, P, U64]),
+        "prism_hip_weight_from_gguf": (I64, [P, P, ctypes.c_char_p, U64]),
+        "prism_gguf_export_ptq1": (I, [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_size_t]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -114,6 +128,137 @@ def lib() -> ctypes.CDLL:
         fn.argtypes = args
     _lib = L
     return L
+
+
+class GgufPolicy(ctypes.Structure):
+    """prism_gguf_policy (include/prism_hip.h): IndexPolicy, tools/gguf/src/stream.rs:44-131."""
+    _fields_ = [("allow_v2", ctypes.c_int), ("allow_zero_tensors", ctypes.c_int), ("allow_zero_metadata", ctypes.c_int),
+                ("max_file_bytes", ctypes.c_uint64), ("max_tensors", ctypes.c_uint64),
+                ("max_metadata", ctypes.c_uint64), ("metadata_budget", ctypes.c_uint64),
+                ("max_key_bytes", ctypes.c_uint64), ("max_string_bytes", ctypes.c_uint64),
+                ("max_array_string_bytes", ctypes.c_uint64), ("max_retained_string_array_bytes", ctypes.c_uint64),
+                ("max_array_items", ctypes.c_uint64), ("max_alignment", ctypes.c_uint64),
+                ("allow_positive_i32_alignment", ctypes.c_int), ("reject_nonfinite_floats", ctypes.c_int),
+                ("reject_interior_nul_keys", ctypes.c_int), ("reject_interior_nul_strings", ctypes.c_int),
+                ("kv_overhead_bytes", ctypes.c_uint64), ("string_overhead_bytes", ctypes.c_uint64),
+                ("tensor_overhead_bytes", ctypes.c_uint64), ("charge_skipped_scalar_arrays", ctypes.c_int),
+                ("prism_dialect", ctypes.c_int), ("retain_string_arrays", ctypes.c_int),
+                ("allowed_types", ctypes.POINTER(ctypes.c_uint32)), ("allowed_type_count", ctypes.c_size_t)]
+
+    @classmethod
+    def default(cls, **overrides):
+        p = cls()
+        lib().prism_gguf_default_policy(ctypes.byref(p))
+        for k, v in overrides.items():
+            setattr(p, k, v)
+        return p
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("type_id", ctypes.c_uint32), ("ndims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 4),
+                ("relative_offset", ctypes.c_uint64), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64),
+                ("elements", ctypes.c_uint64)]
+
+
+class GgufError(RuntimeError):
+    pass
+
+
+class Gguf:
+    """A validated GGUF index (prism_gguf_open); tensors and metadata in name order."""
+
+    def __init__(self, path: str, policy: GgufPolicy | None = None):
+        self._h = None
+        h = ctypes.c_void_p()
+        rc = lib().prism_gguf_open(str(path).encode(), ctypes.byref(policy) if policy is not None else None,
+                                   ctypes.byref(h))
+        if rc:
+            raise GgufError(lib().prism_gguf_last_error().decode())
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().prism_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+    def summary(self) -> dict:
+        v = ctypes.c_uint32()
+        a, d, t, m, b = (ctypes.c_uint64() for _ in range(5))
+        lib().prism_gguf_summary(self._h, *(ctypes.byref(x) for x in (v, a, d, t, m, b)))
+        return {"version": v.value, "alignment": a.value, "data_offset": d.value, "tensors": t.value,
+                "metadata": m.value, "remaining_budget": b.value}
+
+    @staticmethod
+    def _info(t: GgufTensor) -> dict:
+        return {"type_id": t.type_id, "dims": list(t.dims)[:t.ndims], "relative_offset": t.relative_offset,
+                "offset": t.offset, "bytes": t.bytes, "elements": t.elements}
+
+    def tensors(self) -> dict:
+        out = {}
+        for i in range(self.summary()["tensors"]):
+            name = ctypes.c_char_p()
+            t = GgufTensor()
+            lib().prism_gguf_tensor_at(self._h, i, ctypes.byref(name), ctypes.byref(t))
+            out[name.value.decode()] = self._info(t)
+        return out
+
+    def metadata(self) -> dict:
+        out = {}
+        for i in range(self.summary()["metadata"]):
+            key = ctypes.c_char_p()
+            ty, el = ctypes.c_uint32(), ctypes.c_uint32()
+            cnt, ret = ctypes.c_uint64(), ctypes.c_int()
+            lib().prism_gguf_metadata_at(self._h, i, ctypes.byref(key), ctypes.byref(ty), ctypes.byref(el),
+                                         ctypes.byref(cnt), ctypes.byref(ret))
+            out[key.value.decode()] = {"type": ty.value, "element_type": el.value, "count": cnt.value,
+                                       "retained": bool(ret.value)}
+        return out
+
+    def int(self, key: str) -> int:
+        v = ctypes.c_int64()
+        if lib().prism_gguf_metadata_int(self._h, key.encode(), ctypes.byref(v)):
+            raise KeyError(key)
+        return v.value
+
+    def float(self, key: str) -> float:
+        v = ctypes.c_double()
+        if lib().prism_gguf_metadata_float(self._h, key.encode(), ctypes.byref(v)):
+            raise KeyError(key)
+        return v.value
+
+    def string(self, key: str, element: int = 0) -> str:
+        p, n = ctypes.c_char_p(), ctypes.c_uint64()
+        if lib().prism_gguf_metadata_string(self._h, key.encode(), element, ctypes.byref(p), ctypes.byref(n)):
+            raise KeyError(key)
+        return ctypes.string_at(p, n.value).decode()
+
+    def read(self, name: str) -> np.ndarray:
+        t = GgufTensor()
+        if lib().prism_gguf_find_tensor(self._h, name.encode(), ctypes.byref(t)):
+            raise KeyError(name)
+        out = np.empty(t.bytes, np.uint8)
+        if lib().prism_gguf_read_tensor(self._h, name.encode(), _ptr(out), t.bytes):
+            raise GgufError(lib().prism_gguf_last_error().decode())
+        return out
+
+
+def gguf_export_ptq1(src: str, dst: str) -> dict:
+    """Lossless PQ2 -> PTQ1 export into a new file; returns the receipt."""
+    import json
+
+    buf = ctypes.create_string_buffer(1024)
+    if lib().prism_gguf_export_ptq1(str(src).encode(), str(dst).encode(), buf, len(buf)):
+        raise GgufError(lib().prism_gguf_last_error().decode())
+    return json.loads(buf.value.decode())
 
 
 def _ptr(a):
@@ -202,6 +347,13 @@ class Context:
         if wid < 0:
             self._check(int(wid))
         return int(wid)
+
+    def weight_from_gguf(self, g: "Gguf", name: str, key: int | None = None) -> int:
+        key = next(_fresh_keys) if key is None else key
+        wid = lib().prism_hip_weight_from_gguf(self._h, g._h, name.encode(), key & 0xFFFFFFFFFFFFFFFF)
+        if wid < 0:
+            self._check(int(wid))
+        return wid
 
     def weight_device(self, kind: int, cols: int, rows: int, tensor) -> int:
         nbytes = tensor.numel() * tensor.element_size()
