@@ -369,7 +369,9 @@ def main() -> int:
         for kind, rows, cols in [(ph.KIND_PTQ1, 2048, 2048), (ph.KIND_PQ2, 2048, 2048), (ph.KIND_Q2_K, HIDDEN, FFN),
                                  (ph.KIND_PTQ1, 12288, 4096), (ph.KIND_Q2_K, 12288, 4096), (ph.KIND_Q8_0, 12288, 4096),
                                  (ph.KIND_PTQ1, 151936, 4096), (ph.KIND_Q2_K, 151936, 4096),
-                                 (ph.KIND_Q8_0, 151936, 4096)]:
+                                 (ph.KIND_Q8_0, 151936, 4096), (ph.KIND_TQ1_0, 12288, 4096),
+                                 (ph.KIND_TQ2_0, 12288, 4096), (ph.KIND_TQ1_0, 151936, 4096),
+                                 (ph.KIND_TQ2_0, 151936, 4096)]:
             r = bench_matvec_kernel(ctx, kind, rows, cols, launches=100)
             log(f"matvec kind={kind} {rows}x{cols}: {r['avg_us']:.2f} us, {r['GBps']:.1f} GB/s")
             extras["matvec"].append(r)
