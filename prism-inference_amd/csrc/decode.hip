@@ -44,35 +44,43 @@ __device__ __forceinline__ void rope_freqs(DecodeState *st, uint32_t pos, const 
     st->sn[i] = sin_f32(angle);
 }
 
-// rms_norm_rope_round_f16_into::<false> (src/kernels.rs:3679-3733) of one head
-// (kHead values at src) into dst (LDS): (x * scale) * w, rotate the first `rope`
-// dimensions (index i with i + rope/2), round to binary16.  Every thread of the
-// workgroup calls it; returns error bits.
-__device__ int norm_rope_head(const float *__restrict__ src, const float *__restrict__ w, float *dst, float *tmp,
-                              double *red, const float *cs, const float *sn, uint32_t rope, float eps) {
-    const uint32_t tid = threadIdx.x;
-    const float scale = rms_scale_wg(src, kHead, eps, red);
-    int e = scale == 0.0f ? kErrNonfinite : 0;
-    if (tid < kHead) {
-        const float v = (src[tid] * scale) * w[tid];
-        tmp[tid] = v;
-        if (!finite(v)) e |= kErrNonfinite;
-    }
+// rms_norm_rope_round_f16_into::<false> (src/kernels.rs:3679-3733) of two heads at
+// once: threads 0..127 take the query head, threads 128..255 the KV head's key, one
+// element each (x, the norm weight w and the element's RoPE pair cos/sin already
+// loaded).  Per head: binary64 sum of the binary32 squares (wavefront shuffle tree,
+// then the two wavefronts in order), mean rounded to binary32, 1/sqrt(mean + eps),
+// (x * scale) * w, rotation of the first `rope` dimensions (element i with i + rope/2),
+// rounding to binary16.  The results land in dst[0] (query) and dst[1] (key).
+// Returns the thread's error bits.
+__device__ int norm_rope_pair(float x, float w, float c, float sn, uint32_t rope, float eps,
+                              float (*dst)[kHead], float (*tmp)[kHead], double *red) {
+    const uint32_t tid = threadIdx.x, which = tid >> 7, d = tid & (kHead - 1);
+    double s = static_cast<double>(x * x);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    if ((tid & 63u) == 0) red[tid >> 6] = s;
     __syncthreads();
-    if (tid < kHead) {
-        const uint32_t half = rope / 2;
-        float r;
-        if (tid < half)
-            r = tmp[tid] * cs[tid] - tmp[tid + half] * sn[tid];
-        else if (tid < rope)
-            r = tmp[tid - half] * sn[tid - half] + tmp[tid] * cs[tid - half];
-        else
-            r = tmp[tid];
-        if (!finite(r)) e |= kErrNonfinite;
-        r = round_f16(r);
-        if (!finite(r)) e |= kErrNonfinite;
-        dst[tid] = r;
-    }
+    const double t = (0.0 + red[2 * which]) + red[2 * which + 1];
+    const float mean = static_cast<float>(t / static_cast<double>(kHead));
+    float scale = 1.0f / __builtin_sqrtf(mean + eps);
+    scale = (finite(scale) && scale > 0.0f) ? scale : 0.0f;
+    int e = scale == 0.0f ? kErrNonfinite : 0;
+    const float v = (x * scale) * w;
+    tmp[which][d] = v;
+    if (!finite(v)) e |= kErrNonfinite;
+    __syncthreads();
+    const uint32_t half = rope / 2;
+    float r;
+    if (d < half)
+        r = tmp[which][d] * c - tmp[which][d + half] * sn;
+    else if (d < rope)
+        r = tmp[which][d - half] * sn + tmp[which][d] * c;
+    else
+        r = tmp[which][d];
+    if (!finite(r)) e |= kErrNonfinite;
+    r = round_f16(r);
+    if (!finite(r)) e |= kErrNonfinite;
+    dst[which][d] = r;
     __syncthreads();
     return e;
 }
@@ -81,133 +89,194 @@ __device__ int norm_rope_head(const float *__restrict__ src, const float *__rest
 // normalizes and rotates its query head and its KV head's current key, the first
 // workgroup of every KV head appends the current key and value to the binary16
 // caches, and thread t scores position chunk*256 + t <= pos:
-// f16_dot(q, k) * (1/sqrt(head)) with the current key taken from registers.
+// f16_dot(q, k) * (1/sqrt(head)) with the current key taken from LDS.  Every global
+// read that does not depend on another (the cached key row, the head inputs, norm
+// weights, RoPE factors, the value to append) is issued before the first is used.
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
-    __shared__ float qv[kHead], kv[kHead], tmp[kHead];
-    __shared__ double red[16];
+    __shared__ float hv[2][kHead], tmp[2][kHead];  // [0] query, [1] current key
+    __shared__ double red[4];
     const uint32_t tid = threadIdx.x, h = blockIdx.x, chunk = blockIdx.y;
     const uint32_t group = p.heads / p.kv_heads, kh = h / group;
     const uint32_t qw = p.heads * kHead, kw = p.kv_heads * kHead;
-    const uint32_t pos = p.state->pos;
+    // Every load that does not need the position is issued before the position itself
+    // is waited for: the normalization's inputs first (memory counters complete in
+    // issue order, so the norm waits only for these), then the cached key row of this
+    // thread's position (row 0 past the cache, never used).
+    const uint32_t which = tid >> 7, d = tid & (kHead - 1);
+    const float x = p.qkv[which ? qw + kh * kHead + d : h * kHead + d];
+    // Both norm weights are read: selecting the pointer per thread would read it from
+    // the kernel-argument memory with a vector load, one more round trip.
+    const float qn = p.q_norm[d], kn = p.k_norm[d], nw = which ? kn : qn;
+    const uint32_t half = p.rope / 2, j = d < half ? d : d - half;
+    const bool rot = d < p.rope;
+    const float c = rot ? p.state->cs[j] : 1.0f, sn = rot ? p.state->sn[j] : 0.0f;
+    const bool append = h % group == 0 && chunk == 0 && tid < kHead;
+    const float vin = append ? p.qkv[qw + kw + kh * kHead + tid] : 0.0f;
+    const uint32_t t = chunk * kScoreChunk + tid, tr = t < p.max_tokens ? t : 0;
+    uint4 kr[kHead / 8];
+    const uint4 *krow = reinterpret_cast<const uint4 *>(p.kcache + static_cast<size_t>(tr) * kw + kh * kHead);
+#pragma unroll
+    for (uint32_t cc = 0; cc < kHead / 8; ++cc) kr[cc] = krow[cc];
+    const uint32_t pos = vector_load(&p.state->pos);
+
+    // The norm needs no position; the exits come after it, so that no load above is
+    // moved below them.
+    int e = norm_rope_pair(x, nw, c, sn, p.rope, p.eps, hv, tmp, red);
     if (pos >= p.max_tokens) {  // uniform: every workgroup leaves
         if (tid == 0 && h == 0 && chunk == 0) raise_error(p.err, kErrInput);
         return;
     }
-    const float *cs = p.state->cs, *sn = p.state->sn;
-    int e = norm_rope_head(p.qkv + h * kHead, p.q_norm, qv, tmp, red, cs, sn, p.rope, p.eps);
-    e |= norm_rope_head(p.qkv + qw + kh * kHead, p.k_norm, kv, tmp, red, cs, sn, p.rope, p.eps);
-    if (h % group == 0 && chunk == 0 && tid < kHead) {
+    if (chunk * kScoreChunk > pos) return;  // no position of this chunk is scored yet
+    const float *qv = hv[0], *kv = hv[1];
+    if (append) {
         const size_t at = static_cast<size_t>(pos) * kw + kh * kHead + tid;
-        const float v = round_f16(p.qkv[qw + kw + kh * kHead + tid]);
+        const float v = round_f16(vin);
         if (!finite(v)) e |= kErrNonfinite;
         p.kcache[at] = f16_bits(kv[tid]);
         p.vcache[at] = f16_bits(v);
     }
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHead));
-    const uint32_t t = chunk * kScoreChunk + tid;
     if (t <= pos) {
         // Four binary64 partial sums shorten the dependent chain; the terms are binary16
         // x binary16 products (exact in binary32) whose binary64 sums are exact, so the
         // split changes no bit of f16_dot's sequential sum.
         double s[4] = {0.0, 0.0, 0.0, 0.0};
         if (t == pos) {
-            for (uint32_t d = 0; d < kHead; d += 4)
+            for (uint32_t dd = 0; dd < kHead; dd += 4)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) s[j] += static_cast<double>(qv[d + j] * kv[d + j]);
+                for (int q = 0; q < 4; ++q) s[q] += static_cast<double>(qv[dd + q] * kv[dd + q]);
         } else {
-            const uint4 *k = reinterpret_cast<const uint4 *>(p.kcache + static_cast<size_t>(t) * kw + kh * kHead);
-            uint4 w[kHead / 8];
 #pragma unroll
-            for (uint32_t c = 0; c < kHead / 8; ++c) w[c] = k[c];
+            for (uint32_t cc = 0; cc < kHead / 8; ++cc) {
+                const uint32_t w4[4] = {kr[cc].x, kr[cc].y, kr[cc].z, kr[cc].w};
 #pragma unroll
-            for (uint32_t c = 0; c < kHead / 8; ++c) {
-                const uint32_t w4[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    s[j] += static_cast<double>(qv[8 * c + 2 * j] * h2f(w4[j] & 0xffffu));
-                    s[j] += static_cast<double>(qv[8 * c + 2 * j + 1] * h2f(w4[j] >> 16));
+                for (int q = 0; q < 4; ++q) {
+                    s[q] += static_cast<double>(qv[8 * cc + 2 * q] * h2f(w4[q] & 0xffffu));
+                    s[q] += static_cast<double>(qv[8 * cc + 2 * q + 1] * h2f(w4[q] >> 16));
                 }
             }
         }
         p.scores[static_cast<size_t>(h) * p.max_tokens + t] = static_cast<float>((s[0] + s[1]) + (s[2] + s[3])) * scale;
     }
-    if (e && tid == 0) raise_error(p.err, e);
+    if (e) raise_error(p.err, e);  // any element: an overflow can hit one element only
 }
 
-// Grid (heads, kHead / kValueDims), 1024 threads.  softmax_round_f16 (src/kernels.rs:
-// 4431-4462) of the head's pos+1 scores -- every workgroup recomputes it -- then
-// source_value_tile (src/kernels.rs:2971-3011) for this workgroup's kValueDims
-// dimensions: out[d] = sum_t p_t v_t[d] in binary64.  Each term is a binary16 x
-// binary16 product, exact in binary32, and a binary64 sum of such terms is exact
-// unless they span more than 53 bits of magnitude (probabilities below 2^-24 are
-// binary16 zeros), so summing the positions in 128 interleaved groups and then the
-// groups does not change the result.
+// Positions of the value reduction whose rows are loaded before the softmax (per
+// thread: kValueAhead positions g, g + kValueGroups, ...), so that a context of up
+// to kValueAhead * kValueGroups tokens costs one memory round trip.
+constexpr uint32_t kValueAhead = 16;
+
+// Grid (heads, kHead / kValueDims), 1024 threads; SPT scores per thread
+// (SPT * 1024 >= max_tokens).  softmax_round_f16 (src/kernels.rs:4431-4462) of the
+// head's pos+1 scores -- every workgroup recomputes it -- then source_value_tile
+// (src/kernels.rs:2971-3011) for this workgroup's kValueDims dimensions:
+// out[d] = sum_t p_t v_t[d] in binary64.  Each term is a binary16 x binary16
+// product, exact in binary32, and a binary64 sum of such terms is exact unless they
+// span more than 53 bits of magnitude (probabilities below 2^-24 are binary16
+// zeros), so summing the positions in 128 interleaved groups and then the groups
+// does not change the result.  The scores and the first value rows are read
+// unconditionally (clamped to the cache, masked afterwards) before the position is
+// waited for, so the kernel's inputs arrive in one memory round trip.
+template <uint32_t SPT>
 __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     __shared__ float redf[16];
     __shared__ double redd[16];
     __shared__ float prob[kMaxTokens];
     __shared__ double acc[16][kValueDims];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
+    constexpr uint32_t nw = 16;  // wavefronts of the 1024-thread workgroup
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t h = blockIdx.x, d0 = blockIdx.y * kValueDims;
     const uint32_t kh = h / (p.heads / p.kv_heads), kw = p.kv_heads * kHead;
-    const uint32_t pos = p.state->pos;
+    const uint32_t last = p.max_tokens - 1;
+    const float *sc = p.scores + static_cast<size_t>(h) * p.max_tokens;
+    float sv[SPT];
+#pragma unroll
+    for (uint32_t k = 0; k < SPT; ++k) {
+        const uint32_t i = tid + k * 1024u;
+        sv[k] = sc[i < last ? i : last];
+    }
+    // Thread (g, q): positions g, g+128, ... of dimensions d0+4q .. d0+4q+3.
+    const uint32_t g = tid / (kValueDims / 4), q = tid % (kValueDims / 4);
+    const uint16_t *vb = p.vcache + kh * kHead + d0 + 4 * q;
+    uint2 w[kValueAhead];
+#pragma unroll
+    for (uint32_t k = 0; k < kValueAhead; ++k) {
+        const uint32_t i = g + k * kValueGroups;
+        w[k] = *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i < last ? i : last) * kw);
+    }
+    const uint32_t pos = vector_load(&p.state->pos);
     if (pos >= p.max_tokens) return;  // reported by the score kernel
     const uint32_t n = pos + 1;
-    const float *sc = p.scores + static_cast<size_t>(h) * p.max_tokens;
+#pragma unroll
+    for (uint32_t k = 0; k < kValueAhead; ++k)
+        if (g + k * kValueGroups >= n) w[k] = make_uint2(0, 0);
     float m = -__builtin_inff();
     bool bad = false;
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const float v = sc[i];
-        bad |= (v != v) || v == __builtin_inff();
-        m = fmaxf(m, v);
+#pragma unroll
+    for (uint32_t k = 0; k < SPT; ++k) {
+        if (tid + k * 1024u < n) {
+            bad |= (sv[k] != sv[k]) || sv[k] == __builtin_inff();
+            m = fmaxf(m, sv[k]);
+        }
     }
 #pragma unroll
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
     if (lane == 0) redf[wave] = m;
     __syncthreads();
     m = redf[0];
-    for (uint32_t w = 1; w < nw; ++w) m = fmaxf(m, redf[w]);
+    for (uint32_t v = 1; v < nw; ++v) m = fmaxf(m, redf[v]);
     if (__syncthreads_or(bad) || !finite(m)) {
         if (tid == 0 && blockIdx.y == 0) raise_error(p.err, kErrNonfinite);
         return;
     }
     double tot = 0.0;
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const float e = exp_f32(sc[i] - m);
-        prob[i] = e;
-        tot += static_cast<double>(e);
+#pragma unroll
+    for (uint32_t k = 0; k < SPT; ++k) {
+        if (tid + k * 1024u < n) {
+            const float e = exp_f32(sv[k] - m);
+            sv[k] = e;
+            tot += static_cast<double>(e);
+        }
     }
 #pragma unroll
     for (int k = 32; k >= 1; k >>= 1) tot += __shfl_xor(tot, k);
     if (lane == 0) redd[wave] = tot;
     __syncthreads();
     tot = 0.0;
-    for (uint32_t w = 0; w < nw; ++w) tot += redd[w];
+    for (uint32_t v = 0; v < nw; ++v) tot += redd[v];
     const float inv = static_cast<float>(1.0 / tot);
-    for (uint32_t i = tid; i < n; i += blockDim.x) prob[i] = round_f16(prob[i] * inv);
+#pragma unroll
+    for (uint32_t k = 0; k < SPT; ++k) {
+        const uint32_t i = tid + k * 1024u;
+        if (i < n) prob[i] = round_f16(sv[k] * inv);
+    }
     __syncthreads();
-    // Thread (g, q): positions g, g+128, ... of dimensions d0+4q .. d0+4q+3, eight rows
-    // loaded per batch before any is used.
-    const uint32_t g = tid / (kValueDims / 4), q = tid % (kValueDims / 4);
     double a[4] = {0.0, 0.0, 0.0, 0.0};
-    const uint16_t *vb = p.vcache + kh * kHead + d0 + 4 * q;
-    for (uint32_t i0 = g; i0 < n; i0 += 8 * kValueGroups) {
-        uint2 w[8];
+    auto accumulate = [&](const uint2 &r, float pr) {
+        a[0] += static_cast<double>(pr * h2f(r.x & 0xffffu));
+        a[1] += static_cast<double>(pr * h2f(r.x >> 16));
+        a[2] += static_cast<double>(pr * h2f(r.y & 0xffffu));
+        a[3] += static_cast<double>(pr * h2f(r.y >> 16));
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < kValueAhead; ++k) {
+        const uint32_t i = g + k * kValueGroups;
+        accumulate(w[k], i < n ? prob[i] : 0.0f);
+    }
+    // Longer contexts: the remaining positions, eight rows loaded per batch before any
+    // is used.
+    for (uint32_t i0 = g + kValueAhead * kValueGroups; i0 < n; i0 += 8 * kValueGroups) {
+        uint2 r[8];
         float pr[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t i = i0 + k * kValueGroups;
             const bool in = i < n;
-            w[k] = in ? *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i) * kw) : make_uint2(0, 0);
+            r[k] = in ? *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i) * kw) : make_uint2(0, 0);
             pr[k] = in ? prob[i] : 0.0f;
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            a[0] += static_cast<double>(pr[k] * h2f(w[k].x & 0xffffu));
-            a[1] += static_cast<double>(pr[k] * h2f(w[k].x >> 16));
-            a[2] += static_cast<double>(pr[k] * h2f(w[k].y & 0xffffu));
-            a[3] += static_cast<double>(pr[k] * h2f(w[k].y >> 16));
-        }
+        for (int k = 0; k < 8; ++k) accumulate(r[k], pr[k]);
     }
     // A wavefront holds eight groups of the same eight quads (lane = 8 * group + quad):
     // fold them with lane shuffles, then the wavefronts through LDS.
@@ -221,7 +290,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     __syncthreads();
     if (tid < kValueDims) {
         double t = acc[0][tid];
-        for (uint32_t w = 1; w < nw; ++w) t += acc[w][tid];
+        for (uint32_t v = 1; v < nw; ++v) t += acc[v][tid];
         const float o = static_cast<float>(t);
         p.out[h * kHead + d0 + tid] = o;
         if (!finite(o)) raise_error(p.err, kErrNonfinite);
@@ -371,11 +440,19 @@ size_t argmax_scratch_bytes() { return (sizeof(float) + sizeof(uint32_t)) * kArg
 
 int launch_attention(const AttnArgs &a) {
     if (a.head_dim != kHead || a.rope > kHead || a.rope % 2 || a.kv_heads == 0 || a.heads % a.kv_heads ||
-        a.max_tokens > kMaxTokens)
+        a.max_tokens == 0 || a.max_tokens > kMaxTokens)
         return -2;
     const dim3 sg(a.heads, (a.max_tokens + kScoreChunk - 1) / kScoreChunk);
     hipLaunchKernelGGL(k_attn_scores, sg, dim3(256), 0, a.stream, a);
-    hipLaunchKernelGGL(k_attn_values, dim3(a.heads, kHead / kValueDims), dim3(1024), 0, a.stream, a);
+    const dim3 vg(a.heads, kHead / kValueDims), vb(1024);
+    if (a.max_tokens <= 1024)
+        hipLaunchKernelGGL(k_attn_values<1>, vg, vb, 0, a.stream, a);
+    else if (a.max_tokens <= 2048)
+        hipLaunchKernelGGL(k_attn_values<2>, vg, vb, 0, a.stream, a);
+    else if (a.max_tokens <= 4096)
+        hipLaunchKernelGGL(k_attn_values<4>, vg, vb, 0, a.stream, a);
+    else
+        hipLaunchKernelGGL(k_attn_values<8>, vg, vb, 0, a.stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

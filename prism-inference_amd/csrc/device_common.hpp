@@ -124,6 +124,13 @@ __device__ __forceinline__ float swiglu_one(float gate, float up, uint64_t i, ui
     return up * silu;
 }
 
+// A word read with a vector load.  The compiler turns a uniform read from memory that
+// the kernel does not write into a scalar load, and scalar loads complete out of
+// order: every later wait for a kernel argument would then wait for it as well.
+__device__ __forceinline__ uint32_t vector_load(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __device__ __forceinline__ void raise_error(int *flag, int bits) {
     if (flag) __hip_atomic_fetch_or(flag, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

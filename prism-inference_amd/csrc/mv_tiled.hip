@@ -1234,6 +1234,11 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
     }
 }
 
+// Split-mode workgroups hold at most eight wavefronts: the bound leaves each thread up
+// to 256 registers, room for a quantizing prologue's input held in registers next to
+// the weights in flight.
+constexpr uint32_t kSplitMaxWaves = 8, kSplitMaxThreads = 64 * kSplitMaxWaves;
+
 // Small matrices: a workgroup owns rw = 64/lpr rows of a tile; its ks wavefronts
 // (per matrix) and the lpr lane groups of each wavefront split the row's units
 // (lane group c of wavefront w takes units w*lpr+c, +ks*lpr, ...).  Each unit's
@@ -1245,7 +1250,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
 // The first unit's weight loads are issued before the prologue so that their
 // latency overlaps it.
 template <Op O, bool QUANT, int NMAT>
-__global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
+__global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr uint32_t UB = unit_bytes<O>();
     constexpr int TPU = terms_per_unit<O>();
@@ -1272,16 +1277,65 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
 
     const __amdgpu_buffer_rsrc_t rs =
         make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
-    Raw<O> A, B;
+    // A quantizing prologue whose input fits in the wavefronts' registers reads it (and
+    // the norm weights) first, before the weights, in one round trip.
+    using Held = HeldInput<act_is_q8k<O>(), 2>;
+    const bool held = QUANT && Held::fits(p.cols, nwaves);
+    Held hin;
+    if (QUANT && held) {
+        const float *x = static_cast<const float *>(p.act);
+        hin.load(x, p.norm_w ? p.norm_w : x, p.cols, wave, nwaves, lane);
+    }
+    // When every lane takes at most kPre units (the decode-sized projections), all of
+    // them are loaded here, ahead of the prologue, and the main loop issues no load.
+    // Units past the row fall outside the buffer resource and read as zeros.
+    // W[0] and W[1] double as the ping-pong pair of the streaming loop otherwise.
+    // Larger units keep the streaming loop only (their registers are spoken for).
+    constexpr uint32_t kPre = UB <= 36 ? 3 : 2;
+    const uint32_t cmax = (nu + kt - 1) / kt;  // most units any lane takes
+    const bool pre = UB <= 36 && cmax <= kPre;
+    Raw<O> W[kPre];
     uint32_t u = kk;
-    if (u < nu) load_unit<O>(A, rs, u * trp * UB, trp, tr);
+    if (pre) {
+#pragma unroll
+        for (uint32_t j = 0; j < kPre; ++j) load_unit<O>(W[j], rs, (kk + j * kt) * trp * UB, trp, tr);
+    } else if (u < nu) {
+        load_unit<O>(W[0], rs, u * trp * UB, trp, tr);
+    }
+    // The folding lanes' residual is read now, so that its latency hides behind the
+    // prologue and the main loop instead of following the fold.
+    const bool folder = mw == 0 && lane < rw;
+    const bool valid = tr < trows;
+    const size_t row = static_cast<size_t>(tile) * kTile + tr;
+    const float resid = (NMAT == 1 && p.residual && folder && valid) ? p.residual[row] : 0.0f;
 
     // ---- prologue: stage the activation in LDS -------------------------------------
     if constexpr (QUANT) {
         const float *x = static_cast<const float *>(p.act);
         auto *blocks = reinterpret_cast<typename ActBlock<O>::type *>(smem);
         int e;
-        if (p.norm_w) {
+        if (held) {
+            // RMSNorm fused ahead of the quantizer (as below), from the held registers:
+            // lane sums in element order, the wavefront's shuffle tree, then the
+            // wavefronts in order, in binary64 (rms_norm_scale_inner's order up to the
+            // binary64 additions).
+            float scale = 1.0f;
+            e = 0;
+            hin.mask(p.cols, wave, nwaves, lane);
+            if (p.norm_w) {
+                double s = hin.sumsq();
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+                if (lane == 0) red[wave] = s;
+                __syncthreads();
+                double t = 0.0;
+                for (uint32_t v = 0; v < nwaves; ++v) t += red[v];
+                const float mean = static_cast<float>(t / static_cast<double>(p.cols));
+                scale = 1.0f / __builtin_sqrtf(mean + p.eps);
+                if (!(finite(scale) && scale > 0.0f)) e = kErrNonfinite;
+            }
+            if (!e) e = hin.quantize(p.cols, p.qcontract, blocks, wave, nwaves, lane, p.norm_w != nullptr, scale);
+        } else if (p.norm_w) {
             // RMSNorm fused ahead of the quantizer: every workgroup normalizes the whole
             // input itself, so the projection stays one launch.
             const float scale = rms_scale_wg(x, p.cols, p.eps, red);
@@ -1322,20 +1376,23 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
 #pragma unroll
         for (int j = 0; j < TPU; ++j) terms[r * stride + v * TPU + j] = t[j];
     };
-    while (u + kt < nu) {
-        load_unit<O>(B, rs, (u + kt) * trp * UB, trp, tr);
-        step(A, u);
-        if (u + 2 * kt < nu) load_unit<O>(A, rs, (u + 2 * kt) * trp * UB, trp, tr);
-        step(B, u + kt);
-        u += 2 * kt;
+    if (pre) {
+#pragma unroll
+        for (uint32_t j = 0; j < kPre; ++j)
+            if (kk + j * kt < nu) step(W[j], kk + j * kt);
+    } else {
+        while (u + kt < nu) {
+            load_unit<O>(W[1], rs, (u + kt) * trp * UB, trp, tr);
+            step(W[0], u);
+            if (u + 2 * kt < nu) load_unit<O>(W[0], rs, (u + 2 * kt) * trp * UB, trp, tr);
+            step(W[1], u + kt);
+            u += 2 * kt;
+        }
+        if (u < nu) step(W[0], u);
     }
-    if (u < nu) step(A, u);
     __syncthreads();
 
     // ---- fold in unit order and epilogue ---------------------------------------------
-    const bool folder = mw == 0 && lane < rw;
-    const bool valid = tr < trows;
-    const size_t row = static_cast<size_t>(tile) * kTile + tr;
     float o = 0.0f;
     if (folder) {
         Chain<O> ch;
@@ -1345,7 +1402,7 @@ __global__ __launch_bounds__(1024) void k_mv_split(MvParams p) {
     }
     if constexpr (NMAT == 1) {
         if (folder && valid) {
-            if (p.residual) o = o + p.residual[row];
+            if (p.residual) o = o + resid;
             p.out[row] = o;
             if (!finite(o)) raise_error(p.err, kErrNonfinite);
         }
@@ -1405,10 +1462,10 @@ bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t 
     uint32_t lpr = 1;
     while (lpr < 8 && tiles * lpr < cus && lpr * 2 <= nu) lpr *= 2;
     uint32_t ks = 1;
-    while (ks * 2 * nmat <= 16 && ks * 2 * lpr <= nu && tiles * lpr * ks * 2 * nmat <= 8ull * cus) ks *= 2;
+    while (ks * 2 * nmat <= kSplitMaxWaves && ks * 2 * lpr <= nu && tiles * lpr * ks * 2 * nmat <= 8ull * cus) ks *= 2;
     // A quantizing prologue wants several wavefronts per workgroup: trade lane groups
     // for wavefronts while the workgroup has fewer than four.
-    while (quant && ks * nmat < 4 && lpr > 1 && ks * 2 * nmat <= 16) {
+    while (quant && ks * nmat < 4 && lpr > 1 && ks * 2 * nmat <= kSplitMaxWaves) {
         lpr /= 2;
         ks *= 2;
     }

@@ -254,6 +254,106 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
     return e;
 }
 
+// A workgroup's input held in registers for the quantizing prologue: wavefront w
+// holds the block sets w, w + nwaves, ... (at most S of them) of the f32 vector x and,
+// for an RMSNorm ahead of the quantizer, the matching norm weights.  load() issues
+// every read at once (at the top of a kernel, before anything else waits on memory);
+// sumsq() and quantize() then work from registers, so the prologue costs one memory
+// round trip instead of one for the norm's sum and another for the quantizer.  The
+// quantized result is bit-identical to quantize_prologue's for the same scale.
+template <bool Q8K, uint32_t S>
+struct HeldInput {
+    static constexpr uint32_t per_set = Q8K ? 4 : 32, blk = Q8K ? 256 : 32;
+    float v[S][16];
+    float w[S][16];
+
+    // Block sets of `cols` inputs and whether nwaves wavefronts can hold them all.
+    __host__ __device__ static uint32_t sets(uint32_t cols) { return (cols / blk + per_set - 1) / per_set; }
+    __host__ __device__ static bool fits(uint32_t cols, uint32_t nwaves) {
+        return (sets(cols) + nwaves - 1) / nwaves <= S;
+    }
+
+    // nw: the norm weights, or x itself when there is no norm (read, never used).
+    // Lanes past the last block read the last block (zeroed afterwards), so the loads
+    // carry no branches for the compiler to wait on.
+    __device__ __forceinline__ void load(const float *__restrict__ x, const float *__restrict__ nw, uint32_t cols,
+                                         uint32_t wave, uint32_t nwaves, uint32_t lane) {
+        const uint32_t nb = cols / blk;
+        const uint32_t lb = Q8K ? lane >> 4 : lane >> 1, lo = Q8K ? 16u * (lane & 15u) : 16u * (lane & 1u);
+#pragma unroll
+        for (uint32_t j = 0; j < S; ++j) {
+            const uint32_t b = per_set * (wave + j * nwaves) + lb, bc = b < nb ? b : nb - 1;
+            const float4 *xs = reinterpret_cast<const float4 *>(x + static_cast<size_t>(blk) * bc + lo);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 q = xs[i];
+                v[j][4 * i] = q.x;
+                v[j][4 * i + 1] = q.y;
+                v[j][4 * i + 2] = q.z;
+                v[j][4 * i + 3] = q.w;
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < S; ++j) {
+            const uint32_t b = per_set * (wave + j * nwaves) + lb, bc = b < nb ? b : nb - 1;
+            const float4 *ws = reinterpret_cast<const float4 *>(nw + static_cast<size_t>(blk) * bc + lo);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 q = ws[i];
+                w[j][4 * i] = q.x;
+                w[j][4 * i + 1] = q.y;
+                w[j][4 * i + 2] = q.z;
+                w[j][4 * i + 3] = q.w;
+            }
+        }
+    }
+
+    // Zeroes the lanes past the last block.  Called when the values are first used, not
+    // in load(): a use right after the reads would wait for them there.
+    __device__ __forceinline__ void mask(uint32_t cols, uint32_t wave, uint32_t nwaves, uint32_t lane) {
+        const uint32_t nb = cols / blk, lb = Q8K ? lane >> 4 : lane >> 1;
+#pragma unroll
+        for (uint32_t j = 0; j < S; ++j)
+            if (per_set * (wave + j * nwaves) + lb >= nb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[j][i] = 0.0f;
+    }
+
+    // This lane's binary64 sum of the binary32 squares of its inputs (after mask()).
+    __device__ __forceinline__ double sumsq() const {
+        double s = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < S; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s += static_cast<double>(v[j][i] * v[j][i]);
+        return s;
+    }
+
+    // Quantizes the held sets (after mask()) into `o` (LDS); `norm` applies the RMSNorm
+    // (x * scale) * w first.  Returns the error bits seen.
+    template <typename OutPtr>
+    __device__ __forceinline__ int quantize(uint32_t cols, int contract, OutPtr o, uint32_t wave, uint32_t nwaves,
+                                            uint32_t lane, bool norm, float scale) {
+        const uint32_t nb = cols / blk;
+        const uint32_t lb = Q8K ? lane >> 4 : lane >> 1;
+        int e = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < S; ++j) {
+            const uint32_t b0 = per_set * (wave + j * nwaves);
+            if (b0 >= nb) break;
+            const uint32_t n = nb - b0 < per_set ? nb - b0 : per_set;
+            if (norm && lb < n)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[j][i] = (v[j][i] * scale) * w[j][i];
+            if constexpr (Q8K)
+                e |= q8k_process(v[j], n, contract, o + b0, lane);
+            else
+                e |= q8_0_process(v[j], n, contract, o + b0, lane);
+        }
+        return e;
+    }
+};
+
 // RMSNorm scale of x[0..n) over a whole workgroup (rms_norm_scale_inner,
 // src/kernels.rs:3823-3878): binary64 sum of the binary32 squares, mean rounded to
 // binary32, 1 / sqrt(mean + eps).  Threads sum strided elements, wavefronts reduce
@@ -262,10 +362,19 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
 // sum.  `red` is LDS scratch for 16 doubles.  Returns a non-positive or non-finite
 // scale as 0 (the caller raises the error); every thread gets the same value.
 __device__ __forceinline__ float rms_scale_wg(const float *__restrict__ x, uint32_t n, float eps, double *red) {
+    // Eight strided loads in flight before the first is summed: the reduction costs
+    // one memory round trip per eight elements of a thread, not one per element.
     double s = 0.0;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
-        s += static_cast<double>(v * v);
+    for (uint32_t i0 = threadIdx.x; i0 < n; i0 += 8 * blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t i = i0 + k * blockDim.x;
+            v[k] = i < n ? x[i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (i0 + k * blockDim.x < n) s += static_cast<double>(v[k] * v[k]);
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
