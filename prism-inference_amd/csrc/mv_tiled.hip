@@ -1249,7 +1249,9 @@ constexpr uint32_t kSplitMaxWaves = 8, kSplitMaxThreads = 64 * kSplitMaxWaves;
 // up (ks..2ks-1) share the activation and the epilogue writes SwiGLU(gate, up).
 // The first unit's weight loads are issued before the prologue so that their
 // latency overlaps it.
-template <Op O, bool QUANT, int NMAT>
+// HELD (QUANT only): 8 or 16 input values held per lane (HeldInput), 0 to stream the
+// input through the quantizer instead.
+template <Op O, bool QUANT, int NMAT, int HELD>
 __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr uint32_t UB = unit_bytes<O>();
@@ -1278,11 +1280,12 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     const __amdgpu_buffer_rsrc_t rs =
         make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
     // A quantizing prologue whose input fits in the wavefronts' registers reads it (and
-    // the norm weights) first, before the weights, in one round trip.
-    using Held = HeldInput<act_is_q8k<O>(), 2>;
-    const bool held = QUANT && Held::fits(p.cols, nwaves);
+    // the norm weights) first, before the weights, in one round trip.  The holder is
+    // chosen at compile time: a branch around these loads would make the prologue wait
+    // for the weights' loads too.
+    using Held = HeldInput<act_is_q8k<O>(), HELD == 8 ? 8 : 16, HELD == 8 ? 1 : 2>;
     Held hin;
-    if (QUANT && held) {
+    if constexpr (QUANT && HELD != 0) {
         const float *x = static_cast<const float *>(p.act);
         hin.load(x, p.norm_w ? p.norm_w : x, p.cols, wave, nwaves, lane);
     }
@@ -1314,27 +1317,28 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
         const float *x = static_cast<const float *>(p.act);
         auto *blocks = reinterpret_cast<typename ActBlock<O>::type *>(smem);
         int e;
-        if (held) {
-            // RMSNorm fused ahead of the quantizer (as below), from the held registers:
-            // lane sums in element order, the wavefront's shuffle tree, then the
-            // wavefronts in order, in binary64 (rms_norm_scale_inner's order up to the
-            // binary64 additions).
+        // RMSNorm fused ahead of the quantizer (as below), from the held registers:
+        // lane sums in element order, the wavefront's butterfly, then the wavefronts in
+        // order, in binary64 (rms_norm_scale_inner's order up to the binary64 additions).
+        auto held_prologue = [&](auto &hin) -> int {
             float scale = 1.0f;
-            e = 0;
             hin.mask(p.cols, wave, nwaves, lane);
             if (p.norm_w) {
-                double s = hin.sumsq();
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+                const double s = wave_sum(hin.sumsq());
                 if (lane == 0) red[wave] = s;
                 __syncthreads();
                 double t = 0.0;
-                for (uint32_t v = 0; v < nwaves; ++v) t += red[v];
+#pragma unroll
+                for (uint32_t v = 0; v < kSplitMaxWaves; ++v)
+                    if (v < nwaves) t += red[v];
                 const float mean = static_cast<float>(t / static_cast<double>(p.cols));
                 scale = 1.0f / __builtin_sqrtf(mean + p.eps);
-                if (!(finite(scale) && scale > 0.0f)) e = kErrNonfinite;
+                if (!(finite(scale) && scale > 0.0f)) return kErrNonfinite;
             }
-            if (!e) e = hin.quantize(p.cols, p.qcontract, blocks, wave, nwaves, lane, p.norm_w != nullptr, scale);
+            return hin.quantize(p.cols, p.qcontract, blocks, wave, nwaves, lane, p.norm_w != nullptr, scale);
+        };
+        if constexpr (HELD != 0) {
+            e = held_prologue(hin);
         } else if (p.norm_w) {
             // RMSNorm fused ahead of the quantizer: every workgroup normalizes the whole
             // input itself, so the projection stays one launch.
@@ -1512,13 +1516,30 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.ks = pl.ks;
     p.lpr = pl.lpr;
     const dim3 grid(static_cast<uint32_t>(tiles * pl.lpr)), block(64 * pl.ks * nmat);
+    // Held prologue input: eight values per lane when one chunk per wavefront covers the
+    // input, else sixteen in up to two chunks (each chunk's block reductions are a fixed
+    // cost, so fewer chunks win over fewer values), else streamed.
+    const uint32_t nwaves = pl.ks * nmat;
+    constexpr bool q8k = act_is_q8k<O>();
+    const int held = HeldInput<q8k, 8, 1>::fits(p.cols, nwaves) ? 8 : HeldInput<q8k, 16, 2>::fits(p.cols, nwaves) ? 16 : 0;
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, pl.lds, a.stream, p); };
     if (nmat == 2) {
         if (!quant) return -2;
-        hipLaunchKernelGGL((k_mv_split<O, true, 2>), grid, block, pl.lds, a.stream, p);
+        if (held == 8)
+            go(k_mv_split<O, true, 2, 8>);
+        else if (held == 16)
+            go(k_mv_split<O, true, 2, 16>);
+        else
+            go(k_mv_split<O, true, 2, 0>);
     } else if (quant) {
-        hipLaunchKernelGGL((k_mv_split<O, true, 1>), grid, block, pl.lds, a.stream, p);
+        if (held == 8)
+            go(k_mv_split<O, true, 1, 8>);
+        else if (held == 16)
+            go(k_mv_split<O, true, 1, 16>);
+        else
+            go(k_mv_split<O, true, 1, 0>);
     } else {
-        hipLaunchKernelGGL((k_mv_split<O, false, 1>), grid, block, pl.lds, a.stream, p);
+        go(k_mv_split<O, false, 1, 0>);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -11,6 +11,8 @@
 // only 4 (Q8_K) or 1 (Q8_0) DPP steps deep.
 #pragma once
 
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -158,14 +160,18 @@ __device__ __forceinline__ int q8_0_process(const float (&v)[16], uint32_t nbloc
     uint32_t packed[4] = {0, 0, 0, 0};
     int qsum = 0;
     bool range = false;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float p = v[i] * inv;
-        const float r = pinned ? __builtin_rintf(p) : __builtin_roundf(p);
+    auto code = [&](int i, float r) {
         range |= !(r >= -127.0f && r <= 127.0f);
         const int q = static_cast<int>(r);
         qsum += q;
         packed[i >> 2] |= (static_cast<uint32_t>(q) & 0xffu) << (8 * (i & 3));
+    };
+    if (pinned) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) code(i, __builtin_rintf(v[i] * inv));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) code(i, __builtin_roundf(v[i] * inv));
     }
     qsum += dpp_i<kDppQuadSwap>(qsum);
     const float scale = round_f16(d);
@@ -254,38 +260,64 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
     return e;
 }
 
-// A workgroup's input held in registers for the quantizing prologue: wavefront w
-// holds the block sets w, w + nwaves, ... (at most S of them) of the f32 vector x and,
-// for an RMSNorm ahead of the quantizer, the matching norm weights.  load() issues
-// every read at once (at the top of a kernel, before anything else waits on memory);
-// sumsq() and quantize() then work from registers, so the prologue costs one memory
-// round trip instead of one for the norm's sum and another for the quantizer.  The
-// quantized result is bit-identical to quantize_prologue's for the same scale.
-template <bool Q8K, uint32_t S>
-struct HeldInput {
-    static constexpr uint32_t per_set = Q8K ? 4 : 32, blk = Q8K ? 256 : 32;
-    float v[S][16];
-    float w[S][16];
+// Cross-lane steps of the register-held quantizer.  xor 1 and xor 2 are quad
+// permutes, the two mirrors pair lanes within 8 and 16, and lanes 16 and 32 apart
+// are reached with LDS-routed shuffles.  Each step combines a lane with one partner;
+// a sequence of steps whose partner patterns span the lane-index bits 0..k-1 leaves
+// every lane of an aligned group of 2^k lanes with the group's combined value.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E;
 
-    // Block sets of `cols` inputs and whether nwaves wavefronts can hold them all.
-    __host__ __device__ static uint32_t sets(uint32_t cols) { return (cols / blk + per_set - 1) / per_set; }
+// Sum over the 64 lanes of a wavefront, every lane getting the total: four DPP steps
+// within each row of 16 lanes (register speed), then two shuffles across rows.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), CTRL, 0xF, 0xF, false));
+    const uint32_t hi =
+        static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum(double s) {
+    s += dpp_d<kDppXor1>(s);
+    s += dpp_d<kDppXor2>(s);
+    s += dpp_d<kDppHalfMirror>(s);
+    s += dpp_d<kDppRowMirror>(s);
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    return s;
+}
+
+// A workgroup's input held in registers for the quantizing prologue.  The input is
+// cut into chunks of 64*E values; wavefront w holds chunks w, w + nwaves, ... (at
+// most S), lane l the E consecutive values l*E.. of each chunk, and, for an RMSNorm
+// ahead of the quantizer, the matching norm weights.  load() issues every read at
+// once (at the top of a kernel, before anything else waits on memory); sumsq() and
+// quantize() then work from registers.  A Q8_0 block spans 32/E lanes and a Q8_K
+// block 256/E lanes; their maxima, code sums and bsums are combined across those
+// lanes, so the blocks written are bit-identical to q8_0_process / q8k_process's
+// (src/kernels.rs:463-522, 552-617) for the same input.
+template <bool Q8K, uint32_t E, uint32_t S>
+struct HeldInput {
+    static_assert(E == 4 || E == 8 || E == 16, "values per lane");
+    static constexpr uint32_t blk = Q8K ? 256 : 32, lpb = blk / E, chunk = 64 * E;
+    float v[S][E];
+    float w[S][E];
+
     __host__ __device__ static bool fits(uint32_t cols, uint32_t nwaves) {
-        return (sets(cols) + nwaves - 1) / nwaves <= S;
+        return cols % blk == 0 && (cols + chunk - 1) / chunk <= S * nwaves;
     }
 
     // nw: the norm weights, or x itself when there is no norm (read, never used).
-    // Lanes past the last block read the last block (zeroed afterwards), so the loads
-    // carry no branches for the compiler to wait on.
+    // Lanes past the end read the last E values (masked later), so the loads carry no
+    // branches for the compiler to wait on.
     __device__ __forceinline__ void load(const float *__restrict__ x, const float *__restrict__ nw, uint32_t cols,
                                          uint32_t wave, uint32_t nwaves, uint32_t lane) {
-        const uint32_t nb = cols / blk;
-        const uint32_t lb = Q8K ? lane >> 4 : lane >> 1, lo = Q8K ? 16u * (lane & 15u) : 16u * (lane & 1u);
 #pragma unroll
         for (uint32_t j = 0; j < S; ++j) {
-            const uint32_t b = per_set * (wave + j * nwaves) + lb, bc = b < nb ? b : nb - 1;
-            const float4 *xs = reinterpret_cast<const float4 *>(x + static_cast<size_t>(blk) * bc + lo);
+            const uint32_t e = (wave + j * nwaves) * chunk + lane * E, ec = e < cols ? e : cols - E;
+            const float4 *xs = reinterpret_cast<const float4 *>(x + ec);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (uint32_t i = 0; i < E / 4; ++i) {
                 const float4 q = xs[i];
                 v[j][4 * i] = q.x;
                 v[j][4 * i + 1] = q.y;
@@ -295,10 +327,10 @@ struct HeldInput {
         }
 #pragma unroll
         for (uint32_t j = 0; j < S; ++j) {
-            const uint32_t b = per_set * (wave + j * nwaves) + lb, bc = b < nb ? b : nb - 1;
-            const float4 *ws = reinterpret_cast<const float4 *>(nw + static_cast<size_t>(blk) * bc + lo);
+            const uint32_t e = (wave + j * nwaves) * chunk + lane * E, ec = e < cols ? e : cols - E;
+            const float4 *ws = reinterpret_cast<const float4 *>(nw + ec);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (uint32_t i = 0; i < E / 4; ++i) {
                 const float4 q = ws[i];
                 w[j][4 * i] = q.x;
                 w[j][4 * i + 1] = q.y;
@@ -308,15 +340,14 @@ struct HeldInput {
         }
     }
 
-    // Zeroes the lanes past the last block.  Called when the values are first used, not
-    // in load(): a use right after the reads would wait for them there.
+    // Zeroes the values past the end.  Called when the values are first used, not in
+    // load(): a use right after the reads would wait for them there.
     __device__ __forceinline__ void mask(uint32_t cols, uint32_t wave, uint32_t nwaves, uint32_t lane) {
-        const uint32_t nb = cols / blk, lb = Q8K ? lane >> 4 : lane >> 1;
 #pragma unroll
         for (uint32_t j = 0; j < S; ++j)
-            if (per_set * (wave + j * nwaves) + lb >= nb)
+            if ((wave + j * nwaves) * chunk + lane * E >= cols)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) v[j][i] = 0.0f;
+                for (uint32_t i = 0; i < E; ++i) v[j][i] = 0.0f;
     }
 
     // This lane's binary64 sum of the binary32 squares of its inputs (after mask()).
@@ -325,30 +356,165 @@ struct HeldInput {
 #pragma unroll
         for (uint32_t j = 0; j < S; ++j)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s += static_cast<double>(v[j][i] * v[j][i]);
+            for (uint32_t i = 0; i < E; ++i) s += static_cast<double>(v[j][i] * v[j][i]);
         return s;
     }
 
-    // Quantizes the held sets (after mask()) into `o` (LDS); `norm` applies the RMSNorm
-    // (x * scale) * w first.  Returns the error bits seen.
+    template <typename T, typename F>
+    __device__ __forceinline__ static T across(T x, F op) {  // combine over the lpb lanes of a block
+        if constexpr (sizeof(T) == 4) {
+            auto step = [&](auto dpp) {
+                const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(dpp)::value, 0xF,
+                                                          0xF, false);
+                x = op(x, __builtin_bit_cast(T, o));
+            };
+            if constexpr (lpb >= 2) step(std::integral_constant<int, kDppXor1>{});
+            if constexpr (lpb >= 4) step(std::integral_constant<int, kDppXor2>{});
+            if constexpr (lpb >= 8) step(std::integral_constant<int, kDppHalfMirror>{});
+            if constexpr (lpb >= 16) step(std::integral_constant<int, kDppRowMirror>{});
+            if constexpr (lpb >= 32) x = op(x, __shfl_xor(x, 16));
+            if constexpr (lpb >= 64) x = op(x, __shfl_xor(x, 32));
+        }
+        return x;
+    }
+
+    // (|x|, index, x) maximum over a block's lanes, lowest index first among equals.
+    template <int CTRL>
+    __device__ __forceinline__ static void max_dpp(float &best, int &bidx, float &bval) {
+        max_step<CTRL>(best, bidx, bval);
+    }
+    __device__ __forceinline__ static void max_shfl(float &best, int &bidx, float &bval, int m) {
+        const float ob = __shfl_xor(best, m), ov = __shfl_xor(bval, m);
+        const int oi = __shfl_xor(bidx, m);
+        const bool take = ob > best || (ob == best && oi < bidx);
+        best = take ? ob : best;
+        bidx = take ? oi : bidx;
+        bval = take ? ov : bval;
+    }
+
+    // Quantizes the held chunks (after mask()) into `o` (LDS); `norm` applies the
+    // RMSNorm (x * scale) * w first.  Returns the error bits seen.
     template <typename OutPtr>
     __device__ __forceinline__ int quantize(uint32_t cols, int contract, OutPtr o, uint32_t wave, uint32_t nwaves,
                                             uint32_t lane, bool norm, float scale) {
-        const uint32_t nb = cols / blk;
-        const uint32_t lb = Q8K ? lane >> 4 : lane >> 1;
         int e = 0;
+        const uint32_t sub = lane % lpb;  // this lane's place within its block
 #pragma unroll
         for (uint32_t j = 0; j < S; ++j) {
-            const uint32_t b0 = per_set * (wave + j * nwaves);
-            if (b0 >= nb) break;
-            const uint32_t n = nb - b0 < per_set ? nb - b0 : per_set;
-            if (norm && lb < n)
+            const uint32_t c0 = (wave + j * nwaves) * chunk;
+            if (c0 >= cols) break;  // wave-uniform
+            const uint32_t first = c0 + lane * E;
+            const bool active = first < cols;
+            const uint32_t b = first / blk;
+            float *vj = v[j];
+            if (norm && active)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) v[j][i] = (v[j][i] * scale) * w[j][i];
-            if constexpr (Q8K)
-                e |= q8k_process(v[j], n, contract, o + b0, lane);
-            else
-                e |= q8_0_process(v[j], n, contract, o + b0, lane);
+                for (uint32_t i = 0; i < E; ++i) vj[i] = (vj[i] * scale) * w[j][i];
+            bool bad = false;
+#pragma unroll
+            for (uint32_t i = 0; i < E; ++i) bad |= !finite(vj[i]);
+            if (__any(bad)) return e | kErrInput;
+            uint32_t packed[E / 4];
+#pragma unroll
+            for (uint32_t i = 0; i < E / 4; ++i) packed[i] = 0;
+            if constexpr (Q8K) {
+                // q8k_with_input (src/kernels.rs:463-522): the first element with the
+                // strictly largest |x| sets inv = -127 / x.
+                float best = 0.0f, bval = 0.0f;
+                int bidx = 0x7fffffff;
+#pragma unroll
+                for (uint32_t i = 0; i < E; ++i) {
+                    const float a = fabsf(vj[i]);
+                    const bool take = a > best;
+                    best = take ? a : best;
+                    bidx = take ? static_cast<int>(sub * E + i) : bidx;
+                    bval = take ? vj[i] : bval;
+                }
+                if constexpr (lpb >= 2) max_dpp<kDppXor1>(best, bidx, bval);
+                if constexpr (lpb >= 4) max_dpp<kDppXor2>(best, bidx, bval);
+                if constexpr (lpb >= 8) max_dpp<kDppHalfMirror>(best, bidx, bval);
+                if constexpr (lpb >= 16) max_dpp<kDppRowMirror>(best, bidx, bval);
+                if constexpr (lpb >= 32) max_shfl(best, bidx, bval, 16);
+                if constexpr (lpb >= 64) max_shfl(best, bidx, bval, 32);
+                const float inv = best != 0.0f ? -127.0f / bval : 0.0f;
+                if (__any(active && !finite(inv))) return e | kErrQuantRange;
+                const float qscale = best != 0.0f ? 1.0f / inv : 0.0f;
+                if (contract) {
+#pragma unroll
+                    for (uint32_t i = 0; i < E; ++i) {
+                        const float r = __builtin_fmaf(inv, vj[i], 12582912.0f);
+                        int q = static_cast<int>(__float_as_uint(r) & 0x7fffffu) - 0x400000;
+                        q = q > 127 ? 127 : q;
+                        packed[i >> 2] |= (static_cast<uint32_t>(q) & 0xffu) << (8 * (i & 3));
+                    }
+                } else {
+#pragma unroll
+                    for (uint32_t i = 0; i < E; ++i) {
+                        float r = __builtin_rintf(vj[i] * inv);
+                        r = r > 127.0f ? 127.0f : r;
+                        packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xffu) << (8 * (i & 3));
+                    }
+                }
+                // bsums group g = 16 values = 16/E lanes (or a part of one lane's E).
+                int bs = 0;
+#pragma unroll
+                for (uint32_t i = 0; i < E / 4; ++i) bs = sdot4(packed[i], 0x01010101u, bs);
+                if constexpr (E == 4) {
+                    bs += __builtin_bit_cast(int, __builtin_amdgcn_update_dpp(0, bs, kDppXor1, 0xF, 0xF, false));
+                    bs += __builtin_bit_cast(int, __builtin_amdgcn_update_dpp(0, bs, kDppXor2, 0xF, 0xF, false));
+                } else if constexpr (E == 8) {
+                    bs += __builtin_bit_cast(int, __builtin_amdgcn_update_dpp(0, bs, kDppXor1, 0xF, 0xF, false));
+                }
+                if (active) {
+                    uint32_t *vals = reinterpret_cast<uint32_t *>(o[b].values) + sub * (E / 4);
+#pragma unroll
+                    for (uint32_t i = 0; i < E / 4; ++i) vals[i] = packed[i];
+                    if constexpr (E == 16) {
+                        o[b].sums[sub] = static_cast<int16_t>(bs);
+                    } else {
+                        if (sub % (16 / E) == 0) o[b].sums[sub / (16 / E)] = static_cast<int16_t>(bs);
+                    }
+                    if (sub == 0) o[b].scale = qscale;
+                }
+            } else {
+                // q8_with_input (src/kernels.rs:552-617), contracts as in q8_0_process.
+                float m = 0.0f;
+#pragma unroll
+                for (uint32_t i = 0; i < E; ++i) m = fmaxf(m, fabsf(vj[i]));
+                m = across(m, [](float a, float c) { return fmaxf(a, c); });
+                const bool pinned = contract != 0, native = contract == 2;
+                const float d = native ? m * __uint_as_float(0x3c010204u) : m / 127.0f;
+                const float inv = d == 0.0f ? 0.0f : (native ? 127.0f / m : 1.0f / d);
+                int qsum = 0;
+                bool range = false;
+                auto code = [&](uint32_t i, float r) {
+                    range |= !(r >= -127.0f && r <= 127.0f);
+                    const int q = static_cast<int>(r);
+                    qsum += q;
+                    packed[i >> 2] |= (static_cast<uint32_t>(q) & 0xffu) << (8 * (i & 3));
+                };
+                // One loop per rounding (half-even pinned, half-away source): a select
+                // inside one loop would evaluate both roundings of every value.
+                if (pinned) {
+#pragma unroll
+                    for (uint32_t i = 0; i < E; ++i) code(i, __builtin_rintf(vj[i] * inv));
+                } else {
+#pragma unroll
+                    for (uint32_t i = 0; i < E; ++i) code(i, __builtin_roundf(vj[i] * inv));
+                }
+                qsum = across(qsum, [](int a, int c) { return a + c; });
+                const float qscale = round_f16(d);
+                if (__any(active && (range || !finite(qscale)))) return e | kErrQuantRange;
+                if (active) {
+                    uint32_t *vals = reinterpret_cast<uint32_t *>(o[b].values) + sub * (E / 4);
+#pragma unroll
+                    for (uint32_t i = 0; i < E / 4; ++i) vals[i] = packed[i];
+                    if (sub == 0) {
+                        o[b].scale = qscale;
+                        o[b].sum = round_f16(static_cast<float>(qsum) * d);
+                    }
+                }
+            }
         }
         return e;
     }
