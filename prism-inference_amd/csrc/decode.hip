@@ -23,7 +23,8 @@ namespace prism {
 namespace {
 
 constexpr uint32_t kHead = 128;        // head dimension the attention kernels are built for
-constexpr uint32_t kScoreChunk = 256;  // positions per score workgroup
+constexpr uint32_t kScoreLanes = 4;    // lanes per scored position (kHead / 4 dimensions each)
+constexpr uint32_t kScoreChunk = 256 / kScoreLanes;  // positions per score workgroup
 constexpr uint32_t kValueDims = 32;     // dimensions per value workgroup
 constexpr uint32_t kValueGroups = 128;  // position groups per value workgroup (x kValueDims/4 threads)
 constexpr uint32_t kMaxTokens = 8192;   // KV cache positions the value kernel's LDS allows
@@ -88,8 +89,9 @@ __device__ int norm_rope_pair(float x, float w, float c, float sn, uint32_t rope
 // Grid (heads, ceil(max_tokens / kScoreChunk)), 256 threads.  Each workgroup
 // normalizes and rotates its query head and its KV head's current key, the first
 // workgroup of every KV head appends the current key and value to the binary16
-// caches, and thread t scores position chunk*256 + t <= pos:
-// f16_dot(q, k) * (1/sqrt(head)) with the current key taken from LDS.  Every global
+// caches, and the four lanes of quad t score position chunk*64 + t <= pos (a quarter
+// of the dimensions each): f16_dot(q, k) * (1/sqrt(head)) with the current key taken
+// from LDS.  Every global
 // read that does not depend on another (the cached key row, the head inputs, norm
 // weights, RoPE factors, the value to append) is issued before the first is used.
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
@@ -99,8 +101,8 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
     const uint32_t group = p.heads / p.kv_heads, kh = h / group;
     const uint32_t qw = p.heads * kHead, kw = p.kv_heads * kHead;
     // Every load that does not need the position is issued before the position itself
-    // is waited for: the normalization's inputs first (memory counters complete in
-    // issue order, so the norm waits only for these), then the cached key row of this
+    // is waited for: the normalization's inputs first (memory counters complete in issue
+    // order, so the norm waits only for these), then the cached key row of this
     // thread's position (row 0 past the cache, never used).
     const uint32_t which = tid >> 7, d = tid & (kHead - 1);
     const float x = p.qkv[which ? qw + kh * kHead + d : h * kHead + d];
@@ -112,12 +114,19 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
     const float c = rot ? p.state->cs[j] : 1.0f, sn = rot ? p.state->sn[j] : 0.0f;
     const bool append = h % group == 0 && chunk == 0 && tid < kHead;
     const float vin = append ? p.qkv[qw + kw + kh * kHead + tid] : 0.0f;
-    const uint32_t t = chunk * kScoreChunk + tid, tr = t < p.max_tokens ? t : 0;
-    uint4 kr[kHead / 8];
-    const uint4 *krow = reinterpret_cast<const uint4 *>(p.kcache + static_cast<size_t>(tr) * kw + kh * kHead);
+    constexpr uint32_t kPart = kHead / kScoreLanes;  // dimensions per lane
+    const uint32_t t = chunk * kScoreChunk + tid / kScoreLanes, part = tid % kScoreLanes;
+    const uint32_t tr = t < p.max_tokens ? t : 0;
+    uint4 kr[kPart / 8];
+    const uint4 *krow =
+        reinterpret_cast<const uint4 *>(p.kcache + static_cast<size_t>(tr) * kw + kh * kHead + part * kPart);
 #pragma unroll
-    for (uint32_t cc = 0; cc < kHead / 8; ++cc) kr[cc] = krow[cc];
-    const uint32_t pos = vector_load(&p.state->pos);
+    for (uint32_t cc = 0; cc < kPart / 8; ++cc) kr[cc] = krow[cc];
+    // The position through the scalar cache, issued after every vector load: a vector
+    // read would be waited for at once (to move it to a scalar register), behind the
+    // key rows.
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t pos = p.state->pos;
 
     // The norm needs no position; the exits come after it, so that no load above is
     // moved below them.
@@ -136,27 +145,33 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
         p.vcache[at] = f16_bits(v);
     }
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHead));
-    if (t <= pos) {
-        // Four binary64 partial sums shorten the dependent chain; the terms are binary16
-        // x binary16 products (exact in binary32) whose binary64 sums are exact, so the
-        // split changes no bit of f16_dot's sequential sum.
+    if (t <= pos) {  // uniform over a quad
+        // The terms are binary16 x binary16 products, exact in binary32, summed in
+        // binary64: four partial sums per lane, then the quad's four lanes.  Only the
+        // order of the binary64 additions differs from f16_dot's sequential sum.
         double s[4] = {0.0, 0.0, 0.0, 0.0};
+        const float *q = qv + part * kPart;
         if (t == pos) {
-            for (uint32_t dd = 0; dd < kHead; dd += 4)
+            const float *k = kv + part * kPart;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) s[q] += static_cast<double>(qv[dd + q] * kv[dd + q]);
+            for (uint32_t dd = 0; dd < kPart; dd += 4)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[j] += static_cast<double>(q[dd + j] * k[dd + j]);
         } else {
 #pragma unroll
-            for (uint32_t cc = 0; cc < kHead / 8; ++cc) {
+            for (uint32_t cc = 0; cc < kPart / 8; ++cc) {
                 const uint32_t w4[4] = {kr[cc].x, kr[cc].y, kr[cc].z, kr[cc].w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    s[q] += static_cast<double>(qv[8 * cc + 2 * q] * h2f(w4[q] & 0xffffu));
-                    s[q] += static_cast<double>(qv[8 * cc + 2 * q + 1] * h2f(w4[q] >> 16));
+                for (int j = 0; j < 4; ++j) {
+                    s[j] += static_cast<double>(q[8 * cc + 2 * j] * h2f(w4[j] & 0xffffu));
+                    s[j] += static_cast<double>(q[8 * cc + 2 * j + 1] * h2f(w4[j] >> 16));
                 }
             }
         }
-        p.scores[static_cast<size_t>(h) * p.max_tokens + t] = static_cast<float>((s[0] + s[1]) + (s[2] + s[3])) * scale;
+        double d = (s[0] + s[1]) + (s[2] + s[3]);
+        d += dpp_d<kDppXor1>(d);
+        d += dpp_d<kDppXor2>(d);
+        if (part == 0) p.scores[static_cast<size_t>(h) * p.max_tokens + t] = static_cast<float>(d) * scale;
     }
     if (e) raise_error(p.err, e);  // any element: an overflow can hit one element only
 }
@@ -195,6 +210,10 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
         const uint32_t i = tid + k * 1024u;
         sv[k] = sc[i < last ? i : last];
     }
+    const uint32_t pos = vector_load(&p.state->pos);
+    // Scores and position first: memory counters complete in issue order, and the
+    // softmax must not wait for the value rows.
+    __builtin_amdgcn_sched_barrier(0);
     // Thread (g, q): positions g, g+128, ... of dimensions d0+4q .. d0+4q+3.
     const uint32_t g = tid / (kValueDims / 4), q = tid % (kValueDims / 4);
     const uint16_t *vb = p.vcache + kh * kHead + d0 + 4 * q;
@@ -204,12 +223,11 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
         const uint32_t i = g + k * kValueGroups;
         w[k] = *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i < last ? i : last) * kw);
     }
-    const uint32_t pos = vector_load(&p.state->pos);
-    if (pos >= p.max_tokens) return;  // reported by the score kernel
-    const uint32_t n = pos + 1;
-#pragma unroll
-    for (uint32_t k = 0; k < kValueAhead; ++k)
-        if (g + k * kValueGroups >= n) w[k] = make_uint2(0, 0);
+    // A position past the cache is reported by the score kernel; this one then reduces
+    // one position and writes nothing.  (No early return: the compiler would move the
+    // value loads below it, after the wait for the position.)
+    const bool ok = pos < p.max_tokens;
+    const uint32_t n = ok ? pos + 1 : 1;
     float m = -__builtin_inff();
     bool bad = false;
 #pragma unroll
@@ -226,7 +244,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     m = redf[0];
     for (uint32_t v = 1; v < nw; ++v) m = fmaxf(m, redf[v]);
     if (__syncthreads_or(bad) || !finite(m)) {
-        if (tid == 0 && blockIdx.y == 0) raise_error(p.err, kErrNonfinite);
+        if (tid == 0 && blockIdx.y == 0 && ok) raise_error(p.err, kErrNonfinite);
         return;
     }
     double tot = 0.0;
@@ -258,10 +276,13 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
         a[2] += static_cast<double>(pr * h2f(r.y & 0xffffu));
         a[3] += static_cast<double>(pr * h2f(r.y >> 16));
     };
+    // Rows past the position (stale cache rows) are zeroed here, where they are first
+    // used: zeroing them earlier would wait for these loads before the softmax.
 #pragma unroll
     for (uint32_t k = 0; k < kValueAhead; ++k) {
         const uint32_t i = g + k * kValueGroups;
-        accumulate(w[k], i < n ? prob[i] : 0.0f);
+        const bool in = i < n;
+        accumulate(in ? w[k] : make_uint2(0, 0), in ? prob[i] : 0.0f);
     }
     // Longer contexts: the remaining positions, eight rows loaded per batch before any
     // is used.
@@ -288,7 +309,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[wave][4 * q + j] = a[j];
     __syncthreads();
-    if (tid < kValueDims) {
+    if (tid < kValueDims && ok) {
         double t = acc[0][tid];
         for (uint32_t v = 1; v < nw; ++v) t += acc[v][tid];
         const float o = static_cast<float>(t);
