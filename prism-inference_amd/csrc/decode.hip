@@ -25,8 +25,8 @@ namespace {
 constexpr uint32_t kHead = 128;        // head dimension the attention kernels are built for
 constexpr uint32_t kScoreLanes = 4;    // lanes per scored position (kHead / 4 dimensions each)
 constexpr uint32_t kScoreChunk = 256 / kScoreLanes;  // positions per score workgroup
-constexpr uint32_t kValueDims = 32;     // dimensions per value workgroup
-constexpr uint32_t kValueGroups = 128;  // position groups per value workgroup (x kValueDims/4 threads)
+constexpr uint32_t kValueDims = 16;     // dimensions per value workgroup
+constexpr uint32_t kValueGroups = 256;  // position groups per value workgroup (x kValueDims/4 threads)
 constexpr uint32_t kMaxTokens = 8192;   // KV cache positions the value kernel's LDS allows
 
 __device__ __forceinline__ uint16_t f16_bits(float v) {
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
 // Positions of the value reduction whose rows are loaded before the softmax (per
 // thread: kValueAhead positions g, g + kValueGroups, ...), so that a context of up
 // to kValueAhead * kValueGroups tokens costs one memory round trip.
-constexpr uint32_t kValueAhead = 16;
+constexpr uint32_t kValueAhead = 8;
 
 // Grid (heads, kHead / kValueDims), 1024 threads; SPT scores per thread
 // (SPT * 1024 >= max_tokens).  softmax_round_f16 (src/kernels.rs:4431-4462) of the
@@ -188,7 +188,7 @@ constexpr uint32_t kValueAhead = 16;
 // out[d] = sum_t p_t v_t[d] in binary64.  Each term is a binary16 x binary16
 // product, exact in binary32, and a binary64 sum of such terms is exact unless they
 // span more than 53 bits of magnitude (probabilities below 2^-24 are binary16
-// zeros), so summing the positions in 128 interleaved groups and then the groups
+// zeros), so summing the positions in 256 interleaved groups and then the groups
 // does not change the result.  The scores and the first value rows are read
 // unconditionally (clamped to the cache, masked afterwards) before the position is
 // waited for, so the kernel's inputs arrive in one memory round trip.
@@ -299,18 +299,24 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) accumulate(r[k], pr[k]);
     }
-    // A wavefront holds eight groups of the same eight quads (lane = 8 * group + quad):
-    // fold them with lane shuffles, then the wavefronts through LDS.
+    // A wavefront holds sixteen groups of the same four quads (lane = 4 * group + quad):
+    // fold them with row rotations by 4 and 8 (DPP) and shuffles across rows, then the
+    // wavefronts through LDS.
+    constexpr int kDppRor4 = 0x124, kDppRor8 = 0x128;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int k = 8; k <= 32; k <<= 1) a[j] += __shfl_xor(a[j], k);
+    for (int j = 0; j < 4; ++j) {
+        a[j] += dpp_d<kDppRor4>(a[j]);
+        a[j] += dpp_d<kDppRor8>(a[j]);
+        a[j] += __shfl_xor(a[j], 16);
+        a[j] += __shfl_xor(a[j], 32);
+    }
     if (lane < kValueDims / 4)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[wave][4 * q + j] = a[j];
     __syncthreads();
     if (tid < kValueDims && ok) {
         double t = acc[0][tid];
+#pragma unroll
         for (uint32_t v = 1; v < nw; ++v) t += acc[v][tid];
         const float o = static_cast<float>(t);
         p.out[h * kHead + d0 + tid] = o;
