@@ -48,7 +48,7 @@ __device__ __forceinline__ void rope_freqs(DecodeState *st, uint32_t pos, const 
 // rms_norm_rope_round_f16_into::<false> (src/kernels.rs:3679-3733) of two heads at
 // once: threads 0..127 take the query head, threads 128..255 the KV head's key, one
 // element each (x, the norm weight w and the element's RoPE pair cos/sin already
-// loaded).  Per head: binary64 sum of the binary32 squares (wavefront shuffle tree,
+// loaded).  Per head: binary64 sum of the binary32 squares (wavefront butterfly,
 // then the two wavefronts in order), mean rounded to binary32, 1/sqrt(mean + eps),
 // (x * scale) * w, rotation of the first `rope` dimensions (element i with i + rope/2),
 // rounding to binary16.  The results land in dst[0] (query) and dst[1] (key).
@@ -56,9 +56,7 @@ __device__ __forceinline__ void rope_freqs(DecodeState *st, uint32_t pos, const 
 __device__ int norm_rope_pair(float x, float w, float c, float sn, uint32_t rope, float eps,
                               float (*dst)[kHead], float (*tmp)[kHead], double *red) {
     const uint32_t tid = threadIdx.x, which = tid >> 7, d = tid & (kHead - 1);
-    double s = static_cast<double>(x * x);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    const double s = wave_sum(static_cast<double>(x * x));
     if ((tid & 63u) == 0) red[tid >> 6] = s;
     __syncthreads();
     const double t = (0.0 + red[2 * which]) + red[2 * which + 1];
@@ -122,11 +120,14 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
         reinterpret_cast<const uint4 *>(p.kcache + static_cast<size_t>(tr) * kw + kh * kHead + part * kPart);
 #pragma unroll
     for (uint32_t cc = 0; cc < kPart / 8; ++cc) kr[cc] = krow[cc];
-    // The position through the scalar cache, issued after every vector load: a vector
-    // read would be waited for at once (to move it to a scalar register), behind the
-    // key rows.
-    __builtin_amdgcn_sched_barrier(0);
-    const uint32_t pos = p.state->pos;
+    // The position last, through an address the compiler cannot prove uniform: a
+    // uniform read becomes either a scalar load, which every later wait on the scalar
+    // or LDS counter also waits for, or a vector load moved to a scalar register (and
+    // so waited for) at once.  Read per lane, it is waited for where first used, after
+    // the normalization.
+    uint32_t lane0;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(lane0));
+    const uint32_t pos = vector_load(&p.state->pos + lane0);
 
     // The norm needs no position; the exits come after it, so that no load above is
     // moved below them.
@@ -237,8 +238,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
             m = fmaxf(m, sv[k]);
         }
     }
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
+    m = wave_max(m);
     if (lane == 0) redf[wave] = m;
     __syncthreads();
     m = redf[0];
@@ -256,8 +256,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
             tot += static_cast<double>(e);
         }
     }
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) tot += __shfl_xor(tot, k);
+    tot = wave_sum(tot);
     if (lane == 0) redd[wave] = tot;
     __syncthreads();
     tot = 0.0;

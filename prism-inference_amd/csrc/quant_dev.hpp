@@ -267,8 +267,9 @@ __device__ __forceinline__ int quantize_prologue(const float *__restrict__ x, ui
 // every lane of an aligned group of 2^k lanes with the group's combined value.
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E;
 
-// Sum over the 64 lanes of a wavefront, every lane getting the total: four DPP steps
-// within each row of 16 lanes (register speed), then two shuffles across rows.
+// Maximum and sum over the 64 lanes of a wavefront, every lane getting the result:
+// four DPP steps within each row of 16 lanes (register speed), then two shuffles
+// across rows.
 template <int CTRL>
 __device__ __forceinline__ double dpp_d(double v) {
     const uint64_t u = __builtin_bit_cast(uint64_t, v);
@@ -276,6 +277,14 @@ __device__ __forceinline__ double dpp_d(double v) {
     const uint32_t hi =
         static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, 0xF, 0xF, false));
     return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ float wave_max(float m) {
+    m = fmaxf(m, dpp_f<kDppXor1>(m));
+    m = fmaxf(m, dpp_f<kDppXor2>(m));
+    m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
+    m = fmaxf(m, dpp_f<kDppRowMirror>(m));
+    m = fmaxf(m, __shfl_xor(m, 16));
+    return fmaxf(m, __shfl_xor(m, 32));
 }
 __device__ __forceinline__ double wave_sum(double s) {
     s += dpp_d<kDppXor1>(s);
