@@ -582,22 +582,106 @@ __global__ __launch_bounds__(64) void k_mv_rows(MvParams p) {
     rows_tile<O, false>(p, p.act, blockIdx.x, threadIdx.x, 0);
 }
 
+// Units [u0, u1) of one 64-row tile: folded into `ch`, or, with `tout`, their single
+// terms stored to tout[u - u0] for another wavefront to fold (TPU == 1 formats).
+template <Op O, bool LUT>
+__device__ __forceinline__ void rows_part(const MvParams &p, const void *__restrict__ act, uint32_t tile, uint32_t lane,
+                                          uint32_t lbase, uint32_t u0, uint32_t u1, Chain<O> &ch, float *tout) {
+    constexpr uint32_t UB = unit_bytes<O>();
+    const uint32_t row_bytes = p.nu * UB;
+    const uint32_t left = p.rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    auto step = [&](const Raw<O> &w, uint32_t u) {
+        float t[terms_per_unit<O>()];
+        unit_terms<O, LUT>(w, act, u, t, lbase);
+        if (tout)
+            tout[u - u0] = t[0];
+        else
+            ch.fold(t, act, u);
+    };
+    Raw<O> A, B;
+    uint32_t u = u0;
+    load_unit<O>(A, rs, u * trp * UB, trp, lane);
+    while (u + 1 < u1) {
+        load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
+        step(A, u);
+        if (u + 2 < u1) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+        step(B, u + 1);
+        u += 2;
+    }
+    if (u < u1) step(A, u);
+}
+
 // PTQ1 with the LDS decode table: one workgroup per CU builds the 64 KiB table once and
-// its wavefronts take tiles round-robin over the grid (tile = wave * grid + block, ...),
-// which spreads the tiles evenly over the CUs.  The activation comes as its own
-// __restrict__ argument: the row stores of one tile then provably leave it intact for
-// the next, and its loads stay scalar.
+// works through its tiles (tile = block + j * grid, j = 0, 1, ...), which spreads the
+// tiles evenly over the CUs.  The activation comes as its own __restrict__ argument: the
+// row stores of one tile then provably leave it intact for the next, and its loads stay
+// scalar.
+//
+// When a workgroup has at most eight tiles (up to 131072 rows on 256 CUs), single-term
+// formats split every tile's units in two halves run by two wavefronts (wavefront w
+// takes half w % 2 of tile w / 2): the second half stores its terms in LDS, and after a
+// barrier the first half's wavefront continues its chain with them in unit order, so the
+// arithmetic is the unsplit row's.  Two to eight tiles then keep twice as many
+// wavefronts (and SIMDs) busy.  With more tiles the wavefronts already fill the SIMDs
+// and take whole tiles (measured: splitting nine tiles per CU in two rounds was slower).
 constexpr uint32_t kLutThreads = 1024;
+constexpr uint32_t kLutWaves = kLutThreads / 64;
+// SPLIT (single-term formats, at most kLutSlots tiles per workgroup and 64 units per
+// row, lut_split()): the two-wavefront halves; otherwise whole tiles.
+constexpr uint32_t kLutSlots = kLutWaves / 2;
 template <Op O>
+__host__ __device__ constexpr bool lut_can_split() {
+    return terms_per_unit<O>() == 1;
+}
+__host__ __device__ inline bool lut_split(uint32_t tiles, uint32_t grid, uint32_t nu) {
+    return tiles <= kLutSlots * grid && nu - (nu + 1) / 2 <= 32;
+}
+template <Op O, bool SPLIT>
 __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const void *__restrict__ act) {
     ptq1_lut_fill(threadIdx.x, blockDim.x);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t tiles = (p.rows + kTile - 1) / kTile;
-    const uint32_t step = gridDim.x * (blockDim.x >> 6);
-    for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += step)
-        rows_tile<O, true>(p, act, tile, lane, 8u * (lane & 31u));
+    const uint32_t lbase = 8u * (lane & 31u);
+    if constexpr (!SPLIT) {
+        const uint32_t step = gridDim.x * kLutWaves;
+        for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += step)
+            rows_tile<O, true>(p, act, tile, lane, lbase);
+    } else {
+        static_assert(lut_can_split<O>(), "single-term formats only");
+        __shared__ float second[kLutSlots][kTile][33];  // terms of a tile's second half (<= 32 units)
+        const uint32_t mine = blockIdx.x < tiles ? (tiles - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+        const uint32_t nh = (p.nu + 1) / 2;  // units of the first half
+        {
+            const uint32_t slot = wave >> 1, half = wave & 1u, j = slot;
+            const bool active = j < mine;
+            const uint32_t tile = blockIdx.x + j * gridDim.x;
+            Chain<O> ch;
+            if (active) {
+                if (half == 0)
+                    rows_part<O, true>(p, act, tile, lane, lbase, 0, nh, ch, nullptr);
+                else
+                    rows_part<O, true>(p, act, tile, lane, lbase, nh, p.nu, ch, second[slot][lane]);
+            }
+            __syncthreads();
+            if (active && half == 0) {
+                const float *t = second[slot][lane];
+                for (uint32_t u = nh; u < p.nu; ++u) ch.fold(t + (u - nh), act, u);
+                const uint32_t left = p.rows - tile * kTile;
+                if (lane < (left < kTile ? left : kTile)) {
+                    const size_t row = static_cast<size_t>(tile) * kTile + lane;
+                    float o = ch.result();
+                    if (p.residual) o = o + p.residual[row];
+                    p.out[row] = o;
+                    if (!finite(o)) raise_error(p.err, kErrNonfinite);
+                }
+            }
+        }
+    }
 }
 
 // Skinny batches (2..NB tokens, the matvec-to-matmul transition): one wavefront per
@@ -1505,7 +1589,11 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.eps = a.eps;
     if (!quant && nmat == 1 && tiles >= a.cus) {
         if constexpr (kind_of<O>() == kPTQ1) {
-            hipLaunchKernelGGL(k_mv_rows_lut<O>, dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);
+            if (lut_can_split<O>() && lut_split(static_cast<uint32_t>(tiles), a.cus, nu))
+                hipLaunchKernelGGL((k_mv_rows_lut<O, lut_can_split<O>()>), dim3(a.cus), dim3(kLutThreads), 0,
+                                   a.stream, p, act);
+            else
+                hipLaunchKernelGGL((k_mv_rows_lut<O, false>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);
             return hipGetLastError() == hipSuccess ? 0 : -1;
         }
         hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);

@@ -265,7 +265,7 @@ def test_gpu_project_q8_prepared_codes(ctx, kind, rows, cols):
 
 # ---- large matrices: one wavefront per 64-row tile (>= one tile per CU) ----------------
 
-@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 256), (ph.KIND_PQ2, 256), (ph.KIND_PQ2, 384),
+@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 256), (ph.KIND_PTQ1, 8448), (ph.KIND_PQ2, 256), (ph.KIND_PQ2, 384),
                                        (ph.KIND_Q2_K, 256), (ph.KIND_Q8_0, 256), (ph.KIND_TQ1_0, 512),
                                        (ph.KIND_TQ2_0, 512)])
 def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
@@ -289,18 +289,21 @@ def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
     ctx.release(wid)
 
 
-@pytest.mark.parametrize("cols", [384, 1024])
-def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols):
+@pytest.mark.parametrize("per_cu", [5, 16])
+@pytest.mark.parametrize("cols", [128, 384, 1024])
+def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
     """PTQ1 on the row-tile path decodes trits through the LDS table, one workgroup per
-    CU taking tiles round-robin: enough tiles that some wavefronts take two, an odd and
-    an even unit count, a partial last tile, and all three activation contracts."""
+    CU working through its tiles: 5-6 tiles per workgroup (each tile's units split over
+    two wavefronts) or 16-17 (whole tiles, some wavefronts taking two); one unit (an
+    empty second half), an odd and an even unit count, a partial last tile, and all
+    three activation contracts."""
     import oracle
 
     import hiprt
 
     kind = ph.KIND_PTQ1
     cus = hiprt.cu_count(0)
-    rows = 64 * (16 * cus + 3) + 37
+    rows = 64 * (per_cu * cus + 3) + 37
     w = synth.weights(kind, rows, cols, seed=29 + cols)
     x = synth.activations(cols, seed=30)
     wid = ctx.weight(kind, cols, rows, w)
