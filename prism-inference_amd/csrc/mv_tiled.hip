@@ -684,6 +684,64 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
     }
 }
 
+// PTQ1 batches of NB = 2 or 3 tokens on the table kernel: each unit of weights is loaded
+// and decoded once and folded into one chain per token (every chain in its own token's
+// unit order, the batch-1 arithmetic).  Token t's prepared activation sits at
+// act + t * act_stride bytes and its output rows at out + t * rows (residual likewise).
+// With the tokens' decode shared, a few tokens cost little more than one, where the
+// matrix-core skinny kernel pays its own decode.
+template <Op O, int NB>
+__global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut_batch(MvParams p, const void *__restrict__ act,
+                                                                   uint32_t act_stride) {
+    constexpr uint32_t UB = unit_bytes<O>();
+    ptq1_lut_fill(threadIdx.x, blockDim.x);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tiles = (p.rows + kTile - 1) / kTile;
+    const uint32_t lbase = 8u * (lane & 31u);
+    const uint32_t nu = p.nu, row_bytes = nu * UB;
+    for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += gridDim.x * kLutWaves) {
+        const uint32_t left = p.rows - tile * kTile;
+        const uint32_t trows = left < kTile ? left : kTile;
+        const uint32_t trp = (trows + 7u) & ~7u;
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+        Chain<O> ch[NB];
+        auto step = [&](const Raw<O> &w, uint32_t u) {
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
+                float tt[terms_per_unit<O>()];
+                unit_terms<O, true>(w, a, u, tt, lbase);
+                ch[t].fold(tt, a, u);
+            }
+        };
+        Raw<O> A, B;
+        uint32_t u = 0;
+        load_unit<O>(A, rs, 0, trp, lane);
+        while (u + 1 < nu) {
+            load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
+            step(A, u);
+            if (u + 2 < nu) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+            step(B, u + 1);
+            u += 2;
+        }
+        if (u < nu) step(A, u);
+        if (lane < trows) {
+            const size_t row = static_cast<size_t>(tile) * kTile + lane;
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const size_t at = static_cast<size_t>(t) * p.rows + row;
+                float o = ch[t].result();
+                if (p.residual) o = o + p.residual[at];
+                p.out[at] = o;
+                if (!finite(o)) raise_error(p.err, kErrNonfinite);
+            }
+        }
+    }
+}
+
 // Skinny batches (2..NB tokens, the matvec-to-matmul transition): one wavefront per
 // 64-row tile loads each unit of weights once and folds it into one chain per token,
 // every chain in its own token's unit order.  Token t's prepared activation sits at
@@ -1771,8 +1829,42 @@ int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t 
 
 // Row count from which 2..16 tokens run on the matrix cores (16 rows per wavefront).
 constexpr uint64_t kSkinnyMinRows = 1024;
+// PTQ1 batches of two tokens on matrices of at least four tiles per CU, and of three
+// tokens from eight tiles per CU, take the table kernel (decode once, one chain per
+// token).  Measured (4096 inputs): two tokens 40 / 43 / 50 us at 65536 / 131072 /
+// 151936 rows against 52 / 80 / 94 us on the matrix cores; three tokens 71 against
+// 80 and 94 us from 131072 rows, but slower at 65536; four tokens slower everywhere.
+bool lut_batch_eligible(const MatvecArgs &a) {
+    if (a.w2 || a.kind != kPTQ1) return false;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    return (a.tokens == 2 && tiles >= 4ull * a.cus) || (a.tokens == 3 && tiles >= 8ull * a.cus);
+}
+
+template <Op O>
+int launch_lut_batch(const MatvecArgs &a, uint32_t act_stride) {
+    if constexpr (kind_of<O>() != kPTQ1) {
+        return -2;
+    } else {
+        MvParams p{};
+        p.w[0] = p.w[1] = a.w;
+        p.rows = static_cast<uint32_t>(a.rows);
+        p.nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
+        p.cols = static_cast<uint32_t>(a.cols);
+        p.pinned = a.pinned;
+        p.out = a.out;
+        p.residual = a.residual;
+        p.err = a.err;
+        const dim3 grid(a.cus), block(kLutThreads);
+        if (a.tokens == 2)
+            hipLaunchKernelGGL((k_mv_rows_lut_batch<O, 2>), grid, block, 0, a.stream, p, a.act, act_stride);
+        else
+            hipLaunchKernelGGL((k_mv_rows_lut_batch<O, 3>), grid, block, 0, a.stream, p, a.act, act_stride);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+}
+
 bool skinny_eligible(const MatvecArgs &a) {
-    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows) return false;
+    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a)) return false;
     return dispatch(a, [&]<Op O>() { return skinny_supported<O>() ? 1 : 0; }) == 1;
 }
 
@@ -1780,6 +1872,8 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
+    if (a.act_format != kActF32 && lut_batch_eligible(a))
+        return dispatch(a, [&]<Op O>() { return launch_lut_batch<O>(a, static_cast<uint32_t>(in_stride)); });
     if (a.act_format != kActF32 && skinny_eligible(a)) {
         for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
             const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
@@ -1831,7 +1925,7 @@ size_t tiled_scratch_bytes(const MatvecArgs &a) {
 }
 
 bool tiled_needs_prepared(const MatvecArgs &a) {
-    if (skinny_eligible(a) || batch_eligible(a)) return true;
+    if (lut_batch_eligible(a) || skinny_eligible(a) || batch_eligible(a)) return true;
     return dispatch(a, [&]<Op O>() { return op_needs_prepared<O>(a) ? 1 : 0; }) == 1;
 }
 

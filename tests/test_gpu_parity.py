@@ -325,6 +325,44 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("cols", [384, 512])
+@pytest.mark.parametrize("tokens", [2, 3])
+def test_gpu_ptq1_table_batch_matches_per_token_oracle(ctx, cols, tokens):
+    """Two or three PTQ1 tokens on a matrix of eight tiles per CU run the table kernel
+    with the unit decoded once and one chain per token: each token's row must equal its
+    own matvec in every contract (source, pinned, native-scale Q8_0, Q8_K), with an odd
+    unit count and a partial last tile."""
+    import oracle
+
+    import hiprt
+
+    kind = ph.KIND_PTQ1
+    rows = 64 * 8 * hiprt.cu_count(0) + 37
+    w = synth.weights(kind, rows, cols, seed=43)
+    wid = ctx.weight(kind, cols, rows, w)
+    X = synth.activations(cols, seed=44 + tokens, tokens=tokens)
+    for pinned in (False, True):
+        ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+        got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
+        assert_bits_equal(got, ref, f"table batch f32 tokens={tokens} pinned={pinned}")
+    nq8, nq8k = cols // 32, cols // 256
+    for contract, pinned in ((0, False), (2, True), (2, False)):
+        act = np.concatenate([oracle.quantize_q8_0(X[t], contract) for t in range(tokens)])
+        ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * nq8:(t + 1) * nq8], pinned, threads=THREADS)
+                        for t in range(tokens)])
+        got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens, pinned=pinned)
+        assert_bits_equal(got, ref, f"table batch q8 tokens={tokens} contract={contract} pinned={pinned}")
+    if cols % 256 == 0:
+        act = np.concatenate([oracle.quantize_q8k(X[t], False) for t in range(tokens)])
+        got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens)
+        nb = cols // 128 * 28
+        sample = list(range(0, rows, 97)) + list(range(rows - 20, rows))
+        ref = np.array([[oracle.dot_ptq1_q8k(w[r * nb:(r + 1) * nb], act[t * nq8k:(t + 1) * nq8k]) for r in sample]
+                        for t in range(tokens)], np.float32)
+        assert_bits_equal(got[:, sample], ref, f"table batch q8k tokens={tokens}")
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("rows", [1024 + 53, 20480 + 37, 40960 + 37, 65536 + 37, 131072 + 37])
 @pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 384), (ph.KIND_PTQ1, 512), (ph.KIND_PQ2, 512),
                                        (ph.KIND_PQ2, 384), (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256),
