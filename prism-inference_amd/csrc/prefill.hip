@@ -232,22 +232,35 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <int CT>
-__global__ __launch_bounds__(256) void k_prefill_ptq1(const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2 : 3))) void k_prefill_ptq1(const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu,
                                                       const _Float16 *__restrict__ xh, const float *__restrict__ sc,
-                                                      uint32_t M, uint32_t Mp, float *__restrict__ out,
-                                                      int *__restrict__ err) {
+                                                      uint32_t M, uint32_t Mp, uint32_t xcd_major,
+                                                      float *__restrict__ out, int *__restrict__ err) {
     constexpr uint32_t NT = 32 * CT;
     constexpr uint32_t kRun = NT * 16;  // bytes of one (g, j, h) run of one block
-    // act[buffer][g*2+j][h][token][16 bytes]: a lane's operand is 16 contiguous bytes,
-    // and each half-wavefront of a read covers 512 contiguous bytes (no bank
-    // conflicts).  scl[buffer] holds the tokens' four group scales.
-    __shared__ __attribute__((aligned(16))) uint8_t act[2][8][2][kRun];
-    __shared__ __attribute__((aligned(16))) float4 scl[2][NT];
+    // actN[g*2+j][h][token][16 bytes]: a lane's operand is 16 contiguous bytes, and
+    // each half-wavefront of a read covers 512 contiguous bytes (no bank conflicts).
+    // sclN holds the tokens' four group scales.  The two ring buffers are separate
+    // objects, and the loop below names them statically, so the compiler can tell a
+    // read of one from the direct-to-LDS loads in flight into the other and does not
+    // wait for those loads before the current block's reads.
+    __shared__ __attribute__((aligned(16))) uint8_t act0[8][2][kRun];
+    __shared__ __attribute__((aligned(16))) uint8_t act1[8][2][kRun];
+    __shared__ __attribute__((aligned(16))) float4 scl0[NT];
+    __shared__ __attribute__((aligned(16))) float4 scl1[NT];
     const uint32_t lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t tile = 2 * blockIdx.x + (wave >> 1), hw = wave & 1;
+    // Workgroups go to the eight XCDs round-robin in dispatch order (x fastest), each
+    // XCD with its own L2.  With a multiple of eight token groups the grid is (8, row
+    // blocks, token groups / 8): XCD x takes token groups x, x+8, ... and every row
+    // block of each, so its tokens' codes are read into one L2 only and the whole
+    // weight matrix is shared there by its token groups.  Otherwise (row blocks, token
+    // groups).
+    const uint32_t bx = xcd_major ? blockIdx.y : blockIdx.x;
+    const uint32_t by = xcd_major ? blockIdx.x + 8 * blockIdx.z : blockIdx.y;
+    const uint32_t tile = 2 * bx + (wave >> 1), hw = wave & 1;
     const uint32_t tiles = (rows + kTile - 1) / kTile;
-    const uint32_t t0 = blockIdx.y * NT;
+    const uint32_t t0 = by * NT;
     const uint32_t row_bytes = nu * 28;
     uint32_t trows = 0;
     if (tile < tiles) {
@@ -262,20 +275,20 @@ __global__ __launch_bounds__(256) void k_prefill_ptq1(const uint8_t *__restrict_
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc, nu * Mp * 16u);
     const uint32_t row = 32 * hw + r32, out0 = 32 * hw + 4 * h;  // tile rows
 
-    // Block u's codes and scales of the workgroup's tokens -> act[buf], scl[buf]: 16
-    // runs of NT*16 bytes and one of NT*16 bytes, each contiguous in xh / sc; one
-    // wavefront instruction moves 64 tokens' 16 bytes (lanes past a short run idle).
-    auto stage = [&](uint32_t u, uint32_t buf) {
+    // Block u's codes and scales of the workgroup's tokens -> act, scl: 16 runs of
+    // NT*16 bytes and one of NT*16 bytes, each contiguous in xh / sc; one wavefront
+    // instruction moves 64 tokens' 16 bytes (lanes past a short run idle).
+    auto stage = [&](uint32_t u, uint8_t (&act)[8][2][kRun], float4 (&scl)[NT]) {
         constexpr uint32_t per = (NT + 63) / 64;  // instructions per run
 #pragma unroll
         for (uint32_t k = wave; k < 16 * per; k += 4) {
             const uint32_t run = k / per, c = k % per;
             if (64 * c + lane < NT)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(&act[buf][run >> 1][run & 1][1024 * c]), 16,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(&act[run >> 1][run & 1][1024 * c]), 16,
                                                          ((u * 16 + run) * Mp + t0 + 64 * c + lane) * 16u, 0, 0, 0);
         }
         if (wave < per && 64 * wave + lane < NT)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(&scl[buf][64 * wave]), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(&scl[64 * wave]), 16,
                                                      (u * Mp + t0 + 64 * wave + lane) * 16u, 0, 0, 0);
     };
 
@@ -286,12 +299,13 @@ __global__ __launch_bounds__(256) void k_prefill_ptq1(const uint8_t *__restrict_
         for (int r = 0; r < 16; ++r) o[ct][r] = 0.0f;
 
     RawBlock w;
-    stage(0, 0);
+    stage(0, act0, scl0);
     if (active) load_block(rw, 0, trp, row, out0, w);
     wait_vmcnt0();
     lds_barrier();
-    for (uint32_t u = 0; u < nu; ++u) {
-        const uint32_t buf = u & 1u;
+    // Block u from (act, scl) while block u+1 streams into (act_next, scl_next).
+    auto block = [&](uint32_t u, const uint8_t (&act)[8][2][kRun], const float4 (&scl)[NT],
+                     uint8_t (&act_next)[8][2][kRun], float4 (&scl_next)[NT]) {
         uint32_t aw[4][2][4];
         float d[16];
         if (active) {
@@ -306,13 +320,13 @@ __global__ __launch_bounds__(256) void k_prefill_ptq1(const uint8_t *__restrict_
         }
         // The next block streams in while this one is multiplied.
         if (u + 1 < nu) {
-            stage(u + 1, buf ^ 1u);
+            stage(u + 1, act_next, scl_next);
             if (active) load_block(rw, (u + 1) * trp * 28u, trp, row, out0, w);
         }
         if (active) {
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
-                const float4 sg4 = scl[buf][32 * ct + r32];
+                const float4 sg4 = scl[32 * ct + r32];
                 const float sg[4] = {sg4.x, sg4.y, sg4.z, sg4.w};
                 v16f tt;
 #pragma unroll
@@ -320,7 +334,7 @@ __global__ __launch_bounds__(256) void k_prefill_ptq1(const uint8_t *__restrict_
                     v16f a = {};
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const v8h bx = *reinterpret_cast<const v8h *>(&act[buf][2 * g + j][h][(32 * ct + r32) * 16]);
+                        const v8h bx = *reinterpret_cast<const v8h *>(&act[2 * g + j][h][(32 * ct + r32) * 16]);
                         const v8h ax = __builtin_bit_cast(v8h, u32x4{aw[g][j][0], aw[g][j][1], aw[g][j][2], aw[g][j][3]});
                         a = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, bx, a, 0, 0, 0);
                     }
@@ -336,6 +350,10 @@ __global__ __launch_bounds__(256) void k_prefill_ptq1(const uint8_t *__restrict_
         }
         wait_vmcnt0();  // block u+1's codes, scales and weights have landed
         lds_barrier();  // and every wavefront is done with block u's buffers
+    };
+    for (uint32_t u = 0; u < nu; u += 2) {
+        block(u, act0, scl0, act1, scl1);
+        if (u + 1 < nu) block(u + 1, act1, scl1, act0, scl0);
     }
     if (!active) return;
     // Y[t][r]: the lane holds tokens t0 + 32ct + r32 and tile rows out0 + 8q + 0..3.
@@ -392,12 +410,15 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
     // Tokens per workgroup (measured, 6144 x 2048): 64 keeps three wavefronts per SIMD
     // and beats 128 (two per SIMD, the decode shared by more tokens) up to about 4096
     // tokens; 32 keeps CUs busy on short prompts.
-    if (M >= 4096)
-        hipLaunchKernelGGL(k_prefill_ptq1<4>, dim3(gx, Mp / 128), dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, out, err);
-    else if (M >= 256)
-        hipLaunchKernelGGL(k_prefill_ptq1<2>, dim3(gx, Mp / 64), dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, out, err);
+    const uint32_t nt = M >= 4096 ? 128 : M >= 256 ? 64 : 32, groups = Mp / nt;
+    const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
+    const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
+    if (nt == 128)
+        hipLaunchKernelGGL(k_prefill_ptq1<4>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
+    else if (nt == 64)
+        hipLaunchKernelGGL(k_prefill_ptq1<2>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
     else
-        hipLaunchKernelGGL(k_prefill_ptq1<1>, dim3(gx, Mp / 32), dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, out, err);
+        hipLaunchKernelGGL(k_prefill_ptq1<1>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
