@@ -428,12 +428,14 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
 
 
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 16), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
-                                         (192, 512, 1030), (96, 256, 4100)])
+                                         (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
+                                         (96, 256, 4096)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     """PTQ1 source-contract prefill runs as one f16-MFMA GEMM from 16 tokens on; every
     token row must equal the reference's per-token matvec bit for bit (partial row
     tiles, idle wavefronts of a partial 128-row block, an odd block count, 32, 64 and
-    128 tokens per workgroup, padding tokens)."""
+    128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
+    token groups are a multiple of eight: M = 200, 512, 4096)."""
     import oracle
 
     w = synth.ptq1_weights(rows, cols, seed=rows + M)
