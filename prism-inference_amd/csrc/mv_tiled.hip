@@ -582,8 +582,8 @@ __global__ __launch_bounds__(64) void k_mv_rows(MvParams p) {
     rows_tile<O, false>(p, p.act, blockIdx.x, threadIdx.x, 0);
 }
 
-// Units [u0, u1) of one 64-row tile: folded into `ch`, or, with `tout`, their single
-// terms stored to tout[u - u0] for another wavefront to fold (TPU == 1 formats).
+// Units [u0, u1) of one 64-row tile: folded into `ch`, or, with `tout`, their terms
+// stored to tout[(u - u0) * TPU + j] for another wavefront to fold.
 template <Op O, bool LUT>
 __device__ __forceinline__ void rows_part(const MvParams &p, const void *__restrict__ act, uint32_t tile, uint32_t lane,
                                           uint32_t lbase, uint32_t u0, uint32_t u1, Chain<O> &ch, float *tout) {
@@ -596,10 +596,12 @@ __device__ __forceinline__ void rows_part(const MvParams &p, const void *__restr
     auto step = [&](const Raw<O> &w, uint32_t u) {
         float t[terms_per_unit<O>()];
         unit_terms<O, LUT>(w, act, u, t, lbase);
-        if (tout)
-            tout[u - u0] = t[0];
-        else
+        if (tout) {
+#pragma unroll
+            for (int j = 0; j < terms_per_unit<O>(); ++j) tout[(u - u0) * terms_per_unit<O>() + j] = t[j];
+        } else {
             ch.fold(t, act, u);
+        }
     };
     Raw<O> A, B;
     uint32_t u = u0;
@@ -612,6 +614,37 @@ __device__ __forceinline__ void rows_part(const MvParams &p, const void *__restr
         u += 2;
     }
     if (u < u1) step(A, u);
+}
+
+// Two wavefronts per 64-row tile: wavefront 1 computes the terms of the second half of
+// the units into LDS (dynamic, 64 rows x `stride` floats), wavefront 0 folds the first
+// half and then, after one barrier, those terms in unit order: the unsplit row's
+// arithmetic, with twice the wavefronts and half the serial chain each.
+template <Op O>
+__global__ __launch_bounds__(128) void k_mv_rows2(MvParams p, uint32_t stride) {
+    static_assert(O != Op::PTQ1_PINNED, "four-lane chains fold nine terms per unit");
+    extern __shared__ float second[];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tile = blockIdx.x, nh = (p.nu + 1) / 2;
+    float *mine = second + lane * stride;
+    Chain<O> ch;
+    if (half == 0)
+        rows_part<O, false>(p, p.act, tile, lane, 0, 0, nh, ch, nullptr);
+    else
+        rows_part<O, false>(p, p.act, tile, lane, 0, nh, p.nu, ch, mine);
+    __syncthreads();
+    if (half == 0) {
+        for (uint32_t u = nh; u < p.nu; ++u) ch.fold(mine + (u - nh) * terms_per_unit<O>(), p.act, u);
+        const uint32_t left = p.rows - tile * kTile;
+        if (lane < (left < kTile ? left : kTile)) {
+            const size_t row = static_cast<size_t>(tile) * kTile + lane;
+            float o = ch.result();
+            if (p.residual) o = o + p.residual[row];
+            p.out[row] = o;
+            if (!finite(o)) raise_error(p.err, kErrNonfinite);
+        }
+    }
 }
 
 // PTQ1 with the LDS decode table: one workgroup per CU builds the 64 KiB table once and
@@ -1653,6 +1686,21 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
             else
                 hipLaunchKernelGGL((k_mv_rows_lut<O, false>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);
             return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+        if constexpr (O != Op::PTQ1_PINNED) {
+            // Two wavefronts per tile up to eight tiles per CU (Q8_0: two), and for Q2_K at
+            // any size.  Measured at 4096 columns: Q2_K 16.8 -> 12.1 us (32768 rows), 20.5 ->
+            // 18.2 (65536), 41.8 -> 40.7 (151936); TQ2_0 22.5 -> 17.0 (65536); PQ2 25.4 ->
+            // 16.4 and TQ1_0 20.6 -> 16.4 (32768); Q8_0 28.0 -> 27.2 at 32768 rows but 2 %
+            // slower at 65536, and Q8_0 / TQ2_0 1-5 % slower split at 151936 rows.
+            // Second-half terms per row, odd stride (no bank conflicts).
+            const uint32_t stride = ((nu - (nu + 1) / 2) * terms_per_unit<O>()) | 1u;
+            const uint64_t most = O == Op::Q8_0 ? 2ull * a.cus : 8ull * a.cus;
+            if (nu >= 4 && stride <= 129 && (O == Op::Q2K || tiles <= most)) {
+                hipLaunchKernelGGL(k_mv_rows2<O>, dim3(static_cast<uint32_t>(tiles)), dim3(128),
+                                   kTile * stride * sizeof(float), a.stream, p, stride);
+                return hipGetLastError() == hipSuccess ? 0 : -1;
+            }
         }
         hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;

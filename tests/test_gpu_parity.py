@@ -267,10 +267,13 @@ def test_gpu_project_q8_prepared_codes(ctx, kind, rows, cols):
 
 @pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 256), (ph.KIND_PTQ1, 8448), (ph.KIND_PQ2, 256), (ph.KIND_PQ2, 384),
                                        (ph.KIND_Q2_K, 256), (ph.KIND_Q8_0, 256), (ph.KIND_TQ1_0, 512),
-                                       (ph.KIND_TQ2_0, 512)])
+                                       (ph.KIND_TQ2_0, 512), (ph.KIND_Q2_K, 1280), (ph.KIND_Q8_0, 640),
+                                       (ph.KIND_PQ2, 1152), (ph.KIND_TQ1_0, 1280), (ph.KIND_TQ2_0, 1280)])
 def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
     """rows spans more 64-row tiles than the device has CUs (the one-wavefront-per-tile
-    kernel with scalar activation loads), with a partial last tile."""
+    kernel with scalar activation loads), with a partial last tile.  From four units per
+    row the tile's units are split over two wavefronts (odd unit counts here: the second
+    half's terms come back through LDS and must continue the chain in unit order)."""
     import oracle
 
     import hiprt
