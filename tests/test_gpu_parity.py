@@ -451,6 +451,43 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("kind,rows,cols", [(ph.KIND_Q2_K, 151936, 4096), (ph.KIND_Q8_0, 32768, 4096),
+                                         (ph.KIND_PQ2, 32768, 4096), (ph.KIND_TQ2_0, 65536, 4096)])
+def test_gpu_large_matvec_sampled_rows_match_oracle(ctx, kind, rows, cols):
+    """Benchmark-sized matrices on the row-tile kernels (two wavefronts per tile here):
+    every 997th row and the last row equal the oracle's matvec of those rows, in both
+    contracts."""
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=rows + kind) if kind != ph.KIND_PQ2 else \
+        synth.pq2_weights(rows, cols, seed=rows, levels=4)
+    x = synth.activations(cols, seed=cols + kind)
+    sample = np.r_[np.arange(0, rows, 997), rows - 1]
+    wsub = np.ascontiguousarray(w.reshape(rows, -1)[sample]).ravel()
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, len(sample), wsub, x, pinned, threads=THREADS)
+        got = ctx.project_f32(wid, rows, x, pinned=pinned)
+        assert_bits_equal(got[sample], ref, f"kind={kind} {rows}x{cols} pinned={pinned}")
+    ctx.release(wid)
+
+
+def test_gpu_prefill_bench_shape_matches_oracle(ctx):
+    """PTQ1 6144x2048 at 2048 tokens (64 tokens per workgroup, XCD-major grid): sampled
+    token rows equal the oracle's per-token matvec bit for bit."""
+    import oracle
+
+    rows, cols, M = 6144, 2048, 2048
+    w = synth.ptq1_weights(rows, cols, seed=11)
+    X = synth.activations(cols, seed=12, tokens=M)
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
+    Y = ctx.prefill(wid, rows, X, pinned=False)
+    for t in (0, 1, 63, 64, 777, 1024, M - 1):
+        ref = oracle.matvec(ph.KIND_PTQ1, cols, rows, w, X[t], False, threads=THREADS)
+        assert_bits_equal(Y[t], ref, f"prefill token {t}")
+    ctx.release(wid)
+
+
 def test_gpu_project_f32_group_siblings(ctx):
     import oracle
 
