@@ -93,6 +93,7 @@ def lib():
             "po_project_q8k": (I, [U, S, S, P, P, I, P, I]),
             "po_project_q8": (I, [U, S, S, P, P, I, P, I]),
             "po_vector_exp": (ctypes.c_float, [ctypes.c_float]),
+            "po_silu": (None, [P, S, I]),
             "po_swiglu": (None, [P, P, S, I]),
             "po_ffn": (I, [U, S, S, P, P, P, P, P, I, P, P, I]),
             "po_rms_norm": (I, [P, P, S, ctypes.c_float, P]),
@@ -284,6 +285,12 @@ def project_q8(kind: int, cols: int, rows: int, w, act: np.ndarray, pinned: bool
 
 def vector_exp(x: float) -> float:
     return lib().po_vector_exp(x)
+
+
+def silu(x, pinned: bool) -> np.ndarray:
+    v = _f32(x).copy()
+    lib().po_silu(_p(v), v.size, int(pinned))
+    return v
 
 
 def swiglu(gate, up, pinned: bool) -> np.ndarray:

@@ -31,12 +31,14 @@
  *                        bits; KATs [7.0], [0.99993896], odd-PQ2 [11.0], [19.25];
  *                        LCG(99) upstream integer group sums (5000 trials).
  *   dot_q2k / decode Q2_K upstream-kquants.json TypeId 10 (quantize, decode, GenericDot).
- *   dot_q8_0             closed form only: ordered chain checked against an f64
- *                        re-evaluation of the same rounding steps (no fixture).
- *                        => parity unpinned beyond the ordered-chain closed form.
+ *   dot_q8_0             no fixture: representable-exact chains equal the exact sum,
+ *                        and hand-derived binary32 known answers separate the order
+ *                        from a fused last step, a reordered chain and the scales
+ *                        applied in the other order (tests/fixtures_util.py).
  *   dot_ptq1_q8k         equal to dot_pq2 unfused on pack_ptq'd PQ2 rows (lossless codec).
- *   swiglu pinned        vector_exp checked against expf within 2 ulp over 2^20 inputs;
- *                        bitwise parity of the source path (libm exp) is unpinnable.
+ *   silu/swiglu pinned   swift-activation-parity.json: all 45 native SiLU and SwiGLU
+ *                        bits (vector body, libm tail, finite edges); bitwise parity of
+ *                        the source path (libm exp) is unpinnable.
  *   matvec/ffn           compositions of the above; per-token == row dot loop.
  */
 #include "prism_oracle.h"
@@ -878,6 +880,18 @@ float po_vector_exp(float value) {
         return fmaf(s2, poly, s2) * s1;
     }
     return fmaf(poly, k, k);
+}
+
+/* Pinned SiLU row (src/kernels/pinned_activations.rs:110-133): x / (1 + vexp(0 - x))
+ * for the first len/4*4 values, libm exp for the tail; source SiLU
+ * (src/kernels.rs:3365-3368): x / (1 + exp(-x)). */
+void po_silu(float *x, size_t n, int pinned) {
+    size_t vec = n / 4 * 4;
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i];
+        float den = 1.0f + ((pinned && i < vec) ? po_vector_exp(0.0f - v) : expf(-v));
+        x[i] = v / den;
+    }
 }
 
 /* source: src/graph.rs:121-131 with silu = x/(1+exp(-x)) (src/kernels.rs:3365-3368);

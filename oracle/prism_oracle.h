@@ -114,6 +114,7 @@ int po_project_q8(uint32_t kind, size_t cols, size_t rows, const uint8_t *w, con
 
 /* ---- SwiGLU (src/graph.rs:121-131; src/kernels/pinned_activations.rs:26-62,141-178) ---- */
 float po_vector_exp(float x);
+void po_silu(float *x, size_t n, int pinned);
 void po_swiglu(const float *gate, float *up, size_t n, int pinned);
 
 /* ---- FFN chain: gate/up -> SwiGLU -> down (+ residual) (src/graph.rs:3935-3956) ---- */

@@ -479,13 +479,13 @@ int launch_attention(const AttnArgs &a) {
         hipLaunchKernelGGL(k_attn_values<4>, vg, vb, 0, a.stream, a);
     else
         hipLaunchKernelGGL(k_attn_values<8>, vg, vb, 0, a.stream, a);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *q8_out, int *err, hipStream_t s) {
     if (n % 32) return -2;
     hipLaunchKernelGGL(k_lm_prep, dim3(1), dim3(256), 0, s, x, w, n, eps, static_cast<Q8Block *>(q8_out), err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, DecodeState *st, const RopeArgs &rope,
@@ -493,7 +493,7 @@ int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, DecodeStat
     if (rope.rope > 2 * 64) return -2;
     hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, static_cast<const uint8_t *>(emb_tiled), rows, cols, st,
                        rope, out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
@@ -505,7 +505,7 @@ int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_til
     hipLaunchKernelGGL(k_argmax_slices, dim3(kArgmaxGroups), dim3(256), 0, s, logits, vocab, pval, pidx);
     hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(256), 0, s, pval, pidx, vocab,
                        static_cast<const uint8_t *>(emb_tiled), cols, st, rope, tokens, max_steps, out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 }  // namespace prism

@@ -129,21 +129,25 @@ int enqueue_step(prism_hip_decoder *d) {
         at.k_norm = L.k_norm;
         at.kcache = L.kc;
         at.vcache = L.vc;
-        if (launch_attention(at)) return hip_fail(c, hipGetLastError(), "attention launch");
+        rc = launch_result(c, launch_attention(at), "attention launch");
+        if (rc) return rc;
         rc = project(d, L.o, d->att, h1, h0, nullptr);
         if (!rc) rc = project(d, L.gate, h1, d->ffn_h, nullptr, L.post_norm, L.up);
         if (!rc) rc = project(d, L.down, d->ffn_h, h0, h1, nullptr);
         if (rc) return rc;
     }
     const Weight *lm = find(c, d->lm_head);
-    if (launch_lm_prep(h0, d->output_norm, static_cast<uint32_t>(g.hidden), g.eps, d->lm_act, c->err, s))
-        return hip_fail(c, hipGetLastError(), "final norm launch");
-    int rc = matvec(c, *lm, kActQ8, d->lm_act, 1, 0, d->logits, s);
-    if (rc) return rc;
-    if (launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), lm->dev, static_cast<uint32_t>(g.hidden),
-                            d->state, rope_args(g), d->tokens, d->max_steps, h0, d->argmax_scratch, s))
-        return hip_fail(c, hipGetLastError(), "argmax launch");
-    return PRISM_OK;
+    int rc = launch_result(c, launch_lm_prep(h0, d->output_norm, static_cast<uint32_t>(g.hidden), g.eps, d->lm_act,
+                                             c->err, s),
+                           "final norm launch");
+    if (!rc) rc = matvec(c, *lm, kActQ8, d->lm_act, 1, 0, d->logits, s);
+    if (!rc)
+        rc = launch_result(c,
+                           launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), lm->dev,
+                                               static_cast<uint32_t>(g.hidden), d->state, rope_args(g), d->tokens,
+                                               d->max_steps, h0, d->argmax_scratch, s),
+                           "argmax launch");
+    return rc;
 }
 
 void drop_graph(prism_hip_decoder *d) {
@@ -153,11 +157,15 @@ void drop_graph(prism_hip_decoder *d) {
     d->graph = nullptr;
 }
 
-bool ready(const prism_hip_decoder *d) {
-    if (!d->lm_head || !d->output_norm) return false;
+// Every tensor set and still resident: prism_hip_weight_release_all (or a release of
+// one of the decoder's ids) may have dropped weights the captured graph reads, in
+// which case the graph is dropped too and the decoder must be given its tensors again.
+bool ready(prism_hip_decoder *d) {
+    bool ok = d->lm_head && d->output_norm && find(d->ctx, d->lm_head);
     for (const auto &L : d->layers)
-        if (!L.qkv || !L.o || !L.gate || !L.up || !L.down) return false;
-    return true;
+        for (prism_weight_id w : {L.qkv, L.o, L.gate, L.up, L.down}) ok = ok && w && find(d->ctx, w);
+    if (!ok) drop_graph(d);
+    return ok;
 }
 
 }  // namespace
@@ -203,8 +211,10 @@ prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decode
     if (!rc) rc = dalloc(d, &d->tokens, sizeof(uint32_t) * max_steps);
     const size_t gs = argmax_scratch_bytes();
     if (!rc) rc = dalloc(d, &d->argmax_scratch, gs);
-    if (!rc && hipMemset(d->argmax_scratch, 0, gs) != hipSuccess)
-        rc = hip_fail(c, hipGetLastError(), "decoder scratch reset");
+    if (!rc) {
+        const hipError_t e = hipMemset(d->argmax_scratch, 0, gs);
+        if (e != hipSuccess) rc = hip_fail(c, e, "decoder scratch reset");
+    }
     if (rc) {
         prism_hip_decoder_destroy(d);
         return nullptr;
@@ -298,9 +308,11 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
     HIP_OR_FAIL(c, hipMemcpyAsync(d->state, &init, sizeof(init), hipMemcpyHostToDevice, s));
     HIP_OR_FAIL(c, hipStreamSynchronize(s));
     const Weight *lm = find(c, d->lm_head);
-    if (launch_embed(lm->dev, d->g.vocab, static_cast<uint32_t>(d->g.hidden), d->state, rope_args(d->g), d->hidden[0],
-                     s))
-        return hip_fail(c, hipGetLastError(), "embed launch");
+    rc = launch_result(c,
+                       launch_embed(lm->dev, d->g.vocab, static_cast<uint32_t>(d->g.hidden), d->state, rope_args(d->g),
+                                    d->hidden[0], s),
+                       "embed launch");
+    if (rc) return rc;
     if (use_graph && !d->exec) {
         HIP_OR_FAIL(c, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
         rc = enqueue_step(d);

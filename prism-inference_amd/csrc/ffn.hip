@@ -45,19 +45,19 @@ int launch_swiglu(const float *gate, const float *up, float *h, uint64_t n, uint
     if (total == 0) return 0;
     hipLaunchKernelGGL(k_swiglu, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, s, gate, up, h, n,
                        total, pinned, err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 int launch_add_residual(float *out, const float *residual, uint64_t n, int *err, hipStream_t s) {
     if (n == 0) return 0;
     hipLaunchKernelGGL(k_add_residual, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, out, residual,
                        n, err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 int launch_fill_i32(int *p, int v, uint32_t n, hipStream_t s) {
     hipLaunchKernelGGL(k_fill_i32, dim3((n + 63) / 64), dim3(64), 0, s, p, v, n);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 }  // namespace prism

@@ -11,6 +11,13 @@ constexpr int kErrNonfinite = 1;   // non-finite output / scale (PRISM_ERR_NONFI
 constexpr int kErrQuantRange = 2;  // activation quantizer overflow (PRISM_ERR_NONFINITE)
 constexpr int kErrInput = 4;       // non-finite activation input (PRISM_ERR_NONFINITE)
 
+// Launcher status: 0 on success, kLaunchUnsupported for a geometry the kernels do not
+// cover, otherwise the hipError_t the launch left (positive).  hipGetLastError clears
+// the error it returns, so a launcher reads it exactly once, here, and callers map the
+// returned value instead of asking HIP again.
+constexpr int kLaunchUnsupported = -2;
+inline int launch_status() { return static_cast<int>(hipGetLastError()); }
+
 // Activation-side formats consumed by the matvec kernels.  kActF32: f32 input the
 // tiled kernels quantize in their prologue (contract in MatvecArgs::qcontract).
 enum ActFormat : int { kActQ8K = 0, kActQ8 = 1, kActF32 = 2 };
@@ -44,7 +51,7 @@ struct MatvecArgs {
     size_t scratch_bytes = 0;
 };
 
-// Returns 0 on success, -1 when the launch failed, -2 when the shape is unsupported.
+// Return launch_status() values (0, kLaunchUnsupported, or a hipError_t).
 // launch_matvec reads weights in the native row-major layout, launch_matvec_tiled in
 // the 64-row tiled layout of tiled.hpp.
 int launch_matvec(const MatvecArgs &a);
@@ -54,14 +61,15 @@ int launch_matvec_tiled(const MatvecArgs &a);
 bool tiled_needs_prepared(const MatvecArgs &a);
 // Device scratch a tiled call needs (the lane-ordered activations of a skinny batch).
 size_t tiled_scratch_bytes(const MatvecArgs &a);
-// Whether (kind, cols, rows) can be stored tiled, and the native -> tiled repack
+// Whether (kind, cols, rows) can be stored tiled on a device with `cus` compute units
+// (every projection of it then has a tiled kernel), and the native -> tiled repack
 // (the destination must hold tiled_bytes() and be zero-filled beforehand).
-bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows);
+bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t cus);
 int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols, uint64_t rows, hipStream_t s);
 // Tiled-prefill GEMM for PTQ1 weights in the public (source) contract: quantizes
 // x[M][cols] once and multiplies it by the tiled weights on the f16 matrix cores;
 // every output row is bit-identical to its own per-token matvec.
-bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned);
+bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens);
 size_t prefill_scratch_bytes(uint64_t cols, uint32_t tokens);
 int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M, float *out,
                    void *scratch, int *err, hipStream_t s);

@@ -526,7 +526,7 @@ static int launch_waves(const MatvecArgs &a, const void *act, float *out) {
     const uint32_t grid = (tiles + WAVES - 1) / WAVES;
     hipLaunchKernelGGL((k_matvec<O, S, LPR, kTileRows, WAVES>), dim3(grid), dim3(64 * WAVES), lds, a.stream, a.w,
                        static_cast<uint32_t>(a.row_bytes), static_cast<uint32_t>(a.rows), nu, act, out, a.err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 // Four independent wavefronts per workgroup when their LDS tiles fit, else one.
@@ -576,7 +576,7 @@ int launch_matvec(const MatvecArgs &a) {
             hipLaunchKernelGGL(k_matvec_generic, dim3(static_cast<uint32_t>((a.rows + 127) / 128)), dim3(128), 0,
                                a.stream, a.kind, a.act_format == kActQ8K ? 1 : 0, a.pinned, a.w, a.row_bytes,
                                static_cast<uint32_t>(a.rows), static_cast<uint32_t>(a.cols), act, out, a.err);
-            rc = hipGetLastError() == hipSuccess ? 0 : -1;
+            rc = launch_status();
         } else if (a.kind == kPTQ1) {
             if (a.act_format == kActQ8K)
                 rc = launch_sized<Op::PTQ1_Q8K>(a, act, out);

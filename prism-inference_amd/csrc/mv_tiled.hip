@@ -1685,7 +1685,7 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
                                    a.stream, p, act);
             else
                 hipLaunchKernelGGL((k_mv_rows_lut<O, false>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);
-            return hipGetLastError() == hipSuccess ? 0 : -1;
+            return launch_status();
         }
         if constexpr (O != Op::PTQ1_PINNED) {
             // Two wavefronts per tile up to eight tiles per CU (Q8_0: two), and for Q2_K at
@@ -1699,11 +1699,11 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
             if (nu >= 4 && stride <= 129 && (O == Op::Q2K || tiles <= most)) {
                 hipLaunchKernelGGL(k_mv_rows2<O>, dim3(static_cast<uint32_t>(tiles)), dim3(128),
                                    kTile * stride * sizeof(float), a.stream, p, stride);
-                return hipGetLastError() == hipSuccess ? 0 : -1;
+                return launch_status();
             }
         }
         hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+        return launch_status();
     }
     SplitPlan pl;
     if (!plan_split<O>(a.rows, nu, p.cols, quant, nmat, a.cus, &pl)) return -2;
@@ -1735,17 +1735,20 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     } else {
         go(k_mv_split<O, false, 1, 0>);
     }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
+// Whether an f32-input call must quantize in a separate launch: the row-tile kernels take
+// prepared blocks, and the split kernel's quantizing prologue needs its plan to fit LDS.
+// A gate+up pair (w2) has no prepared-block kernel: true there sends the caller to
+// separate gate and up projections.
 template <Op O>
 bool op_needs_prepared(const MatvecArgs &a) {
     const uint64_t tiles = (a.rows + kTile - 1) / kTile;
-    if (a.w2) return false;
-    if (tiles >= a.cus) return true;
+    if (!a.w2 && tiles >= a.cus) return true;
     SplitPlan pl;
     const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
-    return !plan_split<O>(a.rows, nu, static_cast<uint32_t>(a.cols), true, 1, a.cus, &pl);
+    return !plan_split<O>(a.rows, nu, static_cast<uint32_t>(a.cols), true, a.w2 ? 2u : 1u, a.cus, &pl);
 }
 
 // Selects the arithmetic order from (kind, activation format, pinned): the orders of
@@ -1773,12 +1776,38 @@ int dispatch(const MatvecArgs &a, F &&f) {
 
 }  // namespace
 
-bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows) {
+bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t cus) {
     if (rows == 0 || rows > 0xffffffffull) return false;
     TiledFormat f;
     if (!tiled_format(kind, &f) || cols % f.unit_weights) return false;
     const uint64_t row_bytes = cols / f.unit_weights * f.unit_bytes;
-    return row_bytes * kTile < (1ull << 31);  // 32-bit in-tile offsets
+    if (row_bytes * kTile >= (1ull << 31)) return false;  // 32-bit in-tile offsets
+    if ((rows + kTile - 1) / kTile >= cus) return true;   // row-tile kernels: any width
+    // Fewer tiles than CUs run the split kernel, whose LDS holds the prepared activation and
+    // the terms of every unit of its rows: every order the kind can take must fit, or the
+    // tensor stays in the native layout (whose kernels have no width limit).
+    MatvecArgs a;
+    a.kind = kind;
+    a.cols = cols;
+    a.rows = rows;
+    a.cus = cus;
+    for (const int fmt : {static_cast<int>(kActQ8K), static_cast<int>(kActQ8)}) {
+        if (fmt == kActQ8K && (cols % 256 || kind == kQ8_0)) continue;
+        if (fmt == kActQ8 && (kind == kQ2_K || kind == kTQ1_0 || kind == kTQ2_0)) continue;
+        for (const int pinned : {0, 1}) {
+            a.act_format = fmt;
+            a.pinned = pinned;
+            const int fits = dispatch(a, [&]<Op O>() {
+                SplitPlan pl;
+                return plan_split<O>(rows, static_cast<uint32_t>(cols / unit_weights<O>()), static_cast<uint32_t>(cols),
+                                     false, 1, cus, &pl)
+                           ? 1
+                           : 0;
+            });
+            if (fits == 0) return false;
+        }
+    }
+    return true;
 }
 
 int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols, uint64_t rows, hipStream_t s) {
@@ -1788,7 +1817,7 @@ int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols,
     const uint64_t n = rows * nu;
     hipLaunchKernelGGL(k_repack, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s,
                        static_cast<const uint8_t *>(native), static_cast<uint8_t *>(tiled), kind, rows, nu);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 template <Op O>
@@ -1811,7 +1840,7 @@ int launch_batch(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t a
         hipLaunchKernelGGL((k_mv_rows_batch<O, 8>), grid, block, 0, a.stream, p, act, ntok, act_stride);
     else
         hipLaunchKernelGGL((k_mv_rows_batch<O, 16>), grid, block, 0, a.stream, p, act, ntok, act_stride);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 bool batch_eligible(const MatvecArgs &a) { return a.tokens >= 2 && !a.w2 && a.rows >= kBatchMinRows; }
@@ -1872,7 +1901,7 @@ int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t 
         else if (ks == 4) hipLaunchKernelGGL((k_mv_skinny<O, false, 4>), grid, block, 0, a.stream, p);
         else hipLaunchKernelGGL((k_mv_skinny<O, false, 8>), grid, block, 0, a.stream, p);
     }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 // Row count from which 2..16 tokens run on the matrix cores (16 rows per wavefront).
@@ -1907,7 +1936,7 @@ int launch_lut_batch(const MatvecArgs &a, uint32_t act_stride) {
             hipLaunchKernelGGL((k_mv_rows_lut_batch<O, 2>), grid, block, 0, a.stream, p, a.act, act_stride);
         else
             hipLaunchKernelGGL((k_mv_rows_lut_batch<O, 3>), grid, block, 0, a.stream, p, a.act, act_stride);
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+        return launch_status();
     }
 }
 

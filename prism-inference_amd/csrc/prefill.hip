@@ -388,22 +388,24 @@ size_t prefill_scratch_bytes(uint64_t cols, uint32_t tokens) {
     return ((Mp * cols * 2 + 255) & ~size_t(255)) + Mp * (cols / 32) * 4;
 }
 
-bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned) {
+bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens) {
+    // The token codes are addressed with 32-bit buffer offsets.
+    const uint64_t code_bytes = cols / 128 * 8u * padded_tokens(tokens) * 32u;
     return kind == kPTQ1 && !pinned && cols % 128 == 0 && cols <= 65536 && rows > 0 &&
-           (rows * (cols / 128) * 28) < (1ull << 40);
+           (rows * (cols / 128) * 28) < (1ull << 40) && code_bytes < (1ull << 31);
 }
 
 int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M, float *out,
                    void *scratch, int *err, hipStream_t s) {
     const uint32_t K = static_cast<uint32_t>(cols), Mp = padded_tokens(M);
-    if (static_cast<uint64_t>(K / 128) * 8u * Mp * 32u >= (1ull << 31)) return -2;  // buffer ranges are 32-bit
+    if (static_cast<uint64_t>(K / 128) * 8u * Mp * 32u >= (1ull << 31)) return kLaunchUnsupported;
     _Float16 *xh = static_cast<_Float16 *>(scratch);
     float *sc = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + ((static_cast<size_t>(Mp) * K * 2 + 255) & ~size_t(255)));
     const uint32_t chunks = (K + 1023) / 1024;
     const uint64_t items = static_cast<uint64_t>(Mp) * chunks;
     hipLaunchKernelGGL(k_prefill_prep, dim3(static_cast<uint32_t>((items + 3) / 4)), dim3(256), 0, s, x, M, Mp, K, xh,
                        sc, err);
-    if (hipGetLastError() != hipSuccess) return -1;
+    if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
     const auto W = static_cast<const uint8_t *>(w_tiled);
     const uint32_t R = static_cast<uint32_t>(rows), nu = K / 128;
@@ -420,7 +422,7 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
         hipLaunchKernelGGL(k_prefill_ptq1<2>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
     else
         hipLaunchKernelGGL(k_prefill_ptq1<1>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 }  // namespace prism

@@ -41,7 +41,7 @@ int launch_quantize_q8k(const float *x, uint64_t cols, uint32_t tokens, int pinn
     if (nb == 0) return 0;
     hipLaunchKernelGGL(k_quantize_q8k, dim3(static_cast<uint32_t>((nb + 15) / 16)), dim3(256), 0, s, x,
                        static_cast<uint32_t>(nb), pinned, static_cast<Q8KBlock *>(out), err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 int launch_quantize_q8_0(const float *x, uint64_t cols, uint32_t tokens, int contract, void *out, int *err,
@@ -50,7 +50,7 @@ int launch_quantize_q8_0(const float *x, uint64_t cols, uint32_t tokens, int con
     if (nb == 0) return 0;
     hipLaunchKernelGGL(k_quantize_q8_0, dim3(static_cast<uint32_t>((nb + 127) / 128)), dim3(256), 0, s, x,
                        static_cast<uint32_t>(nb), contract, static_cast<Q8Block *>(out), err);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return launch_status();
 }
 
 }  // namespace prism

@@ -20,12 +20,11 @@ constexpr uint32_t kPrefillMinTokens = 16;
 // Quantize device floats with the contract matvec_into would use, then project.
 int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
                     DevBuf &scratch, hipStream_t s, const float *residual = nullptr) {
-    if (w.tiled && tokens >= kPrefillMinTokens && !residual && prefill_supported(w.kind, w.cols, w.rows, pinned)) {
+    if (w.tiled && tokens >= kPrefillMinTokens && !residual && prefill_supported(w.kind, w.cols, w.rows, pinned, tokens)) {
         int rc = ensure(c, c->pre, prefill_scratch_bytes(w.cols, tokens));
         if (rc) return rc;
-        if (launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, c->pre.p, c->err, s))
-            return hip_fail(c, hipGetLastError(), "prefill launch");
-        return PRISM_OK;
+        return launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, c->pre.p, c->err, s),
+                             "prefill launch");
     }
     if (w.tiled) {
         MatvecArgs a = f32_args(c, w, x, tokens, pinned, out, residual, s);
@@ -39,8 +38,8 @@ int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t 
     MatvecArgs a = matvec_args(c, w, contract == 0 ? kActQ8K : kActQ8, scratch.p, tokens, pinned, out, s);
     if (w.tiled) a.residual = residual;
     rc = run_matvec(c, a, w.tiled);
-    if (!rc && residual && !w.tiled && launch_add_residual(out, residual, w.rows * tokens, c->err, s))
-        return hip_fail(c, hipGetLastError(), "residual launch");
+    if (!rc && residual && !w.tiled)
+        rc = launch_result(c, launch_add_residual(out, residual, w.rows * tokens, c->err, s), "residual launch");
     return rc;
 }
 
@@ -63,15 +62,18 @@ void zero(float *p, size_t n) {
     if (p) std::memset(p, 0, sizeof(float) * n);
 }
 
-// Shared front half of the synchronous host-pointer projections.
+// Shared front half of the projections.  *out is the weight whenever the id is known,
+// also when the call then fails, so the caller can clear rows*tokens outputs.
 int prepare_weight(prism_hip_ctx *c, prism_weight_id wid, int path, const Weight **out) {
+    *out = nullptr;
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    const Weight *w = find(c, wid);
+    *out = w;
     int rc = check_ready(c);
     if (rc) return rc;
-    const Weight *w = find(c, wid);
     if (!w) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
     if (!eligible(w->kind, w->cols, w->rows, path))
         return fail(c, PRISM_ERR_UNSUPPORTED, "projection not supported for this tensor");
-    *out = w;
     return PRISM_OK;
 }
 
@@ -118,9 +120,11 @@ int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Wei
         if (!rc)
             rc = matvec(c, u, contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned, static_cast<float *>(c->up.p), s);
         if (rc) return rc;
-        if (launch_swiglu(static_cast<float *>(c->gate.p), static_cast<float *>(c->up.p), hv, g.rows, 1, pinned, c->err,
-                          s))
-            return hip_fail(c, hipGetLastError(), "swiglu launch");
+        rc = launch_result(c,
+                           launch_swiglu(static_cast<float *>(c->gate.p), static_cast<float *>(c->up.p), hv, g.rows, 1,
+                                         pinned, c->err, s),
+                           "swiglu launch");
+        if (rc) return rc;
     }
     if (!d) return PRISM_OK;
     return project_f32_dev(c, *d, hv, 1, pinned, out, c->act2, s, residual);
@@ -214,7 +218,7 @@ static int check_geometry(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64
 // layout when the geometry allows it (the native copy serves every other shape).
 static prism_weight_id store_weight(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
                                     const void *native, uint64_t bytes) {
-    const bool tiled = tiled_supported(kind, cols, rows);
+    const bool tiled = tiled_supported(kind, cols, rows, c->cus);
     const uint64_t row_bytes = bytes / rows;
     const uint64_t dev_bytes = tiled ? tiled_bytes(rows, row_bytes) : bytes;
     void *dev = nullptr;
@@ -222,7 +226,14 @@ static prism_weight_id store_weight(prism_hip_ctx *c, uint64_t key, uint32_t kin
     if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(weights)");
     if (tiled) {
         e = hipMemsetAsync(dev, 0, dev_bytes, c->stream);
-        if (e == hipSuccess && launch_repack(native, dev, kind, cols, rows, c->stream)) e = hipGetLastError();
+        if (e == hipSuccess) {
+            const int lr = launch_repack(native, dev, kind, cols, rows, c->stream);
+            if (lr < 0) {
+                (void)hipFree(dev);
+                return fail(c, PRISM_ERR_UNSUPPORTED, "no tiled layout for this tensor");
+            }
+            e = static_cast<hipError_t>(lr);
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     } else {
         e = hipMemcpy(dev, native, bytes, hipMemcpyDeviceToDevice);
@@ -323,7 +334,7 @@ int prism_hip_project_q8k(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, PRISM_PATH_Q8K, &w);
     if (rc) {
-        if (c && w) zero(out, w->rows * tokens);
+        if (w) zero(out, w->rows * tokens);
         return rc;
     }
     const size_t n = w->rows * tokens;
@@ -348,7 +359,10 @@ int prism_hip_project_q8(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_b
                          uint32_t tokens, int pinned, float *out) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, PRISM_PATH_Q8, &w);
-    if (rc) return rc;
+    if (rc) {
+        if (w) zero(out, w->rows * tokens);
+        return rc;
+    }
     const size_t n = w->rows * tokens;
     if (!act || !out || tokens == 0 || nblocks != w->cols / 32 * tokens) {
         zero(out, n);
@@ -371,7 +385,10 @@ static int project_f32_host(prism_hip_ctx *c, prism_weight_id wid, const float *
                             float *out) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, PRISM_PATH_F32, &w);
-    if (rc) return rc;
+    if (rc) {
+        if (w) zero(out, w->rows * tokens);
+        return rc;
+    }
     const size_t n = w->rows * tokens;
     if (!x || !out || tokens == 0) {
         zero(out, n);
@@ -406,16 +423,26 @@ int prism_hip_mul_mat(prism_hip_ctx *c, prism_weight_id a, const float *b, uint3
 
 int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, int pinned,
                                 float *const *outs) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    if (!ws || !outs || n == 0 || n > 8) return fail(c, PRISM_ERR_INVALID_INPUT, "bad projection group");
+    const Weight *w[8] = {};
+    for (uint32_t i = 0; i < n; ++i) w[i] = find(c, ws[i]);
+    // Clears every output whose weight is known (the others have no known length).
+    auto clear = [&](int code) {
+        for (uint32_t i = 0; i < n; ++i)
+            if (w[i] && outs[i]) zero(outs[i], w[i]->rows);
+        return code;
+    };
     int rc = check_ready(c);
-    if (rc) return rc;
-    if (!ws || !outs || !x || n == 0 || n > 8) return fail(c, PRISM_ERR_INVALID_INPUT, "bad projection group");
-    const Weight *w[8];
+    if (rc) return clear(rc);
+    if (!x) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "null input"));
     for (uint32_t i = 0; i < n; ++i) {
-        w[i] = find(c, ws[i]);
-        if (!w[i] || !outs[i]) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id in group");
+        if (!w[i] || !outs[i]) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id in group"));
+        if (!eligible(w[i]->kind, w[i]->cols, w[i]->rows, PRISM_PATH_F32))
+            return clear(fail(c, PRISM_ERR_UNSUPPORTED, "projection not supported for this tensor"));
         if (w[i]->cols != w[0]->cols ||
             contract_for(w[i]->kind, w[i]->cols, pinned) != contract_for(w[0]->kind, w[0]->cols, pinned))
-            return fail(c, PRISM_ERR_INVALID_INPUT, "group members do not share an activation contract");
+            return clear(fail(c, PRISM_ERR_INVALID_INPUT, "group members do not share an activation contract"));
     }
     uint64_t total = 0;
     for (uint32_t i = 0; i < n; ++i) total += w[i]->rows;
@@ -442,20 +469,29 @@ int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uin
         off += w[i]->rows;
     }
     if (!rc) rc = drain(c, c->stream);
-    if (rc)
-        for (uint32_t i = 0; i < n; ++i)
-            if (w[i]) zero(outs[i], w[i]->rows);
-    return rc;
+    return rc ? clear(rc) : rc;
 }
 
 static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did, const float *x,
                     const float *residual, int pinned, float *out) {
-    int rc = check_ready(c);
-    if (rc) return rc;
+    if (!c) return PRISM_ERR_INVALID_INPUT;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
-    if (!g || !u || (did && !d)) return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
+    // Output length: down's rows, or gate's for the SwiGLU vector; known when those ids are.
+    const Weight *shape = did ? d : g;
+    int rc = check_ready(c);
+    if (rc) {
+        if (shape) zero(out, shape->rows);
+        return rc;
+    }
+    if (!g || !u || (did && !d)) {
+        if (shape) zero(out, shape->rows);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
+    }
     const uint64_t nout = d ? d->rows : g->rows;
-    if (!x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
+    if (!x || !out) {
+        zero(out, nout);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
+    }
     const bool kind_ok = (g->kind == PRISM_KIND_PQ2 || g->kind == PRISM_KIND_Q2_K || g->kind == PRISM_KIND_PTQ1 ||
                           g->kind == PRISM_KIND_Q8_0 || g->kind == PRISM_KIND_TQ1_0 || g->kind == PRISM_KIND_TQ2_0) &&
                          (!d || d->kind == g->kind);
@@ -489,6 +525,7 @@ int prism_hip_ffn_swiglu(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id
 
 int prism_hip_ffn_chain(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                         const float *x, const float *residual, int pinned, float *out) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
     if (down == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "down projection required");
     return ffn_host(c, gate, up, down, x, residual, pinned, out);
 }
@@ -498,7 +535,9 @@ int prism_hip_quantize_q8k_device(prism_hip_ctx *c, const float *x, uint64_t col
     int rc = check_ready(c);
     if (rc) return rc;
     if (!x || !out || cols == 0 || cols % 256) return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_K needs cols % 256 == 0");
-    return quantize(c, 0, x, cols, tokens, pinned, out, stream ? static_cast<hipStream_t>(stream) : c->stream);
+    hipStream_t s;
+    rc = call_stream(c, stream, &s);
+    return rc ? rc : quantize(c, 0, x, cols, tokens, pinned, out, s);
 }
 
 int prism_hip_quantize_q8_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int contract,
@@ -507,9 +546,10 @@ int prism_hip_quantize_q8_device(prism_hip_ctx *c, const float *x, uint64_t cols
     if (rc) return rc;
     if (!x || !out || cols == 0 || cols % 32 || contract < 0 || contract > 2)
         return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_0 needs cols % 32 == 0 and a known contract");
-    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
-    if (launch_quantize_q8_0(x, cols, tokens, contract, out, c->err, s)) return hip_fail(c, hipGetLastError(), "quantize");
-    return PRISM_OK;
+    hipStream_t s;
+    rc = call_stream(c, stream, &s);
+    if (rc) return rc;
+    return launch_result(c, launch_quantize_q8_0(x, cols, tokens, contract, out, c->err, s), "quantize");
 }
 
 int prism_hip_project_device(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act, uint32_t tokens,
@@ -518,7 +558,9 @@ int prism_hip_project_device(prism_hip_ctx *c, prism_weight_id wid, int path, co
     int rc = prepare_weight(c, wid, path, &w);
     if (rc) return rc;
     if (!act || !out || tokens == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
-    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    hipStream_t s;
+    rc = call_stream(c, stream, &s);
+    if (rc) return rc;
     if (path == PRISM_PATH_F32)
         return project_f32_dev(c, *w, static_cast<const float *>(act), tokens, pinned, out, c->act, s);
     return matvec(c, *w, path == PRISM_PATH_Q8K ? kActQ8K : kActQ8, act, tokens, pinned, out, s);
@@ -532,7 +574,9 @@ int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weig
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
     if (!g || !u || (did && !d) || !x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
     if (d && d->kind != g->kind) return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind");
-    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+    hipStream_t s;
+    rc = call_stream(c, stream, &s);
+    if (rc) return rc;
     // Without a down projection the call is project_f32_ffn_swiglu: out receives h.
     if (!d) return ffn_chain_impl(c, *g, *u, nullptr, x, nullptr, pinned, nullptr, out, s);
     return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, s);
@@ -541,7 +585,9 @@ int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weig
 int prism_hip_sync(prism_hip_ctx *c, void *stream) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
-    return drain(c, stream ? static_cast<hipStream_t>(stream) : c->stream);
+    hipStream_t s;
+    const int rc = call_stream(c, stream, &s);
+    return rc ? rc : drain(c, s);
 }
 
 void *prism_hip_stream(prism_hip_ctx *c) { return c ? static_cast<void *>(c->stream) : nullptr; }

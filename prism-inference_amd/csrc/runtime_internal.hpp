@@ -74,12 +74,46 @@ inline int fail(prism_hip_ctx *c, int code, const std::string &msg) {
     return code;
 }
 
-// Maps a HIP failure to the latched device-fault state.
+// HIP errors after which the device or its queue can no longer be trusted: the
+// context latches them.  The reference latches device loss, a submission timeout and
+// a failed fence wait (tools/adreno-vulkan/src/device.rs:1450-1490); argument and
+// launch-configuration errors return an error and leave the context usable.
+inline bool device_fault(hipError_t e) {
+    switch (e) {
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorLaunchTimeOut:
+    case hipErrorPriorLaunchFailure:
+    case hipErrorECCNotCorrectable:
+    case hipErrorAssert:
+    case hipErrorNoDevice:
+    case hipErrorContextIsDestroyed:
+    case hipErrorDeinitialized:
+    case hipErrorRuntimeMemory:
+    case hipErrorRuntimeOther:
+    case hipErrorUnknown: return true;
+    default: return false;
+    }
+}
+
+// Maps a HIP failure to an ABI code; only device faults latch.
 inline int hip_fail(prism_hip_ctx *c, hipError_t e, const char *what) {
     std::string m = std::string(what) + ": " + hipGetErrorString(e);
-    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return fail(c, PRISM_ERR_RESOURCE, m);
-    c->faulted = true;
-    return fail(c, PRISM_ERR_DEVICE_FAULT, m);
+    if (e == hipErrorOutOfMemory || e == hipErrorLaunchOutOfResources) return fail(c, PRISM_ERR_RESOURCE, m);
+    if (device_fault(e)) {
+        c->faulted = true;
+        return fail(c, PRISM_ERR_DEVICE_FAULT, m);
+    }
+    if (e == hipErrorInvalidValue || e == hipErrorInvalidDevicePointer || e == hipErrorInvalidHandle)
+        return fail(c, PRISM_ERR_INVALID_INPUT, m);
+    return fail(c, PRISM_ERR_UNSUPPORTED, m);
+}
+
+// Maps a launcher's status (kernels.hpp launch_status) to an ABI code.
+inline int launch_result(prism_hip_ctx *c, int rc, const char *what) {
+    if (rc == 0) return PRISM_OK;
+    if (rc < 0) return fail(c, PRISM_ERR_UNSUPPORTED, std::string(what) + ": geometry not supported by the kernels");
+    return hip_fail(c, static_cast<hipError_t>(rc), what);
 }
 
 #define HIP_OR_FAIL(ctx, call)                                 \
@@ -88,8 +122,15 @@ inline int hip_fail(prism_hip_ctx *c, hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
     } while (0)
 
+// Grows a scratch buffer.  Work runs on the context stream only, so a capture in
+// progress there means the buffer is about to be baked into a graph: growing it would
+// free memory the graph already references, so that is refused (size the scratch with
+// one uncaptured call first).
 inline int ensure(prism_hip_ctx *c, DevBuf &b, size_t bytes) {
     if (bytes <= b.cap) return PRISM_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(c->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(c, PRISM_ERR_UNSUPPORTED, "scratch would grow during graph capture: run the call once uncaptured");
     if (b.p) (void)hipFree(b.p);
     b.p = nullptr;
     b.cap = 0;
@@ -97,6 +138,16 @@ inline int ensure(prism_hip_ctx *c, DevBuf &b, size_t bytes) {
     hipError_t e = hipMalloc(&b.p, n);
     if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(scratch)");
     b.cap = n;
+    return PRISM_OK;
+}
+
+// The stream a device-pointer call runs on.  The context's scratch buffers and error
+// flag are shared by all of its calls, so they are ordered on the one context stream;
+// another stream would race on them and is rejected.
+inline int call_stream(prism_hip_ctx *c, void *stream, hipStream_t *out) {
+    if (stream && static_cast<hipStream_t>(stream) != c->stream)
+        return fail(c, PRISM_ERR_INVALID_INPUT, "device calls run on the context stream (NULL or prism_hip_stream)");
+    *out = c->stream;
     return PRISM_OK;
 }
 
@@ -117,7 +168,7 @@ inline int drain(prism_hip_ctx *c, hipStream_t s) {
     int flag = 0;
     HIP_OR_FAIL(c, hipMemcpy(&flag, c->err, sizeof(int), hipMemcpyDeviceToHost));
     if (flag) {
-        if (launch_fill_i32(c->err, 0, 1, s)) return hip_fail(c, hipGetLastError(), "reset error flag");
+        if (const int e = launch_fill_i32(c->err, 0, 1, s)) return launch_result(c, e, "reset error flag");
         HIP_OR_FAIL(c, hipStreamSynchronize(s));
         if (flag & kErrInput) return fail(c, PRISM_ERR_NONFINITE, "non-finite activation input");
         if (flag & kErrQuantRange) return fail(c, PRISM_ERR_NONFINITE, "activation quantization scale overflow");
@@ -133,8 +184,7 @@ inline int quantize(prism_hip_ctx *c, int contract, const float *x, uint64_t col
                                                                                 : (pinned ? PRISM_Q8_PINNED
                                                                                           : PRISM_Q8_SOURCE),
                                                   out, c->err, s);
-    if (rc) return hip_fail(c, hipGetLastError(), "quantize launch");
-    return PRISM_OK;
+    return launch_result(c, rc, "quantize launch");
 }
 
 inline size_t act_bytes(int contract, uint64_t cols, uint32_t tokens) {
@@ -172,10 +222,7 @@ inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &args, bool tiled) {
             a.scratch_bytes = c->sk.cap;
         }
     }
-    int rc = tiled ? launch_matvec_tiled(a) : launch_matvec(a);
-    if (rc == -2) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported matvec geometry");
-    if (rc) return hip_fail(c, hipGetLastError(), "matvec launch");
-    return PRISM_OK;
+    return launch_result(c, tiled ? launch_matvec_tiled(a) : launch_matvec(a), "matvec launch");
 }
 
 inline int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,

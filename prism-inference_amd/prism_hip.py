@@ -467,19 +467,24 @@ class Decoder:
         if not self._h:
             raise PrismError(ERR_INVALID_INPUT, lib().prism_hip_last_error(ctx._h).decode())
         try:
+            self.set_weights(model)
             for i, L in enumerate(model["layers"]):
-                arrs = [np.ascontiguousarray(L[n]) for n in ("qkv", "o", "gate", "up", "down")]
-                norms = [np.ascontiguousarray(L[n], np.float32) for n in ("norm", "post_norm", "q_norm", "k_norm")]
-                self._check(lib().prism_hip_decoder_set_layer(self._h, i, *(_ptr(a) for a in arrs + norms)))
                 k = np.ascontiguousarray(L["k_prefill"], np.uint16)
                 v = np.ascontiguousarray(L["v_prefill"], np.uint16)
                 self._check(lib().prism_hip_decoder_set_cache(self._h, i, _ptr(k), _ptr(v), L["kv_prefill"]))
-            lm = np.ascontiguousarray(model["lm_head"])
-            on = np.ascontiguousarray(model["output_norm"], np.float32)
-            self._check(lib().prism_hip_decoder_set_head(self._h, _ptr(lm), _ptr(on)))
         except Exception:
             self.close()
             raise
+
+    def set_weights(self, model: dict) -> None:
+        """Uploads every layer's tensors and the LM head / final norm."""
+        for i, L in enumerate(model["layers"]):
+            arrs = [np.ascontiguousarray(L[n]) for n in ("qkv", "o", "gate", "up", "down")]
+            norms = [np.ascontiguousarray(L[n], np.float32) for n in ("norm", "post_norm", "q_norm", "k_norm")]
+            self._check(lib().prism_hip_decoder_set_layer(self._h, i, *(_ptr(a) for a in arrs + norms)))
+        lm = np.ascontiguousarray(model["lm_head"])
+        on = np.ascontiguousarray(model["output_norm"], np.float32)
+        self._check(lib().prism_hip_decoder_set_head(self._h, _ptr(lm), _ptr(on)))
 
     def _check(self, rc: int) -> None:
         if rc != OK:

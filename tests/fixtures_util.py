@@ -93,3 +93,44 @@ def pq2_block(scale: int, symbols) -> bytes:
         b[2 + idx // 4] &= ~(3 << shift) & 0xFF
         b[2 + idx // 4] |= sym << shift
     return bytes(b)
+
+
+Q8_DTYPE = np.dtype([("scale", "<f4"), ("sum", "<f4"), ("values", "i1", (32,))])
+
+
+def q8_0_order_kats():
+    """Known answers for the Q8_0 x Q8_0 row chain out = fl(out + fl(fl(d_w*d_a)*s))
+    (src/kernels.rs:1204-1248), derived by hand from binary32 round-to-nearest-even:
+
+    A  two blocks, terms 2^-10 and fl((1+2^-10)*16385) = 16401 (16401 + 2^-10 is a tie,
+       kept even); 2^-10 + 16401 ties again -> 16401.  A fused last step would give
+       fl(2^-10 + 16401.0009765625) = 16401.001953125.
+    B  terms 2^24, 1, 1 in block order: (2^24 + 1) ties to 2^24, then 2^24 again.  The
+       reverse order (or a tree) gives 2^24 + 2.
+    C  one block, d_w = 1 - 2^-11, d_a = 2 - 2^-10, s = 8197: d_w*d_a is exact
+       (2 - 2^-9 + 2^-21), times 8197 = 16377.99414300918... -> 16377.994140625.
+       Scaling s by d_a first gives 16385.99609375 (a tie), then 16377.9951171875.
+
+    Returns (name, weight row bytes, activation blocks, expected bits, wrong bits)."""
+    def wblock(d_bits, codes):
+        c = np.zeros(32, np.int8)
+        c[:len(codes)] = codes
+        return int(d_bits).to_bytes(2, "little") + c.tobytes()
+
+    def act(scale, codes):
+        a = np.zeros(1, Q8_DTYPE)
+        a["scale"] = np.float32(scale)
+        a["values"][0, :len(codes)] = codes
+        return a
+
+    cases = []
+    w = wblock(0x1400, [1]) + wblock(0x3C01, [127, 16])
+    a = np.concatenate([act(1.0, [1]), act(1.0, [127, 16])])
+    cases.append(("A unfused step", w, a, 0x46802200, 0x46802201))
+    w = wblock(0x6400, [64, 64, 64, 64]) + wblock(0x3C00, [1]) + wblock(0x3C00, [1])
+    a = np.concatenate([act(1.0, [64, 64, 64, 64]), act(1.0, [1]), act(1.0, [1])])
+    cases.append(("B block order", w, a, 0x4B800000, 0x4B800001))
+    w = wblock(0x3BFF, [127, 23])
+    a = act(np.float16(2 - 2 ** -10), [64, 3])
+    cases.append(("C scale product first", w, a, 0x467FE7FA, 0x467FE7FB))
+    return cases

@@ -17,6 +17,7 @@ Sources (paths relative to the reference checkout):
   tests/fixtures/upstream-kquants.json                K-quant encode/decode/dot records
   tests/upstream_prism/pq2-inputs.bin                 15 upstream PQ2 row-shape inputs
   tests/fixtures/upstream-tquants.json                TQ1_0/TQ2_0 encode/decode/dot records
+  tests/fixtures/swift-activation-parity.json         pinned SiLU / SwiGLU native captures
 """
 
 import hashlib
@@ -40,6 +41,7 @@ COPY = [
     "tests/fixtures/swift-ptq1-dot-parity.json",
     "tests/upstream_prism/pq2-inputs.bin",
     "tests/fixtures/upstream-tquants.json",
+    "tests/fixtures/swift-activation-parity.json",
 ]
 
 

@@ -110,3 +110,23 @@ def test_gpu_decoder_rejects_bad_arguments(ctx):
     bad["geometry"]["head_dim"] = 64
     with pytest.raises(ph.PrismError):
         ph.Decoder(ctx, bad)
+
+
+def test_gpu_decoder_detects_released_weights(ctx):
+    """prism_hip_weight_release_all drops the decoder's tensors too: generate must then
+    fail with INVALID_INPUT (not read freed memory), and setting the tensors again makes
+    the decoder usable."""
+    model = synth.decoder_model(7, kv_prefill=8, **SMALL)
+    dec = ph.Decoder(ctx, model, max_steps=4)
+    try:
+        toks, _, _ = dec.generate(1, 8, 2, graph=True)
+        ctx.release_all()
+        with pytest.raises(ph.PrismError) as e:
+            dec.generate(1, 8, 2, graph=True)
+        assert e.value.code == ph.ERR_INVALID_INPUT
+        assert not ctx.faulted
+        dec.set_weights(model)
+        again, _, _ = dec.generate(1, 8, 2, graph=True)
+        assert np.array_equal(toks, again)
+    finally:
+        dec.close()

@@ -557,6 +557,64 @@ def test_gpu_errors_clear_output_and_do_not_latch(ctx):
     ctx.release(good)
 
 
+def test_gpu_failed_calls_clear_outputs(ctx):
+    """Every failing projection zero-fills the outputs whose length it knows, whatever the
+    failure: an ineligible path (Q8_K activations for a Q8_0 weight), a bad extent, an
+    unknown weight in a group, a null input."""
+    rows, cols = 40, 256
+    q8 = ctx.weight(ph.KIND_Q8_0, cols, rows, synth.q8_0_weights(rows, cols, seed=3))
+    rc, out = ctx.project_q8k(q8, rows, np.zeros(1, ph.Q8K_DTYPE), check=False)
+    assert rc == ph.ERR_UNSUPPORTED and out.shape == (rows,) and not out.any()
+    rc, out = ctx.project_q8(q8, rows, np.zeros(2, ph.Q8_DTYPE), check=False)
+    assert rc == ph.ERR_INVALID_INPUT and not out.any()
+    good = ctx.weight(ph.KIND_PTQ1, cols, rows, synth.ptq1_weights(rows, cols, seed=4))
+    rc, outs = ctx.project_f32_group([good, 987654321], [rows, rows], synth.activations(cols, 5), check=False)
+    assert rc == ph.ERR_INVALID_INPUT and not outs[0].any()
+    assert not ctx.faulted
+    ctx.release(q8)
+    ctx.release(good)
+
+
+def test_gpu_device_calls_reject_a_foreign_stream(ctx):
+    """Device-pointer calls share the context's scratch and error flag, so they run on the
+    context stream only; another stream is an argument error that does not latch."""
+    rows, cols = 64, 256
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, synth.ptq1_weights(rows, cols, seed=6))
+    x = DeviceBuffer.from_numpy(synth.activations(cols, 6))
+    out = DeviceBuffer(rows * 4)
+    with ph.Context(0) as other:
+        foreign = other.stream()
+        with pytest.raises(ph.PrismError) as e:
+            ctx.project_device(wid, ph.PATH_F32, x, 1, False, out, foreign)
+        assert e.value.code == ph.ERR_INVALID_INPUT
+    assert not ctx.faulted
+    ctx.project_device(wid, ph.PATH_F32, x, 1, False, out, ctx.stream())
+    assert ctx.sync() == 0
+    ctx.release(wid)
+
+
+@pytest.mark.parametrize("kind", [ph.KIND_PTQ1, ph.KIND_PQ2, ph.KIND_Q8_0])
+def test_gpu_wide_small_matrix_keeps_a_layout_every_order_can_run(ctx, kind):
+    """One 64-row tile of 32768 inputs: the small-matrix kernel's LDS cannot hold the
+    pinned PTQ1 terms of such rows, so the tensor keeps the native layout (no width limit)
+    where needed; every contract must run and match the oracle, without a latch."""
+    import oracle
+
+    rows, cols = 64, 32768
+    w = synth.weights(kind, rows, cols, seed=kind + 9)
+    x = synth.activations(cols, seed=kind + 10)
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, x, pinned, threads=THREADS)
+        assert_bits_equal(ctx.project_f32(wid, rows, x, pinned=pinned), ref, f"wide pinned={pinned}")
+    if kind != ph.KIND_PQ2:
+        act = oracle.quantize_q8_0(x, 2)
+        ref = oracle.project_q8(kind, cols, rows, w, act, True, threads=THREADS)
+        assert_bits_equal(ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=True), ref, "wide q8 pinned")
+    assert not ctx.faulted
+    ctx.release(wid)
+
+
 def test_gpu_weight_cache_by_key_and_budget():
     with ph.Context(0, max_resident_bytes=4096) as c:
         w = synth.ptq1_weights(16, 256, seed=1)
@@ -570,21 +628,98 @@ def test_gpu_weight_cache_by_key_and_budget():
 
 # ---- device-pointer path and determinism ----------------------------------------------
 
-def test_gpu_device_pointer_path_matches_host_path(ctx):
+def test_gpu_device_pointer_path_matches_oracle(ctx):
+    """prism_hip_project_device on a context-owned (tiled) copy of device bytes, with
+    device input and output, equals the oracle; so does a repeated host call."""
+    import oracle
+
     rows, cols = 300, 4096
     for kind in (ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_Q8_0, ph.KIND_PQ2):
         w = synth.weights(kind, rows, cols, seed=kind + 1)
         x = synth.activations(cols, seed=12)
-        wd = DeviceBuffer.from_numpy(w)
-        wid = ctx.weight_device(kind, cols, rows, wd)
+        wid = ctx.weight_from_device(kind, cols, rows, DeviceBuffer.from_numpy(w))
+        ref = oracle.matvec(kind, cols, rows, w, x, False, threads=THREADS)
         out = DeviceBuffer(rows * 4)
         ctx.project_device(wid, ph.PATH_F32, DeviceBuffer.from_numpy(x), 1, False, out)
         assert ctx.sync() == 0
-        host = ctx.project_f32(wid, rows, x)
-        assert_bits_equal(out.to_numpy(np.float32), host, f"device path kind={kind}")
-        again = ctx.project_f32(wid, rows, x)
-        assert_bits_equal(again, host, "repeat")
+        assert_bits_equal(out.to_numpy(np.float32), ref, f"device path kind={kind}")
+        assert_bits_equal(ctx.project_f32(wid, rows, x), ref, f"host path kind={kind}")
         ctx.release(wid)
+
+
+# Native row-major weights registered with prism_hip_weight_wrap_device run the
+# native-layout kernels (matvec.hip): k_matvec in its unit-count buckets (16, 32, 48,
+# 64 units with 16 lanes per row; 128 and 256 units with 64 lanes), four or one
+# wavefronts per workgroup by the LDS the terms need, and k_matvec_generic for odd-group
+# PQ2 and rows beyond 256 units or the LDS limit.  rows = 37: two full 16-row tiles and
+# a partial one.
+NATIVE = [(k, c) for c in (2048, 4096, 6144, 8192, 16384, 32768)
+          for k in (ph.KIND_PTQ1, ph.KIND_PQ2, ph.KIND_Q2_K, ph.KIND_Q8_0)] + \
+         [(ph.KIND_PQ2, 384), (ph.KIND_PQ2, 1152), (ph.KIND_PTQ1, 33024), (ph.KIND_Q8_0, 33024)]
+
+
+@pytest.mark.parametrize("kind,cols", NATIVE)
+def test_gpu_wrapped_native_rows_match_oracle(ctx, kind, cols):
+    import oracle
+
+    rows = 37
+    w = synth.weights(kind, rows, cols, seed=cols + kind) if kind != ph.KIND_PQ2 else \
+        synth.pq2_weights(rows, cols, seed=cols, levels=4)
+    x = synth.activations(cols, seed=cols + 7)
+    wd = DeviceBuffer.from_numpy(w)
+    wid = ctx.weight_device(kind, cols, rows, wd)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, x, pinned, threads=THREADS)
+        assert_bits_equal(ctx.project_f32(wid, rows, x, pinned=pinned), ref, f"native f32 pinned={pinned}")
+    if kind in (ph.KIND_PTQ1, ph.KIND_Q8_0) or (kind == ph.KIND_PQ2 and cols % 256):
+        for contract in (0, 1, 2):
+            act = oracle.quantize_q8_0(x, contract)
+            for pinned in (False, True):
+                ref = oracle.project_q8(kind, cols, rows, w, act, pinned, threads=THREADS)
+                got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=pinned)
+                assert_bits_equal(got, ref, f"native q8 contract={contract} pinned={pinned}")
+    if kind != ph.KIND_Q8_0 and cols % 256 == 0:
+        for fused in (False, True):
+            act = oracle.quantize_q8k(x, fused)
+            if kind == ph.KIND_PTQ1:
+                nb = cols // 128 * 28
+                ref = np.array([oracle.dot_ptq1_q8k(w[r * nb:(r + 1) * nb], act) for r in range(rows)], np.float32)
+            else:
+                ref = oracle.project_q8k(kind, cols, rows, w, act, fused, threads=THREADS)
+            got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), fused=fused)
+            assert_bits_equal(got, ref, f"native q8k fused={fused}")
+    ctx.release(wid)
+
+
+def test_gpu_wrapped_native_multi_token_matches_oracle(ctx):
+    """Several tokens through the native-layout kernels (one launch per token)."""
+    import oracle
+
+    rows, cols, M = 70, 2048, 3
+    for kind in (ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_Q8_0, ph.KIND_PQ2):
+        w = synth.weights(kind, rows, cols, seed=kind + 3)
+        X = synth.activations(cols, seed=kind, tokens=M)
+        wd = DeviceBuffer.from_numpy(w)
+        wid = ctx.weight_device(kind, cols, rows, wd)
+        for pinned in (False, True):
+            ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+            assert_bits_equal(ctx.project_f32(wid, rows, X, tokens=M, pinned=pinned), ref, f"native tokens {kind}")
+        ctx.release(wid)
+
+
+def test_gpu_q8_0_rounding_order_known_answers(ctx):
+    """The hand-derived Q8_0 x Q8_0 answers (fixtures_util.q8_0_order_kats) on the tiled
+    and the native-layout kernels."""
+    for name, w, act, want, _ in fx.q8_0_order_kats():
+        cols = len(w) // 34 * 32
+        act = act.view(ph.Q8_DTYPE)
+        tiled = ctx.weight(ph.KIND_Q8_0, cols, 1, w)
+        assert int(bits(ctx.project_q8(tiled, 1, act))[0]) == want, name
+        ctx.release(tiled)
+        wd = DeviceBuffer.from_numpy(np.frombuffer(w, np.uint8).copy())
+        native = ctx.weight_device(ph.KIND_Q8_0, cols, 1, wd)
+        assert int(bits(ctx.project_q8(native, 1, act))[0]) == want, name
+        ctx.release(native)
 
 
 @pytest.mark.parametrize("kind", [ph.KIND_TQ1_0, ph.KIND_TQ2_0])

@@ -201,6 +201,27 @@ def test_q8_0_dot_exact_when_every_product_is_representable(oracle):
     assert float(oracle.dot_q8_0(bytes(w), act)) == exact
 
 
+def test_q8_0_dot_rounding_order_known_answers(oracle):
+    """Hand-derived binary32 answers that a fused final step, a reordered block chain or
+    the activation scale applied before the weight scale would each miss (derivations in
+    fixtures_util.q8_0_order_kats)."""
+    for name, w, act, want, wrong in fx.q8_0_order_kats():
+        act = act.view(oracle.Q8_DTYPE)
+        assert _bits(oracle.dot_q8_0(w, act)) == want, name
+        assert want != wrong
+    # The alternative orders really produce the `wrong` bits (so each KAT separates them).
+    f = np.float32
+    (_, _, _, _, wa), (_, _, _, _, wb), (_, _, _, _, wc) = fx.q8_0_order_kats()
+    fused = np.float32(float(2.0 ** -10) + float(f(1 + 2 ** -10)) * 16385)  # one rounding
+    assert _bits(fused) == wa
+    rev = f(0)
+    for t in (1.0, 1.0, 2.0 ** 24):
+        rev = f(rev + f(t))
+    assert _bits(rev) == wb
+    dw, da = f(np.float16(1 - 2 ** -11)), f(np.float16(2 - 2 ** -10))
+    assert _bits(f(dw * f(da * f(8197)))) == wc
+
+
 def test_ptq1_q8k_dot_equals_pq2_unfused_on_lossless_codec(oracle):
     rng = np.random.default_rng(9)
     nb = 8
@@ -294,3 +315,44 @@ def test_vector_exp_close_to_expf(oracle):
     got = np.array([oracle.vector_exp(float(x)) for x in xs], np.float32)
     ref = np.exp(xs.astype(np.float64))
     assert np.max(np.abs(got / ref - 1)) < 4e-7
+
+
+def _native_activation_bits(got, expected, what):
+    """assert_native of src/kernels/pinned_activations.rs:236-247: NaN matches any NaN,
+    everything else bit for bit."""
+    got = np.asarray(got, np.float32).view(np.uint32)
+    for i, (g, e) in enumerate(zip(got, expected)):
+        if np.isnan(np.uint32(e).view(np.float32)):
+            assert np.isnan(np.uint32(g).view(np.float32)), (what, i)
+        else:
+            assert int(g) == int(e), (what, i, hex(int(g)), hex(int(e)))
+
+
+def test_pinned_silu_and_swiglu_match_native_captures(oracle):
+    """src/kernels/pinned_activations.rs:248-282 on tests/fixtures/swift-activation-parity.json:
+    random rows of 5 and 16 values (a vectorised body and a libm tail) and 24 finite edge
+    values (subnormals, +-0, the exp over/underflow range, the largest finite inputs)."""
+    capture = fx.load_json("swift-activation-parity.json")
+    assert capture["runtime_commit"] == "73bfe6cc485554822f80c473a3c0c4f25e80f41b"
+    assert capture["ggml_cpu_sha256"] == "701b354a38b25e5c6dc57a1559f71cd26b2d0f8d69c1576a0e77a59a4273d2ab"
+    assert len(capture["cases"]) == 3
+    checked = 0
+    for case in capture["cases"]:
+        gate = np.array(case["input_bits"], np.uint32).view(np.float32)
+        up = np.array(case["weight_bits"], np.uint32).view(np.float32)
+        _native_activation_bits(oracle.silu(gate, True), case["silu_bits"], case["name"] + " silu")
+        _native_activation_bits(oracle.swiglu(gate, up, True), case["swiglu_bits"], case["name"] + " swiglu")
+        checked += gate.size
+    assert checked == 45
+
+
+def test_pinned_swiglu_reassociates_the_numerator(oracle):
+    """The pinned order divides the rounded product g*u (pinned_activations.rs:163-166); the
+    source order multiplies u by the rounded SiLU (src/graph.rs:121-131).  A planted swap of
+    the two orders must change bits on random rows, so the capture test above sees it."""
+    rng = np.random.default_rng(7)
+    g = rng.uniform(-10, 10, 4096).astype(np.float32)
+    u = rng.uniform(-2, 2, 4096).astype(np.float32)
+    pinned = oracle.swiglu(g, u, True)
+    swapped = (u * oracle.silu(g, True)).astype(np.float32)
+    assert np.count_nonzero(pinned.view(np.uint32) != swapped.view(np.uint32)) > 100
