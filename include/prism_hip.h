@@ -180,6 +180,21 @@ int prism_hip_project_device(prism_hip_ctx *ctx, prism_weight_id w, int path, co
 int prism_hip_ffn_chain_device(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                                const float *x, const float *residual, int pinned, float *out, float *h,
                                void *stream);
+/* prism_hip_project_device without any device allocation: every scratch buffer the
+ * call's kernels use (the quantized activation, the skinny batch's lane-ordered copy,
+ * the prefill token codes) is carved from one fixed, file-scope device array of
+ * PRISM_NOALLOC_SCRATCH_BYTES per GPU, allocated with the code object when the library
+ * first runs on that GPU and held until the process ends; the call itself never calls
+ * hipMalloc or hipFree.  A call needing more scratch than that returns
+ * PRISM_ERR_UNSUPPORTED before launching anything.  Every call on one GPU (from any
+ * context) shares the array: calls that overlap on one GPU race, so order them on one
+ * stream.  Nothing in the array needs to start at zero: each kernel reads only what an
+ * earlier kernel of the same call wrote.  No counterpart in the reference: this is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops).  Arguments and results as prism_hip_project_device. */
+#define PRISM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int prism_hip_project_device_noalloc(prism_hip_ctx *ctx, prism_weight_id w, int path, const void *act,
+                                     uint32_t tokens, int pinned, float *out, void *stream);
 /* Waits for `stream` (NULL = the context stream) and reports any error the
  * device-side checks raised since the last sync (non-finite values, scale
  * overflow).  Clears the device error flag. */

@@ -17,27 +17,33 @@ namespace {
 // tiled-prefill GEMM instead of one matvec per token.
 constexpr uint32_t kPrefillMinTokens = 16;
 
-// Quantize device floats with the contract matvec_into would use, then project.
+// Quantize device floats with the contract matvec_into would use, then project.  `role`
+// is the grow-mode buffer of the quantized activation; sc == nullptr selects grow mode.
 int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t tokens, int pinned, float *out,
-                    DevBuf &scratch, hipStream_t s, const float *residual = nullptr) {
-    if (w.tiled && tokens >= kPrefillMinTokens && !residual && prefill_supported(w.kind, w.cols, w.rows, pinned, tokens)) {
-        int rc = ensure(c, c->pre, prefill_scratch_bytes(w.cols, tokens));
+                    DevBuf &role, hipStream_t s, const float *residual = nullptr, Scratch *sc = nullptr) {
+    Scratch grow{c};
+    Scratch &scr = sc ? *sc : grow;
+    if (w.tiled && tokens >= kPrefillMinTokens && !residual &&
+        prefill_supported(w.kind, w.cols, w.rows, pinned, tokens)) {
+        void *pre = nullptr;
+        int rc = scr.get(c->pre, prefill_scratch_bytes(w.cols, tokens), &pre);
         if (rc) return rc;
-        return launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, c->pre.p, c->err, s),
+        return launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, pre, c->err, s),
                              "prefill launch");
     }
     if (w.tiled) {
         MatvecArgs a = f32_args(c, w, x, tokens, pinned, out, residual, s);
-        if (!tiled_needs_prepared(a)) return run_matvec(c, a, true);
+        if (!tiled_needs_prepared(a)) return run_matvec(c, a, true, &scr);
     }
     const int contract = contract_for(w.kind, w.cols, pinned);
-    int rc = ensure(c, scratch, act_bytes(contract, w.cols, tokens));
+    void *act = nullptr;
+    int rc = scr.get(role, act_bytes(contract, w.cols, tokens), &act);
     if (rc) return rc;
-    rc = quantize(c, contract, x, w.cols, tokens, pinned, scratch.p, s);
+    rc = quantize(c, contract, x, w.cols, tokens, pinned, act, s);
     if (rc) return rc;
-    MatvecArgs a = matvec_args(c, w, contract == 0 ? kActQ8K : kActQ8, scratch.p, tokens, pinned, out, s);
+    MatvecArgs a = matvec_args(c, w, contract == 0 ? kActQ8K : kActQ8, act, tokens, pinned, out, s);
     if (w.tiled) a.residual = residual;
-    rc = run_matvec(c, a, w.tiled);
+    rc = run_matvec(c, a, w.tiled, &scr);
     if (!rc && residual && !w.tiled)
         rc = launch_result(c, launch_add_residual(out, residual, w.rows * tokens, c->err, s), "residual launch");
     return rc;
@@ -149,6 +155,13 @@ prism_hip_ctx *prism_hip_create(int device, uint64_t max_resident_bytes, uint32_
         return nullptr;
     }
     c->cus = static_cast<uint32_t>(prop.multiProcessorCount);
+    // With `device` current: this GPU's copy of the no-allocation entry point's scratch.
+    const hipError_t se = static_scratch_address(device, &c->noalloc, &c->noalloc_bytes);
+    if (se != hipSuccess) {
+        c->noalloc = nullptr;
+        c->noalloc_bytes = 0;
+        c->noalloc_error = std::string("static scratch lookup: ") + hipGetErrorString(se);
+    }
     char buf[256];
     std::snprintf(buf, sizeof buf, "prism-hip/%s/%d-cu/exact-scalar-order", prop.gcnArchName, prop.multiProcessorCount);
     c->identity = buf;
@@ -564,6 +577,22 @@ int prism_hip_project_device(prism_hip_ctx *c, prism_weight_id wid, int path, co
     if (path == PRISM_PATH_F32)
         return project_f32_dev(c, *w, static_cast<const float *>(act), tokens, pinned, out, c->act, s);
     return matvec(c, *w, path == PRISM_PATH_Q8K ? kActQ8K : kActQ8, act, tokens, pinned, out, s);
+}
+
+int prism_hip_project_device_noalloc(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act,
+                                     uint32_t tokens, int pinned, float *out, void *stream) {
+    const Weight *w = nullptr;
+    int rc = prepare_weight(c, wid, path, &w);
+    if (rc) return rc;
+    if (!act || !out || tokens == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    if (!c->noalloc) return fail(c, PRISM_ERR_UNSUPPORTED, c->noalloc_error);
+    hipStream_t s;
+    rc = call_stream(c, stream, &s);
+    if (rc) return rc;
+    Scratch fixed{c, static_cast<uint8_t *>(c->noalloc), c->noalloc_bytes, 0};
+    if (path == PRISM_PATH_F32)
+        return project_f32_dev(c, *w, static_cast<const float *>(act), tokens, pinned, out, c->act, s, nullptr, &fixed);
+    return matvec(c, *w, path == PRISM_PATH_Q8K ? kActQ8K : kActQ8, act, tokens, pinned, out, s, &fixed);
 }
 
 int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,

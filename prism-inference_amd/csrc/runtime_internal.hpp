@@ -65,7 +65,16 @@ struct prism_hip_ctx {
     int64_t next_id = 1;
     int *err = nullptr;  // device error flag
     prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre, sk;
+    // This device's copy of the fixed scratch array (static_scratch.hip), looked up at
+    // creation; nullptr if the lookup failed.
+    void *noalloc = nullptr;
+    size_t noalloc_bytes = 0;
+    std::string noalloc_error;
 };
+
+namespace prism {
+hipError_t static_scratch_address(int device, void **ptr, size_t *bytes);
+}
 
 namespace prism::rt {
 
@@ -151,6 +160,37 @@ inline int call_stream(prism_hip_ctx *c, void *stream, hipStream_t *out) {
     return PRISM_OK;
 }
 
+// Device scratch of one call.  Grow mode (base == nullptr): each role is one of the
+// context's grow-only buffers.  Fixed mode: every request is carved, 256-byte aligned,
+// from one region that is never grown or freed (the static per-device array of the
+// no-allocation entry point); a call that needs more than the region fails cleanly.
+struct Scratch {
+    prism_hip_ctx *c = nullptr;
+    uint8_t *base = nullptr;
+    size_t cap = 0, used = 0;
+
+    int get(DevBuf &role, size_t bytes, void **p, size_t *got = nullptr) {
+        if (!base) {
+            const int rc = ensure(c, role, bytes);
+            if (rc) return rc;
+            *p = role.p;
+            if (got) *got = role.cap;
+            return PRISM_OK;
+        }
+        const size_t at = (used + 255) & ~size_t(255);
+        if (at > cap || bytes > cap - at) {
+            char m[160];
+            std::snprintf(m, sizeof m, "call needs %zu more bytes of scratch than the %zu-byte static scratch holds",
+                          at + bytes - cap, cap);
+            return fail(c, PRISM_ERR_UNSUPPORTED, m);
+        }
+        used = at + bytes;
+        *p = base + at;
+        if (got) *got = bytes;
+        return PRISM_OK;
+    }
+};
+
 inline int check_ready(prism_hip_ctx *c) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
@@ -211,23 +251,23 @@ inline MatvecArgs matvec_args(prism_hip_ctx *c, const Weight &w, int act_format,
     return a;
 }
 
-inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &args, bool tiled) {
+// sc == nullptr: the context's grow-only buffers.
+inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &args, bool tiled, Scratch *sc = nullptr) {
     MatvecArgs a = args;
     if (tiled) {
         const size_t need = tiled_scratch_bytes(a);
         if (need) {
-            const int e = ensure(c, c->sk, need);
+            Scratch grow{c};
+            const int e = (sc ? *sc : grow).get(c->sk, need, &a.scratch, &a.scratch_bytes);
             if (e) return e;
-            a.scratch = c->sk.p;
-            a.scratch_bytes = c->sk.cap;
         }
     }
     return launch_result(c, tiled ? launch_matvec_tiled(a) : launch_matvec(a), "matvec launch");
 }
 
 inline int matvec(prism_hip_ctx *c, const Weight &w, int act_format, const void *act, uint32_t tokens, int pinned,
-           float *out, hipStream_t s) {
-    return run_matvec(c, matvec_args(c, w, act_format, act, tokens, pinned, out, s), w.tiled);
+           float *out, hipStream_t s, Scratch *sc = nullptr) {
+    return run_matvec(c, matvec_args(c, w, act_format, act, tokens, pinned, out, s), w.tiled, sc);
 }
 
 // f32 input for a tiled weight, quantized in the kernel prologue with the contract

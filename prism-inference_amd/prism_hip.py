@@ -98,6 +98,7 @@ def lib() -> ctypes.CDLL:
         "prism_hip_quantize_q8k_device": (I, [P, P, U64, U32, I, P, P]),
         "prism_hip_quantize_q8_device": (I, [P, P, U64, U32, I, P, P]),
         "prism_hip_project_device": (I, [P, I64, I, P, U32, I, P, P]),
+        "prism_hip_project_device_noalloc": (I, [P, I64, I, P, U32, I, P, P]),
         "prism_hip_ffn_chain_device": (I, [P, I64, I64, I64, P, P, I, P, P, P]),
         "prism_hip_sync": (I, [P, P]),
         "prism_hip_stream": (P, [P]),
@@ -436,6 +437,14 @@ class Context:
 
     def project_device(self, wid: int, path: int, act, tokens: int, pinned: bool, out, stream=None):
         self._check(lib().prism_hip_project_device(self._h, wid, path, _ptr(act), tokens, int(pinned), _ptr(out), stream))
+
+    def project_device_noalloc(self, wid: int, path: int, act, tokens: int, pinned: bool, out, stream=None,
+                               check: bool = True) -> int:
+        rc = lib().prism_hip_project_device_noalloc(self._h, wid, path, _ptr(act), tokens, int(pinned), _ptr(out),
+                                                    stream)
+        if check:
+            self._check(rc)
+        return rc
 
     def ffn_chain_device(self, g, u, d, x, residual, pinned, out, h=None, stream=None):
         self._check(lib().prism_hip_ffn_chain_device(self._h, g, u, d, _ptr(x), _ptr(residual), int(pinned), _ptr(out),
