@@ -9,7 +9,8 @@
 //   attention  q/k norm + RoPE + KV append + scores; softmax + values (decode.hip)
 //   o          PTQ1 split matvec + residual                  -> hidden'
 //   gate/up    PTQ1 split matvec pair, RMSNorm(post_norm) prologue, SwiGLU epilogue
-//   down       PTQ1 split matvec + residual                  -> hidden''
+//              that writes the SwiGLU vector as Q8_0 blocks (source contract)
+//   down       PTQ1 split matvec on those blocks + residual  -> hidden''
 // then the final norm + Q8_0 quantization, the Q8_0 LM head (row-tile kernel) and
 // the greedy choice, which also writes the next step's embedding.
 #include <cmath>
@@ -32,7 +33,8 @@ struct prism_hip_decoder {
     prism_weight_id lm_head = 0;
     float *output_norm = nullptr;
     float *hidden[2] = {nullptr, nullptr};
-    float *qkv = nullptr, *att = nullptr, *ffn_h = nullptr, *scores = nullptr, *logits = nullptr;
+    float *qkv = nullptr, *att = nullptr, *scores = nullptr, *logits = nullptr;
+    void *ffn_q8 = nullptr;  // the SwiGLU vector's Q8_0 blocks
     float *logits_all = nullptr;
     size_t logits_all_steps = 0;
     void *lm_act = nullptr;
@@ -82,15 +84,26 @@ int weight(prism_hip_decoder *d, prism_weight_id *id, uint64_t slot, uint32_t ki
 
 // One projection of a resident weight on device floats: RMSNorm (when norm_w) and
 // the source Q8_0 quantization in the prologue, optional residual, optional up
-// matrix (SwiGLU epilogue).
+// matrix (SwiGLU epilogue, whose vector goes to q8_out as source-contract Q8_0 blocks).
 int project(prism_hip_decoder *d, prism_weight_id wid, const float *x, float *out, const float *residual,
-            const float *norm_w, prism_weight_id up = 0) {
+            const float *norm_w, prism_weight_id up = 0, void *q8_out = nullptr) {
     prism_hip_ctx *c = d->ctx;
     const Weight *w = find(c, wid);
     MatvecArgs a = f32_args(c, *w, x, 1, 0, out, residual, c->stream);
     a.norm_w = norm_w;
     a.eps = d->g.eps;
     if (up) a.w2 = static_cast<const uint8_t *>(find(c, up)->dev);
+    a.q8_out = q8_out;
+    a.q8_contract = PRISM_Q8_SOURCE;
+    return run_matvec(c, a, true);
+}
+
+// A projection of prepared Q8_0 blocks (the source contract's dot_q8_groups) + residual.
+int project_q8(prism_hip_decoder *d, prism_weight_id wid, const void *act, float *out, const float *residual) {
+    prism_hip_ctx *c = d->ctx;
+    const Weight *w = find(c, wid);
+    MatvecArgs a = matvec_args(c, *w, kActQ8, act, 1, 0, out, c->stream);
+    a.residual = residual;
     return run_matvec(c, a, true);
 }
 
@@ -132,8 +145,8 @@ int enqueue_step(prism_hip_decoder *d) {
         rc = launch_result(c, launch_attention(at), "attention launch");
         if (rc) return rc;
         rc = project(d, L.o, d->att, h1, h0, nullptr);
-        if (!rc) rc = project(d, L.gate, h1, d->ffn_h, nullptr, L.post_norm, L.up);
-        if (!rc) rc = project(d, L.down, d->ffn_h, h0, h1, nullptr);
+        if (!rc) rc = project(d, L.gate, h1, nullptr, nullptr, L.post_norm, L.up, d->ffn_q8);
+        if (!rc) rc = project_q8(d, L.down, d->ffn_q8, h0, h1);
         if (rc) return rc;
     }
     const Weight *lm = find(c, d->lm_head);
@@ -203,7 +216,7 @@ prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decode
     if (!rc) rc = dalloc(d, &d->hidden[1], sizeof(float) * H);
     if (!rc) rc = dalloc(d, &d->qkv, sizeof(float) * QKV);
     if (!rc) rc = dalloc(d, &d->att, sizeof(float) * g->heads * D);
-    if (!rc) rc = dalloc(d, &d->ffn_h, sizeof(float) * g->ffn);
+    if (!rc) rc = dalloc(d, &d->ffn_q8, sizeof(prism_q8_block) * (g->ffn / 32));
     if (!rc) rc = dalloc(d, &d->scores, sizeof(float) * g->heads * g->max_tokens);
     if (!rc) rc = dalloc(d, &d->logits, sizeof(float) * g->vocab);
     if (!rc) rc = dalloc(d, &d->lm_act, sizeof(prism_q8_block) * (H / 32));

@@ -21,7 +21,7 @@
 
 #include <sys/stat.h>
 
-#include "../../include/prism_hip.h"
+#include "prism_hip.h"
 
 namespace {
 

@@ -44,6 +44,8 @@ struct MatvecArgs {
     const float *residual = nullptr;  // tiled only: [tokens][rows], added to the outputs
     const float *norm_w = nullptr;    // tiled kActF32 only: RMSNorm weights applied before quantizing
     float eps = 0.0f;                 // RMSNorm epsilon
+    void *q8_out = nullptr;           // tiled w2 only: the SwiGLU vector's Q8_0 blocks (rows % 32 == 0)
+    int q8_contract = 0;              // their contract (PRISM_Q8_*)
     int *err = nullptr;           // device error flag
     hipStream_t stream = nullptr;
     uint32_t cus = 256;           // compute units of the device

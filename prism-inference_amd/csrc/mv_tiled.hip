@@ -71,16 +71,22 @@ __device__ __forceinline__ int bsum4(uint32_t a, int c) { return sdot4(a, 0x0101
 // against the activation codes they multiply; sum (t-1)a = sum t*a - sum a.
 // Element map: byte b<16 digit k -> 16k+b; byte 16+b (b<8) digit k -> 80+8k+b;
 // byte 24+b (b<2) digit k<4 -> 120+2k+b.  acc(q) receives quad q (elements 4q..4q+3).
-template <typename Act, typename Acc>
-__device__ __forceinline__ void ptq1_dots(const uint32_t x[7], const Act &a, Acc &&acc) {
+// A PTQ1 unit with its trits extracted: q[i] holds the digits (0..2) of elements
+// 4i..4i+3 as bytes, d the binary16 scale bits.  The extraction needs no activation,
+// so a kernel can run it while its activation is still being staged.
+struct Ptq1Dec {
+    uint32_t q[32];
+    uint32_t d;
+};
+
+__device__ __forceinline__ void ptq1_decode(const uint32_t x[7], Ptq1Dec &o) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         uint32_t L = x[w] & 0x00ff00ffu, H = (x[w] >> 8) & 0x00ff00ffu;
 #pragma unroll
         for (int k = 0; k < 5; ++k) {
             const uint32_t mL = L * 3u, mH = H * 3u;
-            int &r = acc(4 * k + w);
-            r = sdot4(perm(mH, mL, sel(1, 5, 3, 7)), a(4 * k + w), r);
+            o.q[4 * k + w] = perm(mH, mL, sel(1, 5, 3, 7));
             L = mL & 0x00ff00ffu;
             H = mH & 0x00ff00ffu;
         }
@@ -91,8 +97,7 @@ __device__ __forceinline__ void ptq1_dots(const uint32_t x[7], const Act &a, Acc
 #pragma unroll
         for (int k = 0; k < 5; ++k) {
             const uint32_t mL = L * 3u, mH = H * 3u;
-            int &r = acc(20 + 2 * k + w);
-            r = sdot4(perm(mH, mL, sel(1, 5, 3, 7)), a(20 + 2 * k + w), r);
+            o.q[20 + 2 * k + w] = perm(mH, mL, sel(1, 5, 3, 7));
             L = mL & 0x00ff00ffu;
             H = mH & 0x00ff00ffu;
         }
@@ -105,10 +110,25 @@ __device__ __forceinline__ void ptq1_dots(const uint32_t x[7], const Act &a, Acc
     const uint32_t m2 = T * 3u;
     T = m2 & 0x00ff00ffu;
     const uint32_t m3 = T * 3u;
-    int &r30 = acc(30);
-    r30 = sdot4(perm(m1, m0, sel(1, 3, 5, 7)), a(30), r30);
-    int &r31 = acc(31);
-    r31 = sdot4(perm(m3, m2, sel(1, 3, 5, 7)), a(31), r31);
+    o.q[30] = perm(m1, m0, sel(1, 3, 5, 7));
+    o.q[31] = perm(m3, m2, sel(1, 3, 5, 7));
+    o.d = x[6] >> 16;
+}
+
+template <typename Act, typename Acc>
+__device__ __forceinline__ void ptq1_dot(const Ptq1Dec &D, const Act &a, Acc &&acc) {
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        int &r = acc(q);
+        r = sdot4(D.q[q], a(q), r);
+    }
+}
+
+template <typename Act, typename Acc>
+__device__ __forceinline__ void ptq1_dots(const uint32_t x[7], const Act &a, Acc &&acc) {
+    Ptq1Dec D;
+    ptq1_decode(x, D);
+    ptq1_dot(D, a, acc);
 }
 
 // ---- PTQ1 decode table (LDS) ----------------------------------------------------------
@@ -287,11 +307,17 @@ __device__ __forceinline__ void load_unit(Raw<O> &w, __amdgpu_buffer_rsrc_t rs, 
 // LUT selects the PTQ1 decoder: the SWAR digit extraction (trits 0..2, corrected by
 // the activation sums) or the LDS table (trits already minus one); `lbase` is the
 // lane's table-copy offset.
-template <Op O, bool LUT = false>
-__device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restrict__ act, uint32_t u, float *t,
+// W is the unit's Raw<O>, or for the PTQ1 ops (without LUT) its Ptq1Dec.
+__device__ __forceinline__ uint32_t ptq1_scale_bits(const Raw<Op::PTQ1_SRC> &w) { return w.x[6] >> 16; }
+__device__ __forceinline__ uint32_t ptq1_scale_bits(const Ptq1Dec &w) { return w.d; }
+
+template <Op O, bool LUT = false, typename W = Raw<O>>
+__device__ __forceinline__ void unit_terms(const W &w, const void *__restrict__ act, uint32_t u, float *t,
                                            uint32_t lbase = 0) {
     auto trits = [&](const auto &raw, const auto &a, auto &&acc) {
-        if constexpr (LUT)
+        if constexpr (std::is_same_v<W, Ptq1Dec>)
+            ptq1_dot(raw, a, acc);
+        else if constexpr (LUT)
             ptq1_dots_lut(raw.x, lbase, a, acc);
         else
             ptq1_dots(raw.x, a, acc);
@@ -302,7 +328,7 @@ __device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restri
 #pragma unroll
         for (int g = 0; g < 4; ++g) av[g] = reinterpret_cast<const uint32_t *>(b[g].values);
         auto a = [&](int q) -> uint32_t { return av[q >> 3][q & 7]; };
-        const float d = h2f(w.x[6] >> 16);
+        const float d = h2f(ptq1_scale_bits(w));
         if constexpr (O == Op::PTQ1_SRC) {
             int acc[4] = {0, 0, 0, 0};
             trits(w, a, [&](int q) -> int & { return acc[q >> 3]; });
@@ -350,7 +376,7 @@ __device__ __forceinline__ void unit_terms(const Raw<O> &w, const void *__restri
             for (int i = 0; i < 32; ++i) s = bsum4(av[i], s);
         }
         // dot_ptq1_q8k, src/kernels.rs:1026-1034
-        t[0] = (h2f(w.x[6] >> 16) * b->scale) * static_cast<float>(acc - s);
+        t[0] = (h2f(ptq1_scale_bits(w)) * b->scale) * static_cast<float>(acc - s);
     } else if constexpr (O == Op::PQ2_UNFUSED || O == Op::PQ2_FUSED) {
         const Q8KBlock *b = static_cast<const Q8KBlock *>(act) + (u >> 1);
         const uint32_t *av = reinterpret_cast<const uint32_t *>(b->values) + 32 * (u & 1);
@@ -509,12 +535,15 @@ struct MvParams {
     const void *act;      // prepared blocks, or f32 input when the prologue quantizes
     int qcontract;        // prologue quantizer: Q8_K pinned flag / Q8_0 contract
     int pinned;           // SwiGLU order (NMAT == 2)
-    uint32_t ks, lpr;     // split mode: wavefronts per matrix, lanes per row
+    uint32_t ks, lpr;     // split mode: wavefronts per matrix, lanes per row (powers of two)
+    uint32_t lg_ks, lg_lpr;  // their base-2 logarithms
     float *out;
     const float *residual;
     int *err;
     const float *norm_w;  // QUANT prologue: RMSNorm weights applied before quantizing (or null)
     float eps;            // RMSNorm epsilon
+    Q8Block *q8_out;      // NMAT == 2: the SwiGLU vector quantized to Q8_0 blocks (or null)
+    int q8_contract;      // their contract (PRISM_Q8_*)
 };
 
 template <Op O>
@@ -1421,9 +1450,13 @@ constexpr uint32_t kSplitMaxWaves = 8, kSplitMaxThreads = 64 * kSplitMaxWaves;
 // staged in LDS by the prologue: either the prepared blocks are copied (COPY), or
 // the f32 input is quantized with the contract matvec_into uses (QUANT), which
 // makes the whole projection one launch.  NMAT == 2: gate (wavefronts 0..ks-1) and
-// up (ks..2ks-1) share the activation and the epilogue writes SwiGLU(gate, up).
-// The first unit's weight loads are issued before the prologue so that their
-// latency overlaps it.
+// up (ks..2ks-1) share the activation and the epilogue writes SwiGLU(gate, up), and
+// optionally (q8_out) the SwiGLU vector's Q8_0 blocks, so that the projection after
+// it takes prepared blocks.
+// The kernel is latency-bound at decode sizes, so its critical path is kept short:
+// indices are shifts (lpr and ks are powers of two); the activation's reads are
+// issued first, then every weight unit's; a PTQ1 unit's trits are extracted while
+// the activation is staged, so after the staging barrier only the dot products remain.
 // HELD (QUANT only): 8 or 16 input values held per lane (HeldInput), 0 to stream the
 // input through the quantizer instead.
 template <Op O, bool QUANT, int NMAT, int HELD>
@@ -1434,17 +1467,17 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nwaves = blockDim.x >> 6;
-    const uint32_t ks = p.ks, lpr = p.lpr, rw = kTile / lpr;
+    const uint32_t ks = p.ks, lg_lpr = p.lg_lpr, lg_rw = 6u - lg_lpr, rw = 1u << lg_rw;
     const uint32_t mat = (NMAT == 2 && wave >= ks) ? 1u : 0u;
     const uint32_t mw = wave - mat * ks;
-    const uint32_t tile = blockIdx.x / lpr, sub = blockIdx.x % lpr;
-    const uint32_t c = lane / rw, r = lane % rw;
-    const uint32_t kt = ks * lpr, kk = mw * lpr + c;
+    const uint32_t tile = blockIdx.x >> lg_lpr, sub = blockIdx.x & ((1u << lg_lpr) - 1u);
+    const uint32_t c = lane >> lg_rw, r = lane & (rw - 1u);
+    const uint32_t lg_kt = p.lg_ks + lg_lpr, kt = 1u << lg_kt, kk = (mw << lg_lpr) + c;
     const uint32_t nu = p.nu, row_bytes = nu * UB;
     const uint32_t left = p.rows - tile * kTile;
     const uint32_t trows = left < kTile ? left : kTile;
     const uint32_t trp = (trows + 7u) & ~7u;
-    const uint32_t tr = sub * rw + r;  // row within the tile
+    const uint32_t tr = (sub << lg_rw) + r;  // row within the tile
 
     const uint32_t abytes = align16(act_bytes_for<O>(p.cols));
     const uint32_t stride = nu * TPU + 1;
@@ -1452,31 +1485,45 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     float *res = reinterpret_cast<float *>(smem + abytes) + NMAT * rw * stride;
     double *red = reinterpret_cast<double *>(smem + abytes + align16(4u * (NMAT * rw * stride + 2 * rw)));
 
-    const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
-    // A quantizing prologue whose input fits in the wavefronts' registers reads it (and
-    // the norm weights) first, before the weights, in one round trip.  The holder is
-    // chosen at compile time: a branch around these loads would make the prologue wait
-    // for the weights' loads too.
+    // The activation's reads come first: memory counters complete in issue order, so
+    // staging it waits for these reads only, not for the weights behind them.
+    // QUANT: a prologue whose input fits in the wavefronts' registers reads it (and the
+    // norm weights) here, in one round trip.  The holder is chosen at compile time: a
+    // branch around these loads would make the prologue wait for the weights too.
     using Held = HeldInput<act_is_q8k<O>(), HELD == 8 ? 8 : 16, HELD == 8 ? 1 : 2>;
     Held hin;
     if constexpr (QUANT && HELD != 0) {
         const float *x = static_cast<const float *>(p.act);
         hin.load(x, p.norm_w ? p.norm_w : x, p.cols, wave, nwaves, lane);
     }
+    // COPY: the first 16 words per thread of the prepared blocks.
+    constexpr uint32_t kCopy = 16;
+    const uint32_t *asrc = static_cast<const uint32_t *>(p.act);
+    const uint32_t an = act_bytes_for<O>(p.cols) / 4;
+    uint32_t atmp[kCopy];
+    if constexpr (!QUANT) {
+#pragma unroll
+        for (uint32_t j = 0; j < kCopy; ++j) {
+            const uint32_t i = j * blockDim.x + threadIdx.x;
+            atmp[j] = i < an ? asrc[i] : 0u;
+        }
+    }
+
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(p.w[mat] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
     // When every lane takes at most kPre units (the decode-sized projections), all of
     // them are loaded here, ahead of the prologue, and the main loop issues no load.
     // Units past the row fall outside the buffer resource and read as zeros.
     // W[0] and W[1] double as the ping-pong pair of the streaming loop otherwise.
     // Larger units keep the streaming loop only (their registers are spoken for).
     constexpr uint32_t kPre = UB <= 36 ? 3 : 2;
-    const uint32_t cmax = (nu + kt - 1) / kt;  // most units any lane takes
+    const uint32_t cmax = (nu + kt - 1) >> lg_kt;  // most units any lane takes
     const bool pre = UB <= 36 && cmax <= kPre;
     Raw<O> W[kPre];
     uint32_t u = kk;
     if (pre) {
 #pragma unroll
-        for (uint32_t j = 0; j < kPre; ++j) load_unit<O>(W[j], rs, (kk + j * kt) * trp * UB, trp, tr);
+        for (uint32_t j = 0; j < kPre; ++j) load_unit<O>(W[j], rs, (kk + (j << lg_kt)) * trp * UB, trp, tr);
     } else if (u < nu) {
         load_unit<O>(W[0], rs, u * trp * UB, trp, tr);
     }
@@ -1527,29 +1574,44 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
         // Every workgroup sees the same input; the first one reports its errors.
         if (e && lane == 0 && blockIdx.x == 0) raise_error(p.err, e);
     } else {
-        // Copy the prepared blocks: 16 loads per thread in flight before any store.
-        const uint32_t *src = static_cast<const uint32_t *>(p.act);
         uint32_t *dst = reinterpret_cast<uint32_t *>(smem);
-        const uint32_t n = act_bytes_for<O>(p.cols) / 4;
-        for (uint32_t base = 0; base < n; base += 16 * blockDim.x) {
-            uint32_t tmp[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
+        for (uint32_t j = 0; j < kCopy; ++j) {
+            const uint32_t i = j * blockDim.x + threadIdx.x;
+            if (i < an) dst[i] = atmp[j];
+        }
+        // Longer activations: the rest, 16 loads per thread in flight before any store.
+        for (uint32_t base = kCopy * blockDim.x; base < an; base += kCopy * blockDim.x) {
+            uint32_t tmp[kCopy];
+#pragma unroll
+            for (uint32_t j = 0; j < kCopy; ++j) {
                 const uint32_t i = base + j * blockDim.x + threadIdx.x;
-                tmp[j] = i < n ? src[i] : 0u;
+                tmp[j] = i < an ? asrc[i] : 0u;
             }
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
+            for (uint32_t j = 0; j < kCopy; ++j) {
                 const uint32_t i = base + j * blockDim.x + threadIdx.x;
-                if (i < n) dst[i] = tmp[j];
+                if (i < an) dst[i] = tmp[j];
             }
+        }
+    }
+    // PTQ1 units held in registers: their trits are extracted now, ahead of the barrier,
+    // while the other wavefronts finish staging the activation.
+    constexpr bool kDec = kind_of<O>() == kPTQ1;
+    using DecT = typename std::conditional<kDec, Ptq1Dec, Raw<O>>::type;
+    DecT D[kDec ? kPre : 1];
+    if constexpr (kDec) {
+        if (pre) {
+#pragma unroll
+            for (uint32_t j = 0; j < kPre; ++j)
+                if (kk + (j << lg_kt) < nu) ptq1_decode(W[j].x, D[j]);
         }
     }
     __syncthreads();
     const void *act = smem;
 
     // ---- main loop: ping-pong over this lane's units --------------------------------
-    auto step = [&](const Raw<O> &w, uint32_t v) {
+    auto step = [&](const auto &w, uint32_t v) {
         float t[TPU];
         unit_terms<O>(w, act, v, t);
 #pragma unroll
@@ -1557,8 +1619,15 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     };
     if (pre) {
 #pragma unroll
-        for (uint32_t j = 0; j < kPre; ++j)
-            if (kk + j * kt < nu) step(W[j], kk + j * kt);
+        for (uint32_t j = 0; j < kPre; ++j) {
+            const uint32_t v = kk + (j << lg_kt);
+            if (v < nu) {
+                if constexpr (kDec)
+                    step(D[j], v);
+                else
+                    step(W[j], v);
+            }
+        }
     } else {
         while (u + kt < nu) {
             load_unit<O>(W[1], rs, (u + kt) * trp * UB, trp, tr);
@@ -1588,10 +1657,21 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     } else {
         if (folder) res[mat * rw + lane] = o;
         __syncthreads();
-        if (wave == 0 && lane < rw && valid) {
-            const float h = swiglu_one(res[lane], res[rw + lane], row, p.rows, p.pinned);
-            p.out[row] = h;
-            if (!finite(h)) raise_error(p.err, kErrNonfinite);
+        if (wave == 0) {
+            const bool own = lane < rw && valid;
+            float h = 0.0f;
+            if (own) {
+                h = swiglu_one(res[lane], res[rw + lane], row, p.rows, p.pinned);
+                if (p.out) p.out[row] = h;
+                if (!finite(h)) raise_error(p.err, kErrNonfinite);
+            }
+            // Rows 32j..32j+31 of the vector are Q8_0 block j (q8_with_input,
+            // src/kernels.rs:552-617): every 32 lanes hold one block (rw >= 32 and the
+            // row count a multiple of 32, checked at launch).
+            if (p.q8_out) {
+                const int e = q8_0_lanes32(h, own, p.q8_contract, p.q8_out + (row >> 5), lane & 31u);
+                if (e && own) raise_error(p.err, e);
+            }
         }
     }
 }
@@ -1628,18 +1708,20 @@ __global__ void k_repack(const uint8_t *__restrict__ src, uint8_t *__restrict__ 
 constexpr size_t kSplitLds = 64 * 1024;
 
 struct SplitPlan {
-    uint32_t ks, lpr;
+    uint32_t ks, lpr, lg_ks, lg_lpr;
     size_t lds;
 };
 
 // Split-mode geometry: enough lane groups per row that the tiles cover every CU,
 // then enough wavefronts per workgroup for ~8 resident wavefronts per CU, never
 // more K-split ways than the row has units.
+// max_lpr caps the lane groups per row (a workgroup then owns at least 64/max_lpr rows).
 template <Op O>
-bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t nmat, uint32_t cus, SplitPlan *pl) {
+bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t nmat, uint32_t cus, SplitPlan *pl,
+                uint32_t max_lpr = 8) {
     const uint64_t tiles = (rows + kTile - 1) / kTile;
     uint32_t lpr = 1;
-    while (lpr < 8 && tiles * lpr < cus && lpr * 2 <= nu) lpr *= 2;
+    while (lpr < max_lpr && tiles * lpr < cus && lpr * 2 <= nu) lpr *= 2;
     uint32_t ks = 1;
     while (ks * 2 * nmat <= kSplitMaxWaves && ks * 2 * lpr <= nu && tiles * lpr * ks * 2 * nmat <= 8ull * cus) ks *= 2;
     // A quantizing prologue wants several wavefronts per workgroup: trade lane groups
@@ -1651,6 +1733,8 @@ bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t 
     const uint32_t rw = kTile / lpr;
     pl->ks = ks;
     pl->lpr = lpr;
+    pl->lg_ks = static_cast<uint32_t>(__builtin_ctz(ks));
+    pl->lg_lpr = static_cast<uint32_t>(__builtin_ctz(lpr));
     // activation blocks | terms (| SwiGLU inputs) | 16 doubles for the RMSNorm reduction
     pl->lds = align16(act_bytes_for<O>(cols)) +
               align16(static_cast<uint32_t>(sizeof(float) * (nmat * rw * (nu * terms_per_unit<O>() + 1) + 2 * rw))) +
@@ -1678,6 +1762,10 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.err = a.err;
     p.norm_w = a.norm_w;
     p.eps = a.eps;
+    // SwiGLU blocks (q8_out): every 32 rows of a workgroup form one Q8_0 block.
+    if (a.q8_out && (nmat != 2 || a.rows % 32 != 0)) return -2;
+    p.q8_out = static_cast<Q8Block *>(a.q8_out);
+    p.q8_contract = a.q8_contract;
     if (!quant && nmat == 1 && tiles >= a.cus) {
         if constexpr (kind_of<O>() == kPTQ1) {
             if (lut_can_split<O>() && lut_split(static_cast<uint32_t>(tiles), a.cus, nu))
@@ -1706,9 +1794,11 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
         return launch_status();
     }
     SplitPlan pl;
-    if (!plan_split<O>(a.rows, nu, p.cols, quant, nmat, a.cus, &pl)) return -2;
+    if (!plan_split<O>(a.rows, nu, p.cols, quant, nmat, a.cus, &pl, a.q8_out ? 2u : 8u)) return -2;
     p.ks = pl.ks;
     p.lpr = pl.lpr;
+    p.lg_ks = pl.lg_ks;
+    p.lg_lpr = pl.lg_lpr;
     const dim3 grid(static_cast<uint32_t>(tiles * pl.lpr)), block(64 * pl.ks * nmat);
     // Held prologue input: eight values per lane when one chunk per wavefront covers the
     // input, else sixteen in up to two chunks (each chunk's block reductions are a fixed
@@ -1748,7 +1838,8 @@ bool op_needs_prepared(const MatvecArgs &a) {
     if (!a.w2 && tiles >= a.cus) return true;
     SplitPlan pl;
     const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
-    return !plan_split<O>(a.rows, nu, static_cast<uint32_t>(a.cols), true, a.w2 ? 2u : 1u, a.cus, &pl);
+    return !plan_split<O>(a.rows, nu, static_cast<uint32_t>(a.cols), true, a.w2 ? 2u : 1u, a.cus, &pl,
+                          a.q8_out ? 2u : 8u);
 }
 
 // Selects the arithmetic order from (kind, activation format, pinned): the orders of

@@ -564,4 +564,41 @@ __device__ __forceinline__ float rms_scale_wg(const float *__restrict__ x, uint3
     return (finite(scale) && scale > 0.0f) ? scale : 0.0f;
 }
 
+// One Q8_0 block per 32 lanes with one value per lane (lane j of a 32-lane half holds
+// element j): q8_with_input's arithmetic (src/kernels.rs:552-617, as q8_0_process), the
+// block maximum and code sum combined across the 32 lanes.  Every lane of the wavefront
+// calls it; lanes with own == false hold 0 and write nothing.  Returns this lane's
+// error bits.
+__device__ __forceinline__ int q8_0_lanes32(float v, bool own, int contract, Q8Block *blk, uint32_t j) {
+    const bool bad = own && !finite(v);
+    float m = fabsf(v);
+    m = fmaxf(m, dpp_f<kDppXor1>(m));
+    m = fmaxf(m, dpp_f<kDppXor2>(m));
+    m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
+    m = fmaxf(m, dpp_f<kDppRowMirror>(m));
+    m = fmaxf(m, __shfl_xor(m, 16));
+    const bool pinned = contract != 0, native = contract == 2;
+    const float d = native ? m * __uint_as_float(0x3c010204u) : m / 127.0f;
+    const float inv = d == 0.0f ? 0.0f : (native ? 127.0f / m : 1.0f / d);
+    const float r = pinned ? __builtin_rintf(v * inv) : __builtin_roundf(v * inv);
+    const bool range = !(r >= -127.0f && r <= 127.0f);
+    const int q = range ? 0 : static_cast<int>(r);
+    int qs = q;
+    qs += dpp_i<kDppXor1>(qs);
+    qs += dpp_i<kDppXor2>(qs);
+    qs += dpp_i<kDppHalfMirror>(qs);
+    qs += dpp_i<kDppRowMirror>(qs);
+    qs += __shfl_xor(qs, 16);
+    const float scale = round_f16(d);
+    if (own) {
+        blk->values[j] = static_cast<int8_t>(q);
+        if (j == 0) {
+            blk->scale = scale;
+            blk->sum = round_f16(static_cast<float>(qs) * d);
+        }
+    }
+    if (bad) return kErrInput;
+    return own && (range || !finite(scale)) ? kErrQuantRange : 0;
+}
+
 }  // namespace prism

@@ -108,10 +108,25 @@ int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Wei
         // gate, up and SwiGLU in one launch, x quantized in the prologue.
         MatvecArgs a = f32_args(c, g, x, 1, pinned, hv, nullptr, s);
         a.w2 = static_cast<const uint8_t *>(u.dev);
+        // A tiled down matrix on Q8_0 activations takes the SwiGLU vector as blocks the
+        // gate/up epilogue quantizes (its contract, per 32 rows), not as floats.
+        const int dc = d ? contract_for(d->kind, d->cols, pinned) : 0;
+        if (d && d->tiled && dc != 0 && g.rows % 32 == 0) {
+            rc = ensure(c, c->act2, act_bytes(dc, d->cols, 1));
+            if (rc) return rc;
+            a.q8_out = c->act2.p;
+            a.q8_contract = dc == 2 ? PRISM_Q8_PINNED_NATIVE : (pinned ? PRISM_Q8_PINNED : PRISM_Q8_SOURCE);
+            a.out = h;  // the floats only when the caller asked for them
+        }
         if (!tiled_needs_prepared(a)) {
             rc = run_matvec(c, a, true);
             if (rc) return rc;
             fused = true;
+            if (a.q8_out) {
+                MatvecArgs da = matvec_args(c, *d, kActQ8, a.q8_out, 1, pinned, out, s);
+                da.residual = residual;
+                return run_matvec(c, da, true);
+            }
         }
     }
     if (!fused) {

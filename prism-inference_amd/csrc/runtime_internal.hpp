@@ -10,7 +10,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/prism_hip.h"
+#include "prism_hip.h"
 #include "kernels.hpp"
 #include "tiled.hpp"
 

@@ -9,7 +9,7 @@
 #include <map>
 #include <mutex>
 
-#include "../../include/prism_hip.h"
+#include "prism_hip.h"
 
 namespace prism {
 
