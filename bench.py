@@ -1,17 +1,22 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X packed quantized matmul path.
 
-Headline workload (one "step"): the Qwen35-shaped dense FFN decode step at batch 1
-with Q2_K weights -- quantize x (f32 -> Q8_K), gate and up matvecs 2048->6144,
-SwiGLU, quantize h, down matvec 6144->2048 -- in the public (source) arithmetic
-contract.  It runs as two kernels (gate+up+SwiGLU, down).  Weights are rotated over
->= 1 GiB of distinct device copies so every step streams them from HBM; steps are
-captured in HIP graphs on the library's stream and timed with HIP events there.
+Headline workload (one "step" = one generated token): the full synthetic Qwen35-shaped
+decode step at batch 1 -- 28 layers, hidden 2048, 16 query / 4 KV heads of dim 128,
+FFN 6144, every linear layer PTQ1 (ternary, 128-weight blocks), RMSNorm, RoPE, binary16
+KV cache prefilled to 1024 tokens, tied 151936-token LM head in Q8_0 -- greedy, from
+position 1024, one captured HIP graph replayed per token on the library's stream and
+timed with HIP events there.  `value` is tokens/s.
 
-The roofline entry is the step's dominant kernel, the fused gate+up+SwiGLU launch,
-timed with HIP events around back-to-back launches on the same stream.  Its HBM
-traffic comes from the rocprof FETCH_SIZE / WRITE_SIZE summaries committed under
-profiles/ (scaled by a plain device copy of known size; --calibrate-copy runs it).
+The roofline entry is the step's dominant launch family (largest time per step in an
+eager pass with an event around every launch), timed back to back over the 28 layers
+with HIP events on the library stream; its algorithmic bytes per launch are the packed
+weights at native size plus activations, outputs and KV rows read.
+
+Extras: the per-family breakdown of a step, the Q2_K FFN decode step (with its slowest
+kernel, the down projection, as its own roofline), the batch-1 matvec sweep, skinny
+batches, the prefill GEMM, and the CPU baselines (the oracle, a scalar C restatement of
+the reference's CPU kernels, on the host's cores) for every workload.
 
 Prints ONE JSON line on rank 0 (the only rank: this build runs on one GPU).
 """
@@ -37,12 +42,43 @@ import synth  # noqa: E402
 METRIC = "packed matvec HBM GB/s (% peak); prefill int8 TOPS; decode tokens/s at batch 1"
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
 PEAK_I8 = 5.0e15  # MI355X dense int8 MFMA, ops/s
+PEAK_F16 = 2.5e15  # MI355X dense f16 MFMA, flop/s
 ROTATE_BYTES = 1 << 30
 HIDDEN, FFN = 2048, 6144
+CPU_THREADS = 16  # the host-core share of one GPU on the measurement box
+DECODE_POS = 1024
+# Prefill GEMM VALU-issue ceiling: per wavefront and 128-deep block of 32 rows x 64
+# tokens, the counted instruction mix is 440 VALU instructions (16 of them MFMA), and a
+# SIMD issues one wave64 VALU instruction per 4 cycles (profiles/prefill_gemm_6144x2048.md).
+PREFILL_VALU_PER_BLOCK = 440
+PREFILL_OPS_PER_BLOCK = 2 * 32 * 64 * 128
+ENGINE_HZ = 2.4e9
+CUS = 256
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_info() -> dict:
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return {"nproc": os.cpu_count(), "cores_available": avail, "cpu_model": model}
+
+
+def cpu_threads() -> int:
+    return max(1, min(CPU_THREADS, host_info()["cores_available"]))
 
 
 def chunk_for(k: int) -> int:
@@ -68,6 +104,82 @@ class Rotation:
         self.ids = []
 
 
+# ---- headline: the 28-layer decode step ---------------------------------------------
+
+def decode_token_bytes(g: dict, pos: int) -> int:
+    """Algorithmic bytes of one decode step at position `pos`: every packed weight at
+    its native size once (PTQ1 linears, the Q8_0 LM head), the binary16 K and V rows
+    attention reads (pos + 1 tokens per layer), and the embedding row."""
+    H, F, D = g["hidden"], g["ffn"], g["head_dim"]
+    QW, KW = g["heads"] * D, g["kv_heads"] * D
+
+    def ptq1(rows, cols):
+        return rows * cols // 128 * 28
+
+    layer = ptq1(QW + 2 * KW, H) + ptq1(H, QW) + 2 * ptq1(F, H) + ptq1(H, F)
+    kv = 2 * (pos + 1) * KW * 2
+    return g["layers"] * (layer + kv) + g["vocab"] * H // 32 * 34 + H // 32 * 34
+
+
+def bench_decode(ctx: ph.Context, model: dict, steps: int, warmup: int, profile: bool = True):
+    """Greedy generation of `steps` tokens from position 1024 (KV caches prefilled with
+    1024 tokens), one captured HIP graph per step, after `warmup` untimed tokens; then
+    an eager pass with an event around every launch (per-family breakdown) and the
+    dominant family timed back to back."""
+    g = model["geometry"]
+    dec = ph.Decoder(ctx, model, max_steps=max(steps, warmup, 8))
+    if warmup:
+        dec.generate(1, DECODE_POS, warmup, graph=True)  # capture and warm
+    hiprt.synchronize()
+    toks, _, secs = dec.generate(1, DECODE_POS, steps, graph=True)
+    hiprt.synchronize()
+    nbytes = sum(decode_token_bytes(g, DECODE_POS + i) for i in range(steps))
+    out = {"tokens_per_s": steps / secs, "ms_per_token": secs / steps * 1e3, "steps": steps,
+           "bytes_per_token": nbytes // steps, "GBps": nbytes / secs / 1e9, "frac_hbm": nbytes / secs / PEAK_HBM,
+           "first_tokens": [int(t) for t in toks[:8]]}
+    if profile:
+        psteps = 4
+        fams = dec.profile(1, DECODE_POS, psteps)
+        for f in fams:
+            f["us_per_launch"] = f["total_us"] / max(1, f["launches"])
+            f["us_per_step"] = f["total_us"] / psteps
+        out["eager_profile"] = {"steps": psteps, "families": fams,
+                                "ms_per_token": sum(f["total_us"] for f in fams) / psteps / 1e3,
+                                "note": "launches issued one by one, an event before every launch: each time "
+                                        "includes the launch's dispatch gap"}
+        dom = max(fams, key=lambda f: f["us_per_step"])
+        reps = 8 if dom["family"] not in ("lm_prep", "lm_head") else 40
+        dec.generate(1, DECODE_POS, 1, graph=True)  # state at a position inside the cache
+        us, nb = dec.time_family(dom["family"], reps)
+        out["dominant"] = {"family": dom["family"], "us_per_step_eager": dom["us_per_step"],
+                           "avg_launch_us": us, "bytes_per_launch": nb, "launches": reps * (
+                               g["layers"] if dom["family"] not in ("lm_prep", "lm_head") else 1)}
+    dec.close()
+    return out
+
+
+def decode_roofline(d: dict) -> dict:
+    dom = d["dominant"]
+    t = dom["avg_launch_us"] * 1e-6
+    achieved = dom["bytes_per_launch"] / t / 1e9
+    kernel = {"qkv": "k_mv_split<PTQ1 source, quantizing prologue + RMSNorm, 1 matrix, 8 held> (q/k/v 3072x2048)",
+              "o": "k_mv_split<PTQ1 source, quantizing prologue, 1 matrix, 8 held> (o 2048x2048 + residual)",
+              "gate_up": "k_mv_split<PTQ1 source, quantizing prologue + RMSNorm, gate+up, 8 held> (2x 6144x2048, "
+                         "SwiGLU, Q8_0 blocks out)",
+              "down": "k_mv_split<PTQ1 source, prepared Q8_0 blocks, 1 matrix> (down 2048x6144 + residual)",
+              "attn_scores": "k_attn_scores (q/k norm, RoPE, KV append, 16 heads x 1025 positions)",
+              "attn_values": "k_attn_values (softmax_round_f16 + value sums, 16 heads x 1025 positions)",
+              "lm_head": "k_mv_rows<Q8_0> (151936x2048 LM head)",
+              "lm_prep": "k_lm_prep (final RMSNorm + Q8_0)"}.get(dom["family"], dom["family"])
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(achieved * 1e9 / PEAK_HBM, 4), "traffic": None, "kernel": kernel,
+            "family": dom["family"], "bytes_per_launch": dom["bytes_per_launch"],
+            "avg_launch_us": round(dom["avg_launch_us"], 3), "launches_timed": dom["launches"],
+            "method": "back-to-back launches cycling over the 28 layers, HIP events on the library stream"}
+
+
+# ---- config 1: the Q2_K FFN decode step ------------------------------------------------
+
 def ffn_step_bytes() -> int:
     """Algorithmic HBM bytes of one FFN step: packed weights at native block size, the f32
     input, the f32 SwiGLU vector (written by the first kernel, read by the second) and
@@ -76,12 +188,12 @@ def ffn_step_bytes() -> int:
     return w + 4 * HIDDEN + 2 * 4 * FFN + 4 * HIDDEN
 
 
-def gateup_bytes() -> int:
-    """Algorithmic bytes of the gate+up+SwiGLU kernel: both weight matrices, x, and h."""
-    return 2 * FFN * HIDDEN // 256 * 84 + 4 * HIDDEN + 4 * FFN
+def down_bytes() -> int:
+    """Algorithmic bytes of the down projection: weights, the f32 SwiGLU vector, output."""
+    return HIDDEN * FFN // 256 * 84 + 4 * FFN + 4 * HIDDEN
 
 
-def bench_ffn(ctx: ph.Context, steps: int, warmup: int):
+def bench_ffn(ctx: ph.Context, steps: int = 400, warmup: int = 40):
     per_copy = 3 * FFN * HIDDEN // 256 * 84
     chunk = chunk_for(steps)
     copies = math.ceil(ROTATE_BYTES / per_copy / chunk) * chunk
@@ -91,6 +203,7 @@ def bench_ffn(ctx: ph.Context, steps: int, warmup: int):
     d = Rotation(ctx, ph.KIND_Q2_K, HIDDEN, FFN, synth.q2k_weights(HIDDEN, FFN, seed=103), copies)
     x = hiprt.DeviceBuffer.from_numpy(synth.activations(HIDDEN, seed=104))
     out = hiprt.DeviceBuffer(4 * HIDDEN)
+    h = hiprt.DeviceBuffer(4 * FFN)
     stream = ctx.stream()
     ctx.ffn_chain_device(g.ids[0], u.ids[0], d.ids[0], x, None, False, out)  # allocates scratch
     assert ctx.sync() == 0
@@ -108,74 +221,43 @@ def bench_ffn(ctx: ph.Context, steps: int, warmup: int):
     assert ctx.sync() == 0
     e0, e1 = hiprt.Event(), hiprt.Event()
     hiprt.synchronize()
-    t0 = time.perf_counter()
     e0.record(stream)
     for i in range(steps // chunk):
         graphs[i % len(graphs)].launch()
     e1.record(stream)
     e1.synchronize()
     hiprt.synchronize()
-    wall = time.perf_counter() - t0
-    rc = ctx.sync()
-    assert rc == 0, ctx.last_error
+    assert ctx.sync() == 0
     y = out.to_numpy(np.float32)
     assert np.isfinite(y).all()
     ms = e0.elapsed_ms(e1) / steps
     del graphs
-    for r in (g, u, d):
-        r.release(ctx)
-    return ms, wall / steps * 1e3, copies
-
-
-def bench_gateup_kernel(ctx: ph.Context, launches: int = 400):
-    """The FFN step's dominant kernel alone: gate+up+SwiGLU (x quantized in its prologue),
-    back-to-back launches over rotated weight copies, HIP events on the library stream."""
-    per_copy = 2 * FFN * HIDDEN // 256 * 84
-    copies = math.ceil(ROTATE_BYTES / per_copy)
-    g = Rotation(ctx, ph.KIND_Q2_K, FFN, HIDDEN, synth.q2k_weights(FFN, HIDDEN, seed=111), copies)
-    u = Rotation(ctx, ph.KIND_Q2_K, FFN, HIDDEN, synth.q2k_weights(FFN, HIDDEN, seed=112), copies)
-    x = hiprt.DeviceBuffer.from_numpy(synth.activations(HIDDEN, seed=113))
-    h = hiprt.DeviceBuffer(4 * FFN)
-    stream = ctx.stream()
+    # The step's slowest kernel alone: the down projection (SwiGLU vector quantized to
+    # Q8_K in its prologue), back-to-back launches over the rotated copies.
+    ctx.ffn_chain_device(g.ids[0], u.ids[0], 0, x, None, False, h, None, stream)
     for i in range(min(copies, 16)):
-        ctx.ffn_chain_device(g.ids[i], u.ids[i], 0, x, None, False, h, None, stream)
+        ctx.project_device(d.ids[i], ph.PATH_F32, h, 1, False, out, stream)
     assert ctx.sync() == 0
-    e0, e1 = hiprt.Event(), hiprt.Event()
+    launches = 400
     e0.record(stream)
     for i in range(launches):
-        ctx.ffn_chain_device(g.ids[i % copies], u.ids[i % copies], 0, x, None, False, h, None, stream)
+        ctx.project_device(d.ids[i % copies], ph.PATH_F32, h, 1, False, out, stream)
     e1.record(stream)
     e1.synchronize()
     assert ctx.sync() == 0
     t = e0.elapsed_ms(e1) / launches * 1e-3
-    g.release(ctx)
-    u.release(ctx)
-    return {"avg_us": t * 1e6, "bytes_per_launch": gateup_bytes(), "GBps": gateup_bytes() / t / 1e9,
-            "copies": copies}
-
-
-def measured_traffic(name: str):
-    """HBM bytes per launch of a kernel from a committed rocprof summary
-    (profiles/<name>): lines 'fetch_kib_per_dispatch: X', 'write_kib_per_dispatch: Y',
-    'copy_fetch_scale: A', 'copy_write_scale: B' (counter KiB -> bytes of a plain copy).
-    None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", name)
-    if not os.path.exists(path):
-        return None
-    vals = {}
-    with open(path) as f:
-        for line in f:
-            if ":" in line:
-                k, v = line.split(":", 1)
-                try:
-                    vals[k.strip().strip("-* `")] = float(v.strip().strip("`"))
-                except ValueError:
-                    pass
-    need = ("fetch_kib_per_dispatch", "write_kib_per_dispatch", "copy_fetch_scale", "copy_write_scale")
-    if not all(k in vals for k in need):
-        return None
-    return vals["fetch_kib_per_dispatch"] * vals["copy_fetch_scale"] + \
-        vals["write_kib_per_dispatch"] * vals["copy_write_scale"]
+    for r in (g, u, d):
+        r.release(ctx)
+    nbytes = ffn_step_bytes()
+    return {"workload": "Qwen35-shaped dense FFN decode step, batch 1: Q2_K gate/up 2048->6144, SwiGLU, "
+                        "down 6144->2048, source contract, weights rotated over >= 1 GiB of copies",
+            "us_per_step": ms * 1e3, "bytes_per_step": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9,
+            "frac_hbm": nbytes / (ms * 1e-3) / PEAK_HBM, "weight_copies": copies,
+            "roofline": {"bound": "hbm", "kernel": "k_mv_split<Q2K, quantizing prologue, 1 matrix, 16 held> "
+                                                   "(down 2048x6144)",
+                         "avg_launch_us": t * 1e6, "bytes_per_launch": down_bytes(),
+                         "achieved": down_bytes() / t / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                         "frac": down_bytes() / t / PEAK_HBM}}
 
 
 def calibrate_copy(nbytes: int = 256 << 20, reps: int = 10) -> int:
@@ -187,6 +269,8 @@ def calibrate_copy(nbytes: int = 256 << 20, reps: int = 10) -> int:
     print(json.dumps({"calibrate_copy_bytes": nbytes, "reps": reps}), flush=True)
     return 0
 
+
+# ---- configs 0 and 4: batch-1 matvec and skinny batches --------------------------------
 
 def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launches: int = 200, tokens: int = 1):
     """Per-launch duration of one matvec kernel (prepared Q8_K/Q8_0 activations of `tokens`
@@ -225,6 +309,8 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
             "frac_hbm": nbytes / t / PEAK_HBM}
 
 
+# ---- config 2: the tiled prefill GEMM ----------------------------------------------------
+
 def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 20):
     w = synth.ptq1_weights(rows, cols, seed=9)
     wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
@@ -243,96 +329,97 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
     t = e0.elapsed_ms(e1) / reps * 1e-3
     ops = 2.0 * M * rows * cols
     ctx.release(wid)
-    return {"M": M, "ms": t * 1e3, "TOPS": ops / t / 1e12, "frac_int8_peak": ops / t / PEAK_I8}
+    valu_ceiling = PREFILL_OPS_PER_BLOCK * 4 / (PREFILL_VALU_PER_BLOCK * 4) * CUS * ENGINE_HZ
+    return {"M": M, "ms": t * 1e3, "TOPS": ops / t / 1e12, "frac_int8_peak": ops / t / PEAK_I8,
+            "frac_f16_peak": ops / t / PEAK_F16, "valu_issue_ceiling_TOPS": valu_ceiling / 1e12,
+            "frac_valu_ceiling": ops / t / valu_ceiling}
 
 
-def decode_token_bytes(g: dict, pos: int) -> int:
-    """Algorithmic bytes of one decode step at position `pos`: every packed weight at
-    its native size once (PTQ1 linears, the Q8_0 LM head), the binary16 K and V rows
-    attention reads (pos + 1 tokens per layer), and the embedding row."""
-    H, F, D = g["hidden"], g["ffn"], g["head_dim"]
-    QW, KW = g["heads"] * D, g["kv_heads"] * D
+# ---- CPU baselines (the oracle on the host's cores) --------------------------------------
 
-    def ptq1(rows, cols):
-        return rows * cols // 128 * 28
-
-    layer = ptq1(QW + 2 * KW, H) + ptq1(H, QW) + 2 * ptq1(F, H) + ptq1(H, F)
-    kv = 2 * (pos + 1) * KW * 2
-    return g["layers"] * (layer + kv) + g["vocab"] * H // 32 * 34 + H // 32 * 34
+def _time(fn, budget_s: float, min_runs: int = 1, warm: bool = True):
+    if warm:
+        fn()
+    n, t0 = 0, time.perf_counter()
+    while n < min_runs or time.perf_counter() - t0 < budget_s:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
 
 
-def bench_decode(ctx: ph.Context, steps: int = 128, cpu_steps: int = 2, graph: bool = True):
-    """The 28-layer synthetic decode step: greedy generation of `steps` tokens from
-    position 1024 (KV caches prefilled with 1024 tokens), one captured HIP graph per
-    step, timed with HIP events on the library stream; the oracle's step timed beside
-    it on the host for `cpu_steps` tokens."""
-    t0 = time.perf_counter()
-    model = synth.decoder_model(0)
-    g = model["geometry"]
-    log(f"decode model generated in {time.perf_counter() - t0:.1f} s")
-    dec = ph.Decoder(ctx, model, max_steps=steps)
-    dec.generate(1, 1024, 8, graph=graph)  # capture and warm
-    toks, _, secs = dec.generate(1, 1024, steps, graph=graph)
-    dec.close()
-    nbytes = sum(decode_token_bytes(g, 1024 + i) for i in range(steps))
-    out = {"workload": "28-layer synthetic decode, hidden 2048, 16/4 heads x 128, FFN 6144, PTQ1 linears, "
-                       "tied Q8_0 LM head 151936, f16 KV prefilled to 1024, greedy",
-           "steps": steps, "graph": graph, "tokens_per_s": steps / secs, "ms_per_token": secs / steps * 1e3,
-           "bytes_per_token": nbytes // steps, "GBps": nbytes / secs / 1e9, "frac_hbm": nbytes / secs / PEAK_HBM,
-           "first_tokens": [int(t) for t in toks[:8]]}
-    if cpu_steps:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle
-
-        threads = min(16, os.cpu_count() or 1)
-        od = oracle.Decoder(model, threads=threads)
-        tok, cpu_toks, t0 = 1, [], time.perf_counter()
-        for i in range(cpu_steps):
-            tok = oracle.argmax(od.step(tok, 1024 + i))
-            cpu_toks.append(tok)
-        dt = (time.perf_counter() - t0) / cpu_steps
-        out["cpu_baseline"] = {"tokens_per_s": 1.0 / dt, "cores": threads, "kind": "port",
-                               "sample": f"{cpu_steps} decode steps of the scalar C restatement, rows split over "
-                                         f"{threads} threads",
-                               "same_tokens": cpu_toks == [int(t) for t in toks[:cpu_steps]]}
-    return out
-
-
-def cpu_baseline(budget_s: float = 12.0):
+def cpu_baselines(model: dict, budget_s: float = 1.5):
+    """The oracle (scalar C restatement of the reference's CPU kernels, rows split evenly
+    over threads as CpuThreadPool does, src/backend/threadpool.rs:190-196) on the same
+    workloads, at the box's host-core share and at one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    T = cpu_threads()
+    res = {"host": host_info(), "threads": T, "kind": "port", "configs": []}
+
+    def add(name, unit, work, fn, budget=budget_s, sample=""):
+        row = {"config": name, "unit": unit, "sample": sample}
+        for threads in (T, 1):
+            dt, n = _time(lambda: fn(threads), budget)
+            row[f"value_{threads}t" if threads == 1 else "value"] = work / dt
+            row[f"ms_{threads}t" if threads == 1 else "ms"] = dt * 1e3
+            row[f"runs_{threads}t" if threads == 1 else "runs"] = n
+        res["configs"].append(row)
+        log(f"cpu {name}: {row['value']:.3f} {unit} at {T} threads, {row['value_1t']:.3f} at 1")
+
+    w0 = synth.ptq1_weights(2048, 2048, seed=7)
+    x0 = synth.activations(2048, seed=8)
+    add("c0 PTQ1 2048x2048 matvec (Q8_0 source)", "GB/s", (w0.size + 2048 // 32 * 34 + 4 * 2048) / 1e9,
+        lambda t: oracle.matvec(oracle.KIND_PTQ1, 2048, 2048, w0, x0, False, t))
     wg = synth.q2k_weights(FFN, HIDDEN, seed=101)
     wu = synth.q2k_weights(FFN, HIDDEN, seed=102)
     wd = synth.q2k_weights(HIDDEN, FFN, seed=103)
-    x = synth.activations(HIDDEN, seed=104)
-    oracle.ffn(oracle.KIND_Q2_K, HIDDEN, FFN, wg, wu, wd, x, None, False, threads)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        oracle.ffn(oracle.KIND_Q2_K, HIDDEN, FFN, wg, wu, wd, x, None, False, threads)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"value": ffn_step_bytes() / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "ms_per_step": dt * 1e3,
-            "sample": f"{n} FFN decode steps (Q2_K 2048->6144->2048, source contract) on one weight copy, "
-                      f"scalar C restatement, rows split over {threads} threads"}
+    x1 = synth.activations(HIDDEN, seed=104)
+    add("c1 Q2_K FFN step 2048->6144->2048", "GB/s", ffn_step_bytes() / 1e9,
+        lambda t: oracle.ffn(oracle.KIND_Q2_K, HIDDEN, FFN, wg, wu, wd, x1, None, False, t))
+    w2 = synth.ptq1_weights(6144, 2048, seed=9)
+    X2 = synth.activations(2048, seed=10, tokens=16)
+    add("c2 PTQ1 6144x2048 prefill (16 of the M tokens; per-token cost is independent of M)", "Gop/s",
+        2.0 * 16 * 6144 * 2048 / 1e9, lambda t: oracle.prefill(oracle.KIND_PTQ1, 2048, 6144, w2, X2, False, t),
+        sample="16 tokens per run")
+    for kind, name in ((oracle.KIND_PTQ1, "PTQ1"), (oracle.KIND_Q2_K, "Q2_K"), (oracle.KIND_Q8_0, "Q8_0")):
+        w4 = synth.weights(kind, 12288, 4096, seed=7)
+        x4 = synth.activations(4096, seed=8)
+        act = 4096 // 256 * 292 if kind == oracle.KIND_Q2_K else 4096 // 32 * 34
+        add(f"c4 {name} 12288x4096 matvec", "GB/s", (w4.size + act + 4 * 12288) / 1e9,
+            lambda t, w4=w4, x4=x4, kind=kind: oracle.matvec(kind, 4096, 12288, w4, x4, False, t))
+    # c3: the decode step of the oracle (every projection through the scalar dots).
+    od = oracle.Decoder(model, threads=T)
+    pos = [DECODE_POS]
+
+    def step(threads):
+        od.threads = threads
+        oracle.argmax(od.step(1, pos[0]))
+
+    row = {"config": "c3 28-layer decode step", "unit": "tokens/s"}
+    dt, n = _time(lambda: step(T), 8.0, 2)
+    row.update(value=1.0 / dt, ms=dt * 1e3, runs=n)
+    dt1, n1 = _time(lambda: step(1), 0.0, 1, warm=False)
+    row.update(value_1t=1.0 / dt1, ms_1t=dt1 * 1e3, runs_1t=n1)
+    res["configs"].append(row)
+    log(f"cpu c3: {row['value']:.3f} tokens/s at {T} threads, {row['value_1t']:.4f} at 1")
+    return res
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--steps", type=int, default=128, help="decode tokens timed")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode tokens first")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="", help="comma-separated token counts: time only the prefill GEMM")
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
-    ap.add_argument("--decode-only", action="store_true", help="time only the 28-layer decode step")
+    ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
     ap.add_argument("--decode-eager", action="store_true",
-                    help="with --decode-only: launch every kernel each step instead of replaying a HIP graph")
+                    help="time only decode steps launched kernel by kernel (no graph), for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -345,26 +432,33 @@ def main() -> int:
         return calibrate_copy()
     ctx = ph.Context(0)
     log(ctx.identity)
-    if args.decode_only:
-        print(json.dumps(bench_decode(ctx, cpu_steps=0, graph=not args.decode_eager)), flush=True)
-        ctx.close()
-        return 0
-    if args.prefill_only or args.matvec_only:
+    if args.prefill_only or args.matvec_only or args.ffn_only:
         for M in filter(None, args.prefill_only.split(",")):
             print(json.dumps(bench_prefill(ctx, int(M))), flush=True)
         for spec in filter(None, args.matvec_only.split(",")):
             kind, rows, cols, *tok = (int(v) for v in spec.split(":"))
             print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols, tokens=tok[0] if tok else 1)), flush=True)
+        if args.ffn_only:
+            print(json.dumps(bench_ffn(ctx)), flush=True)
         ctx.close()
         return 0
-    ms, wall_ms, copies = bench_ffn(ctx, args.steps, args.warmup)
-    nbytes = ffn_step_bytes()
-    value = nbytes / (ms * 1e-3) / 1e9
-    log(f"ffn step: {ms * 1e3:.2f} us/step (wall {wall_ms * 1e3:.2f}), {value:.1f} GB/s")
-    kern = bench_gateup_kernel(ctx)
-    log(f"gate+up+SwiGLU kernel: {kern['avg_us']:.2f} us, {kern['GBps']:.1f} GB/s")
-    extras = {}
+    t0 = time.perf_counter()
+    model = synth.decoder_model(0)
+    log(f"decode model generated in {time.perf_counter() - t0:.1f} s")
+    if args.decode_eager:
+        dec = ph.Decoder(ctx, model, max_steps=args.steps)
+        _, _, secs = dec.generate(1, DECODE_POS, args.steps, graph=False)
+        dec.close()
+        print(json.dumps({"decode_eager_ms_per_token": secs / args.steps * 1e3}), flush=True)
+        ctx.close()
+        return 0
+    dec = bench_decode(ctx, model, args.steps, args.warmup, profile=True)
+    log(f"decode: {dec['ms_per_token']:.3f} ms/token, {dec['tokens_per_s']:.1f} tok/s; dominant family "
+        f"{dec['dominant']['family']} {dec['dominant']['avg_launch_us']:.2f} us/launch")
+    extras = {"decode_breakdown": dec["eager_profile"]}
     if not args.no_extras:
+        extras["ffn_decode_step"] = bench_ffn(ctx)
+        log(f"ffn step: {extras['ffn_decode_step']['us_per_step']:.2f} us")
         extras["matvec"] = []
         for kind, rows, cols in [(ph.KIND_PTQ1, 2048, 2048), (ph.KIND_PQ2, 2048, 2048), (ph.KIND_Q2_K, HIDDEN, FFN),
                                  (ph.KIND_PTQ1, 12288, 4096), (ph.KIND_Q2_K, 12288, 4096), (ph.KIND_Q8_0, 12288, 4096),
@@ -389,16 +483,23 @@ def main() -> int:
             r = bench_prefill(ctx, M)
             log(f"prefill M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
             extras["prefill_ptq1_6144x2048"].append(r)
-        r = bench_decode(ctx)
-        log(f"decode: {r['ms_per_token']:.3f} ms/token, {r['tokens_per_s']:.1f} tok/s, {r['GBps']:.1f} GB/s")
-        extras["decode_28_layer"] = r
-    cpu = None if args.no_cpu else cpu_baseline()
-    if cpu:
-        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    ctx.close()
+    cpu = None
+    if not args.no_cpu:
+        cb = cpu_baselines(model)
+        extras["cpu_baselines"] = cb
+        c3 = next(r for r in cb["configs"] if r["config"].startswith("c3"))
+        cpu = {"value": c3["value"], "unit": "tokens/s", "cores": cb["threads"], "kind": "port",
+               "value_1_thread": c3["value_1t"], "nproc": cb["host"]["nproc"],
+               "cores_available": cb["host"]["cores_available"], "cpu_model": cb["host"]["cpu_model"],
+               "sample": f"{c3['runs']} decode steps at {cb['threads']} threads and {c3['runs_1t']} at one "
+                         f"thread of the scalar C restatement (every projection through the reference's dot "
+                         f"order), rows split evenly over the threads"}
+    ms = dec["ms_per_token"]
     line = {
         "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "GB/s",
+        "value": round(dec["tokens_per_s"], 2),
+        "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -406,24 +507,19 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int2xint8->int32, f32 chain",
-        "data": "synthetic (seeded; weights rotated over distinct device copies)",
-        "config": {"workload": "Qwen35-shaped dense FFN decode step, batch 1: Q2_K gate/up 2048->6144, "
-                               "SwiGLU, down 6144->2048, source contract",
-                   "hidden": HIDDEN, "ffn": FFN, "format": "Q2_K x Q8_K", "weight_copies": copies,
-                   "bytes_per_step": nbytes, "frac_hbm_peak": round(value * 1e9 / PEAK_HBM, 4),
-                   "tokens_per_s": round(1e3 / ms, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(kern["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": round(kern["GBps"] * 1e9 / PEAK_HBM, 4),
-                     "traffic": measured_traffic("ffn_gateup_traffic.md"),
-                     "kernel": "k_mv_split<Q2K, quantizing prologue, gate+up> (FFN gate+up+SwiGLU, 2x 6144x2048 Q2_K)",
-                     "bytes_per_launch": kern["bytes_per_launch"], "avg_launch_us": round(kern["avg_us"], 3)},
+        "dtype": "ternary/int8 x int8 -> int32, f32 chains; f16 KV",
+        "data": "synthetic (seeded random-init weights of the stated architecture; KV cache prefilled N(0,1))",
+        "config": {"workload": "28-layer synthetic decode step, batch 1, greedy: hidden 2048, 16/4 heads x 128, "
+                               "FFN 6144, PTQ1 linears, RMSNorm, RoPE, f16 KV cache prefilled to 1024 tokens, "
+                               "tied Q8_0 LM head 151936",
+                   "layers": 28, "hidden": HIDDEN, "ffn": FFN, "vocab": 151936, "kv_prefill": DECODE_POS,
+                   "bytes_per_token": dec["bytes_per_token"], "GBps": round(dec["GBps"], 1),
+                   "frac_hbm_peak": round(dec["frac_hbm"], 4), "first_tokens": dec["first_tokens"]},
+        "roofline": decode_roofline(dec),
         "cpu_baseline": cpu,
+        "extras": extras,
     }
-    if extras:
-        line["extras"] = extras
     print(json.dumps(line), flush=True)
-    ctx.close()
     return 0
 
 

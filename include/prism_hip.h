@@ -245,6 +245,32 @@ int prism_hip_decoder_set_head(prism_hip_decoder *d, const uint8_t *lm_head, con
 int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t pos, uint32_t steps, int use_graph,
                                uint32_t *tokens_out, float *logits_out, double *seconds);
 
+/* Measurement hooks of the decoder (no counterpart in the reference; for benchmarks and
+ * profiles).  A step's launches form nine families, in step order: "qkv", "attn_scores",
+ * "attn_values", "o", "gate_up", "down" (per layer), then "lm_prep", "lm_head", "greedy". */
+#define PRISM_DECODER_FAMILIES 9
+typedef struct {
+    const char *name;  /* family name (static storage) */
+    uint32_t launches; /* launches timed */
+    double total_us;   /* their summed event-bracketed times */
+    uint64_t bytes;    /* algorithmic bytes of one launch: packed weights at native size, f32 activations and
+                          outputs, Q8_0 blocks at 34 bytes, binary16 cache rows read and appended */
+} prism_decoder_launch_time;
+/* Runs `steps` greedy steps from (token, pos) with launches issued one by one (no graph)
+ * and a HIP event recorded on the context stream before every launch and after the
+ * last; stats[PRISM_DECODER_FAMILIES] receives, per family, the launches timed, the
+ * summed times between consecutive events (each launch with its dispatch gap) and the
+ * bytes of one launch at position pos.  The decoder state advances as in generate. */
+int prism_hip_decoder_profile(prism_hip_decoder *d, uint32_t token, uint64_t pos, uint32_t steps,
+                              prism_decoder_launch_time *stats);
+/* Launches one family (not "greedy") `reps` times per layer back to back at the
+ * decoder's current position, cycling through the layers (the head's families run
+ * `reps` times), with HIP events around the whole run: *avg_us receives the mean time
+ * per launch and *bytes (may be NULL) the algorithmic bytes of one launch.  The
+ * families other than "greedy" only recompute what a step at that position computes. */
+int prism_hip_decoder_time_family(prism_hip_decoder *d, const char *family, uint32_t reps, double *avg_us,
+                                  uint64_t *bytes);
+
 /* ---- GGUF v3 weights (tools/gguf) --------------------------------------------------
  * A bounded reader of the GGUF header, metadata table and tensor index: the checks of
  * read_index (tools/gguf/src/stream.rs:349-657) -- magic, version, counts, unique keys

@@ -464,12 +464,27 @@ __global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ 
 
 size_t argmax_scratch_bytes() { return (sizeof(float) + sizeof(uint32_t)) * kArgmaxGroups; }
 
+namespace {
+bool attention_supported(const AttnArgs &a) {
+    return a.head_dim == kHead && a.rope <= kHead && a.rope % 2 == 0 && a.kv_heads != 0 && a.heads % a.kv_heads == 0 &&
+           a.max_tokens != 0 && a.max_tokens <= kMaxTokens;
+}
+}  // namespace
+
 int launch_attention(const AttnArgs &a) {
-    if (a.head_dim != kHead || a.rope > kHead || a.rope % 2 || a.kv_heads == 0 || a.heads % a.kv_heads ||
-        a.max_tokens == 0 || a.max_tokens > kMaxTokens)
-        return -2;
+    const int rc = launch_attn_scores(a);
+    return rc ? rc : launch_attn_values(a);
+}
+
+int launch_attn_scores(const AttnArgs &a) {
+    if (!attention_supported(a)) return -2;
     const dim3 sg(a.heads, (a.max_tokens + kScoreChunk - 1) / kScoreChunk);
     hipLaunchKernelGGL(k_attn_scores, sg, dim3(256), 0, a.stream, a);
+    return launch_status();
+}
+
+int launch_attn_values(const AttnArgs &a) {
+    if (!attention_supported(a)) return -2;
     const dim3 vg(a.heads, kHead / kValueDims), vb(1024);
     if (a.max_tokens <= 1024)
         hipLaunchKernelGGL(k_attn_values<1>, vg, vb, 0, a.stream, a);

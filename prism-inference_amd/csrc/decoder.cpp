@@ -14,6 +14,8 @@
 // then the final norm + Q8_0 quantization, the Q8_0 LM head (row-tile kernel) and
 // the greedy choice, which also writes the next step's embedding.
 #include <cmath>
+#include <cstring>
+#include <vector>
 
 #include "runtime_internal.hpp"
 
@@ -116,12 +118,22 @@ RopeArgs rope_args(const prism_decoder_geometry &g) {
     return r;
 }
 
-// Enqueues one decode step on the context stream (also used under graph capture).
-int enqueue_step(prism_hip_decoder *d) {
+// Launch families of one step, in step order (the measurement entry points report
+// them by these names).
+enum Family : int { kQkv, kScores, kValues, kO, kGateUp, kDown, kLmPrep, kLmHead, kGreedy, kFamilies };
+const char *const kFamilyName[kFamilies] = {"qkv",     "attn_scores", "attn_values", "o",     "gate_up",
+                                            "down",    "lm_prep",     "lm_head",     "greedy"};
+
+// Called before every launch of a step (family, layer; layer 0 for the head); used to
+// bracket launches with events.  nullptr in the step the graph captures.
+struct StepHook {
+    virtual int before(Family f, uint32_t layer) = 0;
+    virtual ~StepHook() = default;
+};
+
+AttnArgs attn_args(prism_hip_decoder *d) {
     prism_hip_ctx *c = d->ctx;
     const prism_decoder_geometry &g = d->g;
-    hipStream_t s = c->stream;
-    float *h0 = d->hidden[0], *h1 = d->hidden[1];
     AttnArgs at{};
     at.qkv = d->qkv;
     at.scores = d->scores;
@@ -134,33 +146,84 @@ int enqueue_step(prism_hip_decoder *d) {
     at.max_tokens = static_cast<uint32_t>(g.max_tokens);
     at.eps = g.eps;
     at.err = c->err;
-    at.stream = s;
-    for (const auto &L : d->layers) {
-        int rc = project(d, L.qkv, h0, d->qkv, nullptr, L.norm);
-        if (rc) return rc;
-        at.q_norm = L.q_norm;
-        at.k_norm = L.k_norm;
-        at.kcache = L.kc;
-        at.vcache = L.vc;
-        rc = launch_result(c, launch_attention(at), "attention launch");
-        if (rc) return rc;
-        rc = project(d, L.o, d->att, h1, h0, nullptr);
-        if (!rc) rc = project(d, L.gate, h1, nullptr, nullptr, L.post_norm, L.up, d->ffn_q8);
-        if (!rc) rc = project_q8(d, L.down, d->ffn_q8, h0, h1);
+    at.stream = c->stream;
+    return at;
+}
+
+// One launch family for one layer (the head's families ignore `layer`).
+int launch_family(prism_hip_decoder *d, Family f, uint32_t layer) {
+    prism_hip_ctx *c = d->ctx;
+    const prism_decoder_geometry &g = d->g;
+    float *h0 = d->hidden[0], *h1 = d->hidden[1];
+    const auto &L = d->layers[layer < d->layers.size() ? layer : 0];
+    AttnArgs at = attn_args(d);
+    at.q_norm = L.q_norm;
+    at.k_norm = L.k_norm;
+    at.kcache = L.kc;
+    at.vcache = L.vc;
+    switch (f) {
+    case kQkv: return project(d, L.qkv, h0, d->qkv, nullptr, L.norm);
+    case kScores: return launch_result(c, launch_attn_scores(at), "attention scores launch");
+    case kValues: return launch_result(c, launch_attn_values(at), "attention values launch");
+    case kO: return project(d, L.o, d->att, h1, h0, nullptr);
+    case kGateUp: return project(d, L.gate, h1, nullptr, nullptr, L.post_norm, L.up, d->ffn_q8);
+    case kDown: return project_q8(d, L.down, d->ffn_q8, h0, h1);
+    case kLmPrep:
+        return launch_result(c, launch_lm_prep(h0, d->output_norm, static_cast<uint32_t>(g.hidden), g.eps, d->lm_act,
+                                               c->err, c->stream),
+                             "final norm launch");
+    case kLmHead: return matvec(c, *find(c, d->lm_head), kActQ8, d->lm_act, 1, 0, d->logits, c->stream);
+    case kGreedy:
+        return launch_result(c,
+                             launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), find(c, d->lm_head)->dev,
+                                                 static_cast<uint32_t>(g.hidden), d->state, rope_args(g), d->tokens,
+                                                 d->max_steps, h0, d->argmax_scratch, c->stream),
+                             "argmax launch");
+    default: return fail(c, PRISM_ERR_INVALID_INPUT, "unknown launch family");
+    }
+}
+
+// Enqueues one decode step on the context stream (also used under graph capture).
+int enqueue_step(prism_hip_decoder *d, StepHook *hook = nullptr) {
+    auto run = [&](Family f, uint32_t layer) {
+        if (hook) {
+            const int rc = hook->before(f, layer);
+            if (rc) return rc;
+        }
+        return launch_family(d, f, layer);
+    };
+    for (uint32_t l = 0; l < d->layers.size(); ++l)
+        for (Family f : {kQkv, kScores, kValues, kO, kGateUp, kDown}) {
+            const int rc = run(f, l);
+            if (rc) return rc;
+        }
+    for (Family f : {kLmPrep, kLmHead, kGreedy}) {
+        const int rc = run(f, 0);
         if (rc) return rc;
     }
-    const Weight *lm = find(c, d->lm_head);
-    int rc = launch_result(c, launch_lm_prep(h0, d->output_norm, static_cast<uint32_t>(g.hidden), g.eps, d->lm_act,
-                                             c->err, s),
-                           "final norm launch");
-    if (!rc) rc = matvec(c, *lm, kActQ8, d->lm_act, 1, 0, d->logits, s);
-    if (!rc)
-        rc = launch_result(c,
-                           launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), lm->dev,
-                                               static_cast<uint32_t>(g.hidden), d->state, rope_args(g), d->tokens,
-                                               d->max_steps, h0, d->argmax_scratch, s),
-                           "argmax launch");
-    return rc;
+    return PRISM_OK;
+}
+
+// Algorithmic bytes of one launch of family f at decode position pos: packed weights
+// at their native size, f32 activations and outputs, Q8_0 blocks at 34 bytes, binary16
+// cache rows read (pos + 1 of them) and appended.
+uint64_t family_bytes(const prism_hip_decoder *d, Family f, uint64_t pos) {
+    const prism_decoder_geometry &g = d->g;
+    const uint64_t H = g.hidden, F = g.ffn, D = g.head_dim, QW = g.heads * D, KW = g.kv_heads * D, QKV = QW + 2 * KW;
+    auto ptq1 = [](uint64_t rows, uint64_t cols) { return rows * (cols / 128) * 28; };
+    const uint64_t n = pos + 1;
+    switch (f) {
+    case kQkv: return ptq1(QKV, H) + 4 * H + 4 * H + 4 * QKV;
+    case kScores: return 4 * QKV + 2 * 4 * D + n * KW * 2 + 2 * KW * 2 + 4 * g.heads * n;
+    case kValues: return 4 * g.heads * n + n * KW * 2 + 4 * QW;
+    case kO: return ptq1(H, QW) + 4 * QW + 4 * H + 4 * H;
+    case kGateUp: return 2 * ptq1(F, H) + 4 * H + 4 * H + F / 32 * 34;
+    case kDown: return ptq1(H, F) + F / 32 * 34 + 4 * H + 4 * H;
+    case kLmPrep: return 4 * H + 4 * H + H / 32 * 34;
+    case kLmHead: return g.vocab * (H / 32) * 34 + H / 32 * 34 + 4 * g.vocab;
+    case kGreedy: return 4 * g.vocab + H / 32 * 34 + 4 * H;
+    default: return 0;
+    }
 }
 
 void drop_graph(prism_hip_decoder *d) {
@@ -179,6 +242,56 @@ bool ready(prism_hip_decoder *d) {
         for (prism_weight_id w : {L.qkv, L.o, L.gate, L.up, L.down}) ok = ok && w && find(d->ctx, w);
     if (!ok) drop_graph(d);
     return ok;
+}
+
+// Resets the device state to (token, pos) and writes the token's embedding.
+int start(prism_hip_decoder *d, uint32_t token, uint64_t pos) {
+    prism_hip_ctx *c = d->ctx;
+    hipStream_t s = c->stream;
+    const DecodeState init{static_cast<uint32_t>(pos), token, 0, 0};
+    HIP_OR_FAIL(c, hipMemcpyAsync(d->state, &init, sizeof(init), hipMemcpyHostToDevice, s));
+    HIP_OR_FAIL(c, hipStreamSynchronize(s));
+    const Weight *lm = find(c, d->lm_head);
+    return launch_result(c,
+                         launch_embed(lm->dev, d->g.vocab, static_cast<uint32_t>(d->g.hidden), d->state,
+                                      rope_args(d->g), d->hidden[0], s),
+                         "embed launch");
+}
+
+// Records an event on the context stream before every launch of a step.
+struct EventHook final : StepHook {
+    prism_hip_ctx *c;
+    std::vector<hipEvent_t> ev;
+    std::vector<Family> fam;
+    size_t used = 0;
+    explicit EventHook(prism_hip_ctx *ctx) : c(ctx) {}
+    ~EventHook() override {
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    }
+    int mark() {
+        if (used == ev.size()) {
+            hipEvent_t e = nullptr;
+            HIP_OR_FAIL(c, hipEventCreate(&e));
+            ev.push_back(e);
+        }
+        HIP_OR_FAIL(c, hipEventRecord(ev[used], c->stream));
+        ++used;
+        return PRISM_OK;
+    }
+    int before(Family f, uint32_t) override {
+        fam.push_back(f);
+        return mark();
+    }
+};
+
+int family_of(const char *name, Family *f) {
+    if (!name) return PRISM_ERR_INVALID_INPUT;
+    for (int i = 0; i < kFamilies; ++i)
+        if (std::strcmp(name, kFamilyName[i]) == 0) {
+            *f = static_cast<Family>(i);
+            return PRISM_OK;
+        }
+    return PRISM_ERR_INVALID_INPUT;
 }
 
 }  // namespace
@@ -317,14 +430,7 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
         HIP_OR_FAIL(c, hipMalloc(&d->logits_all, sizeof(float) * vocab * steps));
         d->logits_all_steps = steps;
     }
-    const DecodeState init{static_cast<uint32_t>(pos), token, 0, 0};
-    HIP_OR_FAIL(c, hipMemcpyAsync(d->state, &init, sizeof(init), hipMemcpyHostToDevice, s));
-    HIP_OR_FAIL(c, hipStreamSynchronize(s));
-    const Weight *lm = find(c, d->lm_head);
-    rc = launch_result(c,
-                       launch_embed(lm->dev, d->g.vocab, static_cast<uint32_t>(d->g.hidden), d->state, rope_args(d->g),
-                                    d->hidden[0], s),
-                       "embed launch");
+    rc = start(d, token, pos);
     if (rc) return rc;
     if (use_graph && !d->exec) {
         HIP_OR_FAIL(c, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -382,6 +488,87 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
         if (logits_out) std::memset(logits_out, 0, sizeof(float) * vocab * steps);
     }
     return rc;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int prism_hip_decoder_profile(prism_hip_decoder *d, uint32_t token, uint64_t pos, uint32_t steps,
+                              prism_decoder_launch_time *stats) {
+    if (!d) return PRISM_ERR_INVALID_INPUT;
+    prism_hip_ctx *c = d->ctx;
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!stats) return fail(c, PRISM_ERR_INVALID_INPUT, "stats required");
+    for (int i = 0; i < kFamilies; ++i) {
+        stats[i].name = kFamilyName[i];
+        stats[i].launches = 0;
+        stats[i].total_us = 0.0;
+        stats[i].bytes = family_bytes(d, static_cast<Family>(i), pos);
+    }
+    if (!ready(d)) return fail(c, PRISM_ERR_INVALID_INPUT, "decoder weights not set");
+    if (steps == 0 || steps > d->max_steps || token >= d->g.vocab || pos + steps > d->g.max_tokens)
+        return fail(c, PRISM_ERR_INVALID_INPUT, "bad profile arguments");
+    rc = start(d, token, pos);
+    EventHook hook(c);
+    for (uint32_t i = 0; i < steps && !rc; ++i) {
+        hook.used = 0;
+        hook.fam.clear();
+        rc = enqueue_step(d, &hook);
+        if (!rc) rc = hook.mark();  // end of the step's last launch
+        if (!rc) rc = drain(c, c->stream);
+        for (size_t k = 0; !rc && k + 1 < hook.used; ++k) {
+            float ms = 0.0f;
+            const hipError_t e = hipEventElapsedTime(&ms, hook.ev[k], hook.ev[k + 1]);
+            if (e != hipSuccess) {
+                rc = hip_fail(c, e, "hipEventElapsedTime");
+                break;
+            }
+            prism_decoder_launch_time &st = stats[hook.fam[k]];
+            st.launches += 1;
+            st.total_us += 1e3 * ms;
+        }
+    }
+    return rc;
+}
+
+int prism_hip_decoder_time_family(prism_hip_decoder *d, const char *family, uint32_t reps, double *avg_us,
+                                  uint64_t *bytes) {
+    if (!d) return PRISM_ERR_INVALID_INPUT;
+    prism_hip_ctx *c = d->ctx;
+    int rc = check_ready(c);
+    if (rc) return rc;
+    Family f;
+    if (family_of(family, &f) || f == kGreedy || reps == 0 || !avg_us)
+        return fail(c, PRISM_ERR_INVALID_INPUT, "bad family timing arguments");
+    if (!ready(d)) return fail(c, PRISM_ERR_INVALID_INPUT, "decoder weights not set");
+    DecodeState st{};
+    HIP_OR_FAIL(c, hipMemcpy(&st, d->state, sizeof(st), hipMemcpyDeviceToHost));
+    if (st.pos >= d->g.max_tokens) return fail(c, PRISM_ERR_INVALID_INPUT, "decoder position past the cache");
+    const bool per_layer = f <= kDown;
+    const uint32_t layers = per_layer ? static_cast<uint32_t>(d->layers.size()) : 1;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    HIP_OR_FAIL(c, hipEventCreate(&t0));
+    hipError_t e = hipEventCreate(&t1);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(t0);
+        return hip_fail(c, e, "hipEventCreate");
+    }
+    e = hipEventRecord(t0, c->stream);
+    if (e != hipSuccess) rc = hip_fail(c, e, "hipEventRecord");
+    for (uint32_t r = 0; r < reps && !rc; ++r)
+        for (uint32_t l = 0; l < layers && !rc; ++l) rc = launch_family(d, f, l);
+    if (!rc && (e = hipEventRecord(t1, c->stream)) != hipSuccess) rc = hip_fail(c, e, "hipEventRecord");
+    if (!rc) rc = drain(c, c->stream);
+    float ms = 0.0f;
+    if (!rc && (e = hipEventElapsedTime(&ms, t0, t1)) != hipSuccess) rc = hip_fail(c, e, "hipEventElapsedTime");
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    if (rc) return rc;
+    *avg_us = 1e3 * ms / (static_cast<double>(reps) * layers);
+    if (bytes) *bytes = family_bytes(d, f, st.pos);
+    return PRISM_OK;
 }
 
 }  // extern "C"

@@ -113,8 +113,11 @@ struct AttnArgs {
     int *err;
     hipStream_t stream;
 };
-// q/k norm + RoPE + KV append + scores, then softmax + values: two launches.
+// q/k norm + RoPE + KV append + scores, then softmax + values: two launches
+// (launch_attn_scores, then launch_attn_values).
 int launch_attention(const AttnArgs &a);
+int launch_attn_scores(const AttnArgs &a);
+int launch_attn_values(const AttnArgs &a);
 // Final RMSNorm + Q8_0 (source) quantization of n values into q8_out.
 int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *q8_out, int *err, hipStream_t s);
 // out = dequantized row state->token of the tiled Q8_0 matrix [rows][cols]; the state's

@@ -108,6 +108,8 @@ def lib() -> ctypes.CDLL:
         "prism_hip_decoder_set_cache": (I, [P, U32, P, P, U64]),
         "prism_hip_decoder_set_head": (I, [P, P, P]),
         "prism_hip_decoder_generate": (I, [P, U32, U64, U32, I, P, P, P]),
+        "prism_hip_decoder_profile": (I, [P, U32, U64, U32, P]),
+        "prism_hip_decoder_time_family": (I, [P, ctypes.c_char_p, U32, P, P]),
         "prism_gguf_default_policy": (None, [P]),
         "prism_gguf_open": (I, [ctypes.c_char_p, P, P]),
         "prism_gguf_close": (None, [P]),
@@ -454,6 +456,15 @@ class Context:
         return lib().prism_hip_sync(self._h, stream)
 
 
+class DecoderLaunchTime(ctypes.Structure):
+    """prism_decoder_launch_time."""
+    _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint32), ("total_us", ctypes.c_double),
+                ("bytes", ctypes.c_uint64)]
+
+
+DECODER_FAMILIES = 9
+
+
 class DecoderGeometry(ctypes.Structure):
     """prism_decoder_geometry."""
     _fields_ = [(n, ctypes.c_uint64) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "rope", "vocab",
@@ -507,6 +518,21 @@ class Decoder:
         self._check(lib().prism_hip_decoder_generate(self._h, token, pos, steps, int(graph), _ptr(toks),
                                                      _ptr(lg) if logits else None, ctypes.byref(secs)))
         return toks, lg, secs.value
+
+    def profile(self, token: int, pos: int, steps: int) -> list[dict]:
+        """Eager steps with an event before every launch: per launch family, the launches
+        timed, their summed microseconds (dispatch gaps included) and bytes per launch."""
+        st = (DecoderLaunchTime * DECODER_FAMILIES)()
+        self._check(lib().prism_hip_decoder_profile(self._h, token, pos, steps, st))
+        return [{"family": s.name.decode(), "launches": int(s.launches), "total_us": float(s.total_us),
+                 "bytes_per_launch": int(s.bytes)} for s in st]
+
+    def time_family(self, family: str, reps: int) -> tuple[float, int]:
+        """Back-to-back launches of one family (layers cycled): (mean us per launch, bytes)."""
+        us, nb = ctypes.c_double(0.0), ctypes.c_uint64(0)
+        self._check(lib().prism_hip_decoder_time_family(self._h, family.encode(), reps, ctypes.byref(us),
+                                                        ctypes.byref(nb)))
+        return us.value, int(nb.value)
 
     def close(self) -> None:
         if self._h:

@@ -130,3 +130,44 @@ def test_gpu_decoder_detects_released_weights(ctx):
         assert np.array_equal(toks, again)
     finally:
         dec.close()
+
+
+def test_gpu_decoder_profile_and_family_timing(ctx):
+    """The measurement hooks: an eager profile times every launch of every family
+    (six per layer, three for the head) and leaves the decoder generating the same bits;
+    a family timed back to back reports its algorithmic bytes; 'greedy' (which advances
+    the state) and unknown names are rejected."""
+    model = synth.decoder_model(5, kv_prefill=20, **SMALL)
+    g = model["geometry"]
+    dec = ph.Decoder(ctx, model, max_steps=16)
+    try:
+        toks, logits, _ = dec.generate(3, 20, 4, graph=True, logits=True)
+        fams = dec.profile(3, 20, 2)
+        names = [f["family"] for f in fams]
+        assert names == ["qkv", "attn_scores", "attn_values", "o", "gate_up", "down", "lm_prep", "lm_head", "greedy"]
+        for f in fams:
+            want = 2 * (g["layers"] if f["family"] in names[:6] else 1)
+            assert f["launches"] == want, f
+            assert f["total_us"] > 0.0 and f["bytes_per_launch"] > 0, f
+        D, H, F = g["head_dim"], g["hidden"], g["ffn"]
+        qkv = (g["heads"] + 2 * g["kv_heads"]) * D
+        by = {f["family"]: f["bytes_per_launch"] for f in fams}
+        assert by["qkv"] == qkv * H // 128 * 28 + 8 * H + 4 * qkv
+        assert by["lm_head"] == g["vocab"] * (H // 32) * 34 + H // 32 * 34 + 4 * g["vocab"]
+        assert by["gate_up"] == 2 * F * H // 128 * 28 + 8 * H + F // 32 * 34
+        toks2, logits2, _ = dec.generate(3, 20, 4, graph=True, logits=True)
+        assert np.array_equal(toks, toks2)
+        assert np.array_equal(logits.view(np.uint32), logits2.view(np.uint32))
+        for fam in ("qkv", "attn_values", "down", "lm_head"):
+            us, nb = dec.time_family(fam, 3)
+            assert us > 0.0, (fam, us)
+            if not fam.startswith("attn"):  # attention bytes grow with the position
+                assert nb == by[fam], (fam, nb)
+        for bad in ("greedy", "nope"):
+            with pytest.raises(ph.PrismError) as e:
+                dec.time_family(bad, 1)
+            assert e.value.code == ph.ERR_INVALID_INPUT
+        toks3, logits3, _ = dec.generate(3, 20, 4, graph=True, logits=True)
+        assert np.array_equal(logits.view(np.uint32), logits3.view(np.uint32))
+    finally:
+        dec.close()
