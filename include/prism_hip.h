@@ -101,6 +101,27 @@ int64_t prism_hip_operation_count(const prism_hip_ctx *ctx, uint32_t kind, uint6
  * from geometry alone before any launch.  Returns 1 or 0. */
 int prism_hip_supports(const prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows, int path);
 
+/* A tensor as the trait's eligibility queries see it: Tensor's kind and dimensions
+ * [cols, rows] (src/model.rs:184-193). */
+typedef struct prism_tensor_desc {
+    uint32_t kind;
+    uint64_t cols, rows;
+} prism_tensor_desc;
+/* supports_f32_group (projection.rs:112-114): 1..8 siblings that can share one F32
+ * input -- every member supports F32, one input width, and one activation contract
+ * under both pinned settings.  Returns 1 or 0. */
+int prism_hip_supports_f32_group(const prism_hip_ctx *ctx, const prism_tensor_desc *tensors, uint32_t n);
+/* supports_f32_ffn_swiglu (projection.rs:212-214): gate and up of one packed kind and
+ * one geometry [ffn][hidden]. */
+int prism_hip_supports_f32_ffn_swiglu(const prism_hip_ctx *ctx, const prism_tensor_desc *gate,
+                                      const prism_tensor_desc *up);
+/* supports_f32_ffn_chain (projection.rs:261-263): tensors[3] = gate, up [ffn][hidden]
+ * and down [hidden][ffn], one packed kind.  The chain has no Hadamard transform. */
+int prism_hip_supports_f32_ffn_chain(const prism_hip_ctx *ctx, const prism_tensor_desc *tensors);
+/* supports_tile_tokens (projection.rs:265-269; trait default false): multi-token tiles run batched on the
+ * device (one weight read per batch of tokens).  1 unless faulted. */
+int prism_hip_supports_tile_tokens(const prism_hip_ctx *ctx);
+
 /* ---- weights ------------------------------------------------------------------ */
 
 /* Upload-or-lookup of a packed row-major tensor [rows][cols] (bytes must equal
@@ -118,6 +139,21 @@ prism_weight_id prism_hip_weight_acquire_device(prism_hip_ctx *ctx, uint64_t key
  * caller keeps it alive until release. */
 prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows,
                                              const void *device_ptr, uint64_t bytes);
+/* The fast layout in caller-owned memory: the caller's allocator owns the device buffer
+ * (BufferType{alignment, maximum} / GraphAllocator sizing, src/backend/allocator.rs:10-50)
+ * and the context only references it.
+ * prism_hip_weight_tiled_bytes: device bytes of the 64-row tiled image of a tensor, or 0
+ *   when the tensor has no tiled layout on this device (it then runs on the native-layout
+ *   kernels: use prism_hip_weight_wrap_device).
+ * prism_hip_weight_repack_tiled: writes that image from native bytes in device memory
+ *   (read only during the call) into tiled_dev, which holds exactly tiled_bytes; synchronous.
+ * prism_hip_weight_wrap_tiled: registers a buffer holding that image (no copy); the caller
+ *   keeps it alive until release.  Projections of it run the tiled kernels. */
+uint64_t prism_hip_weight_tiled_bytes(const prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows);
+int prism_hip_weight_repack_tiled(prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows,
+                                  const void *native_dev, uint64_t native_bytes, void *tiled_dev, uint64_t tiled_bytes);
+prism_weight_id prism_hip_weight_wrap_tiled(prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows,
+                                            const void *tiled_dev, uint64_t tiled_bytes);
 int prism_hip_weight_release(prism_hip_ctx *ctx, prism_weight_id w);
 int prism_hip_weight_release_all(prism_hip_ctx *ctx);
 uint64_t prism_hip_resident_bytes(const prism_hip_ctx *ctx);
@@ -144,14 +180,33 @@ int prism_hip_project_f32(prism_hip_ctx *ctx, prism_weight_id w, const float *x,
 /* project_f32_group (projection.rs:115-130): n (1..8) siblings sharing one input. */
 int prism_hip_project_f32_group(prism_hip_ctx *ctx, const prism_weight_id *ws, uint32_t n, const float *x,
                                 int pinned, float *const *outs);
+/* The group over a tile of tokens: x holds tokens*cols floats, outs[i] receives
+ * [tokens][rows_i]; every row equals that token's own project_f32_group.
+ * project_f32_pair_tokens / project_f32_triple_tokens (projection.rs:158-210) are the
+ * n = 2 and n = 3 cases. */
+int prism_hip_project_f32_group_tokens(prism_hip_ctx *ctx, const prism_weight_id *ws, uint32_t n, const float *x,
+                                       uint32_t tokens, int pinned, float *const *outs);
+int prism_hip_project_f32_pair_tokens(prism_hip_ctx *ctx, const prism_weight_id *ws, const float *x, uint32_t tokens,
+                                      int pinned, float *out_a, float *out_b);
+int prism_hip_project_f32_triple_tokens(prism_hip_ctx *ctx, const prism_weight_id *ws, const float *x,
+                                        uint32_t tokens, int pinned, float *out_a, float *out_b, float *out_c);
 /* project_f32_ffn_swiglu (projection.rs:206-222): out[ffn] = SwiGLU(gate(x), up(x)). */
 int prism_hip_ffn_swiglu(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
                          float *out);
 /* project_f32_ffn_chain (projection.rs:250-287) without the Hadamard transform:
- * out[hidden] = down(SwiGLU(gate(x), up(x))) (+ residual if non-NULL).  Accepts
- * PQ2 and Q2_K triples. */
+ * out[hidden] = down(SwiGLU(gate(x), up(x))) (+ residual if non-NULL).  Gate, up
+ * and down share one packed kind (PQ2, PTQ1, Q2_K, Q8_0, TQ1_0 or TQ2_0). */
 int prism_hip_ffn_chain(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                         const float *x, const float *residual, int pinned, float *out);
+/* project_f32_ffn_swiglu_tokens (projection.rs:239-259) and project_f32_ffn_chain_tokens
+ * (projection.rs:328-355) without the Hadamard transform: x [tokens][hidden], residual
+ * (or NULL) and out [tokens][hidden] (SwiGLU: out [tokens][ffn]).  Gate and up run as
+ * one sibling group over all tokens, so each weight is read once per batch of tokens;
+ * every row equals that token's single-token chain. */
+int prism_hip_ffn_swiglu_tokens(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, const float *x,
+                                uint32_t tokens, int pinned, float *out);
+int prism_hip_ffn_chain_tokens(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                               const float *x, const float *residual, uint32_t tokens, int pinned, float *out);
 /* Tiled prefill (src/kernels/prefill.rs:200-725): X[tokens][cols] -> out[tokens][rows];
  * every token row is bit-identical to its own project_f32. */
 int prism_hip_prefill(prism_hip_ctx *ctx, prism_weight_id w, const float *x, uint32_t tokens, int pinned,

@@ -23,13 +23,16 @@ int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t 
                     DevBuf &role, hipStream_t s, const float *residual = nullptr, Scratch *sc = nullptr) {
     Scratch grow{c};
     Scratch &scr = sc ? *sc : grow;
-    if (w.tiled && tokens >= kPrefillMinTokens && !residual &&
-        prefill_supported(w.kind, w.cols, w.rows, pinned, tokens)) {
+    if (w.tiled && tokens >= kPrefillMinTokens && prefill_supported(w.kind, w.cols, w.rows, pinned, tokens)) {
         void *pre = nullptr;
         int rc = scr.get(c->pre, prefill_scratch_bytes(w.cols, tokens), &pre);
         if (rc) return rc;
-        return launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, pre, c->err, s),
-                             "prefill launch");
+        rc = launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, pre, c->err, s), "prefill launch");
+        // The residual joins after the projection, one binary32 add per output (as the
+        // row kernels do in their epilogue).
+        if (!rc && residual)
+            rc = launch_result(c, launch_add_residual(out, residual, w.rows * tokens, c->err, s), "residual launch");
+        return rc;
     }
     if (w.tiled) {
         MatvecArgs a = f32_args(c, w, x, tokens, pinned, out, residual, s);
@@ -63,6 +66,41 @@ bool eligible(uint32_t kind, uint64_t cols, uint64_t rows, int path) {
     default: return false;
     }
 }
+
+// Whether two tensors take one activation contract under both pinned settings, so one
+// quantized input serves both whatever the caller passes as `pinned`.
+bool same_contract(uint32_t k0, uint64_t c0, uint32_t k1, uint64_t c1) {
+    return c0 == c1 && contract_for(k0, c0, 0) == contract_for(k1, c1, 0) &&
+           contract_for(k0, c0, 1) == contract_for(k1, c1, 1);
+}
+
+// supports_f32_group: 1..8 direct-F32 siblings sharing one input width and contract.
+bool group_eligible(const prism_tensor_desc *t, uint32_t n) {
+    if (!t || n == 0 || n > 8) return false;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!eligible(t[i].kind, t[i].cols, t[i].rows, PRISM_PATH_F32)) return false;
+        if (!same_contract(t[0].kind, t[0].cols, t[i].kind, t[i].cols)) return false;
+    }
+    return true;
+}
+
+// The packed kinds the FFN chains run on, one kind for gate, up and down.
+bool ffn_kind(uint32_t kind) {
+    return kind == PRISM_KIND_PQ2 || kind == PRISM_KIND_Q2_K || kind == PRISM_KIND_PTQ1 || kind == PRISM_KIND_Q8_0 ||
+           kind == PRISM_KIND_TQ1_0 || kind == PRISM_KIND_TQ2_0;
+}
+
+// supports_f32_ffn_swiglu / supports_f32_ffn_chain: gate and up [ffn][hidden] of one
+// kind; down (if given) [hidden][ffn] of the same kind.
+bool ffn_eligible(const prism_tensor_desc &g, const prism_tensor_desc &u, const prism_tensor_desc *d) {
+    if (!ffn_kind(g.kind) || g.kind != u.kind || g.cols != u.cols || g.rows != u.rows) return false;
+    if (!eligible(g.kind, g.cols, g.rows, PRISM_PATH_F32)) return false;
+    if (!d) return true;
+    return d->kind == g.kind && d->cols == g.rows && d->rows == g.cols &&
+           eligible(d->kind, d->cols, d->rows, PRISM_PATH_F32);
+}
+
+prism_tensor_desc desc_of(const Weight &w) { return prism_tensor_desc{w.kind, w.cols, w.rows}; }
 
 void zero(float *p, size_t n) {
     if (p) std::memset(p, 0, sizeof(float) * n);
@@ -151,6 +189,69 @@ int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Wei
     return project_f32_dev(c, *d, hv, 1, pinned, out, c->act2, s, residual);
 }
 
+// Sibling projections of `tokens` token rows of one f32 input (device pointers):
+// outs[i] receives [tokens][rows_i].  A member whose kernel prepares its own codes (the
+// tiled-prefill GEMM, or a single token's quantizing prologue) takes x directly; the
+// others share one quantization of x, as the reference's sibling groups share one
+// prepared activation (src/kernels/siblings.rs:30, src/graph.rs:1880-2003).  The
+// members share a contract (group_eligible), so every output is its own
+// project_f32's.
+int group_tokens_impl(prism_hip_ctx *c, const Weight *const *w, uint32_t n, const float *x, uint32_t tokens,
+                      int pinned, float *const *outs, hipStream_t s) {
+    const int contract = contract_for(w[0]->kind, w[0]->cols, pinned);
+    bool prepared = false;
+    for (uint32_t i = 0; i < n; ++i) {
+        const Weight &wi = *w[i];
+        bool own = wi.tiled && tokens >= kPrefillMinTokens && prefill_supported(wi.kind, wi.cols, wi.rows, pinned, tokens);
+        if (!own && wi.tiled && tokens == 1) own = !tiled_needs_prepared(f32_args(c, wi, x, 1, pinned, outs[i], nullptr, s));
+        int rc;
+        if (own) {
+            rc = project_f32_dev(c, wi, x, tokens, pinned, outs[i], c->act, s);
+        } else {
+            if (!prepared) {
+                rc = ensure(c, c->act, act_bytes(contract, wi.cols, tokens));
+                if (!rc) rc = quantize(c, contract, x, wi.cols, tokens, pinned, c->act.p, s);
+                if (rc) return rc;
+                prepared = true;
+            }
+            rc = matvec(c, wi, contract == 0 ? kActQ8K : kActQ8, c->act.p, tokens, pinned, outs[i], s);
+        }
+        if (rc) return rc;
+    }
+    return PRISM_OK;
+}
+
+// The FFN chain over `tokens` token rows (device pointers): x [tokens][hidden] ->
+// SwiGLU [tokens][ffn] -> (down) out [tokens][hidden] (+ residual).  One token runs the
+// fused single-token chain; more run gate and up as one sibling group over all tokens
+// (multi-token kernels read each weight once per batch), one SwiGLU launch, and down
+// over all tokens.  Every token row is its own single-token chain's result.  h, if not
+// NULL, receives the SwiGLU rows; without a down projection `out` is that vector.
+int ffn_tokens_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Weight *d, const float *x,
+                    const float *residual, uint32_t tokens, int pinned, float *out, float *h, hipStream_t s) {
+    const prism_tensor_desc dd = d ? desc_of(*d) : prism_tensor_desc{};
+    if (!ffn_eligible(desc_of(g), desc_of(u), d ? &dd : nullptr))
+        return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs gate/up [ffn][hidden] and down [hidden][ffn] of one packed kind");
+    if (tokens == 1) return ffn_chain_impl(c, g, u, d, x, residual, pinned, d ? out : nullptr, d ? h : out, s);
+    const size_t nh = sizeof(float) * g.rows * tokens;
+    int rc = ensure(c, c->gate, nh);
+    if (!rc) rc = ensure(c, c->up, nh);
+    float *hv = d ? h : out;
+    if (!rc && !hv) {
+        rc = ensure(c, c->h, nh);
+        hv = static_cast<float *>(c->h.p);
+    }
+    if (rc) return rc;
+    const Weight *gu[2] = {&g, &u};
+    float *gu_out[2] = {static_cast<float *>(c->gate.p), static_cast<float *>(c->up.p)};
+    rc = group_tokens_impl(c, gu, 2, x, tokens, pinned, gu_out, s);
+    if (!rc)
+        rc = launch_result(c, launch_swiglu(gu_out[0], gu_out[1], hv, g.rows, tokens, pinned, c->err, s),
+                           "swiglu launch");
+    if (rc || !d) return rc;
+    return project_f32_dev(c, *d, hv, tokens, pinned, out, c->act2, s, residual);
+}
+
 }  // namespace
 
 extern "C" {
@@ -209,6 +310,31 @@ int64_t prism_hip_operation_count(const prism_hip_ctx *c, uint32_t kind, uint64_
 int prism_hip_supports(const prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows, int path) {
     if (!c || c->faulted) return 0;
     return eligible(kind, cols, rows, path) ? 1 : 0;
+}
+
+int prism_hip_supports_f32_group(const prism_hip_ctx *c, const prism_tensor_desc *tensors, uint32_t n) {
+    if (!c || c->faulted) return 0;
+    return group_eligible(tensors, n) ? 1 : 0;
+}
+
+int prism_hip_supports_f32_ffn_swiglu(const prism_hip_ctx *c, const prism_tensor_desc *gate,
+                                      const prism_tensor_desc *up) {
+    if (!c || c->faulted || !gate || !up) return 0;
+    return ffn_eligible(*gate, *up, nullptr) ? 1 : 0;
+}
+
+int prism_hip_supports_f32_ffn_chain(const prism_hip_ctx *c, const prism_tensor_desc *tensors) {
+    if (!c || c->faulted || !tensors) return 0;
+    return ffn_eligible(tensors[0], tensors[1], &tensors[2]) ? 1 : 0;
+}
+
+int prism_hip_supports_tile_tokens(const prism_hip_ctx *c) { return (!c || c->faulted) ? 0 : 1; }
+
+uint64_t prism_hip_weight_tiled_bytes(const prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows) {
+    uint64_t g, b;
+    if (!c || !layout(kind, &g, &b) || cols == 0 || rows == 0 || cols % g) return 0;
+    if (!tiled_supported(kind, cols, rows, c->cus)) return 0;
+    return tiled_bytes(rows, cols / g * b);
 }
 
 static prism_weight_id add_weight(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
@@ -330,6 +456,42 @@ prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *c, uint32_t kind, ui
     return add_weight(c, 0, kind, cols, rows, bytes, false, const_cast<void *>(dev));
 }
 
+int prism_hip_weight_repack_tiled(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,
+                                  const void *native_dev, uint64_t native_bytes, void *tiled_dev,
+                                  uint64_t tiled_bytes_) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!native_dev || !tiled_dev) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    rc = check_geometry(c, kind, cols, rows, native_bytes);
+    if (rc) return rc;
+    const uint64_t need = prism_hip_weight_tiled_bytes(c, kind, cols, rows);
+    if (need == 0) return fail(c, PRISM_ERR_UNSUPPORTED, "no tiled layout for this tensor on this device");
+    if (tiled_bytes_ != need) return fail(c, PRISM_ERR_INVALID_INPUT, "tiled buffer size differs from prism_hip_weight_tiled_bytes");
+    // Padding rows of the last tile must read as zero weights: clear, then scatter the
+    // native bytes.  (The call synchronizes, so it cannot sit inside a graph capture.)
+    HIP_OR_FAIL(c, hipMemsetAsync(tiled_dev, 0, need, c->stream));
+    rc = launch_result(c, launch_repack(native_dev, tiled_dev, kind, cols, rows, c->stream), "repack launch");
+    if (rc) return rc;
+    HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+    return PRISM_OK;
+}
+
+prism_weight_id prism_hip_weight_wrap_tiled(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,
+                                            const void *tiled_dev, uint64_t tiled_bytes_) {
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!tiled_dev) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    uint64_t g, b;
+    if (!layout(kind, &g, &b)) return fail(c, PRISM_ERR_UNSUPPORTED, "unsupported tensor kind");
+    if (cols == 0 || rows == 0 || cols % g) return fail(c, PRISM_ERR_INVALID_INPUT, "incomplete blocks");
+    const uint64_t need = prism_hip_weight_tiled_bytes(c, kind, cols, rows);
+    if (need == 0) return fail(c, PRISM_ERR_UNSUPPORTED, "no tiled layout for this tensor on this device");
+    if (tiled_bytes_ != need) return fail(c, PRISM_ERR_INVALID_INPUT, "tiled buffer size differs from prism_hip_weight_tiled_bytes");
+    const prism_weight_id id = add_weight(c, 0, kind, cols, rows, need, false, const_cast<void *>(tiled_dev));
+    c->weights[id].tiled = true;
+    return id;
+}
+
 int prism_hip_weight_release(prism_hip_ctx *c, prism_weight_id id) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     auto it = c->weights.find(id);
@@ -449,8 +611,9 @@ int prism_hip_mul_mat(prism_hip_ctx *c, prism_weight_id a, const float *b, uint3
     return project_f32_host(c, a, b, ncols, 0, out);
 }
 
-int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, int pinned,
-                                float *const *outs) {
+// Host-pointer sibling group over `tokens` token rows: outs[i] receives [tokens][rows_i].
+static int group_host(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, uint32_t tokens,
+                      int pinned, float *const *outs) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (!ws || !outs || n == 0 || n > 8) return fail(c, PRISM_ERR_INVALID_INPUT, "bad projection group");
     const Weight *w[8] = {};
@@ -458,89 +621,105 @@ int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uin
     // Clears every output whose weight is known (the others have no known length).
     auto clear = [&](int code) {
         for (uint32_t i = 0; i < n; ++i)
-            if (w[i] && outs[i]) zero(outs[i], w[i]->rows);
+            if (w[i] && outs[i]) zero(outs[i], w[i]->rows * tokens);
         return code;
     };
     int rc = check_ready(c);
     if (rc) return clear(rc);
-    if (!x) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "null input"));
+    if (!x || tokens == 0) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "null input or no tokens"));
+    prism_tensor_desc t[8];
     for (uint32_t i = 0; i < n; ++i) {
         if (!w[i] || !outs[i]) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id in group"));
-        if (!eligible(w[i]->kind, w[i]->cols, w[i]->rows, PRISM_PATH_F32))
-            return clear(fail(c, PRISM_ERR_UNSUPPORTED, "projection not supported for this tensor"));
-        if (w[i]->cols != w[0]->cols ||
-            contract_for(w[i]->kind, w[i]->cols, pinned) != contract_for(w[0]->kind, w[0]->cols, pinned))
-            return clear(fail(c, PRISM_ERR_INVALID_INPUT, "group members do not share an activation contract"));
+        t[i] = desc_of(*w[i]);
     }
+    if (!group_eligible(t, n))
+        return clear(fail(c, PRISM_ERR_UNSUPPORTED, "group members do not share an input width and activation contract"));
     uint64_t total = 0;
     for (uint32_t i = 0; i < n; ++i) total += w[i]->rows;
-    const int contract = contract_for(w[0]->kind, w[0]->cols, pinned);
-    rc = ensure(c, c->x, sizeof(float) * w[0]->cols);
-    if (!rc) rc = ensure(c, c->act, act_bytes(contract, w[0]->cols, 1));
-    if (!rc) rc = ensure(c, c->out, sizeof(float) * total);
+    const uint64_t cols = w[0]->cols;
+    rc = ensure(c, c->x, sizeof(float) * cols * tokens);
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * total * tokens);
     if (!rc) {
-        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * w[0]->cols, hipMemcpyHostToDevice, c->stream);
+        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * cols * tokens, hipMemcpyHostToDevice, c->stream);
         rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
     }
-    if (!rc) rc = quantize(c, contract, static_cast<float *>(c->x.p), w[0]->cols, 1, pinned, c->act.p, c->stream);
+    float *dev_out[8];
     uint64_t off = 0;
-    for (uint32_t i = 0; i < n && !rc; ++i) {
-        rc = matvec(c, *w[i], contract == 0 ? kActQ8K : kActQ8, c->act.p, 1, pinned,
-                    static_cast<float *>(c->out.p) + off, c->stream);
-        off += w[i]->rows;
+    for (uint32_t i = 0; i < n; ++i) {
+        dev_out[i] = static_cast<float *>(c->out.p) + off;
+        off += w[i]->rows * tokens;
     }
-    off = 0;
+    if (!rc) rc = group_tokens_impl(c, w, n, static_cast<const float *>(c->x.p), tokens, pinned, dev_out, c->stream);
     for (uint32_t i = 0; i < n && !rc; ++i) {
-        hipError_t e = hipMemcpyAsync(outs[i], static_cast<float *>(c->out.p) + off, sizeof(float) * w[i]->rows,
-                                      hipMemcpyDeviceToHost, c->stream);
+        hipError_t e = hipMemcpyAsync(outs[i], dev_out[i], sizeof(float) * w[i]->rows * tokens, hipMemcpyDeviceToHost,
+                                      c->stream);
         if (e != hipSuccess) rc = hip_fail(c, e, "copy group output");
-        off += w[i]->rows;
     }
     if (!rc) rc = drain(c, c->stream);
     return rc ? clear(rc) : rc;
 }
 
+int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, int pinned,
+                                float *const *outs) {
+    return group_host(c, ws, n, x, 1, pinned, outs);
+}
+
+int prism_hip_project_f32_group_tokens(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x,
+                                       uint32_t tokens, int pinned, float *const *outs) {
+    return group_host(c, ws, n, x, tokens, pinned, outs);
+}
+
+int prism_hip_project_f32_pair_tokens(prism_hip_ctx *c, const prism_weight_id *ws, const float *x, uint32_t tokens,
+                                      int pinned, float *out_a, float *out_b) {
+    float *const outs[2] = {out_a, out_b};
+    return group_host(c, ws, 2, x, tokens, pinned, outs);
+}
+
+int prism_hip_project_f32_triple_tokens(prism_hip_ctx *c, const prism_weight_id *ws, const float *x, uint32_t tokens,
+                                        int pinned, float *out_a, float *out_b, float *out_c) {
+    float *const outs[3] = {out_a, out_b, out_c};
+    return group_host(c, ws, 3, x, tokens, pinned, outs);
+}
+
 static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did, const float *x,
-                    const float *residual, int pinned, float *out) {
+                    const float *residual, uint32_t tokens, int pinned, float *out) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
     // Output length: down's rows, or gate's for the SwiGLU vector; known when those ids are.
     const Weight *shape = did ? d : g;
+    const uint64_t nout = shape ? shape->rows * tokens : 0;
     int rc = check_ready(c);
     if (rc) {
-        if (shape) zero(out, shape->rows);
+        zero(out, nout);
         return rc;
     }
     if (!g || !u || (did && !d)) {
-        if (shape) zero(out, shape->rows);
+        zero(out, nout);
         return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
     }
-    const uint64_t nout = d ? d->rows : g->rows;
-    if (!x || !out) {
+    if (!x || !out || tokens == 0) {
         zero(out, nout);
-        return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
+        return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output, or no tokens");
     }
-    const bool kind_ok = (g->kind == PRISM_KIND_PQ2 || g->kind == PRISM_KIND_Q2_K || g->kind == PRISM_KIND_PTQ1 ||
-                          g->kind == PRISM_KIND_Q8_0 || g->kind == PRISM_KIND_TQ1_0 || g->kind == PRISM_KIND_TQ2_0) &&
-                         (!d || d->kind == g->kind);
-    if (!kind_ok) {
+    const prism_tensor_desc dd = d ? desc_of(*d) : prism_tensor_desc{};
+    if (!ffn_eligible(desc_of(*g), desc_of(*u), d ? &dd : nullptr)) {
         zero(out, nout);
-        return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind for gate, up and down");
+        return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs gate/up [ffn][hidden] and down [hidden][ffn] of one packed kind");
     }
-    rc = ensure(c, c->x, sizeof(float) * g->cols);
+    const uint64_t nx = g->cols * tokens;
+    rc = ensure(c, c->x, sizeof(float) * nx);
     if (!rc) rc = ensure(c, c->out, sizeof(float) * nout);
     if (!rc && residual) rc = ensure(c, c->res, sizeof(float) * nout);
     if (!rc) {
-        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * g->cols, hipMemcpyHostToDevice, c->stream);
+        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * nx, hipMemcpyHostToDevice, c->stream);
         if (e == hipSuccess && residual)
             e = hipMemcpyAsync(c->res.p, residual, sizeof(float) * nout, hipMemcpyHostToDevice, c->stream);
         rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
     }
-    if (!rc) {
-        float *o = static_cast<float *>(c->out.p);
-        rc = ffn_chain_impl(c, *g, *u, d, static_cast<float *>(c->x.p), residual ? static_cast<float *>(c->res.p) : nullptr,
-                            pinned, d ? o : nullptr, d ? nullptr : o, c->stream);
-    }
+    if (!rc)
+        rc = ffn_tokens_impl(c, *g, *u, d, static_cast<float *>(c->x.p),
+                             residual ? static_cast<float *>(c->res.p) : nullptr, tokens, pinned,
+                             static_cast<float *>(c->out.p), nullptr, c->stream);
     if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), nout);
     if (rc) zero(out, nout);
     return rc;
@@ -548,14 +727,26 @@ static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, 
 
 int prism_hip_ffn_swiglu(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
                          float *out) {
-    return ffn_host(c, gate, up, 0, x, nullptr, pinned, out);
+    return ffn_host(c, gate, up, 0, x, nullptr, 1, pinned, out);
+}
+
+int prism_hip_ffn_swiglu_tokens(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, const float *x,
+                                uint32_t tokens, int pinned, float *out) {
+    return ffn_host(c, gate, up, 0, x, nullptr, tokens, pinned, out);
 }
 
 int prism_hip_ffn_chain(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                         const float *x, const float *residual, int pinned, float *out) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (down == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "down projection required");
-    return ffn_host(c, gate, up, down, x, residual, pinned, out);
+    return ffn_host(c, gate, up, down, x, residual, 1, pinned, out);
+}
+
+int prism_hip_ffn_chain_tokens(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                               const float *x, const float *residual, uint32_t tokens, int pinned, float *out) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    if (down == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "down projection required");
+    return ffn_host(c, gate, up, down, x, residual, tokens, pinned, out);
 }
 
 int prism_hip_quantize_q8k_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int pinned,

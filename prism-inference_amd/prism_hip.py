@@ -81,6 +81,13 @@ def lib() -> ctypes.CDLL:
         "prism_hip_operation_capacity": (U64, [P]),
         "prism_hip_operation_count": (I64, [P, U32, U64, U64]),
         "prism_hip_supports": (I, [P, U32, U64, U64, I]),
+        "prism_hip_supports_f32_group": (I, [P, P, U32]),
+        "prism_hip_supports_f32_ffn_swiglu": (I, [P, P, P]),
+        "prism_hip_supports_f32_ffn_chain": (I, [P, P]),
+        "prism_hip_supports_tile_tokens": (I, [P]),
+        "prism_hip_weight_tiled_bytes": (U64, [P, U32, U64, U64]),
+        "prism_hip_weight_repack_tiled": (I, [P, U32, U64, U64, P, U64, P, U64]),
+        "prism_hip_weight_wrap_tiled": (I64, [P, U32, U64, U64, P, U64]),
         "prism_hip_weight_acquire": (I64, [P, U64, U32, U64, U64, P, U64]),
         "prism_hip_weight_acquire_device": (I64, [P, U64, U32, U64, U64, P, U64]),
         "prism_hip_weight_wrap_device": (I64, [P, U32, U64, U64, P, U64]),
@@ -91,8 +98,13 @@ def lib() -> ctypes.CDLL:
         "prism_hip_project_q8": (I, [P, I64, P, U64, U32, I, P]),
         "prism_hip_project_f32": (I, [P, I64, P, U32, I, P]),
         "prism_hip_project_f32_group": (I, [P, P, U32, P, I, P]),
+        "prism_hip_project_f32_group_tokens": (I, [P, P, U32, P, U32, I, P]),
+        "prism_hip_project_f32_pair_tokens": (I, [P, P, P, U32, I, P, P]),
+        "prism_hip_project_f32_triple_tokens": (I, [P, P, P, U32, I, P, P, P]),
         "prism_hip_ffn_swiglu": (I, [P, I64, I64, P, I, P]),
         "prism_hip_ffn_chain": (I, [P, I64, I64, I64, P, P, I, P]),
+        "prism_hip_ffn_swiglu_tokens": (I, [P, I64, I64, P, U32, I, P]),
+        "prism_hip_ffn_chain_tokens": (I, [P, I64, I64, I64, P, P, U32, I, P]),
         "prism_hip_prefill": (I, [P, I64, P, U32, I, P]),
         "prism_hip_mul_mat": (I, [P, I64, P, U32, P]),
         "prism_hip_quantize_q8k_device": (I, [P, P, U64, U32, I, P, P]),
@@ -264,6 +276,18 @@ def gguf_export_ptq1(src: str, dst: str) -> dict:
     return json.loads(buf.value.decode())
 
 
+class TensorDesc(ctypes.Structure):
+    """prism_tensor_desc: a tensor's kind and dimensions [cols, rows]."""
+    _fields_ = [("kind", ctypes.c_uint32), ("cols", ctypes.c_uint64), ("rows", ctypes.c_uint64)]
+
+
+def _descs(tensors):
+    arr = (TensorDesc * len(tensors))()
+    for i, (kind, cols, rows) in enumerate(tensors):
+        arr[i] = TensorDesc(kind, cols, rows)
+    return arr
+
+
 def _ptr(a):
     if a is None:
         return None
@@ -328,6 +352,20 @@ class Context:
     def supports(self, kind: int, cols: int, rows: int, path: int) -> bool:
         return bool(lib().prism_hip_supports(self._h, kind, cols, rows, path))
 
+    def supports_f32_group(self, tensors) -> bool:
+        """tensors: [(kind, cols, rows), ...]"""
+        return bool(lib().prism_hip_supports_f32_group(self._h, _descs(tensors), len(tensors)))
+
+    def supports_f32_ffn_swiglu(self, gate, up) -> bool:
+        d = _descs([gate, up])
+        return bool(lib().prism_hip_supports_f32_ffn_swiglu(self._h, ctypes.byref(d[0]), ctypes.byref(d[1])))
+
+    def supports_f32_ffn_chain(self, gate, up, down) -> bool:
+        return bool(lib().prism_hip_supports_f32_ffn_chain(self._h, _descs([gate, up, down])))
+
+    def supports_tile_tokens(self) -> bool:
+        return bool(lib().prism_hip_supports_tile_tokens(self._h))
+
     def stream(self) -> int:
         return lib().prism_hip_stream(self._h)
 
@@ -361,6 +399,21 @@ class Context:
     def weight_device(self, kind: int, cols: int, rows: int, tensor) -> int:
         nbytes = tensor.numel() * tensor.element_size()
         wid = lib().prism_hip_weight_wrap_device(self._h, kind, cols, rows, _ptr(tensor), nbytes)
+        if wid < 0:
+            self._check(int(wid))
+        return int(wid)
+
+    def tiled_bytes(self, kind: int, cols: int, rows: int) -> int:
+        return lib().prism_hip_weight_tiled_bytes(self._h, kind, cols, rows)
+
+    def repack_tiled(self, kind: int, cols: int, rows: int, native, tiled):
+        """Writes the tiled image of native device bytes into the caller's device buffer."""
+        self._check(lib().prism_hip_weight_repack_tiled(self._h, kind, cols, rows, _ptr(native), native.nbytes,
+                                                        _ptr(tiled), tiled.nbytes))
+
+    def weight_tiled_device(self, kind: int, cols: int, rows: int, tiled) -> int:
+        """Registers a caller-owned device buffer holding the tiled image (no copy)."""
+        wid = lib().prism_hip_weight_wrap_tiled(self._h, kind, cols, rows, _ptr(tiled), tiled.nbytes)
         if wid < 0:
             self._check(int(wid))
         return int(wid)
@@ -416,6 +469,38 @@ class Context:
         ptrs = (ctypes.c_void_p * len(outs))(*[o.ctypes.data for o in outs])
         rc = lib().prism_hip_project_f32_group(self._h, _ptr(ids), len(outs), _ptr(x), int(pinned), ptrs)
         return self._run(rc, outs, check)
+
+    def project_f32_group_tokens(self, wids, rows_list, X, pinned: bool = False, check=True):
+        X = np.ascontiguousarray(X, np.float32)
+        tokens = X.shape[0]
+        outs = [np.full((tokens, r), 7.0, np.float32) for r in rows_list]
+        ids = np.array(wids, np.int64)
+        if len(outs) == 2:
+            rc = lib().prism_hip_project_f32_pair_tokens(self._h, _ptr(ids), _ptr(X), tokens, int(pinned),
+                                                         _ptr(outs[0]), _ptr(outs[1]))
+        elif len(outs) == 3:
+            rc = lib().prism_hip_project_f32_triple_tokens(self._h, _ptr(ids), _ptr(X), tokens, int(pinned),
+                                                           _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]))
+        else:
+            ptrs = (ctypes.c_void_p * len(outs))(*[o.ctypes.data for o in outs])
+            rc = lib().prism_hip_project_f32_group_tokens(self._h, _ptr(ids), len(outs), _ptr(X), tokens,
+                                                          int(pinned), ptrs)
+        return self._run(rc, outs, check)
+
+    def ffn_swiglu_tokens(self, g: int, u: int, ffn: int, X, pinned: bool = False, check=True):
+        X = np.ascontiguousarray(X, np.float32)
+        out = np.full((X.shape[0], ffn), 7.0, np.float32)
+        rc = lib().prism_hip_ffn_swiglu_tokens(self._h, g, u, _ptr(X), X.shape[0], int(pinned), _ptr(out))
+        return self._run(rc, out, check)
+
+    def ffn_chain_tokens(self, g: int, u: int, d: int, hidden: int, X, residual=None, pinned: bool = False,
+                         check=True):
+        X = np.ascontiguousarray(X, np.float32)
+        res = np.ascontiguousarray(residual, np.float32) if residual is not None else None
+        out = np.full((X.shape[0], hidden), 7.0, np.float32)
+        rc = lib().prism_hip_ffn_chain_tokens(self._h, g, u, d, _ptr(X), _ptr(res), X.shape[0], int(pinned),
+                                              _ptr(out))
+        return self._run(rc, out, check)
 
     def ffn_swiglu(self, g: int, u: int, ffn: int, x, pinned: bool = False, check=True):
         x = np.ascontiguousarray(x, np.float32)

@@ -1,0 +1,211 @@
+"""GPU tests of the executor surface beyond single projections: the trait's eligibility
+queries, the multi-token sibling and FFN entry points, and weights whose tiled layout
+lives in caller-owned device memory.
+
+Every projection output is compared with the oracle per token (0 ULP); the pinned FFN
+chain is bit-exact end to end, the source chain (device libm exp in SiLU) is compared
+with max |diff| <= 1e-3 * max |ref|, as the single-token chain tests do.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+import prism_hip as ph
+import synth
+from hiprt import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ph.Context(0)
+    yield c
+    c.close()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def assert_bits_equal(got, ref, what=""):
+    g, r = bits(got), bits(ref)
+    if not np.array_equal(g, r):
+        idx = np.nonzero(g.ravel() != r.ravel())[0]
+        i = idx[0]
+        raise AssertionError(f"{what}: {idx.size} mismatches, first at {i}: gpu={np.float32(got.flat[i])!r} "
+                             f"oracle={np.float32(ref.flat[i])!r}")
+
+
+# ---- eligibility (projection.rs:112-114, 212-214, 261-269) ----------------------------
+
+def test_gpu_eligibility_queries(ctx):
+    P, Q2, PQ, Q8 = ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0
+    assert ctx.supports_tile_tokens()
+    # groups: one width, one contract whatever `pinned` is
+    assert ctx.supports_f32_group([(P, 2048, 2048), (P, 2048, 512), (P, 2048, 512)])
+    assert ctx.supports_f32_group([(Q2, 2048, 6144), (Q2, 2048, 6144)])
+    assert ctx.supports_f32_group([(PQ, 2048, 64), (Q2, 2048, 64)])  # both Q8_K
+    assert not ctx.supports_f32_group([(P, 2048, 64), (Q2, 2048, 64)])  # Q8_0 vs Q8_K
+    assert not ctx.supports_f32_group([(P, 2048, 64), (P, 1024, 64)])  # widths differ
+    # odd-group PQ2 and PTQ1 share Q8_0 in the source contract but not when pinned
+    assert not ctx.supports_f32_group([(PQ, 384, 64), (P, 384, 64)])
+    assert not ctx.supports_f32_group([(P, 2048, 64)] * 9)
+    assert not ctx.supports_f32_group([])
+    assert not ctx.supports_f32_group([(P, 2000, 64)])  # incomplete block
+    # FFN
+    assert ctx.supports_f32_ffn_swiglu((Q2, 2048, 6144), (Q2, 2048, 6144))
+    assert ctx.supports_f32_ffn_swiglu((P, 2048, 6144), (P, 2048, 6144))
+    assert not ctx.supports_f32_ffn_swiglu((Q2, 2048, 6144), (P, 2048, 6144))
+    assert not ctx.supports_f32_ffn_swiglu((Q2, 2048, 6144), (Q2, 2048, 4096))
+    assert ctx.supports_f32_ffn_chain((Q2, 2048, 6144), (Q2, 2048, 6144), (Q2, 6144, 2048))
+    assert ctx.supports_f32_ffn_chain((Q8, 2048, 6144), (Q8, 2048, 6144), (Q8, 6144, 2048))
+    assert not ctx.supports_f32_ffn_chain((Q2, 2048, 6144), (Q2, 2048, 6144), (Q2, 2048, 6144))
+    assert not ctx.supports_f32_ffn_chain((Q2, 2048, 6144), (Q2, 2048, 6144), (P, 6144, 2048))
+    assert not ctx.faulted
+
+
+# ---- multi-token siblings (projection.rs:158-210) -------------------------------------
+
+@pytest.mark.parametrize("kind,tokens", [(ph.KIND_PTQ1, 1), (ph.KIND_PTQ1, 3), (ph.KIND_PTQ1, 16),
+                                         (ph.KIND_PTQ1, 21), (ph.KIND_Q2_K, 5), (ph.KIND_Q8_0, 4),
+                                         (ph.KIND_PQ2, 7)])
+def test_gpu_group_tokens_match_oracle(ctx, kind, tokens):
+    import oracle
+
+    cols = 2048
+    rows = (2048, 512, 512)  # a q/k/v-shaped triple; the pair is its first two
+    ws = [synth.weights(kind, r, cols, seed=100 + i) for i, r in enumerate(rows)]
+    ids = [ctx.weight(kind, cols, r, w) for r, w in zip(rows, ws)]
+    X = synth.activations(cols, seed=7, tokens=tokens).reshape(tokens, cols)
+    for n in (2, 3):
+        for pinned in (False, True):
+            outs = ctx.project_f32_group_tokens(ids[:n], rows[:n], X, pinned=pinned)
+            for i in range(n):
+                for t in sorted({0, tokens // 2, tokens - 1}):
+                    ref = oracle.matvec(kind, cols, rows[i], ws[i], X[t], pinned, threads=THREADS)
+                    assert_bits_equal(outs[i][t], ref, f"member {i} token {t} pinned={pinned}")
+    for i in ids:
+        ctx.release(i)
+
+
+def test_gpu_group_tokens_errors_clear_outputs(ctx):
+    cols = 512
+    a = ctx.weight(ph.KIND_PTQ1, cols, 64, synth.ptq1_weights(64, cols, seed=1))
+    b = ctx.weight(ph.KIND_Q2_K, cols, 64, synth.q2k_weights(64, cols, seed=2))
+    X = synth.activations(cols, seed=3, tokens=4).reshape(4, cols)
+    rc, outs = ctx.project_f32_group_tokens([a, b], [64, 64], X, check=False)
+    assert rc == ph.ERR_UNSUPPORTED and not any(o.any() for o in outs)
+    assert not ctx.faulted
+    ctx.release(a)
+    ctx.release(b)
+
+
+# ---- multi-token FFN (projection.rs:239-259, 328-355) ---------------------------------
+
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PTQ1, ph.KIND_PQ2])
+def test_gpu_ffn_tokens(ctx, kind):
+    import oracle
+
+    hidden, ffn, tokens = 2048, 6144, 5
+    wg = synth.weights(kind, ffn, hidden, seed=1)
+    wu = synth.weights(kind, ffn, hidden, seed=2)
+    wd = synth.weights(kind, hidden, ffn, seed=3)
+    X = synth.activations(hidden, seed=4, tokens=tokens).reshape(tokens, hidden)
+    R = synth.activations(hidden, seed=5, tokens=tokens).reshape(tokens, hidden)
+    g, u, d = (ctx.weight(kind, hidden, ffn, wg), ctx.weight(kind, hidden, ffn, wu), ctx.weight(kind, ffn, hidden, wd))
+    # pinned: bit-exact against the oracle for two tokens, and every token equals the
+    # single-token chain (itself bit-exact against the oracle in the FFN chain tests)
+    H = ctx.ffn_swiglu_tokens(g, u, ffn, X, pinned=True)
+    Y = ctx.ffn_chain_tokens(g, u, d, hidden, X, R, pinned=True)
+    for t in (0, tokens - 1):
+        ref, h = oracle.ffn(kind, hidden, ffn, wg, wu, wd, X[t], R[t], pinned=True, threads=THREADS)
+        assert_bits_equal(H[t], h, f"swiglu pinned token {t}")
+        assert_bits_equal(Y[t], ref, f"chain pinned token {t}")
+    for t in range(tokens):
+        assert_bits_equal(Y[t], ctx.ffn_chain(g, u, d, hidden, X[t], R[t], pinned=True), f"chain vs single {t}")
+    # source: device libm exp in SiLU
+    Y = ctx.ffn_chain_tokens(g, u, d, hidden, X, None, pinned=False)
+    for t in (0, tokens - 1):
+        ref, _ = oracle.ffn(kind, hidden, ffn, wg, wu, wd, X[t], None, pinned=False, threads=THREADS)
+        assert np.max(np.abs(Y[t] - ref)) <= 1e-3 * np.max(np.abs(ref))
+    for i in (g, u, d):
+        ctx.release(i)
+
+
+def test_gpu_ffn_tokens_prefill_sized(ctx):
+    """32 tokens of PTQ1 in the source contract: gate and up take the tiled-prefill GEMM,
+    the down projection too, with the residual added after it."""
+    import oracle
+
+    kind, hidden, ffn, tokens = ph.KIND_PTQ1, 2048, 6144, 32
+    wg = synth.weights(kind, ffn, hidden, seed=11)
+    wu = synth.weights(kind, ffn, hidden, seed=12)
+    wd = synth.weights(kind, hidden, ffn, seed=13)
+    X = synth.activations(hidden, seed=14, tokens=tokens).reshape(tokens, hidden)
+    R = synth.activations(hidden, seed=15, tokens=tokens).reshape(tokens, hidden)
+    g, u, d = (ctx.weight(kind, hidden, ffn, wg), ctx.weight(kind, hidden, ffn, wu), ctx.weight(kind, ffn, hidden, wd))
+    Y = ctx.ffn_chain_tokens(g, u, d, hidden, X, R, pinned=True)
+    for t in (0, 17, 31):
+        ref, _ = oracle.ffn(kind, hidden, ffn, wg, wu, wd, X[t], R[t], pinned=True, threads=THREADS)
+        assert_bits_equal(Y[t], ref, f"pinned token {t}")
+    Y = ctx.ffn_chain_tokens(g, u, d, hidden, X, R, pinned=False)
+    for t in (0, 31):
+        assert np.max(np.abs(Y[t] - ctx.ffn_chain(g, u, d, hidden, X[t], R[t], pinned=False))) == 0.0
+    for i in (g, u, d):
+        ctx.release(i)
+
+
+# ---- tiled layout in caller-owned memory (src/backend/allocator.rs:10-50) ------------
+
+@pytest.mark.parametrize("kind,rows,cols", [(ph.KIND_PTQ1, 2048, 2048), (ph.KIND_PTQ1, 1000, 4096),
+                                            (ph.KIND_Q2_K, 6144, 2048), (ph.KIND_Q8_0, 20000, 1024),
+                                            (ph.KIND_PQ2, 300, 2048)])
+def test_gpu_caller_owned_tiled_weights(ctx, kind, rows, cols):
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=rows + kind)
+    native = DeviceBuffer.from_numpy(w)
+    nbytes = ctx.tiled_bytes(kind, cols, rows)
+    assert nbytes >= w.size and nbytes - w.size < 8 * w.size // rows
+    tiled = DeviceBuffer(nbytes)
+    tiled.upload(np.full(nbytes, 0xA5, np.uint8))  # padding must be cleared by the repack
+    ctx.repack_tiled(kind, cols, rows, native, tiled)
+    native.free()  # the wrapped buffer alone must serve the projections
+    before = ctx.resident_bytes()
+    wid = ctx.weight_tiled_device(kind, cols, rows, tiled)
+    assert ctx.resident_bytes() == before  # the caller owns the memory
+    X = synth.activations(cols, seed=3, tokens=3).reshape(3, cols)
+    for pinned in (False, True):
+        ref = oracle.matvec(kind, cols, rows, w, X[0], pinned, threads=THREADS)
+        assert_bits_equal(ctx.project_f32(wid, rows, X[0], pinned=pinned), ref, f"pinned={pinned}")
+        Y = ctx.project_f32(wid, rows, X, tokens=3, pinned=pinned)
+        assert_bits_equal(Y[2], oracle.matvec(kind, cols, rows, w, X[2], pinned, threads=THREADS), "token 2")
+    ctx.release(wid)
+    tiled.free()
+
+
+def test_gpu_caller_owned_tiled_rejects_bad_sizes(ctx):
+    rows, cols = 256, 2048
+    w = synth.ptq1_weights(rows, cols, seed=1)
+    native = DeviceBuffer.from_numpy(w)
+    nbytes = ctx.tiled_bytes(ph.KIND_PTQ1, cols, rows)
+    small = DeviceBuffer(nbytes - 64)
+    with pytest.raises(ph.PrismError) as e:
+        ctx.repack_tiled(ph.KIND_PTQ1, cols, rows, native, small)
+    assert e.value.code == ph.ERR_INVALID_INPUT
+    with pytest.raises(ph.PrismError) as e:
+        ctx.weight_tiled_device(ph.KIND_PTQ1, cols, rows, small)
+    assert e.value.code == ph.ERR_INVALID_INPUT
+    # one 64-row tile of 32768 Q8_0 inputs has no tiled layout (the small-matrix kernel's
+    # LDS cannot hold its activation): size 0, and the repack refuses it
+    assert ctx.tiled_bytes(ph.KIND_Q8_0, 32768, 64) == 0
+    q8 = DeviceBuffer.from_numpy(synth.q8_0_weights(64, 32768, seed=2))
+    with pytest.raises(ph.PrismError) as e:
+        ctx.repack_tiled(ph.KIND_Q8_0, 32768, 64, q8, small)
+    assert e.value.code == ph.ERR_UNSUPPORTED
+    assert not ctx.faulted
