@@ -890,8 +890,37 @@ struct SkParams {
 
 template <Op O>
 constexpr bool skinny_supported() {
-    return O != Op::PTQ1_PINNED && O != Op::TQ1 && O != Op::TQ2;
+    return O != Op::TQ1 && O != Op::TQ2;
 }
+
+// binary32 terms per unit and (row, token) element of the skinny kernel: those of the
+// row kernels, except pinned PTQ1, whose four group scales are already multiplied by
+// the token's block scales: 8 dwords of packed 16-bit lane sums, then the four dd_g.
+template <Op O>
+constexpr int sk_terms_per_unit() {
+    return O == Op::PTQ1_PINNED ? 12 : terms_per_unit<O>();
+}
+
+// Chain of one (row, token) element of the skinny kernel.
+template <Op O>
+struct SkChain : Chain<O> {
+    __device__ __forceinline__ void fold(const float *t) { Chain<O>::fold(t, nullptr, 0); }
+};
+template <>
+struct SkChain<Op::PTQ1_PINNED> : Chain<Op::PTQ1_PINNED> {
+    // dot_q8_groups_pinned, src/kernels.rs:1134-1146: per group, L[l] = fma(I_l, dd_g, L[l]).
+    __device__ __forceinline__ void fold(const float *t) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float dd = t[8 + g];
+            const uint32_t p0 = __float_as_uint(t[2 * g]), p1 = __float_as_uint(t[2 * g + 1]);
+            L[0] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p0 & 0xffffu)), dd, L[0]);
+            L[1] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p0 >> 16)), dd, L[1]);
+            L[2] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p1 & 0xffffu)), dd, L[2]);
+            L[3] = __builtin_fmaf(static_cast<float>(static_cast<int16_t>(p1 >> 16)), dd, L[3]);
+        }
+    }
+};
 
 // Per-lane geometry: the tile's buffer, the lane's A row and first output row.
 struct SkLane {
@@ -960,6 +989,8 @@ struct SkFrag<Op::PTQ1_SRC> {
 template <>
 struct SkFrag<Op::PTQ1_Q8K> : SkFrag<Op::PTQ1_SRC> {};
 template <>
+struct SkFrag<Op::PTQ1_PINNED> : SkFrag<Op::PTQ1_SRC> {};
+template <>
 struct SkFrag<Op::PQ2_UNFUSED> {
     u32x4 ca, cb;  // code dwords 0..3 and 4..7 of the A row
     u32x2 dd;      // binary16 scales of the four output rows
@@ -1018,7 +1049,7 @@ __device__ __forceinline__ uint32_t sk_elem(uint32_t s, uint32_t k, uint32_t &st
 }
 template <Op O>
 constexpr bool sk_q8_groups() {
-    return O == Op::Q8_0 || O == Op::PTQ1_SRC || O == Op::PQ2_Q8;
+    return O == Op::Q8_0 || O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED || O == Op::PQ2_Q8;
 }
 // Byte of activation element e of unit u in a token's prepared blocks.
 template <Op O>
@@ -1093,7 +1124,7 @@ __device__ __forceinline__ void sk_load_act_raw(SkFrag<O> &f, const uint8_t *a, 
         f.as.x = __float_as_uint(blk->scale);
     } else if constexpr (kind_of<O>() == kPTQ1) {
         uint32_t x[8];
-        if constexpr (O == Op::PTQ1_SRC) {
+        if constexpr (O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED) {
             const Q8Block *blk = reinterpret_cast<const Q8Block *>(a) + 4u * u;
 #pragma unroll
             for (int k = 0; k < 8; ++k)
@@ -1179,7 +1210,7 @@ __device__ __forceinline__ void sk_load(SkFrag<O> &f, const SkLane &L, uint32_t 
 // token), in the order Chain<O>::fold consumes them.
 template <Op O>
 __device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, const Ptq1Plan &pp,
-                                         float tv[4][terms_per_unit<O>()]) {
+                                         float tv[4][sk_terms_per_unit<O>()]) {
     const uint32_t s = L.s;
     const v4i zero = {0, 0, 0, 0};
     if constexpr (O == Op::Q8_0) {
@@ -1247,7 +1278,42 @@ __device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, co
         // Quad order: group 0 = (q0, q1), group 1 = (q2, q3), group 2 = (q4, q5), group 3 = (q6, q7).
         const float as[4] = {__uint_as_float(f.as.x), __uint_as_float(f.as.y), __uint_as_float(f.as.z),
                              __uint_as_float(f.as.w)};
-        if constexpr (O == Op::PTQ1_SRC) {
+        if constexpr (O == Op::PTQ1_PINNED) {
+            // dot_q8_groups_pinned needs, per group g and native lane l, the integer sum
+            // over the group's elements 4l..4l+3 and 16+4l..16+4l+3
+            // (q8_native_lanes, src/kernels.rs:1066-1076).  Every quad of consecutive
+            // elements a lane feeds lies in one such lane subset (its offset within the
+            // group, /4, mod 4), so one MFMA per (g, l) with the other lanes' quads
+            // zeroed gives I_{g,l} exactly.  Quad lanes of lane group s:
+            //   groups 0, 1: (s, s); group 2: (s, lane of 80+8(s%2)+4(s/2));
+            //   group 3: s < 3: (2s%4, (2s+1)%4), s = 3: (2, 3).
+            const uint32_t l5 = (4u + 2u * (s & 1u) + (s >> 1)) & 3u;
+            const uint32_t l6 = s < 3 ? (2u * s) & 3u : 2u, l7 = s < 3 ? (2u * s + 1u) & 3u : 3u;
+            const uint32_t qa[4] = {s, s, s, l6}, qb[4] = {s, s, l5, l7};
+            const uint32_t b0[4] = {f.b[0].x, f.b[0].z, f.b[1].x, f.b[1].z};
+            const uint32_t b1[4] = {f.b[0].y, f.b[0].w, f.b[1].y, f.b[1].w};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                v4i il[4];
+#pragma unroll
+                for (uint32_t l = 0; l < 4; ++l)
+                    il[l] = mfma32(qa[g] == l ? q[2 * g] : 0u, qb[g] == l ? q[2 * g + 1] : 0u, b0[g], b1[g], zero);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    // |I| <= 8 * 127: 16 bits hold it.
+                    tv[v][2 * g] = __uint_as_float((static_cast<uint32_t>(il[0][v]) & 0xffffu) |
+                                                   (static_cast<uint32_t>(il[1][v]) << 16));
+                    tv[v][2 * g + 1] = __uint_as_float((static_cast<uint32_t>(il[2][v]) & 0xffffu) |
+                                                       (static_cast<uint32_t>(il[3][v]) << 16));
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float dw = h2f(f.dd[v] >> 16);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) tv[v][8 + g] = dw * as[g];  // fl(d_w * A_g.scale)
+            }
+        } else if constexpr (O == Op::PTQ1_SRC) {
             v4i acc[4];
             acc[0] = mfma32(q[0], q[1], f.b[0].x, f.b[0].y, zero);
             acc[1] = mfma32(q[2], q[3], f.b[0].z, f.b[0].w, zero);
@@ -1327,7 +1393,7 @@ __device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, co
 template <Op O, bool SW, int KS>
 __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
     constexpr uint32_t UB = unit_bytes<O>();
-    constexpr int TPU = terms_per_unit<O>();
+    constexpr int TPU = sk_terms_per_unit<O>();
     const uint32_t lane = threadIdx.x & 63u, i = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t tile = blockIdx.x >> 2, quarter = blockIdx.x & 3u;
@@ -1360,12 +1426,12 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
         }
     };
     if constexpr (KS == 1) {
-        Chain<O> ch[4];
+        SkChain<O> ch[4];
         auto fold = [&](const SkFrag<O> &f) {
             float tv[4][TPU];
             sk_terms<O>(f, L, pp, tv);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) ch[v].fold(tv[v], nullptr, 0);
+            for (int v = 0; v < 4; ++v) ch[v].fold(tv[v]);
         };
         // Two fragments in ping-pong: the next unit's loads are in flight during a fold.
         SkFrag<O> A, B;
@@ -1385,7 +1451,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
         // terms[parity][wave][term][element], element e = 4 * lane + v
         __shared__ float terms[2][KS][TPU][256];
         constexpr int EPT = KS <= 4 ? 4 / KS : 1;  // elements folded per thread: e = tid + 64 * KS * k
-        Chain<O> ch[EPT];
+        SkChain<O> ch[EPT];
         const uint32_t chunks = (p.nu + KS - 1) / KS;
         auto produce = [&](const SkFrag<O> &f, uint32_t c) {
             float tv[4][TPU];
@@ -1407,7 +1473,7 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
                         float t[TPU];
 #pragma unroll
                         for (int j = 0; j < TPU; ++j) t[j] = terms[c & 1u][w][j][e];
-                        ch[k].fold(t, nullptr, 0);
+                        ch[k].fold(t);
                     }
                 }
             }
@@ -1934,7 +2000,19 @@ int launch_batch(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t a
     return launch_status();
 }
 
-bool batch_eligible(const MatvecArgs &a) { return a.tokens >= 2 && !a.w2 && a.rows >= kBatchMinRows; }
+// Row count from which 2..16 tokens run on the matrix cores (16 rows per wavefront).
+constexpr uint64_t kSkinnyMinRows = 1024;
+
+// The row-tile batch kernel (one wavefront per 64-row tile runs every token's chain, each
+// unit decoded once per batch): large matrices, and TQ1_0 / TQ2_0 (no skinny kernel)
+// from eight tokens on smaller ones.  Measured: TQ1_0 6144x2048 x 16 tokens 45 us
+// against 75 us token by token; 12288x4096 x 4 tokens 34 us against 29 us.
+bool batch_eligible(const MatvecArgs &a) {
+    if (a.tokens < 2 || a.w2) return false;
+    if (a.rows >= kBatchMinRows) return true;
+    const bool tq = a.kind == kTQ1_0 || a.kind == kTQ2_0;
+    return tq && a.rows >= kSkinnyMinRows && a.tokens >= 8;
+}
 
 // Whether a skinny batch first copies its activations into lane order (one more launch,
 // then contiguous loads) instead of gathering them from the prepared blocks in every
@@ -1979,24 +2057,27 @@ int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t 
     // Wavefronts per 16-row block: enough to give the chip about eight per SIMD.
     const uint64_t blocks = tiles * 4;
     const uint64_t want = 32ull * a.cus;
-    const int ks = blocks >= want ? 1 : blocks * 2 >= want ? 2 : blocks * 4 >= want ? 4 : 8;
+    int ks = blocks >= want ? 1 : blocks * 2 >= want ? 2 : blocks * 4 >= want ? 4 : 8;
+    // The LDS terms buffer is 2 * KS * terms * 1 KiB: pinned PTQ1's twelve terms per
+    // element cap it at two wavefronts per block (48 KiB).
+    constexpr int kMaxKs = sk_terms_per_unit<O>() > 8 ? 2 : 8;
+    if (ks > kMaxKs) ks = kMaxKs;
     const dim3 grid(static_cast<uint32_t>(blocks)), block(64 * ks);
-    if (sw) {
-        if (ks == 1) hipLaunchKernelGGL((k_mv_skinny<O, true, 1>), grid, block, 0, a.stream, p);
-        else if (ks == 2) hipLaunchKernelGGL((k_mv_skinny<O, true, 2>), grid, block, 0, a.stream, p);
-        else if (ks == 4) hipLaunchKernelGGL((k_mv_skinny<O, true, 4>), grid, block, 0, a.stream, p);
-        else hipLaunchKernelGGL((k_mv_skinny<O, true, 8>), grid, block, 0, a.stream, p);
-    } else {
-        if (ks == 1) hipLaunchKernelGGL((k_mv_skinny<O, false, 1>), grid, block, 0, a.stream, p);
-        else if (ks == 2) hipLaunchKernelGGL((k_mv_skinny<O, false, 2>), grid, block, 0, a.stream, p);
-        else if (ks == 4) hipLaunchKernelGGL((k_mv_skinny<O, false, 4>), grid, block, 0, a.stream, p);
-        else hipLaunchKernelGGL((k_mv_skinny<O, false, 8>), grid, block, 0, a.stream, p);
-    }
+    auto go = [&]<bool SWv>() {
+        if (ks == 1) hipLaunchKernelGGL((k_mv_skinny<O, SWv, 1>), grid, block, 0, a.stream, p);
+        else if (ks == 2) hipLaunchKernelGGL((k_mv_skinny<O, SWv, 2>), grid, block, 0, a.stream, p);
+        else if constexpr (kMaxKs >= 8) {
+            if (ks == 4) hipLaunchKernelGGL((k_mv_skinny<O, SWv, 4>), grid, block, 0, a.stream, p);
+            else hipLaunchKernelGGL((k_mv_skinny<O, SWv, 8>), grid, block, 0, a.stream, p);
+        }
+    };
+    if (sw)
+        go.template operator()<true>();
+    else
+        go.template operator()<false>();
     return launch_status();
 }
 
-// Row count from which 2..16 tokens run on the matrix cores (16 rows per wavefront).
-constexpr uint64_t kSkinnyMinRows = 1024;
 // PTQ1 batches of two tokens on matrices of at least four tiles per CU, and of three
 // tokens from eight tiles per CU, take the table kernel (decode once, one chain per
 // token).  Measured (4096 inputs): two tokens 40 / 43 / 50 us at 65536 / 131072 /
@@ -2033,6 +2114,12 @@ int launch_lut_batch(const MatvecArgs &a, uint32_t act_stride) {
 
 bool skinny_eligible(const MatvecArgs &a) {
     if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a)) return false;
+    // Pinned PTQ1 (four masked MFMAs per group) on large matrices: up to four tokens the
+    // row-tile batch kernel is faster (151936x4096 x 4: 148 against 165 us), from 16 the
+    // skinny kernel (171 against 558 us).
+    const bool pinned_q8 = a.kind == kPTQ1 && a.pinned && a.act_format != kActQ8K &&
+                           !(a.act_format == kActF32 && a.qcontract_is_q8k);
+    if (pinned_q8 && a.rows >= kBatchMinRows && a.tokens <= 4) return false;
     return dispatch(a, [&]<Op O>() { return skinny_supported<O>() ? 1 : 0; }) == 1;
 }
 

@@ -1,6 +1,7 @@
 """The benchmark workloads at their stated sizes, through the C ABI, against the oracle.
 
 - c0: PTQ1 2048x2048 matvec, every row.
+- c2: PTQ1 6144x2048 prefill, M = 128, 512 and 2048, source and pinned, sampled tokens.
 - c4: W 12288x4096 in PTQ1, Q2_K and Q8_0, every row, batch 1, 4 and 16 (the 192-tile
   split plan of the small-matrix kernel at batch 1, the matrix-core skinny kernel at 4
   and 16); the 151936x4096 LM-head shape in the same formats, sampled rows, batch 1, 4
@@ -90,6 +91,26 @@ def test_gpu_c4_12288x4096_every_row(ctx, kind):
             ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
             got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
             assert_bits_equal(got, ref, f"B={tokens} pinned={pinned}")
+    ctx.release(wid)
+
+
+@pytest.mark.parametrize("M", [128, 512, 2048])
+def test_gpu_c2_prefill_both_contracts_sampled_tokens(ctx, M):
+    """The prefill workload (PTQ1 6144x2048, M tokens) in both contracts: the source
+    contract on the f16-MFMA GEMM, the pinned one (the contract the reference's graph
+    hands the executor) on the int8-MFMA skinny kernel, 16 tokens per launch, each
+    unit decoded once per launch.  Sampled tokens, every row, against the oracle."""
+    import oracle
+
+    rows, cols = 6144, 2048
+    w = synth.ptq1_weights(rows, cols, seed=9)
+    X = synth.activations(cols, seed=10 + M, tokens=M)
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
+    for pinned in (False, True):
+        Y = ctx.prefill(wid, rows, X, pinned=pinned)
+        for t in sorted({0, 1, 15, 16, 17, M // 2, M - 1}):
+            ref = oracle.matvec(ph.KIND_PTQ1, cols, rows, w, X[t], pinned, threads=THREADS)
+            assert_bits_equal(Y[t], ref, f"M={M} token {t} pinned={pinned}")
     ctx.release(wid)
 
 

@@ -367,15 +367,16 @@ def test_gpu_ptq1_table_batch_matches_per_token_oracle(ctx, cols, tokens):
 
 
 @pytest.mark.parametrize("rows", [1024 + 53, 20480 + 37, 40960 + 37, 65536 + 37, 131072 + 37])
-@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 384), (ph.KIND_PTQ1, 512), (ph.KIND_PQ2, 512),
+@pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 128), (ph.KIND_PTQ1, 384), (ph.KIND_PTQ1, 512), (ph.KIND_PQ2, 512),
                                        (ph.KIND_PQ2, 384), (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256),
                                        (ph.KIND_TQ1_0, 512), (ph.KIND_TQ2_0, 256)])
 def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     """2..17 tokens run weights-once on the int8 matrix cores, 16 rows per block: the
     row counts cover 8, 4, 2 and 1 wavefronts per block (K split over the workgroup,
     terms folded through LDS), and rows x tokens cover both activation sources (prepared
-    blocks gathered directly, or a lane-ordered copy); the pinned PTQ1 order runs one
-    wavefront per tile from 65536 rows.  Each token's row must equal its own matvec, in
+    blocks gathered directly, or a lane-ordered copy); pinned PTQ1 takes four masked
+    MFMAs per group (one per native lane subset), at most two wavefronts per block;
+    TQ1_0 / TQ2_0 run the row-tile batch kernel.  Each token's row must equal its own matvec, in
     every contract, with partial chunks of the 16-token batch, a partial last tile and
     16-row block."""
     import oracle
