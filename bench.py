@@ -311,18 +311,20 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
 
 # ---- config 2: the tiled prefill GEMM ----------------------------------------------------
 
-def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 20):
+def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 20,
+                  pinned: bool = False):
+    """The prefill GEMM (quantization prep + GEMM) in the source or the pinned contract."""
     w = synth.ptq1_weights(rows, cols, seed=9)
     wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
     X = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=10, tokens=M))
     out = hiprt.DeviceBuffer(4 * rows * M)
     stream = ctx.stream()
-    ctx.project_device(wid, ph.PATH_F32, X, M, False, out, stream)
+    ctx.project_device(wid, ph.PATH_F32, X, M, pinned, out, stream)
     assert ctx.sync() == 0
     e0, e1 = hiprt.Event(), hiprt.Event()
     e0.record(stream)
     for _ in range(reps):
-        ctx.project_device(wid, ph.PATH_F32, X, M, False, out, stream)
+        ctx.project_device(wid, ph.PATH_F32, X, M, pinned, out, stream)
     e1.record(stream)
     e1.synchronize()
     assert ctx.sync() == 0
@@ -330,9 +332,11 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
     ops = 2.0 * M * rows * cols
     ctx.release(wid)
     valu_ceiling = PREFILL_OPS_PER_BLOCK * 4 / (PREFILL_VALU_PER_BLOCK * 4) * CUS * ENGINE_HZ
-    return {"M": M, "ms": t * 1e3, "TOPS": ops / t / 1e12, "frac_int8_peak": ops / t / PEAK_I8,
-            "frac_f16_peak": ops / t / PEAK_F16, "valu_issue_ceiling_TOPS": valu_ceiling / 1e12,
-            "frac_valu_ceiling": ops / t / valu_ceiling}
+    r = {"M": M, "contract": "pinned" if pinned else "source", "ms": t * 1e3, "TOPS": ops / t / 1e12,
+         "frac_int8_peak": ops / t / PEAK_I8, "frac_f16_peak": ops / t / PEAK_F16}
+    if not pinned:  # the instruction-mix ceiling was counted for the source kernel
+        r.update(valu_issue_ceiling_TOPS=valu_ceiling / 1e12, frac_valu_ceiling=ops / t / valu_ceiling)
+    return r
 
 
 # ---- CPU baselines (the oracle on the host's cores) --------------------------------------
@@ -382,6 +386,9 @@ def cpu_baselines(model: dict, budget_s: float = 1.5):
     add("c2 PTQ1 6144x2048 prefill (16 of the M tokens; per-token cost is independent of M)", "Gop/s",
         2.0 * 16 * 6144 * 2048 / 1e9, lambda t: oracle.prefill(oracle.KIND_PTQ1, 2048, 6144, w2, X2, False, t),
         sample="16 tokens per run")
+    add("c2 PTQ1 6144x2048 prefill, pinned contract (16 of the M tokens)", "Gop/s",
+        2.0 * 16 * 6144 * 2048 / 1e9, lambda t: oracle.prefill(oracle.KIND_PTQ1, 2048, 6144, w2, X2, True, t),
+        sample="16 tokens per run")
     for kind, name in ((oracle.KIND_PTQ1, "PTQ1"), (oracle.KIND_Q2_K, "Q2_K"), (oracle.KIND_Q8_0, "Q8_0")):
         w4 = synth.weights(kind, 12288, 4096, seed=7)
         x4 = synth.activations(4096, seed=8)
@@ -414,7 +421,8 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
-    ap.add_argument("--prefill-only", default="", help="comma-separated token counts: time only the prefill GEMM")
+    ap.add_argument("--prefill-only", default="",
+                    help="comma-separated token counts, each optionally ':pinned': time only the prefill GEMM")
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
@@ -433,8 +441,9 @@ def main() -> int:
     ctx = ph.Context(0)
     log(ctx.identity)
     if args.prefill_only or args.matvec_only or args.ffn_only:
-        for M in filter(None, args.prefill_only.split(",")):
-            print(json.dumps(bench_prefill(ctx, int(M))), flush=True)
+        for spec in filter(None, args.prefill_only.split(",")):
+            M, _, contract = spec.partition(":")  # "2048" or "2048:pinned"
+            print(json.dumps(bench_prefill(ctx, int(M), pinned=contract == "pinned")), flush=True)
         for spec in filter(None, args.matvec_only.split(",")):
             kind, rows, cols, *tok = (int(v) for v in spec.split(":"))
             print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols, tokens=tok[0] if tok else 1)), flush=True)
@@ -479,10 +488,11 @@ def main() -> int:
                     f"({r['us_per_token']:.2f} us/token), {r['GBps']:.1f} GB/s")
                 extras["skinny_batch"].append(r)
         extras["prefill_ptq1_6144x2048"] = []
-        for M in (128, 512, 2048):
-            r = bench_prefill(ctx, M)
-            log(f"prefill M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
-            extras["prefill_ptq1_6144x2048"].append(r)
+        for pinned in (False, True):
+            for M in (128, 512, 2048):
+                r = bench_prefill(ctx, M, pinned=pinned)
+                log(f"prefill {r['contract']} M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
+                extras["prefill_ptq1_6144x2048"].append(r)
     ctx.close()
     cpu = None
     if not args.no_cpu:

@@ -23,9 +23,12 @@
 // stream block by block into a double-buffered LDS ring with direct-to-LDS buffer
 // loads; one barrier per block hands a buffer from the loads to the readers and back.
 //
-// The activation side is prepared once per call by k_prefill_prep: Q8_0 source
-// quantization per token, the codes stored as binary16 in operand order and the f32
-// scales beside them.
+// The activation side is prepared once per call by k_prefill_prep: Q8_0 quantization per
+// token, the codes stored as binary16 in operand order and the f32 scales beside them.
+//
+// The pinned contract (dot_q8_groups_pinned) runs k_prefill_ptq1_pinned on the same
+// tiles with its own operand order, four MFMAs per group (one per native lane) and four
+// FMA chains per output; see there.
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "quant_dev.hpp"
@@ -62,10 +65,21 @@ __host__ __device__ constexpr uint32_t quad_base(uint32_t h, uint32_t g, uint32_
                     : (i < 3 ? 96 + 8 * i + 4 * h : 120 + 4 * h);
 }
 
+// Pinned order (dot_q8_groups_pinned, src/kernels.rs:1102-1147): the chain needs, per
+// group, the sum over each native lane l's elements 4l..4l+3 and 16+4l..16+4l+3
+// (q8_native_lanes, src/kernels.rs:1066-1076), i.e. quads l and l+4 of the group.  The
+// operand order puts native lane l = 2j + h in K-step j, half h: one MFMA with the other
+// half's weights zeroed then returns I_l exactly.
+__host__ __device__ constexpr uint32_t quad_base_pinned(uint32_t h, uint32_t g, uint32_t j, uint32_t qq) {
+    return 32 * g + 4 * ((2 * j + h) + 4 * qq);
+}
+
 // ---- activation prep ------------------------------------------------------------------
-// One wavefront per (token, 1024 inputs): Q8_0 source quantization into LDS, then the
-// codes leave as binary16 in operand order, xh[u][g][j][h][t][8] (u = 128-block, tokens
-// padded to Mp with zeros), and the scales as sc[u][t][g].
+// One wavefront per (token, 1024 inputs): Q8_0 quantization into LDS (the source
+// contract, or the pinned PTQ1 native-scale contract), then the codes leave as binary16
+// in operand order, xh[u][g][j][h][t][8] (u = 128-block, tokens padded to Mp with zeros),
+// and the scales as sc[u][t][g].
+template <bool PINNED>
 __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp, uint32_t K,
                                                       _Float16 *__restrict__ xh, float *__restrict__ sc,
                                                       int *__restrict__ err) {
@@ -79,7 +93,8 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ 
     const bool real = t < M;
     if (real) {
         const float *xr = x + static_cast<size_t>(t) * K + k0;
-        const int e = q8_0_blocks_wave(xr, n / 32, 0 /* source contract */, blk[wave], lane);
+        // Contract 0: source (round half away); 2: pinned PTQ1 native scale (quant_dev.hpp).
+        const int e = q8_0_blocks_wave(xr, n / 32, PINNED ? 2 : 0, blk[wave], lane);
         if (e) {
             if (lane == 0) raise_error(err, e);
             return;
@@ -93,7 +108,7 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ 
         uint32_t packed[4];
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
-            const uint32_t base = 128 * ub + quad_base(h, g, 2 * j + qq);
+            const uint32_t base = 128 * ub + (PINNED ? quad_base_pinned(h, g, j, qq) : quad_base(h, g, 2 * j + qq));
             const uint32_t el[4] = {base, base + 2, base + 1, base + 3};
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
@@ -218,6 +233,36 @@ __device__ __forceinline__ void decode_block(const RawBlock &w, uint32_t h, uint
         const uint32_t trep = perm(w.tl, w.tl, sel_bytes(0, 1, 0, 1));
         quad_at(trep, h ? (9u | (27u << 16)) : (1u | (3u << 16)), aw[3][1][2], aw[3][1][3]);
     }
+}
+
+// The pinned operand order (quad_base_pinned): half h feeds native lane l = h in K-step
+// 0 and l = 2 + h in K-step 1; group g of lane l takes quads l and l + 4, which come
+// from (tools/ternary/src/lib.rs:202-250 element map)
+//   g0: (A_l, 0) (A_l, 1)      g1: (A_l, 2) (A_l, 3)      g2: (A_l, 4) (B_h, l/2)
+//   g3: (B_h, 2 + l/2), then (B_h, 4) for l < 2 or the tail quad 120 + 4h for l >= 2,
+// so half h decodes digits 0..4 of A_h, A_{2+h} and B_h, and one tail quad.
+__device__ __forceinline__ void decode_block_pinned(const RawBlock &w, uint32_t h, uint32_t aw[4][2][4]) {
+    uint32_t alo[5], ahi[5], blo[5], bhi[5], clo[5], chi[5];
+    quads_seq<5>(h ? w.a.y : w.a.x, alo, ahi);  // A_h
+    quads_seq<5>(h ? w.a.w : w.a.z, blo, bhi);  // A_{2+h}
+    quads_seq<5>(h ? w.b.y : w.b.x, clo, chi);  // B_h
+    uint32_t tlo, thi;
+    const uint32_t trep = perm(w.tl, w.tl, sel_bytes(0, 1, 0, 1));
+    quad_at(trep, h ? (9u | (27u << 16)) : (1u | (3u << 16)), tlo, thi);
+    auto put = [&](int g, int j, uint32_t l0, uint32_t h0, uint32_t l1, uint32_t h1) {
+        aw[g][j][0] = l0;
+        aw[g][j][1] = h0;
+        aw[g][j][2] = l1;
+        aw[g][j][3] = h1;
+    };
+    put(0, 0, alo[0], ahi[0], alo[1], ahi[1]);
+    put(0, 1, blo[0], bhi[0], blo[1], bhi[1]);
+    put(1, 0, alo[2], ahi[2], alo[3], ahi[3]);
+    put(1, 1, blo[2], bhi[2], blo[3], bhi[3]);
+    put(2, 0, alo[4], ahi[4], clo[0], chi[0]);
+    put(2, 1, blo[4], bhi[4], clo[1], chi[1]);
+    put(3, 0, clo[2], chi[2], clo[4], chi[4]);
+    put(3, 1, clo[3], chi[3], tlo, thi);
 }
 
 // s_waitcnt through the builtin (gfx9 encoding, other counters left at their maxima),
@@ -379,6 +424,140 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
     if (bad) raise_error(err, kErrNonfinite);
 }
 
+// The pinned contract (dot_q8_groups_pinned, src/kernels.rs:1102-1147) on the same
+// tiles: per (token, row) four binary32 lanes L[l] = fma(I_l, dd_g, L[l]) with
+// dd_g = fl(d_w * A_g.scale), group by group, and (L0 + L1) + (L2 + L3) at the end.  In
+// the pinned operand order K-step j of group g holds native lane 2j in its first half
+// (lanes 0..31 of the wavefront) and lane 2j + 1 in its second, so an MFMA whose weights
+// are zeroed in one half returns that lane's exact integer sum (binary16-exact operands,
+// |I| <= 8*127).  Four MFMAs per group instead of two, and 20 VALU per output and block
+// instead of 6 (the four dd_g and sixteen FMAs): 32 tokens per workgroup keep the 64
+// lane accumulators of a wavefront in registers.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_ptq1_pinned(
+    const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu, const _Float16 *__restrict__ xh,
+    const float *__restrict__ sc, uint32_t M, uint32_t Mp, uint32_t xcd_major, float *__restrict__ out,
+    int *__restrict__ err) {
+    constexpr uint32_t NT = 32;
+    constexpr uint32_t kRun = NT * 16;
+    __shared__ __attribute__((aligned(16))) uint8_t act0[8][2][kRun];
+    __shared__ __attribute__((aligned(16))) uint8_t act1[8][2][kRun];
+    __shared__ __attribute__((aligned(16))) float4 scl0[NT];
+    __shared__ __attribute__((aligned(16))) float4 scl1[NT];
+    const uint32_t lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t bx = xcd_major ? blockIdx.y : blockIdx.x;
+    const uint32_t by = xcd_major ? blockIdx.x + 8 * blockIdx.z : blockIdx.y;
+    const uint32_t tile = 2 * bx + (wave >> 1), hw = wave & 1;
+    const uint32_t tiles = (rows + kTile - 1) / kTile;
+    const uint32_t t0 = by * NT;
+    const uint32_t row_bytes = nu * 28;
+    uint32_t trows = 0;
+    if (tile < tiles) {
+        const uint32_t left = rows - tile * kTile;
+        trows = left < kTile ? left : kTile;
+    }
+    const bool active = 32 * hw < trows;  // uniform per wavefront
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(W + static_cast<size_t>(active ? tile : 0) * kTile * row_bytes, active ? trp * row_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, nu * 8u * Mp * 32u);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc, nu * Mp * 16u);
+    const uint32_t row = 32 * hw + r32, out0 = 32 * hw + 4 * h;  // tile rows
+
+    // Block u's codes (16 runs of NT*16 bytes) and scales of the workgroup's tokens.
+    auto stage = [&](uint32_t u, uint8_t (&act)[8][2][kRun], float4 (&scl)[NT]) {
+        for (uint32_t run = wave; run < 16; run += 4)
+            if (lane < NT)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(&act[run >> 1][run & 1][0]), 16,
+                                                         ((u * 16 + run) * Mp + t0 + lane) * 16u, 0, 0, 0);
+        if (wave == 0 && lane < NT)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(&scl[0]), 16, (u * Mp + t0 + lane) * 16u, 0,
+                                                     0, 0);
+    };
+
+    float L[4][16];
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) L[l][r] = 0.0f;
+    const v16f zero = {};
+
+    RawBlock w;
+    stage(0, act0, scl0);
+    if (active) load_block(rw, 0, trp, row, out0, w);
+    wait_vmcnt0();
+    lds_barrier();
+    auto block = [&](uint32_t u, const uint8_t (&act)[8][2][kRun], const float4 (&scl)[NT],
+                     uint8_t (&act_next)[8][2][kRun], float4 (&scl_next)[NT]) {
+        uint32_t aw[4][2][4];
+        float d[16];
+        if (active) {
+            decode_block_pinned(w, h, aw);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                d[4 * q] = h2f(w.dd[q].x >> 16);
+                d[4 * q + 1] = h2f(w.dd[q].y >> 16);
+                d[4 * q + 2] = h2f(w.dd[q].z >> 16);
+                d[4 * q + 3] = h2f(w.dd[q].w >> 16);
+            }
+        }
+        if (u + 1 < nu) {
+            stage(u + 1, act_next, scl_next);
+            if (active) load_block(rw, (u + 1) * trp * 28u, trp, row, out0, w);
+        }
+        if (active) {
+            const float4 sg4 = scl[r32];
+            const float sg[4] = {sg4.x, sg4.y, sg4.z, sg4.w};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float dd[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dd[r] = d[r] * sg[g];  // fl(d_w * A_g.scale)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const v8h b = *reinterpret_cast<const v8h *>(&act[2 * g + j][h][r32 * 16]);
+                    const u32x4 a = {aw[g][j][0], aw[g][j][1], aw[g][j][2], aw[g][j][3]};
+                    const u32x4 z = {0u, 0u, 0u, 0u};
+                    const v16f i0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, h ? z : a), b, zero,
+                                                                           0, 0, 0);
+                    const v16f i1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, h ? a : z), b, zero,
+                                                                           0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        L[2 * j][r] = __builtin_fmaf(i0[r], dd[r], L[2 * j][r]);
+                        L[2 * j + 1][r] = __builtin_fmaf(i1[r], dd[r], L[2 * j + 1][r]);
+                    }
+                }
+            }
+        }
+        wait_vmcnt0();
+        lds_barrier();
+    };
+    for (uint32_t u = 0; u < nu; u += 2) {
+        block(u, act0, scl0, act1, scl1);
+        if (u + 1 < nu) block(u + 1, act1, scl1, act0, scl0);
+    }
+    if (!active) return;
+    const uint32_t t = t0 + r32;
+    if (t >= M) return;
+    bool bad = false;
+    float *yr = out + static_cast<size_t>(t) * rows + static_cast<size_t>(tile) * kTile;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t r = out0 + 8 * q + e;
+            if (r < trows) {
+                const int k = 4 * q + e;
+                const float v = (L[0][k] + L[1][k]) + (L[2][k] + L[3][k]);
+                yr[r] = v;
+                bad |= !finite(v);
+            }
+        }
+    }
+    if (bad) raise_error(err, kErrNonfinite);
+}
+
 uint32_t padded_tokens(uint32_t M) { return (M + kTokAlign - 1) / kTokAlign * kTokAlign; }
 
 }  // namespace
@@ -388,27 +567,43 @@ size_t prefill_scratch_bytes(uint64_t cols, uint32_t tokens) {
     return ((Mp * cols * 2 + 255) & ~size_t(255)) + Mp * (cols / 32) * 4;
 }
 
+// Tokens from which pinned PTQ1 takes the GEMM rather than the skinny kernel (16 tokens
+// per launch, each unit decoded once per launch).  Measured, 6144 x 2048: 16 tokens 33
+// against 24 us, 32 tokens 34 against 45 us, 2048 tokens 275 against 2629 us.
+constexpr uint32_t kPinnedGemmMinTokens = 32;
+
 bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens) {
     // The token codes are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols / 128 * 8u * padded_tokens(tokens) * 32u;
-    return kind == kPTQ1 && !pinned && cols % 128 == 0 && cols <= 65536 && rows > 0 &&
+    if (pinned && tokens < kPinnedGemmMinTokens) return false;
+    return kind == kPTQ1 && cols % 128 == 0 && cols <= 65536 && rows > 0 &&
            (rows * (cols / 128) * 28) < (1ull << 40) && code_bytes < (1ull << 31);
 }
 
-int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M, float *out,
-                   void *scratch, int *err, hipStream_t s) {
+int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M, int pinned,
+                   float *out, void *scratch, int *err, hipStream_t s) {
     const uint32_t K = static_cast<uint32_t>(cols), Mp = padded_tokens(M);
     if (static_cast<uint64_t>(K / 128) * 8u * Mp * 32u >= (1ull << 31)) return kLaunchUnsupported;
     _Float16 *xh = static_cast<_Float16 *>(scratch);
     float *sc = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + ((static_cast<size_t>(Mp) * K * 2 + 255) & ~size_t(255)));
     const uint32_t chunks = (K + 1023) / 1024;
     const uint64_t items = static_cast<uint64_t>(Mp) * chunks;
-    hipLaunchKernelGGL(k_prefill_prep, dim3(static_cast<uint32_t>((items + 3) / 4)), dim3(256), 0, s, x, M, Mp, K, xh,
-                       sc, err);
+    const dim3 pgrid(static_cast<uint32_t>((items + 3) / 4));
+    if (pinned)
+        hipLaunchKernelGGL(k_prefill_prep<true>, pgrid, dim3(256), 0, s, x, M, Mp, K, xh, sc, err);
+    else
+        hipLaunchKernelGGL(k_prefill_prep<false>, pgrid, dim3(256), 0, s, x, M, Mp, K, xh, sc, err);
     if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
     const auto W = static_cast<const uint8_t *>(w_tiled);
     const uint32_t R = static_cast<uint32_t>(rows), nu = K / 128;
+    if (pinned) {
+        const uint32_t groups = Mp / 32;
+        const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;
+        const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
+        hipLaunchKernelGGL(k_prefill_ptq1_pinned, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
+        return launch_status();
+    }
     // Tokens per workgroup (measured, 6144 x 2048): 64 keeps three wavefronts per SIMD
     // and beats 128 (two per SIMD, the decode shared by more tokens) up to about 4096
     // tokens; 32 keeps CUs busy on short prompts (256 tokens: 181 against 170 TOPS; even

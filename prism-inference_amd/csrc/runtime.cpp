@@ -13,8 +13,8 @@ using namespace prism::rt;
 
 namespace {
 
-// Token count from which f32 projections of PTQ1 weights (source contract) run as one
-// tiled-prefill GEMM instead of one matvec per token.
+// Token count from which f32 projections of PTQ1 weights run as one tiled-prefill GEMM
+// (prefill_supported has the last word: its own threshold for the pinned contract).
 constexpr uint32_t kPrefillMinTokens = 16;
 
 // Quantize device floats with the contract matvec_into would use, then project.  `role`
@@ -27,7 +27,7 @@ int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t 
         void *pre = nullptr;
         int rc = scr.get(c->pre, prefill_scratch_bytes(w.cols, tokens), &pre);
         if (rc) return rc;
-        rc = launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, out, pre, c->err, s), "prefill launch");
+        rc = launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, pinned, out, pre, c->err, s), "prefill launch");
         // The residual joins after the projection, one binary32 add per output (as the
         // row kernels do in their epilogue).
         if (!rc && residual)

@@ -435,11 +435,13 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
                                          (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
                                          (96, 256, 4096)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
-    """PTQ1 source-contract prefill runs as one f16-MFMA GEMM from 16 tokens on; every
+    """PTQ1 prefill runs as one f16-MFMA GEMM from 16 tokens on, in both contracts; every
     token row must equal the reference's per-token matvec bit for bit (partial row
     tiles, idle wavefronts of a partial 128-row block, an odd block count, 32, 64 and
     128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
-    token groups are a multiple of eight: M = 200, 512, 4096)."""
+    token groups are a multiple of eight: M = 200, 512, 4096).  The pinned contract's
+    kernel takes each native lane's integer sum from its own masked MFMA and runs the
+    four FMA lanes of dot_q8_groups_pinned."""
     import oracle
 
     w = synth.ptq1_weights(rows, cols, seed=rows + M)
@@ -449,6 +451,8 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     ref = oracle.prefill(ph.KIND_PTQ1, cols, rows, w, X, False, threads=THREADS)
     assert_bits_equal(ctx.prefill(wid, rows, X, pinned=False), ref, f"prefill gemm {rows}x{cols} M={M}")
     assert_bits_equal(ctx.mul_mat(wid, rows, X), ref, "mul_mat gemm")
+    ref = oracle.prefill(ph.KIND_PTQ1, cols, rows, w, X, True, threads=THREADS)
+    assert_bits_equal(ctx.prefill(wid, rows, X, pinned=True), ref, f"pinned prefill gemm {rows}x{cols} M={M}")
     ctx.release(wid)
 
 
