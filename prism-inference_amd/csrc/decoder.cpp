@@ -226,7 +226,11 @@ uint64_t family_bytes(const prism_hip_decoder *d, Family f, uint64_t pos) {
     }
 }
 
+// Destroys the captured step.  A replay may still be queued on the context stream, so the
+// stream drains first: the executable is never freed under a launch in flight.
 void drop_graph(prism_hip_decoder *d) {
+    if (!d->exec && !d->graph) return;
+    if (d->ctx && d->ctx->stream) (void)hipStreamSynchronize(d->ctx->stream);
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
     d->exec = nullptr;
@@ -443,7 +447,12 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
         }
         if (e != hipSuccess) return hip_fail(c, e, "hipStreamEndCapture");
         d->graph = graph;
-        HIP_OR_FAIL(c, hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+        e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            d->exec = nullptr;
+            drop_graph(d);  // the next call captures again
+            return hip_fail(c, e, "hipGraphInstantiate");
+        }
     }
     hipEvent_t t0 = nullptr, t1 = nullptr;
     HIP_OR_FAIL(c, hipEventCreate(&t0));

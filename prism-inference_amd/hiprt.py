@@ -150,9 +150,14 @@ class Graph:
         check(hip().hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
 
     def __del__(self):
+        # Replays may still be queued: drain the stream before freeing the executable.
         try:
-            hip().hipGraphExecDestroy(self.exec)
-            hip().hipGraphDestroy(self.graph)
+            if getattr(self, "stream", None) is not None:
+                hip().hipStreamSynchronize(self.stream)
+            if getattr(self, "exec", None):
+                hip().hipGraphExecDestroy(self.exec)
+            if getattr(self, "graph", None):
+                hip().hipGraphDestroy(self.graph)
         except Exception:
             pass
 
