@@ -165,11 +165,12 @@ __device__ __forceinline__ uint2 lut_at(uint32_t x, uint32_t lbase, uint32_t b) 
     return *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(g_ptq1_lut) + addr);
 }
 
-// Same contract as ptq1_dots, but acc(q) receives sum (t-1)*a directly.  The four
-// entries of a code dword are transposed (8 v_perm) into the natural quads
-// (digit k of bytes 4w..4w+3), so the activation keeps its natural order.
-template <typename Act, typename Acc>
-__device__ __forceinline__ void ptq1_dots_lut(const uint32_t x[7], uint32_t lbase, const Act &a, Acc &&acc) {
+// The unit's 32 quads from the table: f(q, t) receives quad q (elements 4q..4q+3,
+// trits minus one as signed bytes).  The four entries of a code dword are transposed
+// (8 v_perm) into the natural quads (digit k of bytes 4w..4w+3), so the activation
+// keeps its natural order.
+template <typename F>
+__device__ __forceinline__ void ptq1_quads_lut(const uint32_t x[7], uint32_t lbase, F &&f) {
 #pragma unroll
     for (int w = 0; w < 6; ++w) {
         const uint2 e0 = lut_at(x[w], lbase, 0), e1 = lut_at(x[w], lbase, 1);
@@ -183,17 +184,93 @@ __device__ __forceinline__ void ptq1_dots_lut(const uint32_t x[7], uint32_t lbas
         T[3] = perm(h23, h01, sel(2, 3, 6, 7));
         T[4] = perm(e1.y, e0.y, sel(0, 4, 12, 12)) | perm(e3.y, e2.y, sel(12, 12, 0, 4));
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-            const int q = w < 4 ? 4 * k + w : 20 + 2 * k + (w - 4);
-            int &r = acc(q);
-            r = sdot4(T[k], a(q), r);
-        }
+        for (int k = 0; k < 5; ++k) f(w < 4 ? 4 * k + w : 20 + 2 * k + (w - 4), T[k]);
     }
     const uint2 e0 = lut_at(x[6], lbase, 0), e1 = lut_at(x[6], lbase, 1);
-    int &r30 = acc(30);
-    r30 = sdot4(perm(e1.x, e0.x, sel(0, 4, 1, 5)), a(30), r30);
-    int &r31 = acc(31);
-    r31 = sdot4(perm(e1.x, e0.x, sel(2, 6, 3, 7)), a(31), r31);
+    f(30, perm(e1.x, e0.x, sel(0, 4, 1, 5)));
+    f(31, perm(e1.x, e0.x, sel(2, 6, 3, 7)));
+}
+
+// The unit's 32 quads from the table in slot order, for kernels that stage the
+// activation in the same order (an integer dot is exact in any element order):
+// f(s, t) receives slot s.  Slots 5w..5w+4 come from code dword w < 6 (entries
+// E0..E3 of its bytes): (E0.d0, E0.d1, E1.d0, E1.d1), (E2.d0, E2.d1, E3.d0, E3.d1),
+// the same two with digits 2 and 3, and the four digit-4s -- one v_perm per slot
+// where the natural order takes two.  Every slot lies in one 32-element group.  With
+// NATIVE, dwords 4 and 5 keep the natural quads (digit k of four bytes in slot 5w+k),
+// and every slot also lies in one native lane subset (positions 4l..4l+3 and
+// 16+4l..16+4l+3 of its group).  Slots 30 and 31 are dword 6's two natural quads.
+// ptq1_slot_byte gives each element's slot and byte.
+template <bool NATIVE, typename F>
+__device__ __forceinline__ void ptq1_slots_lut(const uint32_t x[7], uint32_t lbase, F &&f) {
+#pragma unroll
+    for (int w = 0; w < 6; ++w) {
+        const uint2 e0 = lut_at(x[w], lbase, 0), e1 = lut_at(x[w], lbase, 1);
+        const uint2 e2 = lut_at(x[w], lbase, 2), e3 = lut_at(x[w], lbase, 3);
+        const uint32_t d4 = perm(e1.y, e0.y, sel(0, 4, 12, 12)) | perm(e3.y, e2.y, sel(12, 12, 0, 4));
+        if (NATIVE && w >= 4) {
+            const uint32_t l01 = perm(e1.x, e0.x, sel(0, 4, 1, 5)), h01 = perm(e1.x, e0.x, sel(2, 6, 3, 7));
+            const uint32_t l23 = perm(e3.x, e2.x, sel(0, 4, 1, 5)), h23 = perm(e3.x, e2.x, sel(2, 6, 3, 7));
+            f(5 * w + 0, perm(l23, l01, sel(0, 1, 4, 5)));
+            f(5 * w + 1, perm(l23, l01, sel(2, 3, 6, 7)));
+            f(5 * w + 2, perm(h23, h01, sel(0, 1, 4, 5)));
+            f(5 * w + 3, perm(h23, h01, sel(2, 3, 6, 7)));
+        } else {
+            f(5 * w + 0, perm(e1.x, e0.x, sel(0, 1, 4, 5)));
+            f(5 * w + 1, perm(e3.x, e2.x, sel(0, 1, 4, 5)));
+            f(5 * w + 2, perm(e1.x, e0.x, sel(2, 3, 6, 7)));
+            f(5 * w + 3, perm(e3.x, e2.x, sel(2, 3, 6, 7)));
+        }
+        f(5 * w + 4, d4);
+    }
+    const uint2 e0 = lut_at(x[6], lbase, 0), e1 = lut_at(x[6], lbase, 1);
+    f(30, perm(e1.x, e0.x, sel(0, 4, 1, 5)));
+    f(31, perm(e1.x, e0.x, sel(2, 6, 3, 7)));
+}
+
+// 4 * slot + byte of element e (0..127) of a unit in ptq1_slots_lut's order.  Digit k
+// of code byte b < 16 is element 16k + b, of byte 16 + b (b < 8) element 80 + 8k + b,
+// of byte 24 + b (b < 2) element 120 + 2k + b.
+__host__ __device__ constexpr uint32_t ptq1_slot_byte(uint32_t e, bool native) {
+    uint32_t B = 0, k = 0;
+    if (e < 64) {
+        k = e >> 4;
+        B = e & 15u;
+    } else if (e < 80) {
+        B = e - 64;
+        k = 4;
+    } else if (e < 120) {
+        k = (e - 80) >> 3;
+        B = 16 + ((e - 80) & 7u);
+    } else {
+        k = (e - 120) >> 1;
+        B = 24 + ((e - 120) & 1u);
+    }
+    if (B >= 24) return 4 * (30 + (k >> 1)) + 2 * (k & 1u) + (B - 24);
+    const uint32_t w = B >> 2, i = B & 3u;
+    if (k == 4) return 4 * (5 * w + 4) + i;
+    if (native && w >= 4) return 4 * (5 * w + k) + i;
+    return 4 * (5 * w + (i >> 1) + 2 * (k >> 1)) + 2 * (i & 1u) + (k & 1u);
+}
+
+// Slots of 32-element group g in ptq1_slots_lut's order, and (NATIVE) the two slots of
+// native lane l of group g.
+constexpr int kPtq1GroupSlots[4][8] = {{0, 1, 5, 6, 10, 11, 15, 16},
+                                       {2, 3, 7, 8, 12, 13, 17, 18},
+                                       {4, 9, 14, 19, 20, 21, 25, 26},
+                                       {22, 23, 24, 27, 28, 29, 30, 31}};
+constexpr int kPtq1LaneSlots[4][4][2] = {{{0, 1}, {5, 6}, {10, 11}, {15, 16}},
+                                         {{2, 3}, {7, 8}, {12, 13}, {17, 18}},
+                                         {{4, 20}, {9, 25}, {14, 21}, {19, 26}},
+                                         {{22, 24}, {27, 29}, {23, 30}, {28, 31}}};
+
+// Same contract as ptq1_dots, but acc(q) receives sum (t-1)*a directly.
+template <typename Act, typename Acc>
+__device__ __forceinline__ void ptq1_dots_lut(const uint32_t x[7], uint32_t lbase, const Act &a, Acc &&acc) {
+    ptq1_quads_lut(x, lbase, [&](int q, uint32_t t) {
+        int &r = acc(q);
+        r = sdot4(t, a(q), r);
+    });
 }
 
 // PQ2 code dword i holds elements 16i..16i+15, element 16i+4q+p in byte q, bits 2p.
@@ -586,6 +663,8 @@ __device__ __forceinline__ void rows_tile(const MvParams &p, const void *__restr
     };
     // Two register buffers in ping-pong: the next unit's loads are in flight while the
     // current one is decoded, and no buffer is copied (a copy would wait for the loads).
+    // Deeper rings spill at the table kernel's 128 registers (measured: three buffers
+    // 2.5x slower at 151936 rows).
     Raw<O> A, B;
     uint32_t u = 0;
     load_unit<O>(A, rs, 0, trp, lane);
@@ -1742,6 +1821,214 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     }
 }
 
+// ---- batches of up to four tokens on the 4x4x4 matrix cores --------------------------
+// v_mfma_i32_4x4x4_16b_i8 runs sixteen independent 4x4x4 integer products per
+// wavefront: block b = lane/4 takes row i of A from lane 4b+i and column j of B from
+// lane 4b+j, and leaves D[i][j] in register i of lane 4b+j.  With the tokens on A (lane
+// l supplies token l%4's activation quad, from LDS) and the weights on B (lane l
+// supplies a quad of its own row), lane l receives its row's exact integer dots with
+// all four tokens and every product of the instruction is a real one.  The kernel so
+// keeps the batch-1 layout -- one row per lane, each unit decoded once -- and runs four
+// binary32 chains per lane, one per token, with the batch-1 arithmetic: every output
+// equals its own matvec bit for bit.  With fewer than four tokens the missing ones
+// repeat the last token and are not stored.
+constexpr uint32_t kQuadTok = 4;
+constexpr uint32_t kQuadRowDw = 36;  // LDS dwords per (unit, token): 32 codes + 4 of padding
+constexpr uint32_t kQuadMaxCols = 16384;
+
+template <Op O>
+constexpr bool quad_supported() {
+    return O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED || O == Op::Q8_0;
+}
+
+// Threads per workgroup: the PTQ1 table (64 KiB of LDS) is filled once per CU for 16
+// wavefronts; Q8_0 needs no table and runs four.
+template <Op O>
+constexpr uint32_t quad_threads() {
+    return kind_of<O>() == kPTQ1 ? 1024u : 256u;
+}
+
+__device__ __forceinline__ v4i mfma4(uint32_t a, uint32_t b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(a), static_cast<int>(b), c, 0, 0, 0);
+}
+
+// Chains of one row and four tokens.
+template <Op O>
+struct QuadChain {
+    float o[kQuadTok] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float L[4][kQuadTok] = {};  // pinned PTQ1: [native lane][token]
+
+    __device__ __forceinline__ float result(int t) const {
+        if constexpr (O == Op::PTQ1_PINNED) return (L[0][t] + L[1][t]) + (L[2][t] + L[3][t]);
+        return o[t];
+    }
+};
+
+// One unit of one row into the four chains.  `qa` holds the unit's 32 activation dwords
+// of the lane's token (l%4), `qs` the unit's token scales as [group][token].
+template <Op O>
+__device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, const float *qs, uint32_t lbase,
+                                          QuadChain<O> &ch) {
+    uint32_t A[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(qa + 4 * i);
+        A[4 * i] = v.x; A[4 * i + 1] = v.y; A[4 * i + 2] = v.z; A[4 * i + 3] = v.w;
+    }
+    float S[4][kQuadTok];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 v = *reinterpret_cast<const float4 *>(qs + 4 * g);
+        S[g][0] = v.x; S[g][1] = v.y; S[g][2] = v.z; S[g][3] = v.w;
+    }
+    // PTQ1 weights and activations are both in ptq1_slots_lut's slot order; Q8_0's in the
+    // natural order (slot 8g + i is quad i of group g).
+    uint32_t W[32];
+    if constexpr (kind_of<O>() == kPTQ1) {
+        ptq1_slots_lut<O == Op::PTQ1_PINNED>(w.x, lbase, [&](int s, uint32_t t) { W[s] = t; });
+    } else {
+#pragma unroll
+        for (int q = 0; q < 32; ++q) W[q] = w.c[q];
+    }
+    auto slot = [](int g, int i) { return kind_of<O>() == kPTQ1 ? kPtq1GroupSlots[g][i] : 8 * g + i; };
+    if constexpr (O == Op::PTQ1_PINNED) {
+        // dot_q8_groups_pinned, src/kernels.rs:1134-1146: native lane l sums positions
+        // 4l..4l+3 and 16+4l..16+4l+3 of the group (two slots), then
+        // L[l] = fma(I_l, d * scale_g, L[l]).
+        const float d = h2f(ptq1_scale_bits(w));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v4i acc[4];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int s = kPtq1LaneSlots[g][l][0];
+                acc[l] = mfma4(A[s], W[s], v4i{0, 0, 0, 0});
+            }
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int s = kPtq1LaneSlots[g][l][1];
+                acc[l] = mfma4(A[s], W[s], acc[l]);
+            }
+#pragma unroll
+            for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
+                const float dd = d * S[g][t];
+#pragma unroll
+                for (int l = 0; l < 4; ++l)
+                    ch.L[l][t] = __builtin_fmaf(static_cast<float>(acc[l][t]), dd, ch.L[l][t]);
+            }
+        }
+    } else {
+        // The four groups' integer dots as four interleaved accumulator chains.
+        v4i acc[4] = {};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) acc[g] = mfma4(A[slot(g, i)], W[slot(g, i)], acc[g]);
+        if constexpr (O == Op::PTQ1_SRC) {
+            // dot_q8_groups, src/kernels.rs:1043-1064
+            const float d = h2f(ptq1_scale_bits(w));
+#pragma unroll
+            for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
+                float tt = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) tt = tt + S[g][t] * static_cast<float>(acc[g][t]);
+                ch.o[t] = ch.o[t] + d * tt;
+            }
+        } else {
+            // dot_legacy, src/kernels.rs:1241-1244; the row's chain adds the four group
+            // terms in order.
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float sw = h2f((w.s[g >> 1] >> (16 * (g & 1))) & 0xffffu);
+#pragma unroll
+                for (int t = 0; t < static_cast<int>(kQuadTok); ++t)
+                    ch.o[t] = ch.o[t] + (sw * S[g][t]) * static_cast<float>(acc[g][t]);
+            }
+        }
+    }
+}
+
+// LDS bytes per unit: the four tokens' codes, then their 16 scales.
+constexpr uint32_t kQuadUnitLds = (kQuadTok * kQuadRowDw + 4 * kQuadTok) * sizeof(uint32_t);
+
+// 2..4 tokens of prepared Q8_0 blocks (token t at act + t * act_stride bytes, outputs
+// and residual at t * rows).  The workgroup stages every token's activation codes in
+// LDS ([unit][token][36] dwords; PTQ1 codes in the decode's slot order) and their
+// scales ([unit][group][token] floats) once; its wavefronts then walk 64-row tiles as
+// the batch-1 row kernel does.
+template <Op O>
+__global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const void *__restrict__ act,
+                                                              uint32_t act_stride, uint32_t ntok) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
+    constexpr uint32_t UB = unit_bytes<O>();
+    constexpr uint32_t kWaves = quad_threads<O>() / 64;
+    const uint32_t nu = p.nu;
+    uint32_t *codes = quad_lds;
+    float *scales = reinterpret_cast<float *>(quad_lds + nu * kQuadTok * kQuadRowDw);
+    if constexpr (kind_of<O>() == kPTQ1) ptq1_lut_fill(threadIdx.x, blockDim.x);
+    for (uint32_t i = threadIdx.x; i < nu * 128u; i += blockDim.x) {
+        const uint32_t dw = i & 7u, t = (i >> 3) & 3u, g = (i >> 5) & 3u, u = i >> 7;
+        const Q8Block *blk = reinterpret_cast<const Q8Block *>(static_cast<const uint8_t *>(act) +
+                                                               static_cast<size_t>(t < ntok ? t : ntok - 1) *
+                                                                   act_stride) + 4 * u + g;
+        const uint32_t v = reinterpret_cast<const uint32_t *>(blk->values)[dw];
+        uint32_t *row = codes + (u * kQuadTok + t) * kQuadRowDw;
+        if constexpr (kind_of<O>() == kPTQ1) {
+            uint8_t *rb = reinterpret_cast<uint8_t *>(row);
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                rb[ptq1_slot_byte(32 * g + 4 * dw + j, O == Op::PTQ1_PINNED)] = static_cast<uint8_t>(v >> (8 * j));
+        } else {
+            row[8 * g + dw] = v;
+        }
+        if (dw == 0) scales[(u * 4 + g) * kQuadTok + t] = blk->scale;
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tiles = (p.rows + kTile - 1) / kTile;
+    const uint32_t lbase = 8u * (lane & 31u);
+    const uint32_t *qa = codes + (lane & 3u) * kQuadRowDw;
+    const uint32_t row_bytes = nu * UB;
+    // Wave-uniform by construction (the buffer descriptors below must live in SGPRs).
+    const uint32_t grid = __builtin_amdgcn_readfirstlane(gridDim.x);
+    for (uint32_t tile = wave * grid + blockIdx.x; tile < tiles; tile += grid * kWaves) {
+        const uint32_t left = p.rows - tile * kTile;
+        const uint32_t trows = left < kTile ? left : kTile;
+        const uint32_t trp = (trows + 7u) & ~7u;
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+        QuadChain<O> ch;
+        auto step = [&](const Raw<O> &w, uint32_t u) {
+            quad_unit<O>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, ch);
+        };
+        Raw<O> A, B;
+        uint32_t u = 0;
+        load_unit<O>(A, rs, 0, trp, lane);
+        while (u + 1 < nu) {
+            load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
+            step(A, u);
+            if (u + 2 < nu) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+            step(B, u + 1);
+            u += 2;
+        }
+        if (u < nu) step(A, u);
+        if (lane < trows) {
+            const size_t row = static_cast<size_t>(tile) * kTile + lane;
+#pragma unroll
+            for (uint32_t t = 0; t < kQuadTok; ++t) {
+                if (t < ntok) {
+                    const size_t at = static_cast<size_t>(t) * p.rows + row;
+                    float o = ch.result(static_cast<int>(t));
+                    if (p.residual) o = o + p.residual[at];
+                    p.out[at] = o;
+                    if (!finite(o)) raise_error(p.err, kErrNonfinite);
+                }
+            }
+        }
+    }
+}
+
 // ---- native -> tiled repack ------------------------------------------------------------
 // One thread per (row, unit).  Byte copies: this runs once per uploaded tensor.
 __global__ void k_repack(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, uint32_t kind, uint64_t rows,
@@ -2112,8 +2399,43 @@ int launch_lut_batch(const MatvecArgs &a, uint32_t act_stride) {
     }
 }
 
+// Two to four tokens of a large PTQ1 (Q8_0 activations) or Q8_0 matrix run on the 4x4x4
+// matrix cores: one row per lane and each unit decoded once, as at batch 1.
+bool quad_eligible(const MatvecArgs &a) {
+    if (a.w2 || a.tokens < 2 || a.tokens > kQuadTok || a.act_format == kActF32) return false;
+    if (a.cols > kQuadMaxCols || a.rows < kBatchMinRows) return false;
+    return dispatch(a, [&]<Op O>() { return quad_supported<O>() ? 1 : 0; }) == 1;
+}
+
+template <Op O>
+int launch_quad(const MatvecArgs &a, uint32_t act_stride) {
+    if constexpr (!quad_supported<O>()) {
+        return -2;
+    } else {
+        MvParams p{};
+        p.w[0] = p.w[1] = a.w;
+        p.rows = static_cast<uint32_t>(a.rows);
+        p.nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
+        p.cols = static_cast<uint32_t>(a.cols);
+        p.pinned = a.pinned;
+        p.out = a.out;
+        p.residual = a.residual;
+        p.err = a.err;
+        const size_t lds = static_cast<size_t>(p.nu) * kQuadUnitLds;
+        constexpr uint32_t kWaves = quad_threads<O>() / 64;
+        const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+        // PTQ1: one workgroup per CU walks tiles (its table is filled once); Q8_0: one
+        // tile per wavefront.
+        uint64_t grid = kind_of<O>() == kPTQ1 ? a.cus : (tiles + kWaves - 1) / kWaves;
+        if (grid > tiles) grid = tiles;
+        hipLaunchKernelGGL(k_mv_quad<O>, dim3(static_cast<uint32_t>(grid)), dim3(quad_threads<O>()), lds, a.stream,
+                           p, a.act, act_stride, a.tokens);
+        return launch_status();
+    }
+}
+
 bool skinny_eligible(const MatvecArgs &a) {
-    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a)) return false;
+    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a) || quad_eligible(a)) return false;
     // Pinned PTQ1 (four masked MFMAs per group) on large matrices: up to four tokens the
     // row-tile batch kernel is faster (151936x4096 x 4: 148 against 165 us), from 16 the
     // skinny kernel (171 against 558 us).
@@ -2127,6 +2449,8 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
+    if (a.act_format != kActF32 && quad_eligible(a))
+        return dispatch(a, [&]<Op O>() { return launch_quad<O>(a, static_cast<uint32_t>(in_stride)); });
     if (a.act_format != kActF32 && lut_batch_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_lut_batch<O>(a, static_cast<uint32_t>(in_stride)); });
     if (a.act_format != kActF32 && skinny_eligible(a)) {
@@ -2180,7 +2504,7 @@ size_t tiled_scratch_bytes(const MatvecArgs &a) {
 }
 
 bool tiled_needs_prepared(const MatvecArgs &a) {
-    if (lut_batch_eligible(a) || skinny_eligible(a) || batch_eligible(a)) return true;
+    if (quad_eligible(a) || lut_batch_eligible(a) || skinny_eligible(a) || batch_eligible(a)) return true;
     return dispatch(a, [&]<Op O>() { return op_needs_prepared<O>(a) ? 1 : 0; }) == 1;
 }
 

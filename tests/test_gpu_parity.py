@@ -414,6 +414,36 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("kind,cols,rows", [(ph.KIND_PTQ1, 128, 65536 + 37), (ph.KIND_PTQ1, 640, 65536 + 37),
+                                            (ph.KIND_PTQ1, 384, 131072 + 5), (ph.KIND_Q8_0, 128, 65536 + 37),
+                                            (ph.KIND_Q8_0, 640, 65536 + 1), (ph.KIND_Q8_0, 384, 131072 + 63)])
+def test_gpu_quad_batch_matches_per_token_oracle(ctx, kind, cols, rows):
+    """Two to four tokens of a large PTQ1 or Q8_0 matrix run on the 4x4x4 int8 matrix
+    cores, one row per lane (tokens on the A side, the lane's row on the B side); with
+    fewer than four tokens the last one is repeated and not stored.  Every token's row
+    must equal its own matvec in both contracts, through the f32 entry and through
+    prepared blocks of each Q8_0 contract, with a partial last tile and an odd unit
+    count."""
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=43)
+    wid = ctx.weight(kind, cols, rows, w)
+    nq8 = cols // 32
+    for tokens in (2, 3, 4):
+        X = synth.activations(cols, seed=44 + tokens, tokens=tokens)
+        for pinned in (False, True):
+            ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+            got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
+            assert_bits_equal(got, ref, f"quad f32 kind={kind} tokens={tokens} pinned={pinned}")
+        for contract, pinned in ((0, False), (2, True), (1, False)) if kind == ph.KIND_PTQ1 else ((1, False), (0, True)):
+            act = np.concatenate([oracle.quantize_q8_0(X[t], contract) for t in range(tokens)])
+            ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * nq8:(t + 1) * nq8], pinned,
+                                              threads=THREADS) for t in range(tokens)])
+            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens, pinned=pinned)
+            assert_bits_equal(got, ref, f"quad q8 kind={kind} tokens={tokens} contract={contract} pinned={pinned}")
+    ctx.release(wid)
+
+
 # ---- multi-token, groups, backend op -------------------------------------------------
 
 def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
