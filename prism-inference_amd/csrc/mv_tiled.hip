@@ -614,6 +614,7 @@ struct MvParams {
     int pinned;           // SwiGLU order (NMAT == 2)
     uint32_t ks, lpr;     // split mode: wavefronts per matrix, lanes per row (powers of two)
     uint32_t lg_ks, lg_lpr;  // their base-2 logarithms
+    uint32_t xcd_tiles;      // split mode: a tile's lpr workgroups share one XCD (tiles % 8 == 0)
     float *out;
     const float *residual;
     int *err;
@@ -1615,7 +1616,20 @@ __global__ __launch_bounds__(kSplitMaxThreads) void k_mv_split(MvParams p) {
     const uint32_t ks = p.ks, lg_lpr = p.lg_lpr, lg_rw = 6u - lg_lpr, rw = 1u << lg_rw;
     const uint32_t mat = (NMAT == 2 && wave >= ks) ? 1u : 0u;
     const uint32_t mw = wave - mat * ks;
-    const uint32_t tile = blockIdx.x >> lg_lpr, sub = blockIdx.x & ((1u << lg_lpr) - 1u);
+    // Workgroups go to the eight XCDs round-robin in dispatch order, each XCD with its own
+    // L2.  A workgroup of lpr > 1 reads 64/lpr rows of its tile's pieces, less than a
+    // cache line of the 8- and 4-byte pieces, so with xcd_tiles the tile's lpr workgroups
+    // are all placed on one XCD (workgroup b runs on XCD b % 8) and each line is fetched
+    // into one L2 only.
+    uint32_t tile, sub;
+    if (p.xcd_tiles) {
+        const uint32_t k = blockIdx.x >> 3;
+        tile = ((k >> lg_lpr) << 3) + (blockIdx.x & 7u);
+        sub = k & ((1u << lg_lpr) - 1u);
+    } else {
+        tile = blockIdx.x >> lg_lpr;
+        sub = blockIdx.x & ((1u << lg_lpr) - 1u);
+    }
     const uint32_t c = lane >> lg_rw, r = lane & (rw - 1u);
     const uint32_t lg_kt = p.lg_ks + lg_lpr, kt = 1u << lg_kt, kk = (mw << lg_lpr) + c;
     const uint32_t nu = p.nu, row_bytes = nu * UB;
@@ -2152,6 +2166,7 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.lpr = pl.lpr;
     p.lg_ks = pl.lg_ks;
     p.lg_lpr = pl.lg_lpr;
+    p.xcd_tiles = pl.lpr > 1 && tiles % 8 == 0;
     const dim3 grid(static_cast<uint32_t>(tiles * pl.lpr)), block(64 * pl.ks * nmat);
     // Held prologue input: eight values per lane when one chunk per wavefront covers the
     // input, else sixteen in up to two chunks (each chunk's block reductions are a fixed
