@@ -56,6 +56,12 @@ PREFILL_VALU_PER_BLOCK = 440
 PREFILL_OPS_PER_BLOCK = 2 * 32 * 64 * 128
 ENGINE_HZ = 2.4e9
 CUS = 256
+# HBM traffic of the decode step's dominant kernel, per dispatch of each launch family:
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB as counted) over eager decode steps, and
+# the bytes one counted KiB stands for in a plain 256 MiB device copy
+# (profiles/decode_projection_traffic.md).
+DECODE_TRAFFIC_KIB = {"qkv": (833.0, 12.0), "o": (581.1, 8.0)}
+COPY_FETCH_BYTES_PER_KIB, COPY_WRITE_BYTES_PER_KIB = 2047.81, 1024.0
 
 
 def log(msg: str) -> None:
@@ -196,8 +202,14 @@ def decode_roofline(d: dict) -> dict:
     dom = d["dominant"]
     t = dom["avg_launch_us"] * 1e-6
     achieved = dom["bytes_per_launch"] / t / 1e9
+    fams = [f["family"] for f in dom["families"]]
+    traffic = None
+    if all(f in DECODE_TRAFFIC_KIB for f in fams):
+        traffic = round(sum(DECODE_TRAFFIC_KIB[f][0] * COPY_FETCH_BYTES_PER_KIB +
+                            DECODE_TRAFFIC_KIB[f][1] * COPY_WRITE_BYTES_PER_KIB for f in fams) / len(fams))
     return {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(achieved * 1e9 / PEAK_HBM, 4), "traffic": None, "kernel": dom["kernel"],
+            "frac": round(achieved * 1e9 / PEAK_HBM, 4), "traffic": traffic,
+            "traffic_unit": "bytes per launch (mean over the families; counted, not live)", "kernel": dom["kernel"],
             "families": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in f.items()}
                          for f in dom["families"]],
             "bytes_per_launch": round(dom["bytes_per_launch"]), "avg_launch_us": round(dom["avg_launch_us"], 3),
