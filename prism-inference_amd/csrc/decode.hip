@@ -84,6 +84,24 @@ __device__ int norm_rope_pair(float x, float w, float c, float sn, uint32_t rope
     return e;
 }
 
+// Workgroups go to the eight XCDs round-robin in dispatch order (x fastest), each XCD with
+// its own L2.  Workgroups of one "unit" read the same cached rows (the query heads of a KV
+// head, and the value slices that share a 128-byte row segment).  When the units divide
+// by eight, workgroup b takes member (b/8) % members of unit b%8 + 8*((b/8)/members), so a
+// unit's workgroups share one XCD and its rows are fetched into one L2; otherwise the
+// plain order stands (false).  The grid holds units * members workgroups; members is a
+// power of two (the shifts keep integer division off every workgroup's first steps).
+__device__ __forceinline__ bool xcd_unit(uint32_t units, uint32_t lg_members, uint32_t &unit, uint32_t &member) {
+    if (units % 8 != 0) return false;
+    const uint32_t b = blockIdx.x + gridDim.x * blockIdx.y;
+    const uint32_t k = b >> 3;
+    unit = (b & 7u) + ((k >> lg_members) << 3);
+    member = k & ((1u << lg_members) - 1u);
+    return true;
+}
+
+__device__ __forceinline__ bool pow2(uint32_t v) { return v != 0 && (v & (v - 1u)) == 0; }
+
 // Grid (heads, ceil(max_tokens / kScoreChunk)), 256 threads.  Each workgroup
 // normalizes and rotates its query head and its KV head's current key, the first
 // workgroup of every KV head appends the current key and value to the binary16
@@ -95,8 +113,15 @@ __device__ int norm_rope_pair(float x, float w, float c, float sn, uint32_t rope
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
     __shared__ float hv[2][kHead], tmp[2][kHead];  // [0] query, [1] current key
     __shared__ double red[4];
-    const uint32_t tid = threadIdx.x, h = blockIdx.x, chunk = blockIdx.y;
-    const uint32_t group = p.heads / p.kv_heads, kh = h / group;
+    const uint32_t tid = threadIdx.x, group = p.heads / p.kv_heads;
+    uint32_t h = blockIdx.x, chunk = blockIdx.y, unit, member;
+    const uint32_t lg_kv = __builtin_ctz(p.kv_heads), lg_group = __builtin_ctz(group);
+    if (pow2(p.kv_heads) && pow2(group) && xcd_unit(p.kv_heads * gridDim.y, lg_group, unit, member)) {
+        // unit: (KV head, chunk)
+        h = ((unit & (p.kv_heads - 1u)) << lg_group) + member;
+        chunk = unit >> lg_kv;
+    }
+    const uint32_t kh = h / group;
     const uint32_t qw = p.heads * kHead, kw = p.kv_heads * kHead;
     // Every load that does not need the position is issued before the position itself
     // is waited for: the normalization's inputs first (memory counters complete in issue
@@ -201,8 +226,19 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     __shared__ double acc[16][kValueDims];
     constexpr uint32_t nw = 16;  // wavefronts of the 1024-thread workgroup
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kValueDims;
-    const uint32_t kh = h / (p.heads / p.kv_heads), kw = p.kv_heads * kHead;
+    // Unit: (KV head, 128-byte segment of its value rows), whose kLineSlices slices the
+    // group's query heads all read.
+    constexpr uint32_t kSlices = kHead / kValueDims, kLineSlices = 128 / (2 * kValueDims);
+    static_assert((kSlices / kLineSlices) == 2 && kLineSlices == 4, "unit geometry below");
+    const uint32_t group = p.heads / p.kv_heads;
+    uint32_t h = blockIdx.x, slice = blockIdx.y, unit, member;
+    const uint32_t lg_group = __builtin_ctz(group);
+    if (pow2(group) && xcd_unit(p.kv_heads * 2u, lg_group + 2u, unit, member)) {
+        h = ((unit >> 1) << lg_group) + (member & (group - 1u));
+        slice = ((unit & 1u) << 2) + (member >> lg_group);
+    }
+    const uint32_t d0 = slice * kValueDims;
+    const uint32_t kh = h / group, kw = p.kv_heads * kHead;
     const uint32_t last = p.max_tokens - 1;
     const float *sc = p.scores + static_cast<size_t>(h) * p.max_tokens;
     float sv[SPT];
@@ -244,7 +280,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     m = redf[0];
     for (uint32_t v = 1; v < nw; ++v) m = fmaxf(m, redf[v]);
     if (__syncthreads_or(bad) || !finite(m)) {
-        if (tid == 0 && blockIdx.y == 0 && ok) raise_error(p.err, kErrNonfinite);
+        if (tid == 0 && slice == 0 && ok) raise_error(p.err, kErrNonfinite);
         return;
     }
     double tot = 0.0;
