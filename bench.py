@@ -310,12 +310,49 @@ def calibrate_copy(nbytes: int = 256 << 20, reps: int = 10) -> int:
     return 0
 
 
+def bench_launch_floor(ctx: ph.Context, launches: int = 400) -> dict:
+    """The smallest kernel of the library (Q8_0 quantization of one 32-value block, one
+    wavefront), launched back to back on the library stream and timed with HIP events:
+    eagerly as the matvec extras are, and replayed from a captured HIP graph.  What a
+    dependent launch costs before any work."""
+    x = hiprt.DeviceBuffer.from_numpy(synth.activations(32, seed=3))
+    out = hiprt.DeviceBuffer(40)
+    stream = ctx.stream()
+
+    def launch():
+        ctx.quantize_q8_device(x, 32, 1, ph.Q8_SOURCE, out, stream)
+
+    def timed(run) -> float:
+        e0, e1 = hiprt.Event(), hiprt.Event()
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        e1.synchronize()
+        assert ctx.sync() == 0
+        return e0.elapsed_ms(e1) * 1e3
+
+    for _ in range(8):
+        launch()
+    assert ctx.sync() == 0
+    eager = timed(lambda: [launch() for _ in range(launches)]) / launches
+    chunk = 50
+    g = hiprt.Graph(stream, lambda: [launch() for _ in range(chunk)])
+    g.launch()
+    graph = timed(lambda: [g.launch() for _ in range(launches // chunk)]) / (launches // chunk * chunk)
+    del g
+    return {"kernel": "k_quantize_q8_0 (32 inputs, one wavefront)", "eager_us": eager, "graph_us": graph,
+            "launches": launches}
+
+
 # ---- configs 0 and 4: batch-1 matvec and skinny batches --------------------------------
 
 def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launches: int = 200, tokens: int = 1):
     """Per-launch duration of one matvec kernel (prepared Q8_K/Q8_0 activations of `tokens`
-    tokens already in HBM), bracketed by HIP events on the library stream, weights rotated
-    over >= 1 GiB.  tokens > 1 is the skinny batch: each weight byte is read once per launch."""
+    tokens already in HBM), weights rotated over >= 1 GiB: HIP graphs that launch it once
+    per weight copy, replayed until at least `launches` launches, bracketed by HIP events on
+    the library stream (`avg_us`); and the same launches issued one by one from the host
+    (`eager_us`, which for small matrices measures the launch path more than the GPU).
+    tokens > 1 is the skinny batch: each weight byte is read once per launch."""
     w = synth.weights(kind, rows, cols, seed=7)
     copies = max(2, math.ceil(ROTATE_BYTES / w.size))
     rot = Rotation(ctx, kind, rows, cols, w, copies)
@@ -334,19 +371,40 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
     for i in range(min(copies, 8)):
         ctx.project_device(rot.ids[i], path, act, tokens, False, out, stream)
     assert ctx.sync() == 0
-    e0, e1 = hiprt.Event(), hiprt.Event()
-    e0.record(stream)
-    for i in range(launches):
-        ctx.project_device(rot.ids[i % copies], path, act, tokens, False, out, stream)
-    e1.record(stream)
-    e1.synchronize()
-    assert ctx.sync() == 0
-    t = e0.elapsed_ms(e1) / launches * 1e-3
+
+    def timed(run, n) -> float:
+        e0, e1 = hiprt.Event(), hiprt.Event()
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        e1.synchronize()
+        assert ctx.sync() == 0
+        return e0.elapsed_ms(e1) / n * 1e-3
+
+    def eager():
+        for i in range(launches):
+            ctx.project_device(rot.ids[i % copies], path, act, tokens, False, out, stream)
+
+    t_eager = timed(eager, launches)
+    # One pass launches every copy once, 100 launches per graph.
+    graphs = [hiprt.Graph(stream, lambda ids=rot.ids[g0:g0 + 100]: [
+        ctx.project_device(i, path, act, tokens, False, out, stream) for i in ids]) for g0 in range(0, copies, 100)]
+    passes = max(1, math.ceil(launches / copies))
+
+    def replay():
+        for _ in range(passes):
+            for g in graphs:
+                g.launch()
+
+    for g in graphs:
+        g.launch()
+    t = timed(replay, passes * copies)
+    del graphs
     nbytes = w.size + (act_bytes + 4 * rows) * tokens
     rot.release(ctx)
     return {"kind": kind, "rows": rows, "cols": cols, "tokens": tokens, "bytes_per_launch": int(nbytes),
-            "copies": copies, "avg_us": t * 1e6, "us_per_token": t * 1e6 / tokens, "GBps": nbytes / t / 1e9,
-            "frac_hbm": nbytes / t / PEAK_HBM}
+            "copies": copies, "launches": passes * copies, "avg_us": t * 1e6, "eager_us": t_eager * 1e6,
+            "us_per_token": t * 1e6 / tokens, "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM}
 
 
 # ---- config 2: the tiled prefill GEMM ----------------------------------------------------
@@ -466,6 +524,7 @@ def main() -> int:
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
+    ap.add_argument("--floor-only", action="store_true", help="time only the launch floor")
     ap.add_argument("--decode-eager", action="store_true",
                     help="time only decode steps launched kernel by kernel (no graph), for kernel traces")
     args = ap.parse_args()
@@ -480,7 +539,7 @@ def main() -> int:
         return calibrate_copy()
     ctx = ph.Context(0)
     log(ctx.identity)
-    if args.prefill_only or args.matvec_only or args.ffn_only:
+    if args.prefill_only or args.matvec_only or args.ffn_only or args.floor_only:
         for spec in filter(None, args.prefill_only.split(",")):
             M, _, contract = spec.partition(":")  # "2048" or "2048:pinned"
             print(json.dumps(bench_prefill(ctx, int(M), pinned=contract == "pinned")), flush=True)
@@ -489,6 +548,8 @@ def main() -> int:
             print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols, tokens=tok[0] if tok else 1)), flush=True)
         if args.ffn_only:
             print(json.dumps(bench_ffn(ctx)), flush=True)
+        if args.floor_only:
+            print(json.dumps(bench_launch_floor(ctx)), flush=True)
         ctx.close()
         return 0
     t0 = time.perf_counter()
@@ -518,6 +579,9 @@ def main() -> int:
             r = bench_matvec_kernel(ctx, kind, rows, cols, launches=100)
             log(f"matvec kind={kind} {rows}x{cols}: {r['avg_us']:.2f} us, {r['GBps']:.1f} GB/s")
             extras["matvec"].append(r)
+        extras["launch_floor"] = bench_launch_floor(ctx)
+        log(f"launch floor: {extras['launch_floor']['eager_us']:.2f} us eager, "
+            f"{extras['launch_floor']['graph_us']:.2f} us in a graph")
         extras["skinny_batch"] = []
         for kind, rows, cols in [(ph.KIND_PTQ1, 12288, 4096), (ph.KIND_Q2_K, 12288, 4096), (ph.KIND_Q8_0, 12288, 4096),
                                  (ph.KIND_PTQ1, 151936, 4096), (ph.KIND_Q2_K, 151936, 4096),
