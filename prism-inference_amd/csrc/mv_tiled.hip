@@ -1879,10 +1879,13 @@ struct QuadChain {
 };
 
 // One unit of one row into the four chains.  `qa` holds the unit's 32 activation dwords
-// of the lane's token (l%4), `qs` the unit's token scales as [group][token].
-template <Op O>
+// of the lane's token (l%4), `qs` the unit's token scales as [group][token].  TERMS
+// (source PTQ1 only): ch.o[t] receives the unit's term of token t instead, for a chain
+// folded elsewhere.
+template <Op O, bool TERMS = false>
 __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, const float *qs, uint32_t lbase,
                                           QuadChain<O> &ch) {
+    static_assert(!TERMS || O == Op::PTQ1_SRC, "one term per unit and token");
     uint32_t A[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -1946,7 +1949,10 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
                 float tt = 0.0f;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) tt = tt + S[g][t] * static_cast<float>(acc[g][t]);
-                ch.o[t] = ch.o[t] + d * tt;
+                if constexpr (TERMS)
+                    ch.o[t] = d * tt;
+                else
+                    ch.o[t] = ch.o[t] + d * tt;
             }
         } else {
             // dot_legacy, src/kernels.rs:1241-1244; the row's chain adds the four group
@@ -1965,21 +1971,12 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
 // LDS bytes per unit: the four tokens' codes, then their 16 scales.
 constexpr uint32_t kQuadUnitLds = (kQuadTok * kQuadRowDw + 4 * kQuadTok) * sizeof(uint32_t);
 
-// 2..4 tokens of prepared Q8_0 blocks (token t at act + t * act_stride bytes, outputs
-// and residual at t * rows).  The workgroup stages every token's activation codes in
-// LDS ([unit][token][36] dwords; PTQ1 codes in the decode's slot order) and their
-// scales ([unit][group][token] floats) once; its wavefronts then walk 64-row tiles as
-// the batch-1 row kernel does.
+// The workgroup's staging of 2..4 tokens' prepared Q8_0 blocks (token t at act + t *
+// act_stride bytes; missing tokens repeat the last): codes as [unit][token][36 dwords]
+// (PTQ1 in ptq1_slots_lut's slot order), scales as [unit][group][token] floats.
 template <Op O>
-__global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const void *__restrict__ act,
-                                                              uint32_t act_stride, uint32_t ntok) {
-    extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
-    constexpr uint32_t UB = unit_bytes<O>();
-    constexpr uint32_t kWaves = quad_threads<O>() / 64;
-    const uint32_t nu = p.nu;
-    uint32_t *codes = quad_lds;
-    float *scales = reinterpret_cast<float *>(quad_lds + nu * kQuadTok * kQuadRowDw);
-    if constexpr (kind_of<O>() == kPTQ1) ptq1_lut_fill(threadIdx.x, blockDim.x);
+__device__ __forceinline__ void quad_stage(const void *__restrict__ act, uint32_t act_stride, uint32_t ntok,
+                                           uint32_t nu, uint32_t *codes, float *scales) {
     for (uint32_t i = threadIdx.x; i < nu * 128u; i += blockDim.x) {
         const uint32_t dw = i & 7u, t = (i >> 3) & 3u, g = (i >> 5) & 3u, u = i >> 7;
         const Q8Block *blk = reinterpret_cast<const Q8Block *>(static_cast<const uint8_t *>(act) +
@@ -1997,6 +1994,24 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
         }
         if (dw == 0) scales[(u * 4 + g) * kQuadTok + t] = blk->scale;
     }
+}
+
+// 2..4 tokens of prepared Q8_0 blocks (token t at act + t * act_stride bytes, outputs
+// and residual at t * rows).  The workgroup stages every token's activation codes in
+// LDS ([unit][token][36] dwords; PTQ1 codes in the decode's slot order) and their
+// scales ([unit][group][token] floats) once; its wavefronts then walk 64-row tiles as
+// the batch-1 row kernel does.
+template <Op O>
+__global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const void *__restrict__ act,
+                                                              uint32_t act_stride, uint32_t ntok) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
+    constexpr uint32_t UB = unit_bytes<O>();
+    constexpr uint32_t kWaves = quad_threads<O>() / 64;
+    const uint32_t nu = p.nu;
+    uint32_t *codes = quad_lds;
+    float *scales = reinterpret_cast<float *>(quad_lds + nu * kQuadTok * kQuadRowDw);
+    if constexpr (kind_of<O>() == kPTQ1) ptq1_lut_fill(threadIdx.x, blockDim.x);
+    quad_stage<O>(act, act_stride, ntok, nu, codes, scales);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2039,6 +2054,72 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
                     if (!finite(o)) raise_error(p.err, kErrNonfinite);
                 }
             }
+        }
+    }
+}
+
+// Matrices of fewer tiles than CUs (source PTQ1, 2..4 tokens): one 1024-thread workgroup
+// per 64-row tile.  Its wavefronts take the tile's units round-robin, each unit decoded
+// once for all tokens as in k_mv_quad, and leave every (unit, token, row) term in LDS;
+// after one barrier, 256 threads fold the 64 rows x 4 tokens chains in unit order, so each
+// output is its batch-1 chain, only computed later.  LDS: the table, the staged codes
+// and scales, and the terms ([unit][token][row] floats).
+constexpr uint32_t kQuadSplitThreads = 1024;
+constexpr uint32_t kQuadSplitUnitLds = kQuadUnitLds + kQuadTok * kTile * sizeof(float);
+constexpr uint32_t kQuadSplitMaxUnits = 56;  // with the 64 KiB table, at most 155 KiB of LDS
+
+__global__ __launch_bounds__(kQuadSplitThreads) void k_mv_quad_split(MvParams p, const void *__restrict__ act,
+                                                                    uint32_t act_stride, uint32_t ntok) {
+    constexpr Op O = Op::PTQ1_SRC;
+    constexpr uint32_t UB = unit_bytes<O>();
+    extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
+    const uint32_t nu = p.nu;
+    uint32_t *codes = quad_lds;
+    float *scales = reinterpret_cast<float *>(quad_lds + nu * kQuadTok * kQuadRowDw);
+    float *terms = scales + nu * 4 * kQuadTok;
+    ptq1_lut_fill(threadIdx.x, blockDim.x);
+    quad_stage<O>(act, act_stride, ntok, nu, codes, scales);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nwaves = kQuadSplitThreads / 64;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t left = p.rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const uint32_t row_bytes = nu * UB;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    const uint32_t lbase = 8u * (lane & 31u);
+    const uint32_t *qa = codes + (lane & 3u) * kQuadRowDw;
+    auto step = [&](const Raw<O> &w, uint32_t u) {
+        QuadChain<O> ch;
+        quad_unit<O, true>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, ch);
+#pragma unroll
+        for (uint32_t t = 0; t < kQuadTok; ++t) terms[(u * kQuadTok + t) * kTile + lane] = ch.o[t];
+    };
+    Raw<O> A, B;
+    uint32_t u = wave;
+    if (u < nu) load_unit<O>(A, rs, u * trp * UB, trp, lane);
+    while (u + nwaves < nu) {
+        load_unit<O>(B, rs, (u + nwaves) * trp * UB, trp, lane);
+        step(A, u);
+        if (u + 2 * nwaves < nu) load_unit<O>(A, rs, (u + 2 * nwaves) * trp * UB, trp, lane);
+        step(B, u + nwaves);
+        u += 2 * nwaves;
+    }
+    if (u < nu) step(A, u);
+    __syncthreads();
+    if (threadIdx.x < kQuadTok * kTile) {
+        const uint32_t t = threadIdx.x >> 6, r = threadIdx.x & 63u;
+        if (t < ntok && r < trows) {
+            // dot_q8_groups' row chain, src/kernels.rs:1043-1064: ((0 + t_0) + t_1) + ...
+            float o = 0.0f;
+            for (uint32_t v = 0; v < nu; ++v) o = o + terms[(v * kQuadTok + t) * kTile + r];
+            const size_t at = static_cast<size_t>(t) * p.rows + static_cast<size_t>(tile) * kTile + r;
+            if (p.residual) o = o + p.residual[at];
+            p.out[at] = o;
+            if (!finite(o)) raise_error(p.err, kErrNonfinite);
         }
     }
 }
@@ -2415,11 +2496,19 @@ int launch_lut_batch(const MatvecArgs &a, uint32_t act_stride) {
 }
 
 // Two to four tokens of a large PTQ1 (Q8_0 activations) or Q8_0 matrix run on the 4x4x4
-// matrix cores: one row per lane and each unit decoded once, as at batch 1.
+// matrix cores: one row per lane and each unit decoded once, as at batch 1.  Source PTQ1
+// from two tiles per CU (measured at 4096 columns and 4 tokens: 40960 rows 31.8 us against
+// 33.1 split per tile and 38.0 on the skinny kernel); the other orders from 65536 rows.
 bool quad_eligible(const MatvecArgs &a) {
-    if (a.w2 || a.tokens < 2 || a.tokens > kQuadTok || a.act_format == kActF32) return false;
-    if (a.cols > kQuadMaxCols || a.rows < kBatchMinRows) return false;
-    return dispatch(a, [&]<Op O>() { return quad_supported<O>() ? 1 : 0; }) == 1;
+    if (a.w2 || a.tokens < 2 || a.tokens > kQuadTok || a.act_format == kActF32 || a.cols > kQuadMaxCols)
+        return false;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    return dispatch(a, [&]<Op O>() {
+               if constexpr (!quad_supported<O>())
+                   return 0;
+               else
+                   return a.rows >= kBatchMinRows || (O == Op::PTQ1_SRC && tiles > 2ull * a.cus) ? 1 : 0;
+           }) == 1;
 }
 
 template <Op O>
@@ -2449,8 +2538,38 @@ int launch_quad(const MatvecArgs &a, uint32_t act_stride) {
     }
 }
 
+// Source PTQ1, two to four tokens, from 3/8 of a tile per CU up to two tiles per CU: one
+// workgroup per tile, its units split over 16 wavefronts.  Measured at 4 tokens against
+// the skinny kernel (us): 6144x2048 8.0 / 8.9, 12288x4096 12.1 / 19.4, 16384x4096 12.7 /
+// 22.4, 24576x4096 22.9 / 27.3; smaller matrices keep the skinny kernel (2048x2048 6.1
+// against 7.7: the table and the staging are a fixed cost per tile).
+bool quad_split_eligible(const MatvecArgs &a) {
+    if (a.w2 || a.tokens < 2 || a.tokens > kQuadTok || a.act_format == kActF32) return false;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    if (tiles * 8 < 3ull * a.cus || tiles > 2ull * a.cus) return false;
+    if (a.cols / unit_weights<Op::PTQ1_SRC>() > kQuadSplitMaxUnits) return false;
+    return dispatch(a, [&]<Op O>() { return O == Op::PTQ1_SRC ? 1 : 0; }) == 1;
+}
+
+int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
+    MvParams p{};
+    p.w[0] = p.w[1] = a.w;
+    p.rows = static_cast<uint32_t>(a.rows);
+    p.nu = static_cast<uint32_t>(a.cols / unit_weights<Op::PTQ1_SRC>());
+    p.cols = static_cast<uint32_t>(a.cols);
+    p.out = a.out;
+    p.residual = a.residual;
+    p.err = a.err;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    hipLaunchKernelGGL(k_mv_quad_split, dim3(static_cast<uint32_t>(tiles)), dim3(kQuadSplitThreads),
+                       static_cast<size_t>(p.nu) * kQuadSplitUnitLds, a.stream, p, a.act, act_stride, a.tokens);
+    return launch_status();
+}
+
 bool skinny_eligible(const MatvecArgs &a) {
-    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a) || quad_eligible(a)) return false;
+    if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a) || quad_eligible(a) ||
+        quad_split_eligible(a))
+        return false;
     // Pinned PTQ1 (four masked MFMAs per group) on large matrices: up to four tokens the
     // row-tile batch kernel is faster (151936x4096 x 4: 148 against 165 us), from 16 the
     // skinny kernel (171 against 558 us).
@@ -2466,6 +2585,7 @@ int launch_matvec_tiled(const MatvecArgs &a) {
                                                        : sizeof(Q8Block) * (a.cols / 32);
     if (a.act_format != kActF32 && quad_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_quad<O>(a, static_cast<uint32_t>(in_stride)); });
+    if (a.act_format != kActF32 && quad_split_eligible(a)) return launch_quad_split(a, static_cast<uint32_t>(in_stride));
     if (a.act_format != kActF32 && lut_batch_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_lut_batch<O>(a, static_cast<uint32_t>(in_stride)); });
     if (a.act_format != kActF32 && skinny_eligible(a)) {
@@ -2519,7 +2639,9 @@ size_t tiled_scratch_bytes(const MatvecArgs &a) {
 }
 
 bool tiled_needs_prepared(const MatvecArgs &a) {
-    if (quad_eligible(a) || lut_batch_eligible(a) || skinny_eligible(a) || batch_eligible(a)) return true;
+    if (quad_eligible(a) || quad_split_eligible(a) || lut_batch_eligible(a) || skinny_eligible(a) ||
+        batch_eligible(a))
+        return true;
     return dispatch(a, [&]<Op O>() { return op_needs_prepared<O>(a) ? 1 : 0; }) == 1;
 }
 

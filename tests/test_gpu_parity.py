@@ -416,14 +416,20 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
 
 @pytest.mark.parametrize("kind,cols,rows", [(ph.KIND_PTQ1, 128, 65536 + 37), (ph.KIND_PTQ1, 640, 65536 + 37),
                                             (ph.KIND_PTQ1, 384, 131072 + 5), (ph.KIND_Q8_0, 128, 65536 + 37),
-                                            (ph.KIND_Q8_0, 640, 65536 + 1), (ph.KIND_Q8_0, 384, 131072 + 63)])
+                                            (ph.KIND_Q8_0, 640, 65536 + 1), (ph.KIND_Q8_0, 384, 131072 + 63),
+                                            (ph.KIND_PTQ1, 128, 6144 + 37), (ph.KIND_PTQ1, 640, 8192 + 1),
+                                            (ph.KIND_PTQ1, 4096, 6144 + 11), (ph.KIND_PTQ1, 7168, 6144),
+                                            (ph.KIND_PTQ1, 384, 32768 + 77), (ph.KIND_Q8_0, 640, 6144 + 53)])
 def test_gpu_quad_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     """Two to four tokens of a large PTQ1 or Q8_0 matrix run on the 4x4x4 int8 matrix
     cores, one row per lane (tokens on the A side, the lane's row on the B side); with
-    fewer than four tokens the last one is repeated and not stored.  Every token's row
-    must equal its own matvec in both contracts, through the f32 entry and through
-    prepared blocks of each Q8_0 contract, with a partial last tile and an odd unit
-    count."""
+    fewer than four tokens the last one is repeated and not stored.  Source PTQ1 takes that
+    kernel from two tiles per CU (513 tiles here) and, from 3/8 of a tile per CU, splits
+    each tile's units over a workgroup's wavefronts and folds the per-unit terms from LDS
+    (up to 56 units per row; pinned PTQ1 and Q8_0 take the skinny kernel below 65536 rows).
+    Every token's row must equal its own matvec in both contracts, through
+    the f32 entry and through prepared blocks of each Q8_0 contract, with a partial last
+    tile and an odd unit count."""
     import oracle
 
     w = synth.weights(kind, rows, cols, seed=43)
