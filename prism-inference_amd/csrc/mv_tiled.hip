@@ -771,9 +771,14 @@ __global__ __launch_bounds__(128) void k_mv_rows2(MvParams p, uint32_t stride) {
 // and take whole tiles (measured: splitting nine tiles per CU in two rounds was slower).
 constexpr uint32_t kLutThreads = 1024;
 constexpr uint32_t kLutWaves = kLutThreads / 64;
-// SPLIT (single-term formats, at most kLutSlots tiles per workgroup and 64 units per
-// row, lut_split()): the two-wavefront halves; otherwise whole tiles.
+// Modes (single-term formats for the split ones, at most 64 units per row):
+// kLutWhole: every wavefront takes whole tiles round-robin.  kLutSplit (at most kLutSlots
+// tiles per workgroup, lut_split()): the two-wavefront halves above.  kLutTail (8 to 12
+// tiles per CU, lut_tail()): wavefronts 0..7 take one whole tile each, and wavefronts 8..15
+// take the remaining tiles as split pairs, so the last round of tiles costs half a tile
+// on the busiest SIMD instead of a whole one.
 constexpr uint32_t kLutSlots = kLutWaves / 2;
+constexpr int kLutWhole = 0, kLutSplit = 1, kLutTail = 2;
 template <Op O>
 __host__ __device__ constexpr bool lut_can_split() {
     return terms_per_unit<O>() == 1;
@@ -781,7 +786,10 @@ __host__ __device__ constexpr bool lut_can_split() {
 __host__ __device__ inline bool lut_split(uint32_t tiles, uint32_t grid, uint32_t nu) {
     return tiles <= kLutSlots * grid && nu - (nu + 1) / 2 <= 32;
 }
-template <Op O, bool SPLIT>
+__host__ __device__ inline bool lut_tail(uint32_t tiles, uint32_t grid, uint32_t nu) {
+    return tiles > 8 * grid && tiles <= 12 * grid && nu - (nu + 1) / 2 <= 32;
+}
+template <Op O, int MODE>
 __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const void *__restrict__ act) {
     ptq1_lut_fill(threadIdx.x, blockDim.x);
     __syncthreads();
@@ -789,10 +797,39 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t tiles = (p.rows + kTile - 1) / kTile;
     const uint32_t lbase = 8u * (lane & 31u);
-    if constexpr (!SPLIT) {
+    if constexpr (MODE == kLutWhole) {
         const uint32_t step = gridDim.x * kLutWaves;
         for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += step)
             rows_tile<O, true>(p, act, tile, lane, lbase);
+    } else if constexpr (MODE == kLutTail) {
+        static_assert(lut_can_split<O>(), "single-term formats only");
+        __shared__ float second[4][kTile][33];  // terms of a tail tile's second half (<= 32 units)
+        const uint32_t nh = (p.nu + 1) / 2;
+        const uint32_t slot = (wave - 8) >> 1, half = wave & 1u;
+        const uint32_t tile = wave < 8 ? wave * gridDim.x + blockIdx.x : 8 * gridDim.x + slot * gridDim.x + blockIdx.x;
+        const bool active = tile < tiles;
+        Chain<O> ch;
+        if (wave < 8) {
+            rows_tile<O, true>(p, act, tile, lane, lbase);  // tile < 8 * gridDim.x < tiles
+        } else if (active) {
+            if (half == 0)
+                rows_part<O, true>(p, act, tile, lane, lbase, 0, nh, ch, nullptr);
+            else
+                rows_part<O, true>(p, act, tile, lane, lbase, nh, p.nu, ch, second[slot][lane]);
+        }
+        __syncthreads();  // every wavefront reaches this one barrier
+        if (wave >= 8 && active && half == 0) {
+            const float *t = second[slot][lane];
+            for (uint32_t u = nh; u < p.nu; ++u) ch.fold(t + (u - nh), act, u);
+            const uint32_t left = p.rows - tile * kTile;
+            if (lane < (left < kTile ? left : kTile)) {
+                const size_t row = static_cast<size_t>(tile) * kTile + lane;
+                float o = ch.result();
+                if (p.residual) o = o + p.residual[row];
+                p.out[row] = o;
+                if (!finite(o)) raise_error(p.err, kErrNonfinite);
+            }
+        }
     } else {
         static_assert(lut_can_split<O>(), "single-term formats only");
         __shared__ float second[kLutSlots][kTile][33];  // terms of a tile's second half (<= 32 units)
@@ -2216,11 +2253,17 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     p.q8_contract = a.q8_contract;
     if (!quant && nmat == 1 && tiles >= a.cus) {
         if constexpr (kind_of<O>() == kPTQ1) {
+            constexpr int kSplitMode = lut_can_split<O>() ? kLutSplit : kLutWhole;
+            constexpr int kTailMode = lut_can_split<O>() ? kLutTail : kLutWhole;
             if (lut_can_split<O>() && lut_split(static_cast<uint32_t>(tiles), a.cus, nu))
-                hipLaunchKernelGGL((k_mv_rows_lut<O, lut_can_split<O>()>), dim3(a.cus), dim3(kLutThreads), 0,
-                                   a.stream, p, act);
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kSplitMode>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p,
+                                   act);
+            else if (lut_can_split<O>() && lut_tail(static_cast<uint32_t>(tiles), a.cus, nu))
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kTailMode>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p,
+                                   act);
             else
-                hipLaunchKernelGGL((k_mv_rows_lut<O, false>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p, act);
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutWhole>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p,
+                                   act);
             return launch_status();
         }
         if constexpr (O != Op::PTQ1_PINNED) {

@@ -292,12 +292,13 @@ def test_gpu_row_tile_path_matches_oracle(ctx, kind, cols):
     ctx.release(wid)
 
 
-@pytest.mark.parametrize("per_cu", [5, 16])
+@pytest.mark.parametrize("per_cu", [5, 9, 16])
 @pytest.mark.parametrize("cols", [128, 384, 1024])
 def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
     """PTQ1 on the row-tile path decodes trits through the LDS table, one workgroup per
     CU working through its tiles: 5-6 tiles per workgroup (each tile's units split over
-    two wavefronts) or 16-17 (whole tiles, some wavefronts taking two); one unit (an
+    two wavefronts), 9-10 (eight whole tiles per workgroup, the rest as split pairs;
+    single-term orders) or 16-17 (whole tiles, some wavefronts taking two); one unit (an
     empty second half), an odd and an even unit count, a partial last tile, and all
     three activation contracts."""
     import oracle
