@@ -2038,7 +2038,7 @@ __device__ __forceinline__ void quad_stage(const void *__restrict__ act, uint32_
 // LDS ([unit][token][36] dwords; PTQ1 codes in the decode's slot order) and their
 // scales ([unit][group][token] floats) once; its wavefronts then walk 64-row tiles as
 // the batch-1 row kernel does.
-template <Op O>
+template <Op O, bool TAIL = false>
 __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const void *__restrict__ act,
                                                               uint32_t act_stride, uint32_t ntok) {
     extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
@@ -2058,28 +2058,32 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
     const uint32_t row_bytes = nu * UB;
     // Wave-uniform by construction (the buffer descriptors below must live in SGPRs).
     const uint32_t grid = __builtin_amdgcn_readfirstlane(gridDim.x);
-    for (uint32_t tile = wave * grid + blockIdx.x; tile < tiles; tile += grid * kWaves) {
+    // Units [u0, u1) of a tile through step(raw unit, u), two buffers in ping-pong.
+    auto walk = [&](uint32_t tile, uint32_t u0, uint32_t u1, auto &&step) {
         const uint32_t left = p.rows - tile * kTile;
-        const uint32_t trows = left < kTile ? left : kTile;
-        const uint32_t trp = (trows + 7u) & ~7u;
+        const uint32_t trp = ((left < kTile ? left : kTile) + 7u) & ~7u;
         const __amdgpu_buffer_rsrc_t rs =
             make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
-        QuadChain<O> ch;
-        auto step = [&](const Raw<O> &w, uint32_t u) {
-            quad_unit<O>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, ch);
-        };
         Raw<O> A, B;
-        uint32_t u = 0;
-        load_unit<O>(A, rs, 0, trp, lane);
-        while (u + 1 < nu) {
+        uint32_t u = u0;
+        if (u < u1) load_unit<O>(A, rs, u * trp * UB, trp, lane);
+        while (u + 1 < u1) {
             load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
             step(A, u);
-            if (u + 2 < nu) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+            if (u + 2 < u1) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
             step(B, u + 1);
             u += 2;
         }
-        if (u < nu) step(A, u);
-        if (lane < trows) {
+        if (u < u1) step(A, u);
+    };
+    auto chain = [&](QuadChain<O> &ch) {
+        return [&](const Raw<O> &w, uint32_t u) {
+            quad_unit<O>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, ch);
+        };
+    };
+    auto store = [&](uint32_t tile, const QuadChain<O> &ch) {
+        const uint32_t left = p.rows - tile * kTile;
+        if (lane < (left < kTile ? left : kTile)) {
             const size_t row = static_cast<size_t>(tile) * kTile + lane;
 #pragma unroll
             for (uint32_t t = 0; t < kQuadTok; ++t) {
@@ -2091,6 +2095,49 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
                     if (!finite(o)) raise_error(p.err, kErrNonfinite);
                 }
             }
+        }
+    };
+    if constexpr (!TAIL) {
+        for (uint32_t tile = wave * grid + blockIdx.x; tile < tiles; tile += grid * kWaves) {
+            QuadChain<O> ch;
+            walk(tile, 0, nu, chain(ch));
+            store(tile, ch);
+        }
+    } else {
+        // Eight to twelve tiles per workgroup (source PTQ1): wavefronts 0..7 take one whole
+        // tile each; wavefronts 8..15 take the remaining tiles in pairs, the second of a
+        // pair leaving its units' terms in LDS ([slot][unit - nh][token][row]) for the
+        // first, which continues its chains with them in unit order after the barrier.
+        static_assert(O == Op::PTQ1_SRC && kWaves == 16, "single-term order, 16 wavefronts");
+        float *second = scales + nu * 4 * kQuadTok;
+        const uint32_t nh = (nu + 1) / 2, n2 = nu - nh;
+        const uint32_t slot = (wave - 8) >> 1, half = wave & 1u;
+        const uint32_t tile = wave < 8 ? wave * grid + blockIdx.x : 8 * grid + slot * grid + blockIdx.x;
+        const bool active = tile < tiles;
+        QuadChain<O> ch;
+        if (wave < 8) {
+            walk(tile, 0, nu, chain(ch));  // tile < 8 * grid < tiles
+            store(tile, ch);
+        } else if (active) {
+            if (half == 0) {
+                walk(tile, 0, nh, chain(ch));
+            } else {
+                float *mine = second + static_cast<size_t>(slot) * n2 * kQuadTok * kTile;
+                walk(tile, nh, nu, [&](const Raw<O> &w, uint32_t u) {
+                    QuadChain<O> tc;
+                    quad_unit<O, true>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, tc);
+#pragma unroll
+                    for (uint32_t t = 0; t < kQuadTok; ++t) mine[((u - nh) * kQuadTok + t) * kTile + lane] = tc.o[t];
+                });
+            }
+        }
+        __syncthreads();  // every wavefront reaches this one barrier
+        if (wave >= 8 && active && half == 0) {
+            const float *theirs = second + static_cast<size_t>(slot) * n2 * kQuadTok * kTile;
+            for (uint32_t u = 0; u < n2; ++u)
+#pragma unroll
+                for (uint32_t t = 0; t < kQuadTok; ++t) ch.o[t] = ch.o[t] + theirs[(u * kQuadTok + t) * kTile + lane];
+            store(tile, ch);
         }
     }
 }
@@ -2575,6 +2622,18 @@ int launch_quad(const MatvecArgs &a, uint32_t act_stride) {
         // tile per wavefront.
         uint64_t grid = kind_of<O>() == kPTQ1 ? a.cus : (tiles + kWaves - 1) / kWaves;
         if (grid > tiles) grid = tiles;
+        if constexpr (O == Op::PTQ1_SRC) {
+            // Eight to twelve tiles per CU: the last round as split pairs, when their terms
+            // fit LDS beside the table (measured, 151936x4096 x 4 tokens: 49.6 -> see
+            // the tail-mode note in k_mv_quad).
+            const size_t tail_lds =
+                lds + 4 * static_cast<size_t>(p.nu - (p.nu + 1) / 2) * kQuadTok * kTile * sizeof(float);
+            if (tiles > 8ull * a.cus && tiles <= 12ull * a.cus && tail_lds + 64 * 1024 <= 160 * 1024) {
+                hipLaunchKernelGGL((k_mv_quad<O, true>), dim3(a.cus), dim3(quad_threads<O>()), tail_lds, a.stream, p,
+                                   a.act, act_stride, a.tokens);
+                return launch_status();
+            }
+        }
         hipLaunchKernelGGL(k_mv_quad<O>, dim3(static_cast<uint32_t>(grid)), dim3(quad_threads<O>()), lds, a.stream,
                            p, a.act, act_stride, a.tokens);
         return launch_status();
