@@ -2624,8 +2624,8 @@ int launch_quad(const MatvecArgs &a, uint32_t act_stride) {
         if (grid > tiles) grid = tiles;
         if constexpr (O == Op::PTQ1_SRC) {
             // Eight to twelve tiles per CU: the last round as split pairs, when their terms
-            // fit LDS beside the table (measured, 151936x4096 x 4 tokens: 49.6 -> see
-            // the tail-mode note in k_mv_quad).
+            // fit LDS beside the table (measured, 151936x4096: 4 tokens 50.3 -> 46.1 us, 2
+            // tokens 50.1 -> 45.4 us).
             const size_t tail_lds =
                 lds + 4 * static_cast<size_t>(p.nu - (p.nu + 1) / 2) * kQuadTok * kTile * sizeof(float);
             if (tiles > 8ull * a.cus && tiles <= 12ull * a.cus && tail_lds + 64 * 1024 <= 160 * 1024) {
