@@ -771,12 +771,14 @@ __global__ __launch_bounds__(128) void k_mv_rows2(MvParams p, uint32_t stride) {
 // and take whole tiles (measured: splitting nine tiles per CU in two rounds was slower).
 constexpr uint32_t kLutThreads = 1024;
 constexpr uint32_t kLutWaves = kLutThreads / 64;
-// Modes (single-term formats for the split ones, at most 64 units per row):
-// kLutWhole: every wavefront takes whole tiles round-robin.  kLutSplit (at most kLutSlots
-// tiles per workgroup, lut_split()): the two-wavefront halves above.  kLutTail (8 to 12
-// tiles per CU, lut_tail()): wavefronts 0..7 take one whole tile each, and wavefronts 8..15
-// take the remaining tiles as split pairs, so the last round of tiles costs half a tile
-// on the busiest SIMD instead of a whole one.
+// Modes: kLutWhole: every wavefront takes whole tiles round-robin.  kLutSplit (single-term
+// formats, at most kLutSlots tiles per workgroup and 64 units per row, lut_split()): the
+// two-wavefront halves above.  kLutTail (8 to 12 tiles per CU, lut_tail_lds()): wavefronts
+// 0..7 take one whole tile each, and wavefronts 8..15 take the remaining tiles as split
+// pairs, so the last round of tiles costs half a tile on the busiest SIMD instead of a
+// whole one.  Their second halves' terms go to dynamic LDS, 64 rows x lut_tail_stride()
+// floats per pair, beside the 64 KiB table: pinned PTQ1 (nine terms per unit) fits two
+// pairs at 4096 columns, so it takes this form up to ten tiles per CU.
 constexpr uint32_t kLutSlots = kLutWaves / 2;
 constexpr int kLutWhole = 0, kLutSplit = 1, kLutTail = 2;
 template <Op O>
@@ -786,8 +788,18 @@ __host__ __device__ constexpr bool lut_can_split() {
 __host__ __device__ inline bool lut_split(uint32_t tiles, uint32_t grid, uint32_t nu) {
     return tiles <= kLutSlots * grid && nu - (nu + 1) / 2 <= 32;
 }
-__host__ __device__ inline bool lut_tail(uint32_t tiles, uint32_t grid, uint32_t nu) {
-    return tiles > 8 * grid && tiles <= 12 * grid && nu - (nu + 1) / 2 <= 32;
+// Second-half terms per row, odd (no bank conflicts between the rows' lanes).
+template <Op O>
+__host__ __device__ constexpr uint32_t lut_tail_stride(uint32_t nu) {
+    return ((nu - (nu + 1) / 2) * terms_per_unit<O>()) | 1u;
+}
+// Dynamic LDS bytes of the tail form for this launch, 0 where it does not apply.
+template <Op O>
+inline uint32_t lut_tail_lds(uint32_t tiles, uint32_t grid, uint32_t nu) {
+    if (tiles <= 8 * grid || tiles > 12 * grid) return 0;
+    const uint32_t pairs = (tiles - 8 * grid + grid - 1) / grid;
+    const uint32_t bytes = pairs * kTile * lut_tail_stride<O>(nu) * static_cast<uint32_t>(sizeof(float));
+    return bytes + sizeof(g_ptq1_lut) <= 160u * 1024u ? bytes : 0u;
 }
 template <Op O, int MODE>
 __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const void *__restrict__ act) {
@@ -802,12 +814,16 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
         for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += step)
             rows_tile<O, true>(p, act, tile, lane, lbase);
     } else if constexpr (MODE == kLutTail) {
-        static_assert(lut_can_split<O>(), "single-term formats only");
-        __shared__ float second[4][kTile][33];  // terms of a tail tile's second half (<= 32 units)
-        const uint32_t nh = (p.nu + 1) / 2;
+        // Terms of the tail tiles' second halves: pair `slot` at slot * kTile * stride,
+        // row `lane` at lane * stride.  A pair is active only if its tile exists, and the
+        // host sized the buffer for every pair a workgroup can have.
+        extern __shared__ float tail_terms[];
+        constexpr uint32_t TPU = terms_per_unit<O>();
+        const uint32_t nh = (p.nu + 1) / 2, stride = lut_tail_stride<O>(p.nu);
         const uint32_t slot = (wave - 8) >> 1, half = wave & 1u;
         const uint32_t tile = wave < 8 ? wave * gridDim.x + blockIdx.x : 8 * gridDim.x + slot * gridDim.x + blockIdx.x;
         const bool active = tile < tiles;
+        float *mine = tail_terms + (static_cast<size_t>(slot) * kTile + lane) * stride;
         Chain<O> ch;
         if (wave < 8) {
             rows_tile<O, true>(p, act, tile, lane, lbase);  // tile < 8 * gridDim.x < tiles
@@ -815,12 +831,11 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
             if (half == 0)
                 rows_part<O, true>(p, act, tile, lane, lbase, 0, nh, ch, nullptr);
             else
-                rows_part<O, true>(p, act, tile, lane, lbase, nh, p.nu, ch, second[slot][lane]);
+                rows_part<O, true>(p, act, tile, lane, lbase, nh, p.nu, ch, mine);
         }
         __syncthreads();  // every wavefront reaches this one barrier
         if (wave >= 8 && active && half == 0) {
-            const float *t = second[slot][lane];
-            for (uint32_t u = nh; u < p.nu; ++u) ch.fold(t + (u - nh), act, u);
+            for (uint32_t u = nh; u < p.nu; ++u) ch.fold(mine + (u - nh) * TPU, act, u);
             const uint32_t left = p.rows - tile * kTile;
             if (lane < (left < kTile ? left : kTile)) {
                 const size_t row = static_cast<size_t>(tile) * kTile + lane;
@@ -2301,13 +2316,13 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     if (!quant && nmat == 1 && tiles >= a.cus) {
         if constexpr (kind_of<O>() == kPTQ1) {
             constexpr int kSplitMode = lut_can_split<O>() ? kLutSplit : kLutWhole;
-            constexpr int kTailMode = lut_can_split<O>() ? kLutTail : kLutWhole;
+            const uint32_t tail_lds = lut_tail_lds<O>(static_cast<uint32_t>(tiles), a.cus, nu);
             if (lut_can_split<O>() && lut_split(static_cast<uint32_t>(tiles), a.cus, nu))
                 hipLaunchKernelGGL((k_mv_rows_lut<O, kSplitMode>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p,
                                    act);
-            else if (lut_can_split<O>() && lut_tail(static_cast<uint32_t>(tiles), a.cus, nu))
-                hipLaunchKernelGGL((k_mv_rows_lut<O, kTailMode>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p,
-                                   act);
+            else if (tail_lds)
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutTail>), dim3(a.cus), dim3(kLutThreads), tail_lds, a.stream,
+                                   p, act);
             else
                 hipLaunchKernelGGL((k_mv_rows_lut<O, kLutWhole>), dim3(a.cus), dim3(kLutThreads), 0, a.stream, p,
                                    act);

@@ -329,6 +329,36 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("per_cu", [9, 10])
+def test_gpu_ptq1_pinned_table_tail_4096(ctx, per_cu):
+    """Pinned PTQ1 at 4096 columns on the table kernel: nine terms per unit leave room in
+    LDS for two split pairs beside the table, so 9-10 tiles per CU run the last round as
+    split pairs and 10-11 fall back to whole tiles; both must equal the oracle bit for bit
+    (f32 input and both pinned Q8_0 contracts)."""
+    import oracle
+
+    import hiprt
+
+    kind, cols = ph.KIND_PTQ1, 4096
+    cus = hiprt.cu_count(0)
+    rows = 64 * (per_cu * cus + 1) + 21
+    # Every 128-weight unit drawn from a pool of 65536 canonically packed units: rows stay
+    # distinct, and the matrix takes a fraction of the packer's time at this size.
+    pool = synth.weights(kind, 512, 16384, seed=61 + per_cu).reshape(-1, 28)
+    pick = np.random.default_rng(63 + per_cu).integers(0, pool.shape[0], rows * cols // 128)
+    w = pool[pick].reshape(-1)
+    x = synth.activations(cols, seed=62)
+    wid = ctx.weight(kind, cols, rows, w)
+    ref = oracle.matvec(kind, cols, rows, w, x, True, threads=THREADS)
+    assert_bits_equal(ctx.project_f32(wid, rows, x, pinned=True), ref, f"pinned f32 per_cu={per_cu}")
+    for contract in (1, 2):
+        act = oracle.quantize_q8_0(x, contract)
+        ref = oracle.project_q8(kind, cols, rows, w, act, True, threads=THREADS)
+        got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=True)
+        assert_bits_equal(got, ref, f"pinned q8 contract={contract} per_cu={per_cu}")
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("cols", [384, 512])
 @pytest.mark.parametrize("tokens", [2, 3])
 def test_gpu_ptq1_table_batch_matches_per_token_oracle(ctx, cols, tokens):
