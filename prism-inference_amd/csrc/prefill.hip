@@ -27,8 +27,8 @@
 // token, the codes stored as binary16 in operand order and the f32 scales beside them.
 //
 // The pinned contract (dot_q8_groups_pinned) runs k_prefill_ptq1_pinned on the same
-// tiles with its own operand order, four MFMAs per group (one per native lane) and four
-// FMA chains per output; see there.
+// tiles with its own operand order, four K=8 MFMAs per group (one per native lane) and
+// four FMA chains per output; see there.
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "quant_dev.hpp"
@@ -38,6 +38,7 @@ namespace prism {
 
 namespace {
 
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -67,17 +68,20 @@ __host__ __device__ constexpr uint32_t quad_base(uint32_t h, uint32_t g, uint32_
 
 // Pinned order (dot_q8_groups_pinned, src/kernels.rs:1102-1147): the chain needs, per
 // group, the sum over each native lane l's elements 4l..4l+3 and 16+4l..16+4l+3
-// (q8_native_lanes, src/kernels.rs:1066-1076), i.e. quads l and l+4 of the group.  The
-// operand order puts native lane l = 2j + h in K-step j, half h: one MFMA with the other
-// half's weights zeroed then returns I_l exactly.
-__host__ __device__ constexpr uint32_t quad_base_pinned(uint32_t h, uint32_t g, uint32_t j, uint32_t qq) {
-    return 32 * g + 4 * ((2 * j + h) + 4 * qq);
+// (q8_native_lanes, src/kernels.rs:1066-1076), i.e. quads l and l+4 of the group.  One
+// v_mfma_f32_32x32x8_f16 per native lane sums exactly those eight: half h of the
+// wavefront supplies, for both quads, the f16 pair the 16-bit-lane decoder yields for
+// bytes (h, h+2) of the quad, i.e. elements (b+h, b+h+2) of the quad at b.  Pair i of
+// (g, l, h) starts at this element:
+__host__ __device__ constexpr uint32_t pinned_pair_base(uint32_t g, uint32_t l, uint32_t h, uint32_t i) {
+    return 32 * g + 4 * l + 16 * i + h;
 }
 
 // ---- activation prep ------------------------------------------------------------------
 // One wavefront per (token, 1024 inputs): Q8_0 quantization into LDS (the source
 // contract, or the pinned PTQ1 native-scale contract), then the codes leave as binary16
-// in operand order, xh[u][g][j][h][t][8] (u = 128-block, tokens padded to Mp with zeros),
+// in operand order, source xh[u][g][j][h][t][8] and pinned xh[u][g][l][h][t][4] (u =
+// 128-block, tokens padded to Mp with zeros; 256 bytes per block and token either way),
 // and the scales as sc[u][t][g].
 template <bool PINNED>
 __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp, uint32_t K,
@@ -101,24 +105,34 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ 
         }
         __builtin_amdgcn_wave_barrier();
     }
-    // 16 slots (g, j, h) of 16 bytes per block; lane takes slots lane, lane + 64.
-    for (uint32_t s = lane; s < n / 128 * 16; s += 64) {
+    auto code = [&](uint32_t e) -> uint32_t {  // element e's code as binary16 bits
+        const int8_t v = real ? blk[wave][e / 32].values[e % 32] : 0;
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    };
+    if constexpr (PINNED) {
+        // 32 slots (g, l, h) of 8 bytes per block; lane takes slots lane, lane + 64, ...
+        for (uint32_t s = lane; s < n / 128 * 32; s += 64) {
+            const uint32_t ub = s >> 5, g = (s >> 3) & 3u, l = (s >> 1) & 3u, h = s & 1u;
+            const uint32_t u = k0 / 128 + ub;
+            const uint32_t e0 = 128 * ub + pinned_pair_base(g, l, h, 0), e1 = 128 * ub + pinned_pair_base(g, l, h, 1);
+            uint2 *dst = reinterpret_cast<uint2 *>(xh + ((static_cast<size_t>(u) * 32 + (s & 31u)) * Mp + t) * 4);
+            *dst = make_uint2(code(e0) | code(e0 + 2) << 16, code(e1) | code(e1 + 2) << 16);
+        }
+    }
+    // Source: 16 slots (g, j, h) of 16 bytes per block; lane takes slots lane, lane + 64.
+    for (uint32_t s = lane; !PINNED && s < n / 128 * 16; s += 64) {
         const uint32_t ub = s >> 4, g = (s >> 2) & 3u, j = (s >> 1) & 1u, h = s & 1u;
         const uint32_t u = k0 / 128 + ub;
         uint32_t packed[4];
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
-            const uint32_t base = 128 * ub + (PINNED ? quad_base_pinned(h, g, j, qq) : quad_base(h, g, 2 * j + qq));
+            const uint32_t base = 128 * ub + quad_base(h, g, 2 * j + qq);
             const uint32_t el[4] = {base, base + 2, base + 1, base + 3};
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 uint32_t h2 = 0;
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const uint32_t e = el[2 * p + q];
-                    const int8_t v = real ? blk[wave][e / 32].values[e % 32] : 0;
-                    h2 |= static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v))) << (16 * q);
-                }
+                for (int q = 0; q < 2; ++q) h2 |= code(el[2 * p + q]) << (16 * q);
                 packed[2 * qq + p] = h2;
             }
         }
@@ -235,34 +249,49 @@ __device__ __forceinline__ void decode_block(const RawBlock &w, uint32_t h, uint
     }
 }
 
-// The pinned operand order (quad_base_pinned): half h feeds native lane l = h in K-step
-// 0 and l = 2 + h in K-step 1; group g of lane l takes quads l and l + 4, which come
-// from (tools/ternary/src/lib.rs:202-250 element map)
-//   g0: (A_l, 0) (A_l, 1)      g1: (A_l, 2) (A_l, 3)      g2: (A_l, 4) (B_h, l/2)
-//   g3: (B_h, 2 + l/2), then (B_h, 4) for l < 2 or the tail quad 120 + 4h for l >= 2,
-// so half h decodes digits 0..4 of A_h, A_{2+h} and B_h, and one tail quad.
-__device__ __forceinline__ void decode_block_pinned(const RawBlock &w, uint32_t h, uint32_t aw[4][2][4]) {
-    uint32_t alo[5], ahi[5], blo[5], bhi[5], clo[5], chi[5];
-    quads_seq<5>(h ? w.a.y : w.a.x, alo, ahi);  // A_h
-    quads_seq<5>(h ? w.a.w : w.a.z, blo, bhi);  // A_{2+h}
-    quads_seq<5>(h ? w.b.y : w.b.x, clo, chi);  // B_h
-    uint32_t tlo, thi;
-    const uint32_t trep = perm(w.tl, w.tl, sel_bytes(0, 1, 0, 1));
-    quad_at(trep, h ? (9u | (27u << 16)) : (1u | (3u << 16)), tlo, thi);
-    auto put = [&](int g, int j, uint32_t l0, uint32_t h0, uint32_t l1, uint32_t h1) {
-        aw[g][j][0] = l0;
-        aw[g][j][1] = h0;
-        aw[g][j][2] = l1;
-        aw[g][j][3] = h1;
-    };
-    put(0, 0, alo[0], ahi[0], alo[1], ahi[1]);
-    put(0, 1, blo[0], bhi[0], blo[1], bhi[1]);
-    put(1, 0, alo[2], ahi[2], alo[3], ahi[3]);
-    put(1, 1, blo[2], bhi[2], blo[3], bhi[3]);
-    put(2, 0, alo[4], ahi[4], clo[0], chi[0]);
-    put(2, 1, blo[4], bhi[4], clo[1], chi[1]);
-    put(3, 0, clo[2], chi[2], clo[4], chi[4]);
-    put(3, 1, clo[3], chi[3], tlo, thi);
+// The f16 pairs of digits 0..ND-1 of a 16-bit-lane byte pair L (the two bytes, < 256,
+// in the low bytes of its halves), sequentially (remainder times 3).
+template <int ND>
+__device__ __forceinline__ void pairs_seq(uint32_t L, uint32_t *out) {
+#pragma unroll
+    for (int k = 0; k < ND; ++k) {
+        const uint32_t m = L * 3u;
+        out[k] = f16_pair(m);
+        L = m & 0x00ff00ffu;
+    }
+}
+
+// The pinned operand order (pinned_pair_base): for group g and native lane l, half h
+// supplies pair h of quads l and l + 4, which come from (tools/ternary/src/lib.rs:202-250
+// element map; (D, k) = code dword D at digit k)
+//   g0: (A_l, 0) (A_l, 1)      g1: (A_l, 2) (A_l, 3)      g2: (A_l, 4) (B_{l%2}, l/2)
+//   g3: (B_{l%2}, 2 + l/2), then (B_l, 4) for l < 2 or the tail quads 120, 124,
+// so a lane decodes bytes h and h + 2 of every code dword (digits 0..4) and byte 24 + h of
+// the tail (digits 0..3): half of the block's elements, aw[g][l][0..1].
+__device__ __forceinline__ void decode_block_pinned(const RawBlock &w, uint32_t h, uint32_t aw[4][4][2]) {
+    const uint32_t sel = h ? sel_bytes(1, 12, 3, 12) : sel_bytes(0, 12, 2, 12);  // bytes h, h+2
+    uint32_t pa[4][5], pb[2][5];
+    const uint32_t a[4] = {w.a.x, w.a.y, w.a.z, w.a.w}, b[2] = {w.b.x, w.b.y};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) pairs_seq<5>(perm(a[p], a[p], sel), pa[p]);
+#pragma unroll
+    for (int v = 0; v < 2; ++v) pairs_seq<5>(perm(b[v], b[v], sel), pb[v]);
+    // Tail byte 24 + h in both halves at digit multipliers (3^k, 3^(k+1)): the quads at
+    // 120 (digits 0, 1) and 124 (digits 2, 3).
+    const uint32_t tb = perm(w.tl, w.tl, h ? sel_bytes(1, 12, 1, 12) : sel_bytes(0, 12, 0, 12));
+    const uint32_t t0 = f16_pair((pair_mul(tb, 1u | (3u << 16)) & 0x00ff00ffu) * 3u);
+    const uint32_t t1 = f16_pair((pair_mul(tb, 9u | (27u << 16)) & 0x00ff00ffu) * 3u);
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        aw[0][l][0] = pa[l][0];
+        aw[0][l][1] = pa[l][1];
+        aw[1][l][0] = pa[l][2];
+        aw[1][l][1] = pa[l][3];
+        aw[2][l][0] = pa[l][4];
+        aw[2][l][1] = pb[l % 2][l / 2];
+        aw[3][l][0] = pb[l % 2][2 + l / 2];
+        aw[3][l][1] = l < 2 ? pb[l][4] : l == 2 ? t0 : t1;
+    }
 }
 
 // s_waitcnt through the builtin (gfx9 encoding, other counters left at their maxima),
@@ -427,20 +456,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
 // The pinned contract (dot_q8_groups_pinned, src/kernels.rs:1102-1147) on the same
 // tiles: per (token, row) four binary32 lanes L[l] = fma(I_l, dd_g, L[l]) with
 // dd_g = fl(d_w * A_g.scale), group by group, and (L0 + L1) + (L2 + L3) at the end.  In
-// the pinned operand order K-step j of group g holds native lane 2j in its first half
-// (lanes 0..31 of the wavefront) and lane 2j + 1 in its second, so an MFMA whose weights
-// are zeroed in one half returns that lane's exact integer sum (binary16-exact operands,
-// |I| <= 8*127).  Four MFMAs per group instead of two, and 20 VALU per output and block
-// instead of 6 (the four dd_g and sixteen FMAs): 32 tokens per workgroup keep the 64
-// lane accumulators of a wavefront in registers.
+// the pinned operand order one v_mfma_f32_32x32x8_f16 per (group, native lane) sums
+// exactly that lane's eight elements, half h of the wavefront supplying four of them
+// (binary16-exact operands, |I| <= 8*127): four MFMAs per group, each as long as one
+// K=16 MFMA on gfx950, and no masking.  20 VALU per output and block instead of 6 (the
+// four dd_g and sixteen FMAs): 32 tokens per workgroup keep the 64 lane accumulators of
+// a wavefront in registers.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_ptq1_pinned(
     const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu, const _Float16 *__restrict__ xh,
     const float *__restrict__ sc, uint32_t M, uint32_t Mp, uint32_t xcd_major, float *__restrict__ out,
     int *__restrict__ err) {
     constexpr uint32_t NT = 32;
-    constexpr uint32_t kRun = NT * 16;
-    __shared__ __attribute__((aligned(16))) uint8_t act0[8][2][kRun];
-    __shared__ __attribute__((aligned(16))) uint8_t act1[8][2][kRun];
+    constexpr uint32_t kRun = NT * 8;  // bytes of one (g, l, h) run of one block
+    __shared__ __attribute__((aligned(16))) uint8_t act0[32][kRun];
+    __shared__ __attribute__((aligned(16))) uint8_t act1[32][kRun];
     __shared__ __attribute__((aligned(16))) float4 scl0[NT];
     __shared__ __attribute__((aligned(16))) float4 scl1[NT];
     const uint32_t lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
@@ -464,12 +493,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc, nu * Mp * 16u);
     const uint32_t row = 32 * hw + r32, out0 = 32 * hw + 4 * h;  // tile rows
 
-    // Block u's codes (16 runs of NT*16 bytes) and scales of the workgroup's tokens.
-    auto stage = [&](uint32_t u, uint8_t (&act)[8][2][kRun], float4 (&scl)[NT]) {
-        for (uint32_t run = wave; run < 16; run += 4)
-            if (lane < NT)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(&act[run >> 1][run & 1][0]), 16,
-                                                         ((u * 16 + run) * Mp + t0 + lane) * 16u, 0, 0, 0);
+    // Block u's codes (32 runs of NT*8 bytes, each contiguous in xh and in LDS; one
+    // instruction moves four runs, lane l tokens 2(l%16), 2(l%16)+1 of run l/16) and the
+    // scales of the workgroup's tokens.
+    auto stage = [&](uint32_t u, uint8_t (&act)[32][kRun], float4 (&scl)[NT]) {
+        for (uint32_t i = wave; i < 8; i += 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(&act[4 * i][0]), 16,
+                                                     ((u * 32 + 4 * i + lane / 16) * Mp + t0 + 2 * (lane % 16)) * 8u, 0,
+                                                     0, 0);
         if (wave == 0 && lane < NT)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(&scl[0]), 16, (u * Mp + t0 + lane) * 16u, 0,
                                                      0, 0);
@@ -487,9 +518,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     if (active) load_block(rw, 0, trp, row, out0, w);
     wait_vmcnt0();
     lds_barrier();
-    auto block = [&](uint32_t u, const uint8_t (&act)[8][2][kRun], const float4 (&scl)[NT],
-                     uint8_t (&act_next)[8][2][kRun], float4 (&scl_next)[NT]) {
-        uint32_t aw[4][2][4];
+    auto block = [&](uint32_t u, const uint8_t (&act)[32][kRun], const float4 (&scl)[NT],
+                     uint8_t (&act_next)[32][kRun], float4 (&scl_next)[NT]) {
+        uint32_t aw[4][4][2];
         float d[16];
         if (active) {
             decode_block_pinned(w, h, aw);
@@ -514,19 +545,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int r = 0; r < 16; ++r) dd[r] = d[r] * sg[g];  // fl(d_w * A_g.scale)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const v8h b = *reinterpret_cast<const v8h *>(&act[2 * g + j][h][r32 * 16]);
-                    const u32x4 a = {aw[g][j][0], aw[g][j][1], aw[g][j][2], aw[g][j][3]};
-                    const u32x4 z = {0u, 0u, 0u, 0u};
-                    const v16f i0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, h ? z : a), b, zero,
-                                                                           0, 0, 0);
-                    const v16f i1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, h ? a : z), b, zero,
-                                                                           0, 0, 0);
+                for (int l = 0; l < 4; ++l) {
+                    const v4h b = *reinterpret_cast<const v4h *>(&act[(4 * g + l) * 2 + h][r32 * 8]);
+                    const u32x2 a = {aw[g][l][0], aw[g][l][1]};
+                    const v16f i = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, a), b, zero, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        L[2 * j][r] = __builtin_fmaf(i0[r], dd[r], L[2 * j][r]);
-                        L[2 * j + 1][r] = __builtin_fmaf(i1[r], dd[r], L[2 * j + 1][r]);
-                    }
+                    for (int r = 0; r < 16; ++r) L[l][r] = __builtin_fmaf(i[r], dd[r], L[l][r]);
                 }
             }
         }
