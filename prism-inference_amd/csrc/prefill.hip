@@ -187,6 +187,12 @@ struct RawBlock {
     uint32_t tl;
     u32x4 dd[4];
 };
+__device__ __forceinline__ void load_block_codes(__amdgpu_buffer_rsrc_t rs, uint32_t seg, uint32_t trp, uint32_t row,
+                                                 RawBlock &w) {  // a, b and tl only
+    w.a = bload4(rs, seg + 16u * row);
+    w.b = bload2(rs, seg + 16u * trp + 8u * row);
+    w.tl = bload1(rs, seg + 24u * trp + 4u * row);
+}
 __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t rs, uint32_t seg, uint32_t trp, uint32_t row,
                                            uint32_t out0, RawBlock &w) {
     w.a = bload4(rs, seg + 16u * row);
@@ -515,35 +521,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 
     RawBlock w;
     stage(0, act0, scl0);
-    if (active) load_block(rw, 0, trp, row, out0, w);
+    if (active) load_block_codes(rw, 0, trp, row, w);
     wait_vmcnt0();
     lds_barrier();
     auto block = [&](uint32_t u, const uint8_t (&act)[32][kRun], const float4 (&scl)[NT],
                      uint8_t (&act_next)[32][kRun], float4 (&scl_next)[NT]) {
         uint32_t aw[4][4][2];
-        float d[16];
+        float dw = 0.0f;  // the lane's row scale in half 0, zero in half 1
         if (active) {
             decode_block_pinned(w, h, aw);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                d[4 * q] = h2f(w.dd[q].x >> 16);
-                d[4 * q + 1] = h2f(w.dd[q].y >> 16);
-                d[4 * q + 2] = h2f(w.dd[q].z >> 16);
-                d[4 * q + 3] = h2f(w.dd[q].w >> 16);
-            }
+            dw = h ? 0.0f : h2f(w.tl >> 16);
         }
         if (u + 1 < nu) {
             stage(u + 1, act_next, scl_next);
-            if (active) load_block(rw, (u + 1) * trp * 28u, trp, row, out0, w);
+            if (active) load_block_codes(rw, (u + 1) * trp * 28u, trp, row, w);
         }
         if (active) {
             const float4 sg4 = scl[r32];
             const float sg[4] = {sg4.x, sg4.y, sg4.z, sg4.w};
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                float dd[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) dd[r] = d[r] * sg[g];  // fl(d_w * A_g.scale)
+                // dd[r] = fl(d_w * A_g.scale) for every (row, token) of the tile, as the
+                // outer product of the rows' and tokens' scales on the matrix pipe: K = 2
+                // with the second term zero, one rounding (no product is subnormal: both
+                // scales are binary16 values).
+                const v16f dd = __builtin_amdgcn_mfma_f32_32x32x2f32(dw, h ? 0.0f : sg[g], zero, 0, 0, 0);
 #pragma unroll
                 for (int l = 0; l < 4; ++l) {
                     const v4h b = *reinterpret_cast<const v4h *>(&act[(4 * g + l) * 2 + h][r32 * 8]);
