@@ -255,50 +255,57 @@ __device__ __forceinline__ void decode_block(const RawBlock &w, uint32_t h, uint
     }
 }
 
-// The f16 pairs of digits 0..ND-1 of a 16-bit-lane byte pair L (the two bytes, < 256,
-// in the low bytes of its halves), sequentially (remainder times 3).
-template <int ND>
-__device__ __forceinline__ void pairs_seq(uint32_t L, uint32_t *out) {
-#pragma unroll
-    for (int k = 0; k < ND; ++k) {
-        const uint32_t m = L * 3u;
-        out[k] = f16_pair(m);
-        L = m & 0x00ff00ffu;
-    }
-}
-
 // The pinned operand order (pinned_pair_base): for group g and native lane l, half h
 // supplies pair h of quads l and l + 4, which come from (tools/ternary/src/lib.rs:202-250
 // element map; (D, k) = code dword D at digit k)
 //   g0: (A_l, 0) (A_l, 1)      g1: (A_l, 2) (A_l, 3)      g2: (A_l, 4) (B_{l%2}, l/2)
 //   g3: (B_{l%2}, 2 + l/2), then (B_l, 4) for l < 2 or the tail quads 120, 124,
 // so a lane decodes bytes h and h + 2 of every code dword (digits 0..4) and byte 24 + h of
-// the tail (digits 0..3): half of the block's elements, aw[g][l][0..1].
-__device__ __forceinline__ void decode_block_pinned(const RawBlock &w, uint32_t h, uint32_t aw[4][4][2]) {
-    const uint32_t sel = h ? sel_bytes(1, 12, 3, 12) : sel_bytes(0, 12, 2, 12);  // bytes h, h+2
-    uint32_t pa[4][5], pb[2][5];
-    const uint32_t a[4] = {w.a.x, w.a.y, w.a.z, w.a.w}, b[2] = {w.b.x, w.b.y};
-#pragma unroll
-    for (int p = 0; p < 4; ++p) pairs_seq<5>(perm(a[p], a[p], sel), pa[p]);
-#pragma unroll
-    for (int v = 0; v < 2; ++v) pairs_seq<5>(perm(b[v], b[v], sel), pb[v]);
-    // Tail byte 24 + h in both halves at digit multipliers (3^k, 3^(k+1)): the quads at
-    // 120 (digits 0, 1) and 124 (digits 2, 3).
-    const uint32_t tb = perm(w.tl, w.tl, h ? sel_bytes(1, 12, 1, 12) : sel_bytes(0, 12, 0, 12));
-    const uint32_t t0 = f16_pair((pair_mul(tb, 1u | (3u << 16)) & 0x00ff00ffu) * 3u);
-    const uint32_t t1 = f16_pair((pair_mul(tb, 9u | (27u << 16)) & 0x00ff00ffu) * 3u);
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-        aw[0][l][0] = pa[l][0];
-        aw[0][l][1] = pa[l][1];
-        aw[1][l][0] = pa[l][2];
-        aw[1][l][1] = pa[l][3];
-        aw[2][l][0] = pa[l][4];
-        aw[2][l][1] = pb[l % 2][l / 2];
-        aw[3][l][0] = pb[l % 2][2 + l / 2];
-        aw[3][l][1] = l < 2 ? pb[l][4] : l == 2 ? t0 : t1;
+// the tail (digits 0..3): half of the block's elements.  Every dword's digits are used in
+// order, so the decoder runs group by group, holding one group's operands at a time:
+// group(g, aw) yields aw[l][0..1] for the four native lanes.
+struct PinnedDecoder {
+    uint32_t la[4], lb[2], tb;  // remaining 16-bit-lane byte pairs; the tail byte twice
+
+    __device__ __forceinline__ PinnedDecoder(const RawBlock &w, uint32_t h) {
+        const uint32_t sel = h ? sel_bytes(1, 12, 3, 12) : sel_bytes(0, 12, 2, 12);  // bytes h, h+2
+        la[0] = perm(w.a.x, w.a.x, sel);
+        la[1] = perm(w.a.y, w.a.y, sel);
+        la[2] = perm(w.a.z, w.a.z, sel);
+        la[3] = perm(w.a.w, w.a.w, sel);
+        lb[0] = perm(w.b.x, w.b.x, sel);
+        lb[1] = perm(w.b.y, w.b.y, sel);
+        tb = perm(w.tl, w.tl, h ? sel_bytes(1, 12, 1, 12) : sel_bytes(0, 12, 0, 12));
     }
-}
+    // The next digit's f16 pair of a byte pair (remainder times 3).
+    __device__ __forceinline__ static uint32_t next(uint32_t &L) {
+        const uint32_t m = L * 3u;
+        L = m & 0x00ff00ffu;
+        return f16_pair(m);
+    }
+    __device__ __forceinline__ void group(int g, uint32_t aw[4][2]) {
+        if (g < 2) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                aw[l][0] = next(la[l]);
+                aw[l][1] = next(la[l]);
+            }
+        } else if (g == 2) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) aw[l][0] = next(la[l]);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) aw[l][1] = next(lb[l % 2]);
+        } else {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) aw[l][0] = next(lb[l % 2]);
+            aw[0][1] = next(lb[0]);
+            aw[1][1] = next(lb[1]);
+            // The tail byte at digit multipliers (3^k, 3^(k+1)): quads 120 (k = 0), 124 (k = 2).
+            aw[2][1] = f16_pair((pair_mul(tb, 1u | (3u << 16)) & 0x00ff00ffu) * 3u);
+            aw[3][1] = f16_pair((pair_mul(tb, 9u | (27u << 16)) & 0x00ff00ffu) * 3u);
+        }
+    }
+};
 
 // s_waitcnt through the builtin (gfx9 encoding, other counters left at their maxima),
 // so the compiler's own wait bookkeeping sees it: vmcnt(0) / lgkmcnt(0).
@@ -468,7 +475,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
 // K=16 MFMA on gfx950, and no masking.  20 VALU per output and block instead of 6 (the
 // four dd_g and sixteen FMAs): 32 tokens per workgroup keep the 64 lane accumulators of
 // a wavefront in registers.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_ptq1_pinned(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_prefill_ptq1_pinned(
     const uint8_t *__restrict__ W, uint32_t rows, uint32_t nu, const _Float16 *__restrict__ xh,
     const float *__restrict__ sc, uint32_t M, uint32_t Mp, uint32_t xcd_major, float *__restrict__ out,
     int *__restrict__ err) {
@@ -519,19 +526,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         for (int r = 0; r < 16; ++r) L[l][r] = 0.0f;
     const v16f zero = {};
 
-    RawBlock w;
+    RawBlock w = {};  // stays zero in an inactive wavefront
     stage(0, act0, scl0);
     if (active) load_block_codes(rw, 0, trp, row, w);
     wait_vmcnt0();
     lds_barrier();
     auto block = [&](uint32_t u, const uint8_t (&act)[32][kRun], const float4 (&scl)[NT],
                      uint8_t (&act_next)[32][kRun], float4 (&scl_next)[NT]) {
-        uint32_t aw[4][4][2];
-        float dw = 0.0f;  // the lane's row scale in half 0, zero in half 1
-        if (active) {
-            decode_block_pinned(w, h, aw);
-            dw = h ? 0.0f : h2f(w.tl >> 16);
-        }
+        PinnedDecoder dec(w, h);
+        const float dw = h ? 0.0f : h2f(w.tl >> 16);  // the lane's row scale in half 0, zero in half 1
         if (u + 1 < nu) {
             stage(u + 1, act_next, scl_next);
             if (active) load_block_codes(rw, (u + 1) * trp * 28u, trp, row, w);
@@ -546,10 +549,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 // with the second term zero, one rounding (no product is subnormal: both
                 // scales are binary16 values).
                 const v16f dd = __builtin_amdgcn_mfma_f32_32x32x2f32(dw, h ? 0.0f : sg[g], zero, 0, 0, 0);
+                uint32_t aw[4][2];
+                dec.group(g, aw);
 #pragma unroll
                 for (int l = 0; l < 4; ++l) {
                     const v4h b = *reinterpret_cast<const v4h *>(&act[(4 * g + l) * 2 + h][r32 * 8]);
-                    const u32x2 a = {aw[g][l][0], aw[g][l][1]};
+                    const u32x2 a = {aw[l][0], aw[l][1]};
                     const v16f i = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, a), b, zero, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 16; ++r) L[l][r] = __builtin_fmaf(i[r], dd[r], L[l][r]);
