@@ -78,12 +78,9 @@ __host__ __device__ constexpr uint32_t pinned_pair_base(uint32_t g, uint32_t l, 
 }
 
 // ---- activation prep ------------------------------------------------------------------
-// One wavefront per (token, 1024 inputs): Q8_0 quantization into LDS (the source
-// contract, or the pinned PTQ1 native-scale contract), then the codes leave as binary16
-// in operand order, source xh[u][g][j][h][t][8] and pinned xh[u][g][l][h][t][4] (u =
-// 128-block, tokens padded to Mp with zeros; 256 bytes per block and token either way),
-// and the scales as sc[u][t][g].
-template <bool PINNED>
+// Source contract: one wavefront per (token, 1024 inputs): Q8_0 quantization into LDS,
+// then the codes leave as binary16 in operand order, xh[u][g][j][h][t][8] (u = 128-block,
+// tokens padded to Mp with zeros), and the scales as sc[u][t][g].
 __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp, uint32_t K,
                                                       _Float16 *__restrict__ xh, float *__restrict__ sc,
                                                       int *__restrict__ err) {
@@ -97,30 +94,16 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ 
     const bool real = t < M;
     if (real) {
         const float *xr = x + static_cast<size_t>(t) * K + k0;
-        // Contract 0: source (round half away); 2: pinned PTQ1 native scale (quant_dev.hpp).
-        const int e = q8_0_blocks_wave(xr, n / 32, PINNED ? 2 : 0, blk[wave], lane);
+        // Contract 0: source, round half away (quant_dev.hpp).
+        const int e = q8_0_blocks_wave(xr, n / 32, 0, blk[wave], lane);
         if (e) {
             if (lane == 0) raise_error(err, e);
             return;
         }
         __builtin_amdgcn_wave_barrier();
     }
-    auto code = [&](uint32_t e) -> uint32_t {  // element e's code as binary16 bits
-        const int8_t v = real ? blk[wave][e / 32].values[e % 32] : 0;
-        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
-    };
-    if constexpr (PINNED) {
-        // 32 slots (g, l, h) of 8 bytes per block; lane takes slots lane, lane + 64, ...
-        for (uint32_t s = lane; s < n / 128 * 32; s += 64) {
-            const uint32_t ub = s >> 5, g = (s >> 3) & 3u, l = (s >> 1) & 3u, h = s & 1u;
-            const uint32_t u = k0 / 128 + ub;
-            const uint32_t e0 = 128 * ub + pinned_pair_base(g, l, h, 0), e1 = 128 * ub + pinned_pair_base(g, l, h, 1);
-            uint2 *dst = reinterpret_cast<uint2 *>(xh + ((static_cast<size_t>(u) * 32 + (s & 31u)) * Mp + t) * 4);
-            *dst = make_uint2(code(e0) | code(e0 + 2) << 16, code(e1) | code(e1 + 2) << 16);
-        }
-    }
-    // Source: 16 slots (g, j, h) of 16 bytes per block; lane takes slots lane, lane + 64.
-    for (uint32_t s = lane; !PINNED && s < n / 128 * 16; s += 64) {
+    // 16 slots (g, j, h) of 16 bytes per block; lane takes slots lane, lane + 64.
+    for (uint32_t s = lane; s < n / 128 * 16; s += 64) {
         const uint32_t ub = s >> 4, g = (s >> 2) & 3u, j = (s >> 1) & 1u, h = s & 1u;
         const uint32_t u = k0 / 128 + ub;
         uint32_t packed[4];
@@ -132,7 +115,11 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ 
             for (int p = 0; p < 2; ++p) {
                 uint32_t h2 = 0;
 #pragma unroll
-                for (int q = 0; q < 2; ++q) h2 |= code(el[2 * p + q]) << (16 * q);
+                for (int q = 0; q < 2; ++q) {
+                    const uint32_t e = el[2 * p + q];
+                    const int8_t v = real ? blk[wave][e / 32].values[e % 32] : 0;
+                    h2 |= static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v))) << (16 * q);
+                }
                 packed[2 * qq + p] = h2;
             }
         }
@@ -142,6 +129,49 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ 
     if (lane < n / 32) {
         const uint32_t u = k0 / 128 + lane / 4;
         sc[(static_cast<size_t>(u) * Mp + t) * 4 + lane % 4] = real ? blk[wave][lane].scale : 0.0f;
+    }
+}
+
+// Pinned contract: a workgroup of kPrepTokens wavefronts quantizes kPrepTokens
+// consecutive tokens (one each, 1024 inputs, the pinned PTQ1 native-scale Q8_0), then
+// writes their codes as xh[u][g][l][h][t][4] (binary16, pinned_pair_base order): each
+// thread stores two tokens' 8 bytes of one slot, so a slot's kPrepTokens tokens leave as
+// one contiguous 128-byte segment.  Scales as sc[u][t][g].  Mp is a multiple of
+// kPrepTokens; the grid holds Mp / kPrepTokens * chunks workgroups.  A quantizer error is
+// raised and the wavefront carries on (the call then reports it and clears the output).
+constexpr uint32_t kPrepTokens = 16;
+__global__ __launch_bounds__(64 * kPrepTokens) void k_prefill_prep_pinned(const float *__restrict__ x, uint32_t M,
+                                                                          uint32_t Mp, uint32_t K,
+                                                                          _Float16 *__restrict__ xh,
+                                                                          float *__restrict__ sc, int *__restrict__ err) {
+    __shared__ Q8Block blk[kPrepTokens][32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t chunks = (K + 1023) / 1024;
+    const uint32_t c = blockIdx.x % chunks, tb = blockIdx.x / chunks * kPrepTokens;
+    const uint32_t k0 = c * 1024, n = K - k0 < 1024 ? K - k0 : 1024;  // multiple of 128
+    const uint32_t t = tb + wave;
+    if (t < M) {
+        const int e = q8_0_blocks_wave(x + static_cast<size_t>(t) * K + k0, n / 32, 2, blk[wave], lane);
+        if (e && lane == 0) raise_error(err, e);
+    }
+    __syncthreads();
+    if (lane < n / 32) {
+        const uint32_t u = k0 / 128 + lane / 4;
+        sc[(static_cast<size_t>(u) * Mp + t) * 4 + lane % 4] = t < M ? blk[wave][lane].scale : 0.0f;
+    }
+    auto code = [&](uint32_t w, uint32_t e) -> uint32_t {  // token tb + w, element e: binary16 bits
+        const int8_t v = tb + w < M ? blk[w][e / 32].values[e % 32] : 0;
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    };
+    constexpr uint32_t kPairs = kPrepTokens / 2;
+    for (uint32_t i = tid; i < n / 128 * 32 * kPairs; i += 64 * kPrepTokens) {
+        const uint32_t p = i % kPairs, s = (i / kPairs) % 32, ub = i / (32 * kPairs);
+        const uint32_t g = s >> 3, l = (s >> 1) & 3u, h = s & 1u;
+        const uint32_t e0 = 128 * ub + pinned_pair_base(g, l, h, 0), e1 = 128 * ub + pinned_pair_base(g, l, h, 1);
+        const uint32_t w0 = 2 * p, w1 = 2 * p + 1;
+        uint4 *dst = reinterpret_cast<uint4 *>(xh + ((static_cast<size_t>(k0 / 128 + ub) * 32 + s) * Mp + tb + w0) * 4);
+        *dst = make_uint4(code(w0, e0) | code(w0, e0 + 2) << 16, code(w0, e1) | code(w0, e1 + 2) << 16,
+                          code(w1, e0) | code(w1, e0 + 2) << 16, code(w1, e1) | code(w1, e1 + 2) << 16);
     }
 }
 
@@ -619,11 +649,13 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
     float *sc = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + ((static_cast<size_t>(Mp) * K * 2 + 255) & ~size_t(255)));
     const uint32_t chunks = (K + 1023) / 1024;
     const uint64_t items = static_cast<uint64_t>(Mp) * chunks;
-    const dim3 pgrid(static_cast<uint32_t>((items + 3) / 4));
+    static_assert(kTokAlign % kPrepTokens == 0, "pinned prep takes whole token groups");
     if (pinned)
-        hipLaunchKernelGGL(k_prefill_prep<true>, pgrid, dim3(256), 0, s, x, M, Mp, K, xh, sc, err);
+        hipLaunchKernelGGL(k_prefill_prep_pinned, dim3(static_cast<uint32_t>(items / kPrepTokens)),
+                           dim3(64 * kPrepTokens), 0, s, x, M, Mp, K, xh, sc, err);
     else
-        hipLaunchKernelGGL(k_prefill_prep<false>, pgrid, dim3(256), 0, s, x, M, Mp, K, xh, sc, err);
+        hipLaunchKernelGGL(k_prefill_prep, dim3(static_cast<uint32_t>((items + 3) / 4)), dim3(256), 0, s, x, M, Mp, K,
+                           xh, sc, err);
     if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
     const auto W = static_cast<const uint8_t *>(w_tiled);
