@@ -53,105 +53,47 @@ constexpr uint32_t sel_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3)
 // Operand order.  Code dword D of a PTQ1 block, digit k, gives a "quad" of four
 // consecutive elements (tools/ternary/src/lib.rs:202-250): A-piece dword w -> 16k+4w,
 // B-piece dword v -> 80+8k+4v, and the two tail bytes repeated (b24 b25 b24 b25) with
-// digits (k, k, k+1, k+1) -> 120+2k.  Half h of group g holds quads i = 0..3; K-step j
-// of the group takes quads 2j and 2j+1.  A quad's four f16 sit in the order of the
-// 16-bit-lane decoder: elements (0, 2) then (1, 3).
-//   g0: (A_{2h+i/2}, i%2)           g1: (A_{2h+i/2}, 2+i%2)
-//   g2: h=0: (A_i, 4)               h=1: (B_{i/2}, i%2)
-//   g3: i<3: (B_h, 2+i)             i=3: tail digits 2h, 2h+1
-__host__ __device__ constexpr uint32_t quad_base(uint32_t h, uint32_t g, uint32_t i) {
-    return g == 0   ? 16 * (i & 1) + 4 * (2 * h + (i >> 1))
-           : g == 1 ? 32 + 16 * (i & 1) + 4 * (2 * h + (i >> 1))
-           : g == 2 ? (h == 0 ? 64 + 4 * i : 80 + 8 * (i & 1) + 4 * (i >> 1))
-                    : (i < 3 ? 96 + 8 * i + 4 * h : 120 + 4 * h);
-}
-
+// digits (k, k, k+1, k+1) -> 120+2k.  The 16-bit-lane decoder turns bytes (0, 2) and
+// (1, 3) of a quad's dword into two f16 pairs: elements (b, b+2) and (b+1, b+3) of the
+// quad at b.  Half h of the wavefront (lanes 32h..32h+31) supplies, for every quad, its
+// pair h, i.e. elements (b+h, b+h+2): a lane decodes bytes h and h+2 of every code dword
+// and tail byte 24+h, half of the block's elements, in PairDecoder.
+//
+// Source order: K-step j (K = 16) of group g takes, in half h, pair h of the group's
+// quads 4j .. 4j+3 (dword i of the operand: quad 4j + i).
 // Pinned order (dot_q8_groups_pinned, src/kernels.rs:1102-1147): the chain needs, per
 // group, the sum over each native lane l's elements 4l..4l+3 and 16+4l..16+4l+3
 // (q8_native_lanes, src/kernels.rs:1066-1076), i.e. quads l and l+4 of the group.  One
-// v_mfma_f32_32x32x8_f16 per native lane sums exactly those eight: half h of the
-// wavefront supplies, for both quads, the f16 pair the 16-bit-lane decoder yields for
-// bytes (h, h+2) of the quad, i.e. elements (b+h, b+h+2) of the quad at b.  Pair i of
-// (g, l, h) starts at this element:
-__host__ __device__ constexpr uint32_t pinned_pair_base(uint32_t g, uint32_t l, uint32_t h, uint32_t i) {
-    return 32 * g + 4 * l + 16 * i + h;
-}
+// v_mfma_f32_32x32x8_f16 per native lane sums exactly those eight: half h supplies pair
+// h of quads l and l+4.
+// Either way the operand dword for (group g, quad q) starts at this element:
+__host__ __device__ constexpr uint32_t pair_base(uint32_t g, uint32_t q, uint32_t h) { return 32 * g + 4 * q + h; }
 
 // ---- activation prep ------------------------------------------------------------------
-// Source contract: one wavefront per (token, 1024 inputs): Q8_0 quantization into LDS,
-// then the codes leave as binary16 in operand order, xh[u][g][j][h][t][8] (u = 128-block,
-// tokens padded to Mp with zeros), and the scales as sc[u][t][g].
-__global__ __launch_bounds__(256) void k_prefill_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp, uint32_t K,
-                                                      _Float16 *__restrict__ xh, float *__restrict__ sc,
-                                                      int *__restrict__ err) {
-    __shared__ Q8Block blk[4][32];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t chunks = (K + 1023) / 1024;
-    const uint32_t item = blockIdx.x * 4 + wave;
-    if (item >= Mp * chunks) return;  // uniform per wavefront
-    const uint32_t t = item / chunks, c = item % chunks;
-    const uint32_t k0 = c * 1024, n = K - k0 < 1024 ? K - k0 : 1024;  // multiple of 128
-    const bool real = t < M;
-    if (real) {
-        const float *xr = x + static_cast<size_t>(t) * K + k0;
-        // Contract 0: source, round half away (quant_dev.hpp).
-        const int e = q8_0_blocks_wave(xr, n / 32, 0, blk[wave], lane);
-        if (e) {
-            if (lane == 0) raise_error(err, e);
-            return;
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
-    // 16 slots (g, j, h) of 16 bytes per block; lane takes slots lane, lane + 64.
-    for (uint32_t s = lane; s < n / 128 * 16; s += 64) {
-        const uint32_t ub = s >> 4, g = (s >> 2) & 3u, j = (s >> 1) & 1u, h = s & 1u;
-        const uint32_t u = k0 / 128 + ub;
-        uint32_t packed[4];
-#pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-            const uint32_t base = 128 * ub + quad_base(h, g, 2 * j + qq);
-            const uint32_t el[4] = {base, base + 2, base + 1, base + 3};
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                uint32_t h2 = 0;
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const uint32_t e = el[2 * p + q];
-                    const int8_t v = real ? blk[wave][e / 32].values[e % 32] : 0;
-                    h2 |= static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v))) << (16 * q);
-                }
-                packed[2 * qq + p] = h2;
-            }
-        }
-        uint4 *dst = reinterpret_cast<uint4 *>(xh + (((static_cast<size_t>(u * 4 + g) * 2 + j) * 2 + h) * Mp + t) * 8);
-        *dst = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    }
-    if (lane < n / 32) {
-        const uint32_t u = k0 / 128 + lane / 4;
-        sc[(static_cast<size_t>(u) * Mp + t) * 4 + lane % 4] = real ? blk[wave][lane].scale : 0.0f;
-    }
-}
-
-// Pinned contract: a workgroup of kPrepTokens wavefronts quantizes kPrepTokens
-// consecutive tokens (one each, 1024 inputs, the pinned PTQ1 native-scale Q8_0), then
-// writes their codes as xh[u][g][l][h][t][4] (binary16, pinned_pair_base order): each
-// thread stores two tokens' 8 bytes of one slot, so a slot's kPrepTokens tokens leave as
-// one contiguous 128-byte segment.  Scales as sc[u][t][g].  Mp is a multiple of
-// kPrepTokens; the grid holds Mp / kPrepTokens * chunks workgroups.  A quantizer error is
-// raised and the wavefront carries on (the call then reports it and clears the output).
-constexpr uint32_t kPrepTokens = 16;
-__global__ __launch_bounds__(64 * kPrepTokens) void k_prefill_prep_pinned(const float *__restrict__ x, uint32_t M,
-                                                                          uint32_t Mp, uint32_t K,
-                                                                          _Float16 *__restrict__ xh,
-                                                                          float *__restrict__ sc, int *__restrict__ err) {
-    __shared__ Q8Block blk[kPrepTokens][32];
+// A workgroup of TOK wavefronts quantizes TOK consecutive tokens (one each, 1024 inputs;
+// Q8_0 in the source contract, or the pinned PTQ1 native-scale contract), then writes
+// their codes as binary16 in operand order, one 16-byte store per thread, so a slot's TOK
+// tokens leave as one contiguous segment:
+//   source xh[u][g][j][h][t][8]  (16 slots of 16 bytes per block and token),
+//   pinned xh[u][g][l][h][t][4]  (32 slots of 8 bytes; a store covers two tokens),
+// u = 128-block, tokens padded to Mp (a multiple of TOK) with zeros; 256 bytes per block
+// and token either way.  Scales as sc[u][t][g].  The grid holds Mp / TOK * chunks
+// workgroups.  A quantizer error is raised and the wavefront carries on (the call then
+// reports it and clears the output).  TOK = 16 fills whole 128-byte lines per pinned slot;
+// short prompts take TOK = 4, which spreads their few tokens over four times as many CUs.
+template <bool PINNED, uint32_t TOK>
+__global__ __launch_bounds__(64 * TOK) void k_prefill_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp,
+                                                           uint32_t K, _Float16 *__restrict__ xh,
+                                                           float *__restrict__ sc, int *__restrict__ err) {
+    __shared__ Q8Block blk[TOK][32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t chunks = (K + 1023) / 1024;
-    const uint32_t c = blockIdx.x % chunks, tb = blockIdx.x / chunks * kPrepTokens;
+    const uint32_t c = blockIdx.x % chunks, tb = blockIdx.x / chunks * TOK;
     const uint32_t k0 = c * 1024, n = K - k0 < 1024 ? K - k0 : 1024;  // multiple of 128
     const uint32_t t = tb + wave;
     if (t < M) {
-        const int e = q8_0_blocks_wave(x + static_cast<size_t>(t) * K + k0, n / 32, 2, blk[wave], lane);
+        // Contract 0: source (round half away); 2: pinned PTQ1 native scale (quant_dev.hpp).
+        const int e = q8_0_blocks_wave(x + static_cast<size_t>(t) * K + k0, n / 32, PINNED ? 2 : 0, blk[wave], lane);
         if (e && lane == 0) raise_error(err, e);
     }
     __syncthreads();
@@ -159,19 +101,33 @@ __global__ __launch_bounds__(64 * kPrepTokens) void k_prefill_prep_pinned(const 
         const uint32_t u = k0 / 128 + lane / 4;
         sc[(static_cast<size_t>(u) * Mp + t) * 4 + lane % 4] = t < M ? blk[wave][lane].scale : 0.0f;
     }
-    auto code = [&](uint32_t w, uint32_t e) -> uint32_t {  // token tb + w, element e: binary16 bits
-        const int8_t v = tb + w < M ? blk[w][e / 32].values[e % 32] : 0;
-        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    // Operand dword of token tb + w: the f16 pair (e, e + 2).
+    auto pair = [&](uint32_t w, uint32_t e) -> uint32_t {
+        const bool real = tb + w < M;
+        const int8_t v0 = real ? blk[w][e / 32].values[e % 32] : 0;
+        const int8_t v1 = real ? blk[w][(e + 2) / 32].values[(e + 2) % 32] : 0;
+        return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v0))) |
+               static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v1))) << 16;
     };
-    constexpr uint32_t kPairs = kPrepTokens / 2;
-    for (uint32_t i = tid; i < n / 128 * 32 * kPairs; i += 64 * kPrepTokens) {
-        const uint32_t p = i % kPairs, s = (i / kPairs) % 32, ub = i / (32 * kPairs);
-        const uint32_t g = s >> 3, l = (s >> 1) & 3u, h = s & 1u;
-        const uint32_t e0 = 128 * ub + pinned_pair_base(g, l, h, 0), e1 = 128 * ub + pinned_pair_base(g, l, h, 1);
-        const uint32_t w0 = 2 * p, w1 = 2 * p + 1;
-        uint4 *dst = reinterpret_cast<uint4 *>(xh + ((static_cast<size_t>(k0 / 128 + ub) * 32 + s) * Mp + tb + w0) * 4);
-        *dst = make_uint4(code(w0, e0) | code(w0, e0 + 2) << 16, code(w0, e1) | code(w0, e1 + 2) << 16,
-                          code(w1, e0) | code(w1, e0 + 2) << 16, code(w1, e1) | code(w1, e1 + 2) << 16);
+    // 16 * TOK stores of 16 bytes per block: (slot, token) for the source order (16 slots),
+    // (slot, token pair) for the pinned one (32 slots); consecutive threads take
+    // consecutive tokens of one slot.
+    for (uint32_t i = tid; i < n / 128 * 16 * TOK; i += 64 * TOK) {
+        const uint32_t ub = i / (16 * TOK), u = k0 / 128 + ub, base = 128 * ub;
+        if constexpr (PINNED) {
+            constexpr uint32_t kPairs = TOK / 2;
+            const uint32_t p = i % kPairs, s = (i / kPairs) % 32;
+            const uint32_t g = s >> 3, l = (s >> 1) & 3u, h = s & 1u;
+            const uint32_t e0 = base + pair_base(g, l, h), e1 = base + pair_base(g, l + 4, h);
+            uint4 *dst = reinterpret_cast<uint4 *>(xh + ((static_cast<size_t>(u) * 32 + s) * Mp + tb + 2 * p) * 4);
+            *dst = make_uint4(pair(2 * p, e0), pair(2 * p, e1), pair(2 * p + 1, e0), pair(2 * p + 1, e1));
+        } else {
+            const uint32_t w = i % TOK, s = (i / TOK) % 16;
+            const uint32_t g = s >> 2, j = (s >> 1) & 1u, h = s & 1u;
+            uint4 *dst = reinterpret_cast<uint4 *>(xh + ((static_cast<size_t>(u) * 16 + s) * Mp + tb + w) * 8);
+            *dst = make_uint4(pair(w, base + pair_base(g, 4 * j, h)), pair(w, base + pair_base(g, 4 * j + 1, h)),
+                              pair(w, base + pair_base(g, 4 * j + 2, h)), pair(w, base + pair_base(g, 4 * j + 3, h)));
+        }
     }
 }
 
@@ -185,27 +141,6 @@ __device__ __forceinline__ uint32_t f16_pair(uint32_t m) {
 __device__ __forceinline__ uint32_t pair_mul(uint32_t v, uint32_t m) {  // two 16-bit lanes times (m.lo, m.hi)
     typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v) * __builtin_bit_cast(u16x2, m));
-}
-// The quad of dword x at per-16-bit-lane digit multipliers p (3^k): f16 pairs of the
-// bytes (0, 2) and (1, 3).
-__device__ __forceinline__ void quad_at(uint32_t x, uint32_t p, uint32_t &lo, uint32_t &hi) {
-    const uint32_t L = pair_mul(x & 0x00ff00ffu, p) & 0x00ff00ffu;
-    const uint32_t H = pair_mul((x >> 8) & 0x00ff00ffu, p) & 0x00ff00ffu;
-    lo = f16_pair(L * 3u);
-    hi = f16_pair(H * 3u);
-}
-// Digits 0..ND-1 of both 16-bit-lane pairs of x, sequentially (remainder times 3).
-template <int ND>
-__device__ __forceinline__ void quads_seq(uint32_t x, uint32_t *lo, uint32_t *hi) {
-    uint32_t L = x & 0x00ff00ffu, H = (x >> 8) & 0x00ff00ffu;
-#pragma unroll
-    for (int k = 0; k < ND; ++k) {
-        const uint32_t mL = L * 3u, mH = H * 3u;
-        lo[k] = f16_pair(mL);
-        hi[k] = f16_pair(mH);
-        L = mL & 0x00ff00ffu;
-        H = mH & 0x00ff00ffu;
-    }
 }
 
 // Raw weight dwords of one block for a lane: the A piece (16 B), the B piece (8 B) and
@@ -232,72 +167,20 @@ __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t rs, uint32_t s
     for (int q = 0; q < 4; ++q) w.dd[q] = bload4(rs, seg + 24u * trp + 4u * (out0 + 8u * q));
 }
 
-// Decodes the lane's operand dwords aw[g][j][0..3] (8 f16 each) for half h.
-__device__ __forceinline__ void decode_block(const RawBlock &w, uint32_t h, uint32_t aw[4][2][4]) {
-    // g0 / g1: A_{2h}, A_{2h+1}, digits 0..3
-    {
-        uint32_t lo[4], hi[4];
-        quads_seq<4>(h ? w.a.z : w.a.x, lo, hi);
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            aw[g][0][0] = lo[2 * g];
-            aw[g][0][1] = hi[2 * g];
-            aw[g][0][2] = lo[2 * g + 1];
-            aw[g][0][3] = hi[2 * g + 1];
-        }
-        quads_seq<4>(h ? w.a.w : w.a.y, lo, hi);
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            aw[g][1][0] = lo[2 * g];
-            aw[g][1][1] = hi[2 * g];
-            aw[g][1][2] = lo[2 * g + 1];
-            aw[g][1][3] = hi[2 * g + 1];
-        }
-    }
-    // g2: h=0: (A_i, 4); h=1: (B_{i/2}, i%2)
-    {
-        const uint32_t src[4] = {h ? w.b.x : w.a.x, h ? w.b.x : w.a.y, h ? w.b.y : w.a.z, h ? w.b.y : w.a.w};
-        const uint32_t p0 = h ? 0x00010001u : 0x00510051u, p1 = h ? 0x00030003u : 0x00510051u;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) quad_at(src[i], (i & 1) ? p1 : p0, aw[2][i >> 1][2 * (i & 1)], aw[2][i >> 1][2 * (i & 1) + 1]);
-    }
-    // g3: (B_h, 2..4) and the tail digits 2h, 2h+1
-    {
-        uint32_t lo[3], hi[3];
-        const uint32_t y = h ? w.b.y : w.b.x;
-        uint32_t L = ((y & 0x00ff00ffu) * 9u) & 0x00ff00ffu, H = (((y >> 8) & 0x00ff00ffu) * 9u) & 0x00ff00ffu;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            const uint32_t mL = L * 3u, mH = H * 3u;
-            lo[k] = f16_pair(mL);
-            hi[k] = f16_pair(mH);
-            L = mL & 0x00ff00ffu;
-            H = mH & 0x00ff00ffu;
-        }
-        aw[3][0][0] = lo[0];
-        aw[3][0][1] = hi[0];
-        aw[3][0][2] = lo[1];
-        aw[3][0][3] = hi[1];
-        aw[3][1][0] = lo[2];
-        aw[3][1][1] = hi[2];
-        const uint32_t trep = perm(w.tl, w.tl, sel_bytes(0, 1, 0, 1));
-        quad_at(trep, h ? (9u | (27u << 16)) : (1u | (3u << 16)), aw[3][1][2], aw[3][1][3]);
-    }
-}
-
-// The pinned operand order (pinned_pair_base): for group g and native lane l, half h
-// supplies pair h of quads l and l + 4, which come from (tools/ternary/src/lib.rs:202-250
-// element map; (D, k) = code dword D at digit k)
-//   g0: (A_l, 0) (A_l, 1)      g1: (A_l, 2) (A_l, 3)      g2: (A_l, 4) (B_{l%2}, l/2)
-//   g3: (B_{l%2}, 2 + l/2), then (B_l, 4) for l < 2 or the tail quads 120, 124,
+// The weight side of the operand order (pair_base): half h needs pair h of every quad of
+// the block.  Quad q of group g comes from (tools/ternary/src/lib.rs:202-250 element map;
+// (D, k) = code dword D at digit k)
+//   g0: q<4 (A_q, 0), else (A_{q-4}, 1)        g1: q<4 (A_q, 2), else (A_{q-4}, 3)
+//   g2: q<4 (A_q, 4), else (B_{q%2}, (q-4)/2)  g3: q<4 (B_{q%2}, 2 + q/2), q = 4, 5 (B_{q-4}, 4),
+//   q = 6, 7 the tail quads 120, 124,
 // so a lane decodes bytes h and h + 2 of every code dword (digits 0..4) and byte 24 + h of
 // the tail (digits 0..3): half of the block's elements.  Every dword's digits are used in
-// order, so the decoder runs group by group, holding one group's operands at a time:
-// group(g, aw) yields aw[l][0..1] for the four native lanes.
-struct PinnedDecoder {
+// order, so the decoder runs group by group: group(g, aw) yields aw[l][i] = pair h of quad
+// l + 4i (l = 0..3, i = 0..1).
+struct PairDecoder {
     uint32_t la[4], lb[2], tb;  // remaining 16-bit-lane byte pairs; the tail byte twice
 
-    __device__ __forceinline__ PinnedDecoder(const RawBlock &w, uint32_t h) {
+    __device__ __forceinline__ PairDecoder(const RawBlock &w, uint32_t h) {
         const uint32_t sel = h ? sel_bytes(1, 12, 3, 12) : sel_bytes(0, 12, 2, 12);  // bytes h, h+2
         la[0] = perm(w.a.x, w.a.x, sel);
         la[1] = perm(w.a.y, w.a.y, sel);
@@ -423,10 +306,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
     // Block u from (act, scl) while block u+1 streams into (act_next, scl_next).
     auto block = [&](uint32_t u, const uint8_t (&act)[8][2][kRun], const float4 (&scl)[NT],
                      uint8_t (&act_next)[8][2][kRun], float4 (&scl_next)[NT]) {
-        uint32_t aw[4][2][4];
+        uint32_t aw[4][4][2];  // [g][i][j]: pair h of quad 4j + i of group g
         float d[16];
         if (active) {
-            decode_block(w, h, aw);
+            PairDecoder dec(w, h);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) dec.group(g, aw[g]);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 d[4 * q] = h2f(w.dd[q].x >> 16);
@@ -452,7 +337,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const v8h bx = *reinterpret_cast<const v8h *>(&act[2 * g + j][h][(32 * ct + r32) * 16]);
-                        const v8h ax = __builtin_bit_cast(v8h, u32x4{aw[g][j][0], aw[g][j][1], aw[g][j][2], aw[g][j][3]});
+                        const v8h ax = __builtin_bit_cast(v8h, u32x4{aw[g][0][j], aw[g][1][j], aw[g][2][j], aw[g][3][j]});
                         a = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, bx, a, 0, 0, 0);
                     }
                     // T = fl(T + sc_g * I_g): sc_g * I_g is exact, so one FMA (the first
@@ -563,7 +448,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     lds_barrier();
     auto block = [&](uint32_t u, const uint8_t (&act)[32][kRun], const float4 (&scl)[NT],
                      uint8_t (&act_next)[32][kRun], float4 (&scl_next)[NT]) {
-        PinnedDecoder dec(w, h);
+        PairDecoder dec(w, h);
         const float dw = h ? 0.0f : h2f(w.tl >> 16);  // the lane's row scale in half 0, zero in half 1
         if (u + 1 < nu) {
             stage(u + 1, act_next, scl_next);
@@ -649,13 +534,17 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
     float *sc = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + ((static_cast<size_t>(Mp) * K * 2 + 255) & ~size_t(255)));
     const uint32_t chunks = (K + 1023) / 1024;
     const uint64_t items = static_cast<uint64_t>(Mp) * chunks;
-    static_assert(kTokAlign % kPrepTokens == 0, "pinned prep takes whole token groups");
-    if (pinned)
-        hipLaunchKernelGGL(k_prefill_prep_pinned, dim3(static_cast<uint32_t>(items / kPrepTokens)),
-                           dim3(64 * kPrepTokens), 0, s, x, M, Mp, K, xh, sc, err);
+    static_assert(kTokAlign % 16 == 0, "the prep takes whole token groups");
+    const bool wide = Mp >= 1024;  // measured: 16 tokens per workgroup from 1024 tokens
+    const dim3 pgrid(static_cast<uint32_t>(items / (wide ? 16 : 4))), pblock(wide ? 1024 : 256);
+    if (pinned && wide)
+        hipLaunchKernelGGL((k_prefill_prep<true, 16>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
+    else if (pinned)
+        hipLaunchKernelGGL((k_prefill_prep<true, 4>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
+    else if (wide)
+        hipLaunchKernelGGL((k_prefill_prep<false, 16>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
     else
-        hipLaunchKernelGGL(k_prefill_prep, dim3(static_cast<uint32_t>((items + 3) / 4)), dim3(256), 0, s, x, M, Mp, K,
-                           xh, sc, err);
+        hipLaunchKernelGGL((k_prefill_prep<false, 4>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
     if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
     const auto W = static_cast<const uint8_t *>(w_tiled);
