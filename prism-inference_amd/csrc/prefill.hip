@@ -300,32 +300,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
 
     RawBlock w;
     stage(0, act0, scl0);
-    if (active) load_block(rw, 0, trp, row, out0, w);
+    if (active) load_block_codes(rw, 0, trp, row, w);
     wait_vmcnt0();
     lds_barrier();
     // Block u from (act, scl) while block u+1 streams into (act_next, scl_next).
     auto block = [&](uint32_t u, const uint8_t (&act)[8][2][kRun], const float4 (&scl)[NT],
                      uint8_t (&act_next)[8][2][kRun], float4 (&scl_next)[NT]) {
         uint32_t aw[4][4][2];  // [g][i][j]: pair h of quad 4j + i of group g
-        float d[16];
+        float dw = 0.0f;       // the lane's row scale in half 0, zero in half 1
         if (active) {
             PairDecoder dec(w, h);
 #pragma unroll
             for (int g = 0; g < 4; ++g) dec.group(g, aw[g]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                d[4 * q] = h2f(w.dd[q].x >> 16);
-                d[4 * q + 1] = h2f(w.dd[q].y >> 16);
-                d[4 * q + 2] = h2f(w.dd[q].z >> 16);
-                d[4 * q + 3] = h2f(w.dd[q].w >> 16);
-            }
+            dw = h ? 0.0f : h2f(w.tl >> 16);
         }
         // The next block streams in while this one is multiplied.
         if (u + 1 < nu) {
             stage(u + 1, act_next, scl_next);
-            if (active) load_block(rw, (u + 1) * trp * 28u, trp, row, out0, w);
+            if (active) load_block_codes(rw, (u + 1) * trp * 28u, trp, row, w);
         }
         if (active) {
+            // The scales d_w of the lane's 16 output rows, in the MFMA output layout: the
+            // outer product of the rows' scales with ones (exact).
+            const v16f d = __builtin_amdgcn_mfma_f32_32x32x2f32(dw, h ? 0.0f : 1.0f, v16f{}, 0, 0, 0);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
                 const float4 sg4 = scl[32 * ct + r32];
