@@ -555,9 +555,9 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
     }
     // Tokens per workgroup (measured, 6144 x 2048): 64 keeps three wavefronts per SIMD
     // and beats 128 (two per SIMD, the decode shared by more tokens) up to about 4096
-    // tokens; 32 keeps CUs busy on short prompts (256 tokens: 181 against 170 TOPS; even
-    // at 512).
-    const uint32_t nt = M >= 4096 ? 128 : M >= 512 ? 64 : 32, groups = Mp / nt;
+    // tokens (4096: 232 against 241-246 us); 32 (four wavefronts per SIMD) keeps CUs busy
+    // on short prompts up to 512 tokens (512: 45.0 against 46.6 us; 768: 65.4 against 64.2).
+    const uint32_t nt = M >= 4096 ? 128 : M > 512 ? 64 : 32, groups = Mp / nt;
     const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
     const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
     if (nt == 128)
