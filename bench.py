@@ -50,9 +50,9 @@ HIDDEN, FFN = 2048, 6144
 CPU_THREADS = 16  # the host-core share of one GPU on the measurement box
 DECODE_POS = 1024
 # Prefill GEMM VALU-issue ceiling: per wavefront and 128-deep block of 32 rows x 64
-# tokens, the counted instruction mix is 440 VALU instructions (16 of them MFMA), and a
+# tokens, the counted instruction mix is 399 VALU instructions (17 of them MFMA), and a
 # SIMD issues one wave64 VALU instruction per 4 cycles (profiles/prefill_gemm_6144x2048.md).
-PREFILL_VALU_PER_BLOCK = 440
+PREFILL_VALU_PER_BLOCK = 399
 PREFILL_OPS_PER_BLOCK = 2 * 32 * 64 * 128
 ENGINE_HZ = 2.4e9
 CUS = 256
