@@ -165,32 +165,6 @@ __device__ __forceinline__ uint2 lut_at(uint32_t x, uint32_t lbase, uint32_t b) 
     return *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(g_ptq1_lut) + addr);
 }
 
-// The unit's 32 quads from the table: f(q, t) receives quad q (elements 4q..4q+3,
-// trits minus one as signed bytes).  The four entries of a code dword are transposed
-// (8 v_perm) into the natural quads (digit k of bytes 4w..4w+3), so the activation
-// keeps its natural order.
-template <typename F>
-__device__ __forceinline__ void ptq1_quads_lut(const uint32_t x[7], uint32_t lbase, F &&f) {
-#pragma unroll
-    for (int w = 0; w < 6; ++w) {
-        const uint2 e0 = lut_at(x[w], lbase, 0), e1 = lut_at(x[w], lbase, 1);
-        const uint2 e2 = lut_at(x[w], lbase, 2), e3 = lut_at(x[w], lbase, 3);
-        const uint32_t l01 = perm(e1.x, e0.x, sel(0, 4, 1, 5)), h01 = perm(e1.x, e0.x, sel(2, 6, 3, 7));
-        const uint32_t l23 = perm(e3.x, e2.x, sel(0, 4, 1, 5)), h23 = perm(e3.x, e2.x, sel(2, 6, 3, 7));
-        uint32_t T[5];
-        T[0] = perm(l23, l01, sel(0, 1, 4, 5));
-        T[1] = perm(l23, l01, sel(2, 3, 6, 7));
-        T[2] = perm(h23, h01, sel(0, 1, 4, 5));
-        T[3] = perm(h23, h01, sel(2, 3, 6, 7));
-        T[4] = perm(e1.y, e0.y, sel(0, 4, 12, 12)) | perm(e3.y, e2.y, sel(12, 12, 0, 4));
-#pragma unroll
-        for (int k = 0; k < 5; ++k) f(w < 4 ? 4 * k + w : 20 + 2 * k + (w - 4), T[k]);
-    }
-    const uint2 e0 = lut_at(x[6], lbase, 0), e1 = lut_at(x[6], lbase, 1);
-    f(30, perm(e1.x, e0.x, sel(0, 4, 1, 5)));
-    f(31, perm(e1.x, e0.x, sel(2, 6, 3, 7)));
-}
-
 // The unit's 32 quads from the table in slot order, for kernels that stage the
 // activation in the same order (an integer dot is exact in any element order):
 // f(s, t) receives slot s.  Slots 5w..5w+4 come from code dword w < 6 (entries
@@ -264,13 +238,52 @@ constexpr int kPtq1LaneSlots[4][4][2] = {{{0, 1}, {5, 6}, {10, 11}, {15, 16}},
                                          {{4, 20}, {9, 25}, {14, 21}, {19, 26}},
                                          {{22, 24}, {27, 29}, {23, 30}, {28, 31}}};
 
-// Same contract as ptq1_dots, but acc(q) receives sum (t-1)*a directly.
-template <typename Act, typename Acc>
+// Same contract as ptq1_dots, but acc(q) receives sum (t-1)*a directly, from the table
+// in a "pair" order that costs one v_perm per dword on the weight side: for code dword w
+// (bytes b0..b3) and digits (k, k+1), (E0.dk, E1.dk, E0.dk+1, E1.dk+1) and the same of E2,
+// E3 pair with the activation halves pk_ll / pk_hh of the natural dwords of digits k and
+// k+1 -- wave-uniform values, so the repacking runs on the scalar unit (s_pack_*_b32_b16)
+// beside the vector decode.  Digit 4 of each dword and code dword 6 keep their natural
+// quads.  acc(q) is called with the natural index q of the slot's first quad; the slot's
+// elements lie in q's 32-element group and, for NATIVE below, in q's native lane subset
+// (positions 4l..4l+3 and 16+4l..16+4l+3 of the group): code dwords 4 and 5 pair positions
+// of two native lanes, so NATIVE keeps their natural quads.
+template <bool NATIVE = false, typename Act, typename Acc>
 __device__ __forceinline__ void ptq1_dots_lut(const uint32_t x[7], uint32_t lbase, const Act &a, Acc &&acc) {
-    ptq1_quads_lut(x, lbase, [&](int q, uint32_t t) {
+    auto dot = [&](int q, uint32_t t, uint32_t av) {
         int &r = acc(q);
-        r = sdot4(t, a(q), r);
-    });
+        r = sdot4(t, av, r);
+    };
+#pragma unroll
+    for (int w = 0; w < 6; ++w) {
+        const uint2 e0 = lut_at(x[w], lbase, 0), e1 = lut_at(x[w], lbase, 1);
+        const uint2 e2 = lut_at(x[w], lbase, 2), e3 = lut_at(x[w], lbase, 3);
+        auto nat = [&](int k) { return w < 4 ? 4 * k + w : 20 + 2 * k + (w - 4); };  // natural quad of digit k
+        if (NATIVE && w >= 4) {
+            const uint32_t l01 = perm(e1.x, e0.x, sel(0, 4, 1, 5)), h01 = perm(e1.x, e0.x, sel(2, 6, 3, 7));
+            const uint32_t l23 = perm(e3.x, e2.x, sel(0, 4, 1, 5)), h23 = perm(e3.x, e2.x, sel(2, 6, 3, 7));
+            dot(nat(0), perm(l23, l01, sel(0, 1, 4, 5)), a(nat(0)));
+            dot(nat(1), perm(l23, l01, sel(2, 3, 6, 7)), a(nat(1)));
+            dot(nat(2), perm(h23, h01, sel(0, 1, 4, 5)), a(nat(2)));
+            dot(nat(3), perm(h23, h01, sel(2, 3, 6, 7)), a(nat(3)));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k += 2) {
+                const uint32_t x0 = a(nat(k)), x1 = a(nat(k + 1));
+                typedef uint16_t h2 __attribute__((ext_vector_type(2)));  // s_pack_ll / s_pack_hh
+                const uint32_t lo = __builtin_bit_cast(uint32_t, h2{static_cast<uint16_t>(x0), static_cast<uint16_t>(x1)});
+                const uint32_t hi =
+                    __builtin_bit_cast(uint32_t, h2{static_cast<uint16_t>(x0 >> 16), static_cast<uint16_t>(x1 >> 16)});
+                const uint32_t s01 = k ? sel(2, 6, 3, 7) : sel(0, 4, 1, 5);
+                dot(nat(k), perm(e1.x, e0.x, s01), lo);
+                dot(nat(k), perm(e3.x, e2.x, s01), hi);
+            }
+        }
+        dot(nat(4), perm(e1.y, e0.y, sel(0, 4, 12, 12)) | perm(e3.y, e2.y, sel(12, 12, 0, 4)), a(nat(4)));
+    }
+    const uint2 e0 = lut_at(x[6], lbase, 0), e1 = lut_at(x[6], lbase, 1);
+    dot(30, perm(e1.x, e0.x, sel(0, 4, 1, 5)), a(30));
+    dot(31, perm(e1.x, e0.x, sel(2, 6, 3, 7)), a(31));
 }
 
 // PQ2 code dword i holds elements 16i..16i+15, element 16i+4q+p in byte q, bits 2p.
@@ -395,7 +408,7 @@ __device__ __forceinline__ void unit_terms(const W &w, const void *__restrict__ 
         if constexpr (std::is_same_v<W, Ptq1Dec>)
             ptq1_dot(raw, a, acc);
         else if constexpr (LUT)
-            ptq1_dots_lut(raw.x, lbase, a, acc);
+            ptq1_dots_lut<O == Op::PTQ1_PINNED>(raw.x, lbase, a, acc);
         else
             ptq1_dots(raw.x, a, acc);
     };
