@@ -532,14 +532,16 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
     const uint32_t chunks = (K + 1023) / 1024;
     const uint64_t items = static_cast<uint64_t>(Mp) * chunks;
     static_assert(kTokAlign % 16 == 0, "the prep takes whole token groups");
-    const bool wide = Mp >= 1024;  // measured: 16 tokens per workgroup from 1024 tokens
+    // Measured (prep alone, 2048 tokens): pinned 8.5 us with 16 tokens per workgroup, 13.4
+    // with one token per wavefront and 8-byte stores; source 8.2 with 4 tokens, 10.6 with
+    // 16, 9.3 with one token per wavefront.  Short prompts take 4 in both: 16 would leave
+    // most CUs idle.
+    const bool wide = pinned && Mp >= 1024;
     const dim3 pgrid(static_cast<uint32_t>(items / (wide ? 16 : 4))), pblock(wide ? 1024 : 256);
-    if (pinned && wide)
+    if (wide)
         hipLaunchKernelGGL((k_prefill_prep<true, 16>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
     else if (pinned)
         hipLaunchKernelGGL((k_prefill_prep<true, 4>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
-    else if (wide)
-        hipLaunchKernelGGL((k_prefill_prep<false, 16>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
     else
         hipLaunchKernelGGL((k_prefill_prep<false, 4>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
     if (const int e = launch_status()) return e;
