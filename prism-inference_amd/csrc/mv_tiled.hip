@@ -1917,11 +1917,27 @@ constexpr uint32_t kQuadMaxCols = 16384;
 
 template <Op O>
 constexpr bool quad_supported() {
-    return O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED || O == Op::Q8_0;
+    return O == Op::PTQ1_SRC || O == Op::PTQ1_PINNED || O == Op::Q8_0 || O == Op::Q2K;
+}
+
+// Staged activation per unit: LDS dwords per (unit, token) row -- Q8_0 units (128
+// elements) 32 codes, Q2_K units (one Q8_K block of 256) 64, plus 4 of padding -- and
+// scales per unit (Q8_0: [group][token], Q8_K: [token]).
+template <Op O>
+constexpr uint32_t quad_row_dw() {
+    return O == Op::Q2K ? 68u : kQuadRowDw;
+}
+template <Op O>
+constexpr uint32_t quad_unit_scales() {
+    return O == Op::Q2K ? kQuadTok : 4u * kQuadTok;
+}
+template <Op O>
+constexpr uint32_t quad_unit_lds() {
+    return (kQuadTok * quad_row_dw<O>() + quad_unit_scales<O>()) * static_cast<uint32_t>(sizeof(uint32_t));
 }
 
 // Threads per workgroup: the PTQ1 table (64 KiB of LDS) is filled once per CU for 16
-// wavefronts; Q8_0 needs no table and runs four.
+// wavefronts; Q8_0 and Q2_K need no table and run four.
 template <Op O>
 constexpr uint32_t quad_threads() {
     return kind_of<O>() == kPTQ1 ? 1024u : 256u;
@@ -1951,83 +1967,124 @@ template <Op O, bool TERMS = false>
 __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, const float *qs, uint32_t lbase,
                                           QuadChain<O> &ch) {
     static_assert(!TERMS || O == Op::PTQ1_SRC, "one term per unit and token");
-    uint32_t A[32];
+    if constexpr (O == Op::Q2K) {
+        // kquants::dot per token (dot_q2_k_block, src/kernels/kquants.rs:193-196): isum =
+        // sum_g scale_g * dot_g and msum = sum_g min_g * bsum_g, exact integers.  The weight
+        // operand carries scale_g * q (at most 45, still a byte); a second product with
+        // min_g repeated gives min_g times the sub-block's activation sum.  Code dword 8h +
+        // wh, field p holds elements 128h + 32p + 4wh..+3 of sub-block g = 8h + 2p + wh/4,
+        // which meet the natural activation dword 32h + 8p + wh; four interleaved
+        // accumulator chains of each sum, added at the end.
+        v4i is[4] = {}, ms[4] = {};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(qa + 4 * i);
-        A[4 * i] = v.x; A[4 * i + 1] = v.y; A[4 * i + 2] = v.z; A[4 * i + 3] = v.w;
-    }
-    float S[4][kQuadTok];
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const float4 v = *reinterpret_cast<const float4 *>(qs + 4 * g);
-        S[g][0] = v.x; S[g][1] = v.y; S[g][2] = v.z; S[g][3] = v.w;
-    }
-    // PTQ1 weights and activations are both in ptq1_slots_lut's slot order; Q8_0's in the
-    // natural order (slot 8g + i is quad i of group g).
-    uint32_t W[32];
-    if constexpr (kind_of<O>() == kPTQ1) {
-        ptq1_slots_lut<O == Op::PTQ1_PINNED>(w.x, lbase, [&](int s, uint32_t t) { W[s] = t; });
-    } else {
+            for (int p = 0; p < 4; ++p) {
+                const u32x4 a0 = *reinterpret_cast<const u32x4 *>(qa + 32 * h + 8 * p);
+                const u32x4 a1 = *reinterpret_cast<const u32x4 *>(qa + 32 * h + 8 * p + 4);
+                const uint32_t A[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
-        for (int q = 0; q < 32; ++q) W[q] = w.c[q];
-    }
-    auto slot = [](int g, int i) { return kind_of<O>() == kPTQ1 ? kPtq1GroupSlots[g][i] : 8 * g + i; };
-    if constexpr (O == Op::PTQ1_PINNED) {
-        // dot_q8_groups_pinned, src/kernels.rs:1134-1146: native lane l sums positions
-        // 4l..4l+3 and 16+4l..16+4l+3 of the group (two slots), then
-        // L[l] = fma(I_l, d * scale_g, L[l]).
-        const float d = h2f(ptq1_scale_bits(w));
+                for (int half = 0; half < 2; ++half) {
+                    const int g = 8 * h + 2 * p + half;
+                    const uint32_t byte = (w.sc[g >> 2] >> (8 * (g & 3))) & 0xffu;
+                    const uint32_t scale = byte & 15u, mn = (byte >> 4) * 0x01010101u;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v4i acc[4];
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const int s = kPtq1LaneSlots[g][l][0];
-                acc[l] = mfma4(A[s], W[s], v4i{0, 0, 0, 0});
-            }
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const int s = kPtq1LaneSlots[g][l][1];
-                acc[l] = mfma4(A[s], W[s], acc[l]);
-            }
-#pragma unroll
-            for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
-                const float dd = d * S[g][t];
-#pragma unroll
-                for (int l = 0; l < 4; ++l)
-                    ch.L[l][t] = __builtin_fmaf(static_cast<float>(acc[l][t]), dd, ch.L[l][t]);
+                    for (int i = 0; i < 4; ++i) {
+                        const int wh = 4 * half + i;
+                        const uint32_t q = (w.q[8 * h + wh] >> (2 * p)) & 0x03030303u;
+                        is[i] = mfma4(A[wh], bytes_times(q, scale), is[i]);
+                        ms[i] = mfma4(A[wh], mn, ms[i]);
+                    }
+                }
             }
         }
+        const float d = h2f(w.dm & 0xffffu), dmin = h2f(w.dm >> 16);
+#pragma unroll
+        for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
+            const int isum = (is[0][t] + is[1][t]) + (is[2][t] + is[3][t]);
+            const int msum = (ms[0][t] + ms[1][t]) + (ms[2][t] + ms[3][t]);
+            const float as = qs[t];
+            ch.o[t] = ch.o[t] + ((as * d) * static_cast<float>(isum) - (as * dmin) * static_cast<float>(msum));
+        }
     } else {
-        // The four groups' integer dots as four interleaved accumulator chains.
-        v4i acc[4] = {};
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) acc[g] = mfma4(A[slot(g, i)], W[slot(g, i)], acc[g]);
-        if constexpr (O == Op::PTQ1_SRC) {
-            // dot_q8_groups, src/kernels.rs:1043-1064
+        uint32_t A[32];
+    #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(qa + 4 * i);
+            A[4 * i] = v.x; A[4 * i + 1] = v.y; A[4 * i + 2] = v.z; A[4 * i + 3] = v.w;
+        }
+        float S[4][kQuadTok];
+    #pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 v = *reinterpret_cast<const float4 *>(qs + 4 * g);
+            S[g][0] = v.x; S[g][1] = v.y; S[g][2] = v.z; S[g][3] = v.w;
+        }
+        // PTQ1 weights and activations are both in ptq1_slots_lut's slot order; Q8_0's in the
+        // natural order (slot 8g + i is quad i of group g).
+        uint32_t W[32];
+        if constexpr (kind_of<O>() == kPTQ1) {
+            ptq1_slots_lut<O == Op::PTQ1_PINNED>(w.x, lbase, [&](int s, uint32_t t) { W[s] = t; });
+        } else {
+    #pragma unroll
+            for (int q = 0; q < 32; ++q) W[q] = w.c[q];
+        }
+        auto slot = [](int g, int i) { return kind_of<O>() == kPTQ1 ? kPtq1GroupSlots[g][i] : 8 * g + i; };
+        if constexpr (O == Op::PTQ1_PINNED) {
+            // dot_q8_groups_pinned, src/kernels.rs:1134-1146: native lane l sums positions
+            // 4l..4l+3 and 16+4l..16+4l+3 of the group (two slots), then
+            // L[l] = fma(I_l, d * scale_g, L[l]).
             const float d = h2f(ptq1_scale_bits(w));
-#pragma unroll
-            for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
-                float tt = 0.0f;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) tt = tt + S[g][t] * static_cast<float>(acc[g][t]);
-                if constexpr (TERMS)
-                    ch.o[t] = d * tt;
-                else
-                    ch.o[t] = ch.o[t] + d * tt;
+    #pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                v4i acc[4];
+    #pragma unroll
+                for (int l = 0; l < 4; ++l) {
+                    const int s = kPtq1LaneSlots[g][l][0];
+                    acc[l] = mfma4(A[s], W[s], v4i{0, 0, 0, 0});
+                }
+    #pragma unroll
+                for (int l = 0; l < 4; ++l) {
+                    const int s = kPtq1LaneSlots[g][l][1];
+                    acc[l] = mfma4(A[s], W[s], acc[l]);
+                }
+    #pragma unroll
+                for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
+                    const float dd = d * S[g][t];
+    #pragma unroll
+                    for (int l = 0; l < 4; ++l)
+                        ch.L[l][t] = __builtin_fmaf(static_cast<float>(acc[l][t]), dd, ch.L[l][t]);
+                }
             }
         } else {
-            // dot_legacy, src/kernels.rs:1241-1244; the row's chain adds the four group
-            // terms in order.
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float sw = h2f((w.s[g >> 1] >> (16 * (g & 1))) & 0xffffu);
-#pragma unroll
-                for (int t = 0; t < static_cast<int>(kQuadTok); ++t)
-                    ch.o[t] = ch.o[t] + (sw * S[g][t]) * static_cast<float>(acc[g][t]);
+            // The four groups' integer dots as four interleaved accumulator chains.
+            v4i acc[4] = {};
+    #pragma unroll
+            for (int i = 0; i < 8; ++i)
+    #pragma unroll
+                for (int g = 0; g < 4; ++g) acc[g] = mfma4(A[slot(g, i)], W[slot(g, i)], acc[g]);
+            if constexpr (O == Op::PTQ1_SRC) {
+                // dot_q8_groups, src/kernels.rs:1043-1064
+                const float d = h2f(ptq1_scale_bits(w));
+    #pragma unroll
+                for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
+                    float tt = 0.0f;
+    #pragma unroll
+                    for (int g = 0; g < 4; ++g) tt = tt + S[g][t] * static_cast<float>(acc[g][t]);
+                    if constexpr (TERMS)
+                        ch.o[t] = d * tt;
+                    else
+                        ch.o[t] = ch.o[t] + d * tt;
+                }
+            } else {
+                // dot_legacy, src/kernels.rs:1241-1244; the row's chain adds the four group
+                // terms in order.
+    #pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float sw = h2f((w.s[g >> 1] >> (16 * (g & 1))) & 0xffffu);
+    #pragma unroll
+                    for (int t = 0; t < static_cast<int>(kQuadTok); ++t)
+                        ch.o[t] = ch.o[t] + (sw * S[g][t]) * static_cast<float>(acc[g][t]);
+                }
             }
         }
     }
@@ -2042,6 +2099,18 @@ constexpr uint32_t kQuadUnitLds = (kQuadTok * kQuadRowDw + 4 * kQuadTok) * sizeo
 template <Op O>
 __device__ __forceinline__ void quad_stage(const void *__restrict__ act, uint32_t act_stride, uint32_t ntok,
                                            uint32_t nu, uint32_t *codes, float *scales) {
+    if constexpr (O == Op::Q2K) {
+        // Q8_K blocks, one per unit: codes as [unit][token][68 dwords], scales as [unit][token].
+        for (uint32_t i = threadIdx.x; i < nu * kQuadTok * 64u; i += blockDim.x) {
+            const uint32_t dw = i & 63u, t = (i >> 6) & 3u, u = i >> 8;
+            const Q8KBlock *blk = reinterpret_cast<const Q8KBlock *>(static_cast<const uint8_t *>(act) +
+                                                                     static_cast<size_t>(t < ntok ? t : ntok - 1) *
+                                                                         act_stride) + u;
+            codes[(u * kQuadTok + t) * quad_row_dw<O>() + dw] = reinterpret_cast<const uint32_t *>(blk->values)[dw];
+            if (dw == 0) scales[u * kQuadTok + t] = blk->scale;
+        }
+        return;
+    }
     for (uint32_t i = threadIdx.x; i < nu * 128u; i += blockDim.x) {
         const uint32_t dw = i & 7u, t = (i >> 3) & 3u, g = (i >> 5) & 3u, u = i >> 7;
         const Q8Block *blk = reinterpret_cast<const Q8Block *>(static_cast<const uint8_t *>(act) +
@@ -2072,9 +2141,10 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
     extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
     constexpr uint32_t UB = unit_bytes<O>();
     constexpr uint32_t kWaves = quad_threads<O>() / 64;
+    constexpr uint32_t RDW = quad_row_dw<O>(), USC = quad_unit_scales<O>();
     const uint32_t nu = p.nu;
     uint32_t *codes = quad_lds;
-    float *scales = reinterpret_cast<float *>(quad_lds + nu * kQuadTok * kQuadRowDw);
+    float *scales = reinterpret_cast<float *>(quad_lds + nu * kQuadTok * RDW);
     if constexpr (kind_of<O>() == kPTQ1) ptq1_lut_fill(threadIdx.x, blockDim.x);
     quad_stage<O>(act, act_stride, ntok, nu, codes, scales);
     __syncthreads();
@@ -2082,7 +2152,7 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t tiles = (p.rows + kTile - 1) / kTile;
     const uint32_t lbase = 8u * (lane & 31u);
-    const uint32_t *qa = codes + (lane & 3u) * kQuadRowDw;
+    const uint32_t *qa = codes + (lane & 3u) * RDW;
     const uint32_t row_bytes = nu * UB;
     // Wave-uniform by construction (the buffer descriptors below must live in SGPRs).
     const uint32_t grid = __builtin_amdgcn_readfirstlane(gridDim.x);
@@ -2105,9 +2175,7 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
         if (u < u1) step(A, u);
     };
     auto chain = [&](QuadChain<O> &ch) {
-        return [&](const Raw<O> &w, uint32_t u) {
-            quad_unit<O>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, ch);
-        };
+        return [&](const Raw<O> &w, uint32_t u) { quad_unit<O>(w, qa + u * kQuadTok * RDW, scales + u * USC, lbase, ch); };
     };
     auto store = [&](uint32_t tile, const QuadChain<O> &ch) {
         const uint32_t left = p.rows - tile * kTile;
@@ -2137,7 +2205,7 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
         // pair leaving its units' terms in LDS ([slot][unit - nh][token][row]) for the
         // first, which continues its chains with them in unit order after the barrier.
         static_assert(O == Op::PTQ1_SRC && kWaves == 16, "single-term order, 16 wavefronts");
-        float *second = scales + nu * 4 * kQuadTok;
+        float *second = scales + nu * USC;
         const uint32_t nh = (nu + 1) / 2, n2 = nu - nh;
         const uint32_t slot = (wave - 8) >> 1, half = wave & 1u;
         const uint32_t tile = wave < 8 ? wave * grid + blockIdx.x : 8 * grid + slot * grid + blockIdx.x;
@@ -2153,7 +2221,7 @@ __global__ __launch_bounds__(quad_threads<O>()) void k_mv_quad(MvParams p, const
                 float *mine = second + static_cast<size_t>(slot) * n2 * kQuadTok * kTile;
                 walk(tile, nh, nu, [&](const Raw<O> &w, uint32_t u) {
                     QuadChain<O> tc;
-                    quad_unit<O, true>(w, qa + u * kQuadTok * kQuadRowDw, scales + u * 4 * kQuadTok, lbase, tc);
+                    quad_unit<O, true>(w, qa + u * kQuadTok * RDW, scales + u * USC, lbase, tc);
 #pragma unroll
                     for (uint32_t t = 0; t < kQuadTok; ++t) mine[((u - nh) * kQuadTok + t) * kTile + lane] = tc.o[t];
                 });
@@ -2643,7 +2711,7 @@ int launch_quad(const MatvecArgs &a, uint32_t act_stride) {
         p.out = a.out;
         p.residual = a.residual;
         p.err = a.err;
-        const size_t lds = static_cast<size_t>(p.nu) * kQuadUnitLds;
+        const size_t lds = static_cast<size_t>(p.nu) * quad_unit_lds<O>();
         constexpr uint32_t kWaves = quad_threads<O>() / 64;
         const uint64_t tiles = (a.rows + kTile - 1) / kTile;
         // PTQ1: one workgroup per CU walks tiles (its table is filled once); Q8_0: one

@@ -481,6 +481,34 @@ def test_gpu_quad_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("cols,rows", [(256, 65536 + 37), (768, 65536 + 1), (1024, 131072 + 63)])
+def test_gpu_q2k_quad_batch_matches_per_token_oracle(ctx, cols, rows):
+    """Two to four tokens of a Q2_K matrix of 65536 rows or more run on the 4x4x4 int8
+    matrix cores, one row per lane: the weight operand carries scale * code and a second
+    product with the sub-block's min gives min * bsum, so both integer sums of
+    dot_q2_k_block are exact.  Every token's row must equal its own matvec, through the f32
+    entry (both Q8_K contracts) and through prepared Q8_K blocks, with a partial last tile
+    and one to four units per row."""
+    import oracle
+
+    kind = ph.KIND_Q2_K
+    w = synth.weights(kind, rows, cols, seed=47)
+    wid = ctx.weight(kind, cols, rows, w)
+    nq8k = cols // 256
+    for tokens in (2, 3, 4):
+        X = synth.activations(cols, seed=48 + tokens, tokens=tokens)
+        for pinned in (False, True):
+            ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+            got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned)
+            assert_bits_equal(got, ref, f"q2k quad f32 tokens={tokens} pinned={pinned}")
+            act = np.concatenate([oracle.quantize_q8k(X[t], pinned) for t in range(tokens)])
+            ref = np.stack([oracle.project_q8k(kind, cols, rows, w, act[t * nq8k:(t + 1) * nq8k], False,
+                                               threads=THREADS) for t in range(tokens)])
+            got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens)
+            assert_bits_equal(got, ref, f"q2k quad q8k tokens={tokens} pinned={pinned}")
+    ctx.release(wid)
+
+
 # ---- multi-token, groups, backend op -------------------------------------------------
 
 def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
