@@ -2008,13 +2008,13 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
         }
     } else {
         uint32_t A[32];
-    #pragma unroll
+#pragma unroll
         for (int i = 0; i < 8; ++i) {
             const u32x4 v = *reinterpret_cast<const u32x4 *>(qa + 4 * i);
             A[4 * i] = v.x; A[4 * i + 1] = v.y; A[4 * i + 2] = v.z; A[4 * i + 3] = v.w;
         }
         float S[4][kQuadTok];
-    #pragma unroll
+#pragma unroll
         for (int g = 0; g < 4; ++g) {
             const float4 v = *reinterpret_cast<const float4 *>(qs + 4 * g);
             S[g][0] = v.x; S[g][1] = v.y; S[g][2] = v.z; S[g][3] = v.w;
@@ -2025,7 +2025,7 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
         if constexpr (kind_of<O>() == kPTQ1) {
             ptq1_slots_lut<O == Op::PTQ1_PINNED>(w.x, lbase, [&](int s, uint32_t t) { W[s] = t; });
         } else {
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < 32; ++q) W[q] = w.c[q];
         }
         auto slot = [](int g, int i) { return kind_of<O>() == kPTQ1 ? kPtq1GroupSlots[g][i] : 8 * g + i; };
@@ -2034,23 +2034,23 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
             // 4l..4l+3 and 16+4l..16+4l+3 of the group (two slots), then
             // L[l] = fma(I_l, d * scale_g, L[l]).
             const float d = h2f(ptq1_scale_bits(w));
-    #pragma unroll
+#pragma unroll
             for (int g = 0; g < 4; ++g) {
                 v4i acc[4];
-    #pragma unroll
+#pragma unroll
                 for (int l = 0; l < 4; ++l) {
                     const int s = kPtq1LaneSlots[g][l][0];
                     acc[l] = mfma4(A[s], W[s], v4i{0, 0, 0, 0});
                 }
-    #pragma unroll
+#pragma unroll
                 for (int l = 0; l < 4; ++l) {
                     const int s = kPtq1LaneSlots[g][l][1];
                     acc[l] = mfma4(A[s], W[s], acc[l]);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
                     const float dd = d * S[g][t];
-    #pragma unroll
+#pragma unroll
                     for (int l = 0; l < 4; ++l)
                         ch.L[l][t] = __builtin_fmaf(static_cast<float>(acc[l][t]), dd, ch.L[l][t]);
                 }
@@ -2058,17 +2058,17 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
         } else {
             // The four groups' integer dots as four interleaved accumulator chains.
             v4i acc[4] = {};
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < 8; ++i)
-    #pragma unroll
+#pragma unroll
                 for (int g = 0; g < 4; ++g) acc[g] = mfma4(A[slot(g, i)], W[slot(g, i)], acc[g]);
             if constexpr (O == Op::PTQ1_SRC) {
                 // dot_q8_groups, src/kernels.rs:1043-1064
                 const float d = h2f(ptq1_scale_bits(w));
-    #pragma unroll
+#pragma unroll
                 for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
                     float tt = 0.0f;
-    #pragma unroll
+#pragma unroll
                     for (int g = 0; g < 4; ++g) tt = tt + S[g][t] * static_cast<float>(acc[g][t]);
                     if constexpr (TERMS)
                         ch.o[t] = d * tt;
@@ -2078,10 +2078,10 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
             } else {
                 // dot_legacy, src/kernels.rs:1241-1244; the row's chain adds the four group
                 // terms in order.
-    #pragma unroll
+#pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const float sw = h2f((w.s[g >> 1] >> (16 * (g & 1))) & 0xffffu);
-    #pragma unroll
+#pragma unroll
                     for (int t = 0; t < static_cast<int>(kQuadTok); ++t)
                         ch.o[t] = ch.o[t] + (sw * S[g][t]) * static_cast<float>(acc[g][t]);
                 }
