@@ -792,8 +792,17 @@ constexpr uint32_t kLutWaves = kLutThreads / 64;
 // whole one.  Their second halves' terms go to dynamic LDS, 64 rows x lut_tail_stride()
 // floats per pair, beside the 64 KiB table: pinned PTQ1 (nine terms per unit) fits two
 // pairs at 4096 columns, so it takes this form up to ten tiles per CU.
+// kLutSpread (fewer tiles than CUs, prepared activations): one workgroup per tile, its units
+// round-robin over the 16 wavefronts, each unit's terms for the tile's 64 rows left in
+// dynamic LDS ([unit][term][row], lut_spread_lds()), then wavefront 0 folds them in unit
+// order: the unsplit row's arithmetic with sixteen wavefronts decoding.
 constexpr uint32_t kLutSlots = kLutWaves / 2;
-constexpr int kLutWhole = 0, kLutSplit = 1, kLutTail = 2;
+constexpr int kLutWhole = 0, kLutSplit = 1, kLutTail = 2, kLutSpread = 3;
+template <Op O>
+inline uint32_t lut_spread_lds(uint32_t nu) {
+    const uint32_t bytes = nu * terms_per_unit<O>() * kTile * static_cast<uint32_t>(sizeof(float));
+    return bytes + sizeof(g_ptq1_lut) <= 160u * 1024u ? bytes : 0u;
+}
 template <Op O>
 __host__ __device__ constexpr bool lut_can_split() {
     return terms_per_unit<O>() == 1;
@@ -826,6 +835,50 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
         const uint32_t step = gridDim.x * kLutWaves;
         for (uint32_t tile = wave * gridDim.x + blockIdx.x; tile < tiles; tile += step)
             rows_tile<O, true>(p, act, tile, lane, lbase);
+    } else if constexpr (MODE == kLutSpread) {
+        extern __shared__ float spread_terms[];
+        constexpr uint32_t UB = unit_bytes<O>(), TPU = terms_per_unit<O>();
+        const uint32_t tile = blockIdx.x, nu = p.nu;
+        const uint32_t left = p.rows - tile * kTile;
+        const uint32_t trows = left < kTile ? left : kTile;
+        const uint32_t trp = (trows + 7u) & ~7u;
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * nu * UB, trp * nu * UB);
+        auto terms = [&](const Raw<O> &w, uint32_t u) {
+            float t[TPU];
+            unit_terms<O, true>(w, act, u, t, lbase);
+#pragma unroll
+            for (uint32_t j = 0; j < TPU; ++j) spread_terms[(u * TPU + j) * kTile + lane] = t[j];
+        };
+        // Units wave, wave + 16, ...: two register buffers in ping-pong.
+        Raw<O> A, B;
+        uint32_t u = wave;
+        if (u < nu) load_unit<O>(A, rs, u * trp * UB, trp, lane);
+        while (u + kLutWaves < nu) {
+            load_unit<O>(B, rs, (u + kLutWaves) * trp * UB, trp, lane);
+            terms(A, u);
+            if (u + 2 * kLutWaves < nu) load_unit<O>(A, rs, (u + 2 * kLutWaves) * trp * UB, trp, lane);
+            terms(B, u + kLutWaves);
+            u += 2 * kLutWaves;
+        }
+        if (u < nu) terms(A, u);
+        __syncthreads();
+        if (wave == 0) {
+            Chain<O> ch;
+            for (uint32_t v = 0; v < nu; ++v) {
+                float t[TPU];
+#pragma unroll
+                for (uint32_t j = 0; j < TPU; ++j) t[j] = spread_terms[(v * TPU + j) * kTile + lane];
+                ch.fold(t, act, v);
+            }
+            if (lane < trows) {
+                const size_t row = static_cast<size_t>(tile) * kTile + lane;
+                float o = ch.result();
+                if (p.residual) o = o + p.residual[row];
+                p.out[row] = o;
+                if (!finite(o)) raise_error(p.err, kErrNonfinite);
+            }
+        }
     } else if constexpr (MODE == kLutTail) {
         // Terms of the tail tiles' second halves: pair `slot` at slot * kTile * stride,
         // row `lane` at lane * stride.  A pair is active only if its tile exists, and the
@@ -2394,6 +2447,18 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     if (a.q8_out && (nmat != 2 || a.rows % 32 != 0)) return -2;
     p.q8_out = static_cast<Q8Block *>(a.q8_out);
     p.q8_contract = a.q8_contract;
+    if constexpr (kind_of<O>() == kPTQ1) {
+        // Measured, prepared activations (us, split kernel -> spread): 12288x4096 8.6 -> 6.9
+        // (pinned 14.0 -> 10.8), 8192x4096 6.7 -> 6.6; fewer tiles or longer rows lose to
+        // the split kernel (2048x2048 4.2 -> 4.8, 6144x2048 5.0 -> 5.1, 2048x6144 5.4 -> 7.6).
+        if (!quant && nmat == 1 && tiles < a.cus && 2 * tiles > a.cus && nu <= 32) {
+            if (const uint32_t lds = lut_spread_lds<O>(nu)) {
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutSpread>), dim3(static_cast<uint32_t>(tiles)),
+                                   dim3(kLutThreads), lds, a.stream, p, act);
+                return launch_status();
+            }
+        }
+    }
     if (!quant && nmat == 1 && tiles >= a.cus) {
         if constexpr (kind_of<O>() == kPTQ1) {
             constexpr int kSplitMode = lut_can_split<O>() ? kLutSplit : kLutWhole;

@@ -329,6 +329,37 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("cols", [384, 4096])
+def test_gpu_ptq1_table_spread_matches_oracle(ctx, cols):
+    """Between half a tile and one tile per CU, prepared-activation PTQ1 runs one table
+    workgroup per 64-row tile, its units spread over 16 wavefronts and their terms folded in
+    unit order from LDS: bit-exact in every contract (source, pinned, native-scale pinned
+    Q8_0, and Q8_K), with an odd unit count and a partial last tile."""
+    import oracle
+
+    import hiprt
+
+    kind = ph.KIND_PTQ1
+    cus = hiprt.cu_count(0)
+    rows = 64 * (3 * cus // 4) + 37
+    w = synth.weights(kind, rows, cols, seed=71 + cols)
+    x = synth.activations(cols, seed=72)
+    wid = ctx.weight(kind, cols, rows, w)
+    for contract, pinned in ((0, False), (1, True), (2, True), (1, False)):
+        act = oracle.quantize_q8_0(x, contract)
+        ref = oracle.project_q8(kind, cols, rows, w, act, pinned, threads=THREADS)
+        got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=pinned)
+        assert_bits_equal(got, ref, f"spread q8 contract={contract} pinned={pinned}")
+    if cols % 256 == 0:
+        act = oracle.quantize_q8k(x, False)
+        nb = cols // 128 * 28
+        sample = list(range(0, rows, 97)) + list(range(rows - 20, rows))
+        ref = np.array([oracle.dot_ptq1_q8k(w[r * nb:(r + 1) * nb], act) for r in sample], np.float32)
+        got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE))
+        assert_bits_equal(got[sample], ref, "spread q8k")
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("per_cu", [9, 10])
 def test_gpu_ptq1_pinned_table_tail_4096(ctx, per_cu):
     """Pinned PTQ1 at 4096 columns on the table kernel: nine terms per unit leave room in
