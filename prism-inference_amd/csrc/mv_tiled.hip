@@ -792,15 +792,24 @@ constexpr uint32_t kLutWaves = kLutThreads / 64;
 // whole one.  Their second halves' terms go to dynamic LDS, 64 rows x lut_tail_stride()
 // floats per pair, beside the 64 KiB table: pinned PTQ1 (nine terms per unit) fits two
 // pairs at 4096 columns, so it takes this form up to ten tiles per CU.
-// kLutSpread (fewer tiles than CUs, prepared activations): one workgroup per tile, its units
-// round-robin over the 16 wavefronts, each unit's terms for the tile's 64 rows left in
-// dynamic LDS ([unit][term][row], lut_spread_lds()), then wavefront 0 folds them in unit
-// order: the unsplit row's arithmetic with sixteen wavefronts decoding.
+// kLutSpread (prepared activations, half a tile to eight tiles per CU): a workgroup takes
+// `per` = 1, 2, 4 or 8 tiles (lut_spread_slots) and gives each 16 / per wavefronts, which
+// take its units round-robin and leave each unit's terms for the tile's 64 rows in dynamic
+// LDS ([tile slot][unit][term][row], lut_spread_lds()); after one barrier the first
+// wavefront of each tile folds them in unit order: the unsplit row's arithmetic.
 constexpr uint32_t kLutSlots = kLutWaves / 2;
 constexpr int kLutWhole = 0, kLutSplit = 1, kLutTail = 2, kLutSpread = 3;
+__host__ __device__ inline uint32_t lut_spread_slots(uint32_t tiles, uint32_t grid) {
+    const uint32_t need = (tiles + grid - 1) / grid;
+    return need <= 1 ? 1u : need <= 2 ? 2u : need <= 4 ? 4u : 8u;
+}
+// Dynamic LDS bytes of the spread form for this launch (grid = min(tiles, CUs)), 0 where
+// it does not apply.
 template <Op O>
-inline uint32_t lut_spread_lds(uint32_t nu) {
-    const uint32_t bytes = nu * terms_per_unit<O>() * kTile * static_cast<uint32_t>(sizeof(float));
+inline uint32_t lut_spread_lds(uint32_t tiles, uint32_t grid, uint32_t nu) {
+    if (tiles > 8 * grid) return 0u;
+    const uint32_t bytes =
+        lut_spread_slots(tiles, grid) * nu * terms_per_unit<O>() * kTile * static_cast<uint32_t>(sizeof(float));
     return bytes + sizeof(g_ptq1_lut) <= 160u * 1024u ? bytes : 0u;
 }
 template <Op O>
@@ -838,37 +847,44 @@ __global__ __launch_bounds__(kLutThreads) void k_mv_rows_lut(MvParams p, const v
     } else if constexpr (MODE == kLutSpread) {
         extern __shared__ float spread_terms[];
         constexpr uint32_t UB = unit_bytes<O>(), TPU = terms_per_unit<O>();
-        const uint32_t tile = blockIdx.x, nu = p.nu;
-        const uint32_t left = p.rows - tile * kTile;
+        const uint32_t nu = p.nu, grid = __builtin_amdgcn_readfirstlane(gridDim.x);
+        const uint32_t per = lut_spread_slots(tiles, grid), W = kLutWaves / per;
+        const uint32_t slot = wave / W, sub = wave % W;
+        const uint32_t tile = blockIdx.x + slot * grid;
+        const bool active = tile < tiles;  // uniform per wavefront
+        float *mine = spread_terms + static_cast<size_t>(slot) * nu * TPU * kTile;
+        const uint32_t left = active ? p.rows - tile * kTile : 0u;
         const uint32_t trows = left < kTile ? left : kTile;
         const uint32_t trp = (trows + 7u) & ~7u;
-        const __amdgpu_buffer_rsrc_t rs =
-            make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * nu * UB, trp * nu * UB);
-        auto terms = [&](const Raw<O> &w, uint32_t u) {
-            float t[TPU];
-            unit_terms<O, true>(w, act, u, t, lbase);
+        if (active) {
+            const __amdgpu_buffer_rsrc_t rs =
+                make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * nu * UB, trp * nu * UB);
+            auto terms = [&](const Raw<O> &w, uint32_t u) {
+                float t[TPU];
+                unit_terms<O, true>(w, act, u, t, lbase);
 #pragma unroll
-            for (uint32_t j = 0; j < TPU; ++j) spread_terms[(u * TPU + j) * kTile + lane] = t[j];
-        };
-        // Units wave, wave + 16, ...: two register buffers in ping-pong.
-        Raw<O> A, B;
-        uint32_t u = wave;
-        if (u < nu) load_unit<O>(A, rs, u * trp * UB, trp, lane);
-        while (u + kLutWaves < nu) {
-            load_unit<O>(B, rs, (u + kLutWaves) * trp * UB, trp, lane);
-            terms(A, u);
-            if (u + 2 * kLutWaves < nu) load_unit<O>(A, rs, (u + 2 * kLutWaves) * trp * UB, trp, lane);
-            terms(B, u + kLutWaves);
-            u += 2 * kLutWaves;
+                for (uint32_t j = 0; j < TPU; ++j) mine[(u * TPU + j) * kTile + lane] = t[j];
+            };
+            // Units sub, sub + W, ...: two register buffers in ping-pong.
+            Raw<O> A, B;
+            uint32_t u = sub;
+            if (u < nu) load_unit<O>(A, rs, u * trp * UB, trp, lane);
+            while (u + W < nu) {
+                load_unit<O>(B, rs, (u + W) * trp * UB, trp, lane);
+                terms(A, u);
+                if (u + 2 * W < nu) load_unit<O>(A, rs, (u + 2 * W) * trp * UB, trp, lane);
+                terms(B, u + W);
+                u += 2 * W;
+            }
+            if (u < nu) terms(A, u);
         }
-        if (u < nu) terms(A, u);
-        __syncthreads();
-        if (wave == 0) {
+        __syncthreads();  // every wavefront reaches this one barrier
+        if (active && sub == 0) {
             Chain<O> ch;
             for (uint32_t v = 0; v < nu; ++v) {
                 float t[TPU];
 #pragma unroll
-                for (uint32_t j = 0; j < TPU; ++j) t[j] = spread_terms[(v * TPU + j) * kTile + lane];
+                for (uint32_t j = 0; j < TPU; ++j) t[j] = mine[(v * TPU + j) * kTile + lane];
                 ch.fold(t, act, v);
             }
             if (lane < trows) {
@@ -2451,10 +2467,11 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
         // Measured, prepared activations (us, split kernel -> spread): 12288x4096 8.6 -> 6.9
         // (pinned 14.0 -> 10.8), 8192x4096 6.7 -> 6.6; fewer tiles or longer rows lose to
         // the split kernel (2048x2048 4.2 -> 4.8, 6144x2048 5.0 -> 5.1, 2048x6144 5.4 -> 7.6).
-        if (!quant && nmat == 1 && tiles < a.cus && 2 * tiles > a.cus && nu <= 32) {
-            if (const uint32_t lds = lut_spread_lds<O>(nu)) {
-                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutSpread>), dim3(static_cast<uint32_t>(tiles)),
-                                   dim3(kLutThreads), lds, a.stream, p, act);
+        const uint32_t sgrid = static_cast<uint32_t>(tiles < a.cus ? tiles : a.cus);
+        if (!quant && nmat == 1 && 2 * tiles > a.cus && nu <= 32) {
+            if (const uint32_t lds = lut_spread_lds<O>(static_cast<uint32_t>(tiles), sgrid, nu)) {
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutSpread>), dim3(sgrid), dim3(kLutThreads), lds, a.stream, p,
+                                   act);
                 return launch_status();
             }
         }

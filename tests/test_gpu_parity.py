@@ -329,20 +329,23 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("per_cu4", [3, 6, 14])
 @pytest.mark.parametrize("cols", [384, 4096])
-def test_gpu_ptq1_table_spread_matches_oracle(ctx, cols):
-    """Between half a tile and one tile per CU, prepared-activation PTQ1 runs one table
-    workgroup per 64-row tile, its units spread over 16 wavefronts and their terms folded in
-    unit order from LDS: bit-exact in every contract (source, pinned, native-scale pinned
-    Q8_0, and Q8_K), with an odd unit count and a partial last tile."""
+def test_gpu_ptq1_table_spread_matches_oracle(ctx, cols, per_cu4):
+    """From half a tile to eight tiles per CU, prepared-activation PTQ1 runs table
+    workgroups of one, two or four tiles (per_cu4 / 4 tiles per CU here), each tile's units
+    spread over 16, 8 or 4 wavefronts and their terms folded in unit order from LDS (pinned
+    PTQ1 at 4096 columns only with one tile per workgroup; beyond, its earlier forms):
+    bit-exact in every contract (source, pinned, native-scale pinned Q8_0, and Q8_K), with
+    an odd unit count and a partial last tile."""
     import oracle
 
     import hiprt
 
     kind = ph.KIND_PTQ1
     cus = hiprt.cu_count(0)
-    rows = 64 * (3 * cus // 4) + 37
-    w = synth.weights(kind, rows, cols, seed=71 + cols)
+    rows = 64 * (per_cu4 * cus // 4) + 37
+    w = synth.weights(kind, rows, cols, seed=71 + cols + per_cu4)
     x = synth.activations(cols, seed=72)
     wid = ctx.weight(kind, cols, rows, w)
     for contract, pinned in ((0, False), (1, True), (2, True), (1, False)):
