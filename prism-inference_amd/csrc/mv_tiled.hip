@@ -769,6 +769,39 @@ __global__ __launch_bounds__(128) void k_mv_rows2(MvParams p, uint32_t stride) {
     }
 }
 
+// NW wavefronts per 64-row tile (fewer tiles than CUs, prepared activations): wavefront
+// k walks the contiguous units [k * nu / NW, (k + 1) * nu / NW); wavefront 0 folds its own
+// units straight into the chain and the others leave their units' terms in LDS (row-major,
+// odd `stride`), which wavefront 0 folds after one barrier in unit order: the unsplit
+// row's arithmetic with NW wavefronts loading and decoding.
+template <Op O, uint32_t NW>
+__global__ __launch_bounds__(64 * NW) void k_mv_rowsn(MvParams p, uint32_t stride) {
+    static_assert(O != Op::PTQ1_PINNED, "four-lane chains fold nine terms per unit");
+    extern __shared__ float later[];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tile = blockIdx.x, nu = p.nu, c1 = nu / NW;
+    const uint32_t u0 = k * nu / NW, u1 = (k + 1) * nu / NW;
+    float *mine = later + lane * stride;
+    Chain<O> ch;
+    if (k == 0)
+        rows_part<O, false>(p, p.act, tile, lane, 0, 0, c1, ch, nullptr);
+    else if (u0 < u1)
+        rows_part<O, false>(p, p.act, tile, lane, 0, u0, u1, ch, mine + (u0 - c1) * terms_per_unit<O>());
+    __syncthreads();
+    if (k == 0) {
+        for (uint32_t u = c1; u < nu; ++u) ch.fold(mine + (u - c1) * terms_per_unit<O>(), p.act, u);
+        const uint32_t left = p.rows - tile * kTile;
+        if (lane < (left < kTile ? left : kTile)) {
+            const size_t row = static_cast<size_t>(tile) * kTile + lane;
+            float o = ch.result();
+            if (p.residual) o = o + p.residual[row];
+            p.out[row] = o;
+            if (!finite(o)) raise_error(p.err, kErrNonfinite);
+        }
+    }
+}
+
 // PTQ1 with the LDS decode table: one workgroup per CU builds the 64 KiB table once and
 // works through its tiles (tile = block + j * grid, j = 0, 1, ...), which spreads the
 // tiles evenly over the CUs.  The activation comes as its own __restrict__ argument: the
@@ -2474,6 +2507,25 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
                                    act);
                 return launch_status();
             }
+        }
+    }
+    if constexpr (kind_of<O>() != kPTQ1) {
+        // Half a tile to one tile per CU, prepared activations: 16 wavefronts per tile from
+        // 16 units per row, 8 from 8.  Measured (us, split kernel -> N wavefronts), 12288
+        // rows x 4096: Q8_0 12.6 -> 12.0, Q2_K 7.4 -> 6.0, PQ2 7.9 -> 6.9, TQ1_0 8.2 -> 6.7,
+        // TQ2_0 6.9 -> 5.5; 10240 x 4096 Q8_0 12.2 -> 10.9; 12288 x 2048 Q2_K 5.6 -> 4.2 (8
+        // wavefronts; 4 gave 4.4).
+        auto rowsn = [&]<uint32_t NW>() -> int {
+            const uint32_t c1 = nu / NW;
+            const uint32_t stride = ((nu - c1) * terms_per_unit<O>()) | 1u;
+            if (kTile * stride * sizeof(float) > 64u * 1024u) return -1;
+            hipLaunchKernelGGL((k_mv_rowsn<O, NW>), dim3(static_cast<uint32_t>(tiles)), dim3(64 * NW),
+                               kTile * stride * sizeof(float), a.stream, p, stride);
+            return launch_status();
+        };
+        if (!quant && nmat == 1 && tiles < a.cus && 2 * tiles > a.cus && nu >= 8) {
+            const int rc = nu >= 16 ? rowsn.template operator()<16>() : rowsn.template operator()<8>();
+            if (rc >= 0) return rc;
         }
     }
     if (!quant && nmat == 1 && tiles >= a.cus) {

@@ -363,6 +363,40 @@ def test_gpu_ptq1_table_spread_matches_oracle(ctx, cols, per_cu4):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("kind,cols", [(ph.KIND_Q8_0, 2048), (ph.KIND_Q8_0, 4224), (ph.KIND_PQ2, 2048),
+                                       (ph.KIND_PQ2, 4224), (ph.KIND_Q2_K, 2048), (ph.KIND_Q2_K, 4352),
+                                       (ph.KIND_TQ1_0, 2304), (ph.KIND_TQ1_0, 4096), (ph.KIND_TQ2_0, 2048),
+                                       (ph.KIND_TQ2_0, 4352)])
+def test_gpu_rows_n_wavefronts_matches_oracle(ctx, kind, cols):
+    """Between half a tile and one tile per CU, prepared activations of the non-PTQ1
+    formats run 16 wavefronts per tile (8 with 8 to 15 units per row), each walking a
+    contiguous unit range whose terms wavefront 0 folds from LDS in unit order: bit-exact
+    in every contract, with even and odd unit counts and a partial last tile."""
+    import oracle
+
+    import hiprt
+
+    cus = hiprt.cu_count(0)
+    rows = 64 * (3 * cus // 4) + 37
+    w = synth.weights(kind, rows, cols, seed=81 + cols) if kind != ph.KIND_PQ2 else \
+        synth.pq2_weights(rows, cols, 81 + cols, 4)
+    x = synth.activations(cols, seed=82)
+    wid = ctx.weight(kind, cols, rows, w)
+    if kind in (ph.KIND_Q8_0, ph.KIND_PQ2):
+        for contract, pinned in ((1, False), (0, True)):
+            act = oracle.quantize_q8_0(x, contract)
+            ref = oracle.project_q8(kind, cols, rows, w, act, pinned, threads=THREADS)
+            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=pinned)
+            assert_bits_equal(got, ref, f"rows-n q8 kind={kind} contract={contract} pinned={pinned}")
+    if cols % 256 == 0 and kind != ph.KIND_Q8_0:
+        for fused in (False, True):
+            act = oracle.quantize_q8k(x, fused)
+            ref = oracle.project_q8k(kind, cols, rows, w, act, fused, threads=THREADS)
+            got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), fused=fused)
+            assert_bits_equal(got, ref, f"rows-n q8k kind={kind} fused={fused}")
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("per_cu", [9, 10])
 def test_gpu_ptq1_pinned_table_tail_4096(ctx, per_cu):
     """Pinned PTQ1 at 4096 columns on the table kernel: nine terms per unit leave room in
