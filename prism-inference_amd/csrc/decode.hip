@@ -374,28 +374,52 @@ __global__ __launch_bounds__(256) void k_lm_prep(const float *__restrict__ x, co
 }
 
 // Element i of row r of a Q8_0 matrix held in the 64-row tiled layout, dequantized
-// as decode_row_into does (src/kernels.rs:303, d * q).
+// as decode_row_into does (src/kernels.rs:303, d * q).  The Q8_0 unit (128 weights,
+// 136 bytes) holds 16-byte code pieces p = 0..7 at p * 16 * TRP (element j in piece
+// j / 16) and the four binary16 scales at 128 * TRP, 8 bytes per row; the offsets are
+// written out so that nothing indexes a format table at run time (a table in private
+// memory would cost a scratch round trip per element).
 __device__ __forceinline__ float q8_0_tiled_at(const uint8_t *__restrict__ w, uint64_t rows, uint32_t cols, uint32_t r,
                                                uint32_t i) {
-    TiledFormat f;
-    tiled_format(kQ8_0, &f);
-    const uint64_t row_bytes = static_cast<uint64_t>(cols) / 128 * f.unit_bytes;
+    constexpr uint32_t kUnitBytes = 136;
+    const uint64_t row_bytes = static_cast<uint64_t>(cols) / 128 * kUnitBytes;
     const uint64_t tile = r / kTile;
     const uint32_t lr = r % kTile;
     const uint32_t trp = tile_rows_padded(rows, tile);
     const uint32_t u = i / 128, j = i % 128;
-    const uint8_t *seg = w + tile * kTile * row_bytes + static_cast<uint64_t>(u) * trp * f.unit_bytes;
-    const int8_t q = static_cast<int8_t>(seg[f.poff[j / 16] * trp + lr * 16 + j % 16]);
-    const uint8_t *sp = seg + f.poff[8] * trp + lr * 8 + 2 * (j / 32);
+    const uint8_t *seg = w + tile * kTile * row_bytes + static_cast<uint64_t>(u) * trp * kUnitBytes;
+    const int8_t q = static_cast<int8_t>(seg[(j / 16) * 16 * trp + lr * 16 + j % 16]);
+    const uint8_t *sp = seg + 128 * trp + lr * 8 + 2 * (j / 32);
     const float d = h2f(static_cast<uint32_t>(sp[0]) | (static_cast<uint32_t>(sp[1]) << 8));
     return d * static_cast<float>(q);
+}
+
+// Row `token` of a tiled Q8_0 matrix, dequantized into out[0, cols) by the workgroup.  Each
+// thread issues the loads of up to eight elements before its first store, so a row of up to
+// 8 * blockDim.x elements costs one memory round trip rather than one per element.
+__device__ __forceinline__ void embed_row(const uint8_t *__restrict__ emb, uint64_t rows, uint32_t cols,
+                                          uint32_t token, float *__restrict__ out) {
+    constexpr uint32_t kPer = 8;
+    for (uint32_t i0 = threadIdx.x; i0 < cols; i0 += kPer * blockDim.x) {
+        float v[kPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t i = i0 + k * blockDim.x;
+            v[k] = i < cols ? q8_0_tiled_at(emb, rows, cols, token, i) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t i = i0 + k * blockDim.x;
+            if (i < cols) out[i] = v[k];
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_embed(const uint8_t *__restrict__ emb, uint64_t rows, uint32_t cols,
                                                DecodeState *__restrict__ st, RopeArgs rope, float *__restrict__ out) {
     const uint32_t token = st->token;
     rope_freqs(st, st->pos, rope);
-    for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) out[i] = q8_0_tiled_at(emb, rows, cols, token, i);
+    embed_row(emb, rows, cols, token, out);
 }
 
 // Greedy choice: the first index of the largest logit.  k_argmax_slices reduces
@@ -476,13 +500,13 @@ __global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ 
     __shared__ uint32_t bi[4];
     const uint32_t tid = threadIdx.x;
     const uint32_t pos = st->pos;  // read before thread 0 advances it
-    float best = -__builtin_inff();
-    uint32_t idx = 0xffffffffu;
-    for (uint32_t g = tid; g < kArgmaxGroups; g += blockDim.x)
-        if (better(pval[g], pidx[g], best, idx)) {
-            best = pval[g];
-            idx = pidx[g];
-        }
+    // One slice per thread (launched with 256 threads); the next position's RoPE
+    // frequencies are computed while the slices' loads are in flight.
+    static_assert(kArgmaxGroups <= 256, "one slice per thread");
+    const bool has = tid < kArgmaxGroups;
+    float best = has ? pval[tid] : -__builtin_inff();
+    uint32_t idx = has ? pidx[tid] : 0xffffffffu;
+    rope_freqs(st, pos + 1, rope);
     reduce_best(best, idx, bv, bi);
     const uint32_t token = idx < vocab ? idx : 0;  // a slice always holds a valid index
     if (tid == 0) {
@@ -492,8 +516,7 @@ __global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ 
         st->step = step + 1;
         st->pos = pos + 1;
     }
-    rope_freqs(st, pos + 1, rope);
-    for (uint32_t i = tid; i < cols; i += blockDim.x) out[i] = q8_0_tiled_at(emb, vocab, cols, token, i);
+    embed_row(emb, vocab, cols, token, out);
 }
 
 }  // namespace
