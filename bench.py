@@ -194,7 +194,7 @@ FAMILY_KERNEL = {
     "attn_values": "k_attn_values (softmax_round_f16 + value sums, 16 heads x 1025 positions)",
     "lm_head": "k_mv_rows<Q8_0> (151936x2048 LM head)",
     "lm_prep": "k_lm_prep (final RMSNorm + Q8_0)",
-    "greedy": "k_argmax_slices + k_argmax_embed (greedy choice, next embedding)",
+    "greedy": "k_argmax_embed (greedy choice from the LM head tile maxima, next embedding)",
 }
 
 

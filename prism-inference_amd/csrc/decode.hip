@@ -422,12 +422,13 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t *__restrict__ emb, 
     embed_row(emb, rows, cols, token, out);
 }
 
-// Greedy choice: the first index of the largest logit.  k_argmax_slices reduces
-// contiguous slices to their (largest value, first index); k_argmax_embed reduces the
-// slices in order, records the token in the state and the token history, advances
-// the position, and writes the chosen token's embedding (the tied LM head row) as the
-// next step's hidden state.
-constexpr uint32_t kArgmaxGroups = 128;
+// Greedy choice: the first index of the largest logit.  The LM head's row-tile kernel
+// leaves each 64-row tile's (largest value, first row); k_argmax_embed reduces them,
+// records the token in the state and the token history, advances the position, and
+// writes the chosen token's embedding (the tied LM head row) as the next step's hidden
+// state.
+constexpr uint32_t kArgmaxThreads = 1024, kArgmaxPer = 4;
+constexpr uint32_t kArgmaxTiles = kArgmaxThreads * kArgmaxPer;  // 262144 vocabulary rows
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
     return bi == 0xffffffffu || (i != 0xffffffffu && (v > bv || (v == bv && i < bi)));
@@ -459,56 +460,34 @@ __device__ void reduce_best(float &best, uint32_t &idx, float *bv, uint32_t *bi)
         }
 }
 
-__global__ __launch_bounds__(256) void k_argmax_slices(const float *__restrict__ logits, uint32_t vocab,
-                                                       float *__restrict__ pval, uint32_t *__restrict__ pidx) {
-    __shared__ float bv[4];
-    __shared__ uint32_t bi[4];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t span = (vocab + gridDim.x - 1) / gridDim.x;
-    const uint32_t lo = blockIdx.x * span, hi = lo + span < vocab ? lo + span : vocab;
-    float best = -__builtin_inff();
-    uint32_t idx = 0xffffffffu;
-    for (uint32_t i0 = lo + tid; i0 < hi; i0 += 8 * blockDim.x) {
-        float v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t i = i0 + k * blockDim.x;
-            v[k] = i < hi ? logits[i] : 0.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t i = i0 + k * blockDim.x;
-            if (i < hi && better(v[k], i, best, idx)) {
-                best = v[k];
-                idx = i;
-            }
-        }
-    }
-    reduce_best(best, idx, bv, bi);
-    if (tid == 0) {
-        pval[blockIdx.x] = best;
-        pidx[blockIdx.x] = idx;
-    }
-}
-
-__global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ pval, const uint32_t *__restrict__ pidx,
-                                                      uint32_t vocab, const uint8_t *__restrict__ emb, uint32_t cols,
-                                                      DecodeState *__restrict__ st, RopeArgs rope,
-                                                      uint32_t *__restrict__ tokens, uint32_t max_steps,
-                                                      float *__restrict__ out) {
-    __shared__ float bv[4];
-    __shared__ uint32_t bi[4];
+__global__ __launch_bounds__(kArgmaxThreads) void k_argmax_embed(const TileBest *__restrict__ tb, uint32_t ntiles,
+                                                                 uint32_t vocab, const uint8_t *__restrict__ emb,
+                                                                 uint32_t cols, DecodeState *__restrict__ st,
+                                                                 RopeArgs rope, uint32_t *__restrict__ tokens,
+                                                                 uint32_t max_steps, float *__restrict__ out) {
+    __shared__ float bv[kArgmaxThreads / 64];
+    __shared__ uint32_t bi[kArgmaxThreads / 64];
     const uint32_t tid = threadIdx.x;
     const uint32_t pos = st->pos;  // read before thread 0 advances it
-    // One slice per thread (launched with 256 threads); the next position's RoPE
-    // frequencies are computed while the slices' loads are in flight.
-    static_assert(kArgmaxGroups <= 256, "one slice per thread");
-    const bool has = tid < kArgmaxGroups;
-    float best = has ? pval[tid] : -__builtin_inff();
-    uint32_t idx = has ? pidx[tid] : 0xffffffffu;
+    // Up to kArgmaxPer tiles per thread, every load issued before the first comparison;
+    // the next position's RoPE frequencies are computed while they are in flight.
+    TileBest t[kArgmaxPer];
+#pragma unroll
+    for (uint32_t k = 0; k < kArgmaxPer; ++k) {
+        const uint32_t g = tid + k * kArgmaxThreads;
+        t[k] = g < ntiles ? tb[g] : TileBest{0.0f, 0xffffffffu};
+    }
     rope_freqs(st, pos + 1, rope);
+    float best = -__builtin_inff();
+    uint32_t idx = 0xffffffffu;
+#pragma unroll
+    for (uint32_t k = 0; k < kArgmaxPer; ++k)
+        if (better(t[k].value, t[k].row, best, idx)) {
+            best = t[k].value;
+            idx = t[k].row;
+        }
     reduce_best(best, idx, bv, bi);
-    const uint32_t token = idx < vocab ? idx : 0;  // a slice always holds a valid index
+    const uint32_t token = idx < vocab ? idx : 0;  // every tile holds a row
     if (tid == 0) {
         const uint32_t step = st->step;
         if (step < max_steps) tokens[step] = token;
@@ -521,7 +500,7 @@ __global__ __launch_bounds__(256) void k_argmax_embed(const float *__restrict__ 
 
 }  // namespace
 
-size_t argmax_scratch_bytes() { return (sizeof(float) + sizeof(uint32_t)) * kArgmaxGroups; }
+size_t argmax_scratch_bytes(uint64_t vocab) { return sizeof(TileBest) * ((vocab + kTile - 1) / kTile); }
 
 namespace {
 bool attention_supported(const AttnArgs &a) {
@@ -570,14 +549,11 @@ int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, DecodeStat
     return launch_status();
 }
 
-int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
-                        const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, void *scratch,
-                        hipStream_t s) {
-    if (rope.rope > 2 * 64) return -2;
-    float *pval = static_cast<float *>(scratch);
-    uint32_t *pidx = reinterpret_cast<uint32_t *>(pval + kArgmaxGroups);
-    hipLaunchKernelGGL(k_argmax_slices, dim3(kArgmaxGroups), dim3(256), 0, s, logits, vocab, pval, pidx);
-    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(256), 0, s, pval, pidx, vocab,
+int launch_argmax_embed(const TileBest *best, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
+                        const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, hipStream_t s) {
+    const uint32_t ntiles = (vocab + kTile - 1) / kTile;
+    if (rope.rope > 2 * 64 || vocab == 0 || ntiles > kArgmaxTiles) return -2;
+    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(kArgmaxThreads), 0, s, best, ntiles, vocab,
                        static_cast<const uint8_t *>(emb_tiled), cols, st, rope, tokens, max_steps, out);
     return launch_status();
 }

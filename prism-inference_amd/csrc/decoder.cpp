@@ -172,12 +172,19 @@ int launch_family(prism_hip_decoder *d, Family f, uint32_t layer) {
         return launch_result(c, launch_lm_prep(h0, d->output_norm, static_cast<uint32_t>(g.hidden), g.eps, d->lm_act,
                                                c->err, c->stream),
                              "final norm launch");
-    case kLmHead: return matvec(c, *find(c, d->lm_head), kActQ8, d->lm_act, 1, 0, d->logits, c->stream);
+    case kLmHead: {
+        // The row-tile kernel also leaves each 64-row tile's largest logit and first row.
+        const Weight &w = *find(c, d->lm_head);
+        MatvecArgs a = matvec_args(c, w, kActQ8, d->lm_act, 1, 0, d->logits, c->stream);
+        a.tile_best = d->argmax_scratch;
+        return run_matvec(c, a, w.tiled);
+    }
     case kGreedy:
         return launch_result(c,
-                             launch_argmax_embed(d->logits, static_cast<uint32_t>(g.vocab), find(c, d->lm_head)->dev,
+                             launch_argmax_embed(static_cast<const TileBest *>(d->argmax_scratch),
+                                                 static_cast<uint32_t>(g.vocab), find(c, d->lm_head)->dev,
                                                  static_cast<uint32_t>(g.hidden), d->state, rope_args(g), d->tokens,
-                                                 d->max_steps, h0, d->argmax_scratch, c->stream),
+                                                 d->max_steps, h0, c->stream),
                              "argmax launch");
     default: return fail(c, PRISM_ERR_INVALID_INPUT, "unknown launch family");
     }
@@ -339,7 +346,7 @@ prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decode
     if (!rc) rc = dalloc(d, &d->lm_act, sizeof(prism_q8_block) * (H / 32));
     if (!rc) rc = dalloc(d, &d->state, sizeof(DecodeState));
     if (!rc) rc = dalloc(d, &d->tokens, sizeof(uint32_t) * max_steps);
-    const size_t gs = argmax_scratch_bytes();
+    const size_t gs = argmax_scratch_bytes(g->vocab);
     if (!rc) rc = dalloc(d, &d->argmax_scratch, gs);
     if (!rc) {
         const hipError_t e = hipMemset(d->argmax_scratch, 0, gs);

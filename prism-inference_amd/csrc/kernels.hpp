@@ -47,6 +47,10 @@ struct MatvecArgs {
     void *q8_out = nullptr;           // tiled w2 only: the SwiGLU vector's Q8_0 blocks (rows % 32 == 0)
     int q8_contract = 0;              // their contract (PRISM_Q8_*)
     int *err = nullptr;           // device error flag
+    // Tiled, one token, prepared activations, non-PTQ1 formats, row-tile kernel only: per
+    // 64-row tile, the tile's largest output and the first row holding it, as
+    // {float value, uint32_t row} pairs (TileBest), for the greedy choice.
+    void *tile_best = nullptr;
     hipStream_t stream = nullptr;
     uint32_t cus = 256;           // compute units of the device
     void *scratch = nullptr;      // tiled only: tiled_scratch_bytes() of device memory
@@ -125,13 +129,18 @@ int launch_lm_prep(const float *x, const float *w, uint32_t n, float eps, void *
 // RoPE frequencies are set for state->pos.
 int launch_embed(const void *emb_tiled, uint64_t rows, uint32_t cols, DecodeState *st, const RopeArgs &rope,
                  float *out, hipStream_t s);
-// Greedy token from logits[vocab], recorded and advanced in the state (with the RoPE
-// frequencies of the new position), and its embedding (row of the tiled Q8_0 matrix [vocab][cols]) written to out; two launches.
-// scratch: argmax_scratch_bytes() of device memory.
-size_t argmax_scratch_bytes();
-int launch_argmax_embed(const float *logits, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
-                        const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, void *scratch,
-                        hipStream_t s);
+// One 64-row tile's largest output and the first row that holds it.
+struct TileBest {
+    float value;
+    uint32_t row;
+};
+// Greedy token from the LM head's TileBest pairs (MatvecArgs::tile_best, one per 64-row
+// tile of the vocabulary), recorded and advanced in the state (with the RoPE frequencies
+// of the new position), and its embedding (row of the tiled Q8_0 matrix [vocab][cols])
+// written to out; one launch.
+size_t argmax_scratch_bytes(uint64_t vocab);
+int launch_argmax_embed(const TileBest *best, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
+                        const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, hipStream_t s);
 
 
 }  // namespace prism

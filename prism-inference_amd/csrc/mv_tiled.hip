@@ -635,6 +635,7 @@ struct MvParams {
     float eps;            // RMSNorm epsilon
     Q8Block *q8_out;      // NMAT == 2: the SwiGLU vector quantized to Q8_0 blocks (or null)
     int q8_contract;      // their contract (PRISM_Q8_*)
+    TileBest *tile_best;  // k_mv_rows: per tile, its largest output and first row (or null)
 };
 
 template <Op O>
@@ -690,12 +691,28 @@ __device__ __forceinline__ void rows_tile(const MvParams &p, const void *__restr
         u += 2;
     }
     if (u < nu) step(A, u);
+    const size_t row = static_cast<size_t>(tile) * kTile + lane;
+    float o = 0.0f;
     if (lane < trows) {
-        const size_t row = static_cast<size_t>(tile) * kTile + lane;
-        float o = ch.result();
+        o = ch.result();
         if (p.residual) o = o + p.residual[row];
         p.out[row] = o;
         if (!finite(o)) raise_error(p.err, kErrNonfinite);
+    }
+    if (p.tile_best) {
+        // The tile's largest output and its first row: lanes past the tile's rows hold no
+        // row, and of equal values the lower row wins (the order of a first-index argmax).
+        uint32_t r = lane < trows ? static_cast<uint32_t>(row) : 0xffffffffu;
+#pragma unroll
+        for (int k = 32; k >= 1; k >>= 1) {
+            const float ov = __shfl_xor(o, k);
+            const uint32_t orow = __shfl_xor(r, k);
+            if (r == 0xffffffffu || (orow != 0xffffffffu && (ov > o || (ov == o && orow < r)))) {
+                o = ov;
+                r = orow;
+            }
+        }
+        if (lane == 0) p.tile_best[tile] = TileBest{o, r};
     }
 }
 
@@ -2496,6 +2513,16 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
     if (a.q8_out && (nmat != 2 || a.rows % 32 != 0)) return -2;
     p.q8_out = static_cast<Q8Block *>(a.q8_out);
     p.q8_contract = a.q8_contract;
+    p.tile_best = static_cast<TileBest *>(a.tile_best);
+    if constexpr (kind_of<O>() != kPTQ1) {
+        if (p.tile_best) {
+            if (quant || nmat != 1) return -2;
+            hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);
+            return launch_status();
+        }
+    } else {
+        if (p.tile_best) return -2;
+    }
     if constexpr (kind_of<O>() == kPTQ1) {
         // Measured, prepared activations (us, split kernel -> spread): 12288x4096 8.6 -> 6.9
         // (pinned 14.0 -> 10.8), 8192x4096 6.7 -> 6.6; fewer tiles or longer rows lose to
@@ -2912,6 +2939,11 @@ bool skinny_eligible(const MatvecArgs &a) {
 }
 
 int launch_matvec_tiled(const MatvecArgs &a) {
+    if (a.tile_best) {
+        // Only the one-token row-tile path writes the tile maxima (launch_op).
+        if (a.tokens != 1 || a.act_format == kActF32 || a.w2 || a.kind == kPTQ1) return -2;
+        return dispatch(a, [&]<Op O>() { return launch_op<O>(a, a.act, a.out); });
+    }
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
