@@ -277,8 +277,8 @@ typedef struct {
     float rope_base, eps;
 } prism_decoder_geometry;
 
-/* head_dim must be 128; hidden, ffn multiples of 128; max_tokens <= 8192.  max_steps bounds one
- * generate(). */
+/* head_dim must be 128; hidden, ffn multiples of 128; max_tokens <= 8192; vocab <= 262144.
+ * max_steps bounds one generate(). */
 prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *ctx, const prism_decoder_geometry *g, uint32_t max_steps);
 void prism_hip_decoder_destroy(prism_hip_decoder *d);
 /* Host tensors of layer l, native layouts: qkv PTQ1 [(heads+2kv)*head_dim][hidden]

@@ -428,7 +428,8 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t *__restrict__ emb, 
 // writes the chosen token's embedding (the tied LM head row) as the next step's hidden
 // state.
 constexpr uint32_t kArgmaxThreads = 1024, kArgmaxPer = 4;
-constexpr uint32_t kArgmaxTiles = kArgmaxThreads * kArgmaxPer;  // 262144 vocabulary rows
+constexpr uint32_t kArgmaxTiles = kArgmaxThreads * kArgmaxPer;
+static_assert(static_cast<uint64_t>(kArgmaxTiles) * kTile == kGreedyMaxVocab, "greedy vocabulary limit");
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
     return bi == 0xffffffffu || (i != 0xffffffffu && (v > bv || (v == bv && i < bi)));

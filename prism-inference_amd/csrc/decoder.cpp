@@ -227,8 +227,10 @@ uint64_t family_bytes(const prism_hip_decoder *d, Family f, uint64_t pos) {
     case kGateUp: return 2 * ptq1(F, H) + 4 * H + 4 * H + F / 32 * 34;
     case kDown: return ptq1(H, F) + F / 32 * 34 + 4 * H + 4 * H;
     case kLmPrep: return 4 * H + 4 * H + H / 32 * 34;
-    case kLmHead: return g.vocab * (H / 32) * 34 + H / 32 * 34 + 4 * g.vocab;
-    case kGreedy: return 4 * g.vocab + H / 32 * 34 + 4 * H;
+    // The LM head also writes each 64-row tile's (largest logit, first row) pair, which
+    // the greedy launch reads back instead of the logits.
+    case kLmHead: return g.vocab * (H / 32) * 34 + H / 32 * 34 + 4 * g.vocab + 8 * ((g.vocab + 63) / 64);
+    case kGreedy: return 8 * ((g.vocab + 63) / 64) + H / 32 * 34 + 4 * H;
     default: return 0;
     }
 }
@@ -314,7 +316,7 @@ prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decode
     const bool ok = g->head_dim == 128 && g->heads && g->kv_heads && g->heads % g->kv_heads == 0 && g->rope &&
                     g->rope <= g->head_dim && g->rope % 2 == 0 && g->hidden && g->hidden % 128 == 0 && g->ffn &&
                     g->ffn % 128 == 0 && (g->heads * g->head_dim) % 128 == 0 && g->vocab && g->layers && g->layers <= 500 &&
-                    g->max_tokens && g->max_tokens <= 8192 && g->vocab < (1u << 31) && max_steps &&
+                    g->max_tokens && g->max_tokens <= 8192 && g->vocab <= kGreedyMaxVocab && max_steps &&
                     std::isfinite(g->eps) && g->eps >= 0.0f && std::isfinite(g->rope_base) && g->rope_base > 0.0f;
     if (!ok) {
         fail(c, PRISM_ERR_INVALID_INPUT, "unsupported decoder geometry");

@@ -138,6 +138,8 @@ struct TileBest {
 // tile of the vocabulary), recorded and advanced in the state (with the RoPE frequencies
 // of the new position), and its embedding (row of the tiled Q8_0 matrix [vocab][cols])
 // written to out; one launch.
+// Largest vocabulary the greedy launch reduces (4096 tiles of 64 rows).
+constexpr uint64_t kGreedyMaxVocab = 262144;
 size_t argmax_scratch_bytes(uint64_t vocab);
 int launch_argmax_embed(const TileBest *best, uint32_t vocab, const void *emb_tiled, uint32_t cols, DecodeState *st,
                         const RopeArgs &rope, uint32_t *tokens, uint32_t max_steps, float *out, hipStream_t s);

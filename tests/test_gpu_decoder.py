@@ -110,6 +110,11 @@ def test_gpu_decoder_rejects_bad_arguments(ctx):
     bad["geometry"]["head_dim"] = 64
     with pytest.raises(ph.PrismError):
         ph.Decoder(ctx, bad)
+    # The greedy launch reduces at most 4096 tiles of 64 vocabulary rows.
+    big = synth.decoder_model(6, kv_prefill=0, **dict(SMALL, layers=1))
+    big["geometry"]["vocab"] = 262144 + 1
+    with pytest.raises(ph.PrismError):
+        ph.Decoder(ctx, big)
 
 
 def test_gpu_decoder_detects_released_weights(ctx):
@@ -153,7 +158,11 @@ def test_gpu_decoder_profile_and_family_timing(ctx):
         qkv = (g["heads"] + 2 * g["kv_heads"]) * D
         by = {f["family"]: f["bytes_per_launch"] for f in fams}
         assert by["qkv"] == qkv * H // 128 * 28 + 8 * H + 4 * qkv
-        assert by["lm_head"] == g["vocab"] * (H // 32) * 34 + H // 32 * 34 + 4 * g["vocab"]
+        # The LM head also writes one (largest logit, first row) pair of 8 bytes per 64-row
+        # tile; the greedy launch reads those pairs, the Q8_0 input and the embedding row.
+        tiles = (g["vocab"] + 63) // 64
+        assert by["lm_head"] == g["vocab"] * (H // 32) * 34 + H // 32 * 34 + 4 * g["vocab"] + 8 * tiles
+        assert by["greedy"] == 8 * tiles + H // 32 * 34 + 4 * H
         assert by["gate_up"] == 2 * F * H // 128 * 28 + 8 * H + F // 32 * 34
         toks2, logits2, _ = dec.generate(3, 20, 4, graph=True, logits=True)
         assert np.array_equal(toks, toks2)
