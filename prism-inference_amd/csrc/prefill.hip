@@ -144,27 +144,17 @@ __device__ __forceinline__ uint32_t pair_mul(uint32_t v, uint32_t m) {  // two 1
 }
 
 // Raw weight dwords of one block for a lane: the A piece (16 B), the B piece (8 B) and
-// the tail dword of the lane's row, and the tail dwords (d in the high half) of the
-// lane's 16 output rows 8q + 4h + 0..3.
+// the tail dword (d in the high half) of the lane's row.
 struct RawBlock {
     u32x4 a;
     u32x2 b;
     uint32_t tl;
-    u32x4 dd[4];
 };
 __device__ __forceinline__ void load_block_codes(__amdgpu_buffer_rsrc_t rs, uint32_t seg, uint32_t trp, uint32_t row,
-                                                 RawBlock &w) {  // a, b and tl only
+                                                 RawBlock &w) {
     w.a = bload4(rs, seg + 16u * row);
     w.b = bload2(rs, seg + 16u * trp + 8u * row);
     w.tl = bload1(rs, seg + 24u * trp + 4u * row);
-}
-__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t rs, uint32_t seg, uint32_t trp, uint32_t row,
-                                           uint32_t out0, RawBlock &w) {
-    w.a = bload4(rs, seg + 16u * row);
-    w.b = bload2(rs, seg + 16u * trp + 8u * row);
-    w.tl = bload1(rs, seg + 24u * trp + 4u * row);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) w.dd[q] = bload4(rs, seg + 24u * trp + 4u * (out0 + 8u * q));
 }
 
 // The weight side of the operand order (pair_base): half h needs pair h of every quad of

@@ -596,13 +596,14 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
 
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 16), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
                                          (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
-                                         (96, 256, 4096)])
+                                         (96, 256, 4096), (130, 1152, 1100), (6144, 2048, 1024)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     """PTQ1 prefill runs as one f16-MFMA GEMM from 16 tokens on, in both contracts; every
     token row must equal the reference's per-token matvec bit for bit (partial row
     tiles, idle wavefronts of a partial 128-row block, an odd block count, 32, 64 and
     128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
-    token groups are a multiple of eight: M = 200, 512, 4096).  The pinned contract's
+    token groups are a multiple of eight: M = 200, 512, 4096; nine blocks per row at 1152
+    columns, the benchmark's matrix at 1024 tokens).  The pinned contract's
     kernel takes each native lane's integer sum from its own masked MFMA and runs the
     four FMA lanes of dot_q8_groups_pinned."""
     import oracle
@@ -642,7 +643,9 @@ def test_gpu_large_matvec_sampled_rows_match_oracle(ctx, kind, rows, cols):
 
 def test_gpu_prefill_bench_shape_matches_oracle(ctx):
     """PTQ1 6144x2048 at 2048 tokens (64 tokens per workgroup, XCD-major grid): sampled
-    token rows equal the oracle's per-token matvec bit for bit."""
+    token rows equal the oracle's per-token matvec bit for bit, and every token row equals
+    the GPU's skinny-batch kernel (15 tokens per launch), itself bit-exact against the
+    oracle."""
     import oracle
 
     rows, cols, M = 6144, 2048, 2048
@@ -653,6 +656,10 @@ def test_gpu_prefill_bench_shape_matches_oracle(ctx):
     for t in (0, 1, 63, 64, 777, 1024, M - 1):
         ref = oracle.matvec(ph.KIND_PTQ1, cols, rows, w, X[t], False, threads=THREADS)
         assert_bits_equal(Y[t], ref, f"prefill token {t}")
+    for t0 in range(0, M, 15):
+        n = min(15, M - t0)
+        got = ctx.project_f32(wid, rows, X[t0:t0 + n], tokens=n, pinned=False).reshape(n, rows)
+        assert_bits_equal(Y[t0:t0 + n], got, f"prefill tokens {t0}..{t0 + n - 1} against the skinny kernel")
     ctx.release(wid)
 
 
