@@ -48,6 +48,7 @@ extern "C" {
 #define PRISM_ERR_NONFINITE (-3)
 #define PRISM_ERR_DEVICE_FAULT (-4)
 #define PRISM_ERR_UNSUPPORTED (-5)
+#define PRISM_ERR_CANCELLED (-6)
 
 /* Activation paths for prism_hip_supports (project / project_q8 / project_f32). */
 #define PRISM_PATH_Q8K 0
@@ -95,6 +96,56 @@ uint64_t prism_hip_operation_capacity(const prism_hip_ctx *ctx);
  * supported projection, -1 (unknown) otherwise. */
 int64_t prism_hip_operation_count(const prism_hip_ctx *ctx, uint32_t kind, uint64_t cols, uint64_t rows);
 
+/* Work counted by one context over its lifetime, as MatvecStatistics counts it for one
+ * scratch owner (src/kernels.rs:1792-1865).  Counts include failed work, saturate at
+ * UINT64_MAX and survive errors, faults and weight releases; they describe dispatch,
+ * not timing.
+ *  - preparations: activation preparations attempted by the F32 entry points (one per
+ *    call, shared by the call's matrices, as siblings share one prepared activation)
+ *    and by the quantize entry points;
+ *  - preparation_failures: those rejected before a matrix could be attempted (a null
+ *    or empty input, an extent the quantizer cannot take); no matrix attempt is
+ *    counted for them.  A non-finite input found by the device-side quantizer fails
+ *    the dispatched call instead (it is counted as a failed device operation);
+ *  - matrix_attempts / matrix_successes: matrices of every projection call, grouped
+ *    matrices counted individually (a gate/up/down chain is three);
+ *  - rejected_before_dispatch: attempts rejected before any launch (unknown weight,
+ *    ineligible geometry, extent mismatch, latched fault);
+ *  - device_operations: attempts dispatched to the GPU, including later failures (the
+ *    reference's scalar_operations / neon_operations: this library has one backend);
+ *  - grouped_dispatches: single calls submitting two or more matrices together
+ *    (grouped_row_dispatches). */
+typedef struct prism_hip_statistics {
+    uint64_t preparations;
+    uint64_t preparation_failures;
+    uint64_t matrix_attempts;
+    uint64_t matrix_successes;
+    uint64_t rejected_before_dispatch;
+    uint64_t device_operations;
+    uint64_t grouped_dispatches;
+} prism_hip_statistics;
+/* The most recent projection call's record, as MatvecDiagnostics keeps it for the most
+ * recent matrix attempt (src/kernels.rs:1725-1790): dispatched = launched after the
+ * weight, activation and output checks; succeeded = complete, finite output returned.
+ * Both 0 after a call rejected before dispatch. */
+typedef struct prism_hip_diagnostics {
+    int32_t dispatched;
+    int32_t succeeded;
+} prism_hip_diagnostics;
+/* Copy the counters / the last record; PRISM_ERR_INVALID_INPUT for a null argument. */
+int prism_hip_get_statistics(const prism_hip_ctx *ctx, prism_hip_statistics *out);
+int prism_hip_get_diagnostics(const prism_hip_ctx *ctx, prism_hip_diagnostics *out);
+
+/* Cancellation shared with the request owner (src/runtime.rs:35-60): registers a
+ * caller-owned flag, read with acquire ordering, nonzero meaning cancelled; NULL
+ * unregisters.  Every projection, quantize and decoder call checks it on entry and
+ * prism_hip_decoder_generate between steps; with a flag registered a generate keeps at
+ * most two steps in flight, so at most two complete after the flag is set (the
+ * reference's "an executing scalar operation completes first").  A cancelled call waits
+ * for the work it enqueued, zero-fills its outputs and returns PRISM_ERR_CANCELLED.  The
+ * flag stays cancelled until its owner clears it, and must outlive the registration. */
+int prism_hip_set_cancellation(prism_hip_ctx *ctx, const int32_t *flag);
+
 /* ---- eligibility -------------------------------------------------------------- */
 
 /* supports / supports_q8 / supports_f32 (projection.rs:38-44,59-66,89-92), decided
@@ -118,6 +169,9 @@ int prism_hip_supports_f32_ffn_swiglu(const prism_hip_ctx *ctx, const prism_tens
 /* supports_f32_ffn_chain (projection.rs:261-263): tensors[3] = gate, up [ffn][hidden]
  * and down [hidden][ffn], one packed kind.  The chain has no Hadamard transform. */
 int prism_hip_supports_f32_ffn_chain(const prism_hip_ctx *ctx, const prism_tensor_desc *tensors);
+/* supports_f32_ffn_chain_lora (projection.rs:290-296; trait default false): the FFN
+ * chain's own eligibility -- the rank-one A dot adds no geometry of its own. */
+int prism_hip_supports_f32_ffn_chain_lora(const prism_hip_ctx *ctx, const prism_tensor_desc *tensors);
 /* supports_tile_tokens (projection.rs:265-269; trait default false): multi-token tiles run batched on the
  * device (one weight read per batch of tokens).  1 unless faulted. */
 int prism_hip_supports_tile_tokens(const prism_hip_ctx *ctx);
@@ -198,6 +252,18 @@ int prism_hip_ffn_swiglu(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_
  * and down share one packed kind (PQ2, PTQ1, Q2_K, Q8_0, TQ1_0 or TQ2_0). */
 int prism_hip_ffn_chain(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                         const float *x, const float *residual, int pinned, float *out);
+/* project_f32_ffn_chain_lora (projection.rs:298-326, called from
+ * matvec_ffn_chain_lora_with_executor :653-697) without the Hadamard transform: the chain
+ * of prism_hip_ffn_chain, plus *lora_dot = lora_a . SwiGLU(gate(x), up(x)) with lora_a[ffn]
+ * (ffn = down's columns), in lora_a_dot's arithmetic (src/kernels.rs:2336-2357): pinned with
+ * ffn % 16 == 0, sixteen binary32 FMA lanes combined as pinned_gdn::dot_scalar
+ * (src/kernels/pinned_gdn.rs:205-230); otherwise the binary32 products summed in binary64
+ * in index order (float_dot, src/kernels.rs:1256-1273).  A non-finite lora_a is rejected
+ * before any launch (PRISM_ERR_INVALID_INPUT); a non-finite dot or output fails the call.
+ * On any error out is zero-filled and *lora_dot is 0. */
+int prism_hip_ffn_chain_lora(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                             const float *x, const float *residual, const float *lora_a, int pinned, float *out,
+                             float *lora_dot);
 /* project_f32_ffn_swiglu_tokens (projection.rs:239-259) and project_f32_ffn_chain_tokens
  * (projection.rs:328-355) without the Hadamard transform: x [tokens][hidden], residual
  * (or NULL) and out [tokens][hidden] (SwiGLU: out [tokens][ffn]).  Gate and up run as

@@ -95,6 +95,7 @@ def lib():
             "po_vector_exp": (ctypes.c_float, [ctypes.c_float]),
             "po_silu": (None, [P, S, I]),
             "po_swiglu": (None, [P, P, S, I]),
+            "po_lora_a_dot": (I, [P, P, S, I, P]),
             "po_ffn": (I, [U, S, S, P, P, P, P, P, I, P, P, I]),
             "po_rms_norm": (I, [P, P, S, ctypes.c_float, P]),
             "po_rope_frequencies": (None, [S, P, P, ctypes.c_float, P, P]),
@@ -298,6 +299,14 @@ def swiglu(gate, up, pinned: bool) -> np.ndarray:
     u = _f32(up).copy()
     lib().po_swiglu(_p(g), _p(u), g.size, int(pinned))
     return u
+
+
+def lora_a_dot(a, h, pinned: bool) -> np.float32:
+    """lora_a_dot (src/kernels.rs:2336-2357) of the LoRA A factor with the SwiGLU vector."""
+    a, h = _f32(a), _f32(h)
+    out = np.zeros(1, np.float32)
+    _check(lib().po_lora_a_dot(_p(a), _p(h), a.size, int(pinned), _p(out)), "lora_a_dot")
+    return out[0]
 
 
 def ffn(kind: int, hidden: int, ffn_dim: int, wg, wu, wd, x, residual=None, pinned: bool = False, threads: int = 1):

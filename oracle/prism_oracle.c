@@ -40,6 +40,11 @@
  *                        bits (vector body, libm tail, finite edges); bitwise parity of
  *                        the source path (libm exp) is unpinnable.
  *   matvec/ffn           compositions of the above; per-token == row dot loop.
+ *   lora_a_dot           pinned: sixteen FMA lanes on inputs whose products and sums are
+ *                        exact equal the exact dot, and a constructed input whose lane
+ *                        sums differ from the ordered sum pins the lane combination;
+ *                        source: constructed inputs where the ordered binary64 sum
+ *                        absorbs a term (1e20 + 1 - 1e20 + 1 == 1, not 2) pin the order.
  */
 #include "prism_oracle.h"
 
@@ -909,6 +914,41 @@ void po_swiglu(const float *gate, float *up, size_t n, int pinned) {
             up[i] = up[i] * s;
         }
     }
+}
+
+/* lora_a_dot (src/kernels.rs:2336-2357): a . input with a finite input of matching
+ * length.  Pinned with n % 16 == 0: pinned_gdn::dot_scalar (src/kernels/pinned_gdn.rs:
+ * 205-230), sixteen binary32 fused multiply-add lanes, register r lane l holding
+ * element offset + 4r + l, reduced as (s0 + s2) + (s1 + s3) per lane, then
+ * (l0 + l1) + (l2 + l3).  Otherwise float_dot (src/kernels.rs:1256-1273): the binary32
+ * products summed in binary64 in index order, rounded to binary32.  A non-finite result
+ * is an error (finite, src/kernels.rs:152-163). */
+int po_lora_a_dot(const float *a, const float *input, size_t n, int pinned, float *out) {
+    *out = 0.0f;
+    if (n == 0) return PO_ERR_INVALID_INPUT;
+    for (size_t i = 0; i < n; i++)
+        if (!is_finite(input[i])) return PO_ERR_INVALID_INPUT;
+    float r;
+    if (pinned && n % 16 == 0) {
+        float sums[4][4] = {{0}};
+        for (size_t off = 0; off < n; off += 16)
+            for (int reg = 0; reg < 4; reg++)
+                for (int lane = 0; lane < 4; lane++) {
+                    const size_t i = off + (size_t)reg * 4 + (size_t)lane;
+                    sums[reg][lane] = fmaf(a[i], input[i], sums[reg][lane]);
+                }
+        float lanes[4];
+        for (int lane = 0; lane < 4; lane++)
+            lanes[lane] = (sums[0][lane] + sums[2][lane]) + (sums[1][lane] + sums[3][lane]);
+        r = (lanes[0] + lanes[1]) + (lanes[2] + lanes[3]);
+    } else {
+        double s = 0.0;
+        for (size_t i = 0; i < n; i++) s += (double)(a[i] * input[i]);
+        r = (float)s;
+    }
+    if (!is_finite(r)) return PO_ERR_NONFINITE;
+    *out = r;
+    return PO_OK;
 }
 
 /* gate/up projections sharing one preparation, SwiGLU into up, then down

@@ -117,6 +117,9 @@ float po_vector_exp(float x);
 void po_silu(float *x, size_t n, int pinned);
 void po_swiglu(const float *gate, float *up, size_t n, int pinned);
 
+/* ---- LoRA A dot beside the FFN chain (src/kernels.rs:2336-2357) ---- */
+int po_lora_a_dot(const float *a, const float *input, size_t n, int pinned, float *out);
+
 /* ---- FFN chain: gate/up -> SwiGLU -> down (+ residual) (src/graph.rs:3935-3956) ---- */
 int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const uint8_t *wu,
            const uint8_t *wd, const float *x, const float *residual, int pinned, float *out,

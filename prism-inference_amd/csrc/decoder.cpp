@@ -312,7 +312,7 @@ int family_of(const char *name, Family *f) {
 extern "C" {
 
 prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decoder_geometry *g, uint32_t max_steps) {
-    if (check_ready(c) || !g) return nullptr;
+    if (check_live(c) || !g) return nullptr;
     const bool ok = g->head_dim == 128 && g->heads && g->kv_heads && g->heads % g->kv_heads == 0 && g->rope &&
                     g->rope <= g->head_dim && g->rope % 2 == 0 && g->hidden && g->hidden % 128 == 0 && g->ffn &&
                     g->ffn % 128 == 0 && (g->heads * g->head_dim) % 128 == 0 && g->vocab && g->layers && g->layers <= 500 &&
@@ -380,7 +380,7 @@ int prism_hip_decoder_set_layer(prism_hip_decoder *d, uint32_t layer, const uint
                                 const uint8_t *gate, const uint8_t *up, const uint8_t *down, const float *norm,
                                 const float *post_norm, const float *q_norm, const float *k_norm) {
     if (!d) return PRISM_ERR_INVALID_INPUT;
-    int rc = check_ready(d->ctx);
+    int rc = check_live(d->ctx);
     if (rc) return rc;
     if (layer >= d->layers.size() || !qkv || !o || !gate || !up || !down || !norm || !post_norm || !q_norm || !k_norm)
         return fail(d->ctx, PRISM_ERR_INVALID_INPUT, "bad decoder layer arguments");
@@ -404,7 +404,7 @@ int prism_hip_decoder_set_layer(prism_hip_decoder *d, uint32_t layer, const uint
 int prism_hip_decoder_set_cache(prism_hip_decoder *d, uint32_t layer, const uint16_t *k, const uint16_t *v,
                                 uint64_t tokens) {
     if (!d) return PRISM_ERR_INVALID_INPUT;
-    int rc = check_ready(d->ctx);
+    int rc = check_live(d->ctx);
     if (rc) return rc;
     if (layer >= d->layers.size() || tokens > d->g.max_tokens || (tokens && (!k || !v)))
         return fail(d->ctx, PRISM_ERR_INVALID_INPUT, "bad decoder cache arguments");
@@ -416,7 +416,7 @@ int prism_hip_decoder_set_cache(prism_hip_decoder *d, uint32_t layer, const uint
 
 int prism_hip_decoder_set_head(prism_hip_decoder *d, const uint8_t *lm_head, const float *output_norm) {
     if (!d) return PRISM_ERR_INVALID_INPUT;
-    int rc = check_ready(d->ctx);
+    int rc = check_live(d->ctx);
     if (rc) return rc;
     if (!lm_head || !output_norm) return fail(d->ctx, PRISM_ERR_INVALID_INPUT, "bad decoder head arguments");
     drop_graph(d);
@@ -467,7 +467,29 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
     HIP_OR_FAIL(c, hipEventCreate(&t0));
     HIP_OR_FAIL(c, hipEventCreate(&t1));
     HIP_OR_FAIL(c, hipEventRecord(t0, s));
+    // With a cancellation flag registered, steps are checked between launches and at most
+    // two are in flight: step i waits for step i - 2 before it is enqueued.
+    hipEvent_t inflight[2] = {nullptr, nullptr};
+    if (c->cancel) {
+        for (hipEvent_t &e : inflight) {
+            const hipError_t he = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+            if (he != hipSuccess && !rc) rc = hip_fail(c, he, "hipEventCreate");
+        }
+    }
     for (uint32_t i = 0; i < steps && !rc; ++i) {
+        if (c->cancel) {
+            if (i >= 2) {
+                const hipError_t he = hipEventSynchronize(inflight[i % 2]);
+                if (he != hipSuccess) {
+                    rc = hip_fail(c, he, "hipEventSynchronize");
+                    break;
+                }
+            }
+            if (cancelled(c)) {
+                rc = fail(c, PRISM_ERR_CANCELLED, "cancelled by the request owner");
+                break;
+            }
+        }
         if (use_graph) {
             hipError_t e = hipGraphLaunch(d->exec, s);
             if (e != hipSuccess) rc = hip_fail(c, e, "hipGraphLaunch");
@@ -479,7 +501,18 @@ int prism_hip_decoder_generate(prism_hip_decoder *d, uint32_t token, uint64_t po
                                           hipMemcpyDeviceToDevice, s);
             if (e != hipSuccess) rc = hip_fail(c, e, "copy logits");
         }
+        if (!rc && c->cancel) {
+            const hipError_t he = hipEventRecord(inflight[i % 2], s);
+            if (he != hipSuccess) rc = hip_fail(c, he, "hipEventRecord");
+        }
     }
+    if (rc == PRISM_ERR_CANCELLED) {  // the enqueued steps complete first (and report their errors)
+        const int drc = drain(c, s);
+        if (drc) rc = drc;
+        else fail(c, PRISM_ERR_CANCELLED, "cancelled by the request owner");
+    }
+    for (hipEvent_t e : inflight)
+        if (e) (void)hipEventDestroy(e);
     if (!rc) {
         hipError_t e = hipEventRecord(t1, s);
         if (e != hipSuccess) rc = hip_fail(c, e, "hipEventRecord");

@@ -89,6 +89,8 @@ int launch_swiglu(const float *gate, const float *up, float *h, uint64_t n, uint
                   hipStream_t s);
 // out += residual, flagging non-finite sums.
 int launch_add_residual(float *out, const float *residual, uint64_t n, int *err, hipStream_t s);
+// lora_a_dot of a[0..n) with the SwiGLU vector h into *out (one workgroup).
+int launch_lora_dot(const float *a, const float *h, uint32_t n, int pinned, float *out, int *err, hipStream_t s);
 // p[0..n) = v with a kernel (safe inside captured graphs, unlike a memset node).
 int launch_fill_i32(int *p, int v, uint32_t n, hipStream_t s);
 

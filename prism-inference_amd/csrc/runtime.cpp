@@ -8,6 +8,8 @@
 // context as unsupported (tools/adreno-vulkan/src/executor.rs:1507-1530).
 #include "runtime_internal.hpp"
 
+#include <cmath>
+
 using namespace prism;
 using namespace prism::rt;
 
@@ -289,7 +291,7 @@ void prism_hip_destroy(prism_hip_ctx *c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     prism_hip_weight_release_all(c);
-    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res, &c->pre, &c->sk})
+    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res, &c->pre, &c->sk, &c->lora})
         if (b->p) (void)hipFree(b->p);
     if (c->err) (void)hipFree(c->err);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -326,6 +328,10 @@ int prism_hip_supports_f32_ffn_swiglu(const prism_hip_ctx *c, const prism_tensor
 int prism_hip_supports_f32_ffn_chain(const prism_hip_ctx *c, const prism_tensor_desc *tensors) {
     if (!c || c->faulted || !tensors) return 0;
     return ffn_eligible(tensors[0], tensors[1], &tensors[2]) ? 1 : 0;
+}
+
+int prism_hip_supports_f32_ffn_chain_lora(const prism_hip_ctx *c, const prism_tensor_desc *tensors) {
+    return prism_hip_supports_f32_ffn_chain(c, tensors);
 }
 
 int prism_hip_supports_tile_tokens(const prism_hip_ctx *c) { return (!c || c->faulted) ? 0 : 1; }
@@ -405,7 +411,7 @@ static prism_weight_id store_weight(prism_hip_ctx *c, uint64_t key, uint32_t kin
 
 prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols, uint64_t rows,
                                          const void *host, uint64_t bytes) {
-    int rc = check_ready(c);
+    int rc = check_live(c);
     if (rc) return rc;
     if (!host) return fail(c, PRISM_ERR_INVALID_INPUT, "null weight bytes");
     rc = check_geometry(c, kind, cols, rows, bytes);
@@ -430,7 +436,7 @@ prism_weight_id prism_hip_weight_acquire(prism_hip_ctx *c, uint64_t key, uint32_
 
 prism_weight_id prism_hip_weight_acquire_device(prism_hip_ctx *c, uint64_t key, uint32_t kind, uint64_t cols,
                                                 uint64_t rows, const void *device_ptr, uint64_t bytes) {
-    int rc = check_ready(c);
+    int rc = check_live(c);
     if (rc) return rc;
     if (!device_ptr) return fail(c, PRISM_ERR_INVALID_INPUT, "null weight bytes");
     rc = check_geometry(c, kind, cols, rows, bytes);
@@ -448,7 +454,7 @@ prism_weight_id prism_hip_weight_acquire_device(prism_hip_ctx *c, uint64_t key, 
 
 prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,
                                              const void *dev, uint64_t bytes) {
-    int rc = check_ready(c);
+    int rc = check_live(c);
     if (rc) return rc;
     if (!dev) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
     rc = check_geometry(c, kind, cols, rows, bytes);
@@ -459,7 +465,7 @@ prism_weight_id prism_hip_weight_wrap_device(prism_hip_ctx *c, uint32_t kind, ui
 int prism_hip_weight_repack_tiled(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,
                                   const void *native_dev, uint64_t native_bytes, void *tiled_dev,
                                   uint64_t tiled_bytes_) {
-    int rc = check_ready(c);
+    int rc = check_live(c);
     if (rc) return rc;
     if (!native_dev || !tiled_dev) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
     rc = check_geometry(c, kind, cols, rows, native_bytes);
@@ -478,7 +484,7 @@ int prism_hip_weight_repack_tiled(prism_hip_ctx *c, uint32_t kind, uint64_t cols
 
 prism_weight_id prism_hip_weight_wrap_tiled(prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows,
                                             const void *tiled_dev, uint64_t tiled_bytes_) {
-    int rc = check_ready(c);
+    int rc = check_live(c);
     if (rc) return rc;
     if (!tiled_dev) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
     uint64_t g, b;
@@ -519,8 +525,8 @@ int prism_hip_weight_release_all(prism_hip_ctx *c) {
 
 uint64_t prism_hip_resident_bytes(const prism_hip_ctx *c) { return c ? c->resident : 0; }
 
-int prism_hip_project_q8k(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k_block *act, uint64_t nblocks,
-                          uint32_t tokens, int fused, float *out) {
+static int project_q8k_host(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k_block *act, uint64_t nblocks,
+                            uint32_t tokens, int fused, float *out, Tally &t) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, PRISM_PATH_Q8K, &w);
     if (rc) {
@@ -532,6 +538,7 @@ int prism_hip_project_q8k(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k
         zero(out, n);
         return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_K activation extent mismatch");
     }
+    t.dispatch();
     const size_t ab = sizeof(prism_q8k_block) * nblocks;
     rc = ensure(c, c->act, ab);
     if (!rc) rc = ensure(c, c->out, sizeof(float) * n);
@@ -545,8 +552,14 @@ int prism_hip_project_q8k(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k
     return rc;
 }
 
-int prism_hip_project_q8(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_block *act, uint64_t nblocks,
-                         uint32_t tokens, int pinned, float *out) {
+int prism_hip_project_q8k(prism_hip_ctx *c, prism_weight_id wid, const prism_q8k_block *act, uint64_t nblocks,
+                          uint32_t tokens, int fused, float *out) {
+    Tally t(c, 1, false);
+    return t(project_q8k_host(c, wid, act, nblocks, tokens, fused, out, t));
+}
+
+static int project_q8_host(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_block *act, uint64_t nblocks,
+                           uint32_t tokens, int pinned, float *out, Tally &t) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, PRISM_PATH_Q8, &w);
     if (rc) {
@@ -558,6 +571,7 @@ int prism_hip_project_q8(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_b
         zero(out, n);
         return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_0 activation extent mismatch");
     }
+    t.dispatch();
     const size_t ab = sizeof(prism_q8_block) * nblocks;
     rc = ensure(c, c->act, ab);
     if (!rc) rc = ensure(c, c->out, sizeof(float) * n);
@@ -571,8 +585,14 @@ int prism_hip_project_q8(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_b
     return rc;
 }
 
-static int project_f32_host(prism_hip_ctx *c, prism_weight_id wid, const float *x, uint32_t tokens, int pinned,
-                            float *out) {
+int prism_hip_project_q8(prism_hip_ctx *c, prism_weight_id wid, const prism_q8_block *act, uint64_t nblocks,
+                         uint32_t tokens, int pinned, float *out) {
+    Tally t(c, 1, false);
+    return t(project_q8_host(c, wid, act, nblocks, tokens, pinned, out, t));
+}
+
+static int project_f32_checked(prism_hip_ctx *c, prism_weight_id wid, const float *x, uint32_t tokens, int pinned,
+                               float *out, Tally &t) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, PRISM_PATH_F32, &w);
     if (rc) {
@@ -581,9 +601,11 @@ static int project_f32_host(prism_hip_ctx *c, prism_weight_id wid, const float *
     }
     const size_t n = w->rows * tokens;
     if (!x || !out || tokens == 0) {
+        t.bad_input();
         zero(out, n);
         return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output");
     }
+    t.dispatch();
     rc = ensure(c, c->x, sizeof(float) * w->cols * tokens);
     if (!rc) rc = ensure(c, c->out, sizeof(float) * n);
     if (!rc) {
@@ -596,6 +618,12 @@ static int project_f32_host(prism_hip_ctx *c, prism_weight_id wid, const float *
     if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), n);
     if (rc) zero(out, n);
     return rc;
+}
+
+static int project_f32_host(prism_hip_ctx *c, prism_weight_id wid, const float *x, uint32_t tokens, int pinned,
+                            float *out) {
+    Tally t(c, 1, true);
+    return t(project_f32_checked(c, wid, x, tokens, pinned, out, t));
 }
 
 int prism_hip_project_f32(prism_hip_ctx *c, prism_weight_id w, const float *x, uint32_t tokens, int pinned,
@@ -612,8 +640,8 @@ int prism_hip_mul_mat(prism_hip_ctx *c, prism_weight_id a, const float *b, uint3
 }
 
 // Host-pointer sibling group over `tokens` token rows: outs[i] receives [tokens][rows_i].
-static int group_host(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, uint32_t tokens,
-                      int pinned, float *const *outs) {
+static int group_checked(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, uint32_t tokens,
+                         int pinned, float *const *outs, Tally &tally) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (!ws || !outs || n == 0 || n > 8) return fail(c, PRISM_ERR_INVALID_INPUT, "bad projection group");
     const Weight *w[8] = {};
@@ -626,7 +654,10 @@ static int group_host(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, c
     };
     int rc = check_ready(c);
     if (rc) return clear(rc);
-    if (!x || tokens == 0) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "null input or no tokens"));
+    if (!x || tokens == 0) {
+        tally.bad_input();
+        return clear(fail(c, PRISM_ERR_INVALID_INPUT, "null input or no tokens"));
+    }
     prism_tensor_desc t[8];
     for (uint32_t i = 0; i < n; ++i) {
         if (!w[i] || !outs[i]) return clear(fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id in group"));
@@ -634,6 +665,7 @@ static int group_host(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, c
     }
     if (!group_eligible(t, n))
         return clear(fail(c, PRISM_ERR_UNSUPPORTED, "group members do not share an input width and activation contract"));
+    tally.dispatch();
     uint64_t total = 0;
     for (uint32_t i = 0; i < n; ++i) total += w[i]->rows;
     const uint64_t cols = w[0]->cols;
@@ -659,6 +691,12 @@ static int group_host(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, c
     return rc ? clear(rc) : rc;
 }
 
+static int group_host(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, uint32_t tokens,
+                      int pinned, float *const *outs) {
+    Tally t(c, ws && outs && n <= 8 ? n : 1, true);
+    return t(group_checked(c, ws, n, x, tokens, pinned, outs, t));
+}
+
 int prism_hip_project_f32_group(prism_hip_ctx *c, const prism_weight_id *ws, uint32_t n, const float *x, int pinned,
                                 float *const *outs) {
     return group_host(c, ws, n, x, 1, pinned, outs);
@@ -681,8 +719,8 @@ int prism_hip_project_f32_triple_tokens(prism_hip_ctx *c, const prism_weight_id 
     return group_host(c, ws, 3, x, tokens, pinned, outs);
 }
 
-static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did, const float *x,
-                    const float *residual, uint32_t tokens, int pinned, float *out) {
+static int ffn_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
+                       const float *x, const float *residual, uint32_t tokens, int pinned, float *out, Tally &t) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
     // Output length: down's rows, or gate's for the SwiGLU vector; known when those ids are.
@@ -698,6 +736,7 @@ static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, 
         return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
     }
     if (!x || !out || tokens == 0) {
+        t.bad_input();
         zero(out, nout);
         return fail(c, PRISM_ERR_INVALID_INPUT, "null input or output, or no tokens");
     }
@@ -706,6 +745,7 @@ static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, 
         zero(out, nout);
         return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs gate/up [ffn][hidden] and down [hidden][ffn] of one packed kind");
     }
+    t.dispatch();
     const uint64_t nx = g->cols * tokens;
     rc = ensure(c, c->x, sizeof(float) * nx);
     if (!rc) rc = ensure(c, c->out, sizeof(float) * nout);
@@ -725,6 +765,12 @@ static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, 
     return rc;
 }
 
+static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did, const float *x,
+                    const float *residual, uint32_t tokens, int pinned, float *out) {
+    Tally t(c, did ? 3 : 2, true);
+    return t(ffn_checked(c, gid, uid, did, x, residual, tokens, pinned, out, t));
+}
+
 int prism_hip_ffn_swiglu(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
                          float *out) {
     return ffn_host(c, gate, up, 0, x, nullptr, 1, pinned, out);
@@ -738,83 +784,200 @@ int prism_hip_ffn_swiglu_tokens(prism_hip_ctx *c, prism_weight_id gate, prism_we
 int prism_hip_ffn_chain(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                         const float *x, const float *residual, int pinned, float *out) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
-    if (down == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "down projection required");
+    if (down == 0) return Tally(c, 3, true)(fail(c, PRISM_ERR_INVALID_INPUT, "down projection required"));
     return ffn_host(c, gate, up, down, x, residual, 1, pinned, out);
 }
 
 int prism_hip_ffn_chain_tokens(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
                                const float *x, const float *residual, uint32_t tokens, int pinned, float *out) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
-    if (down == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "down projection required");
+    if (down == 0) return Tally(c, 3, true)(fail(c, PRISM_ERR_INVALID_INPUT, "down projection required"));
     return ffn_host(c, gate, up, down, x, residual, tokens, pinned, out);
+}
+
+static int ffn_lora_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
+                            const float *x, const float *residual, const float *lora_a, int pinned, float *out,
+                            float *lora_dot, Tally &t) {
+    if (lora_dot) *lora_dot = 0.0f;
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    const Weight *g = find(c, gid), *u = find(c, uid), *d = find(c, did);
+    const uint64_t nout = d ? d->rows : 0;
+    int rc = check_ready(c);
+    if (rc) {
+        zero(out, nout);
+        return rc;
+    }
+    if (!g || !u || !d) {
+        zero(out, nout);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "unknown weight id");
+    }
+    const prism_tensor_desc dd = desc_of(*d);
+    if (!ffn_eligible(desc_of(*g), desc_of(*u), &dd)) {
+        zero(out, nout);
+        return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs gate/up [ffn][hidden] and down [hidden][ffn] of one packed kind");
+    }
+    if (!x || !out || !lora_a || !lora_dot) {
+        t.bad_input();
+        zero(out, nout);
+        return fail(c, PRISM_ERR_INVALID_INPUT, "null input, output, LoRA factor or dot");
+    }
+    // The caller's own check (matvec_ffn_chain_lora_with_executor, projection.rs:664-670):
+    // a non-finite LoRA A factor never reaches a submission.
+    const uint64_t nl = d->cols;
+    for (uint64_t i = 0; i < nl; ++i) {
+        if (!std::isfinite(lora_a[i])) {
+            zero(out, nout);
+            return fail(c, PRISM_ERR_INVALID_INPUT, "non-finite LoRA A factor");
+        }
+    }
+    t.dispatch();
+    rc = ensure(c, c->x, sizeof(float) * g->cols);
+    if (!rc) rc = ensure(c, c->out, sizeof(float) * nout);
+    if (!rc) rc = ensure(c, c->h, sizeof(float) * g->rows);
+    if (!rc) rc = ensure(c, c->lora, sizeof(float) * (nl + 1));
+    if (!rc && residual) rc = ensure(c, c->res, sizeof(float) * nout);
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(c->x.p, x, sizeof(float) * g->cols, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(c->lora.p, lora_a, sizeof(float) * nl, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess && residual)
+            e = hipMemcpyAsync(c->res.p, residual, sizeof(float) * nout, hipMemcpyHostToDevice, c->stream);
+        rc = e == hipSuccess ? PRISM_OK : hip_fail(c, e, "upload activations");
+    }
+    float *hv = static_cast<float *>(c->h.p), *dot = static_cast<float *>(c->lora.p) + nl;
+    if (!rc)
+        rc = ffn_chain_impl(c, *g, *u, d, static_cast<const float *>(c->x.p),
+                            residual ? static_cast<const float *>(c->res.p) : nullptr, pinned,
+                            static_cast<float *>(c->out.p), hv, c->stream);
+    if (!rc)
+        rc = launch_result(c, launch_lora_dot(static_cast<const float *>(c->lora.p), hv, static_cast<uint32_t>(nl),
+                                              pinned, dot, c->err, c->stream),
+                           "LoRA dot launch");
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(lora_dot, dot, sizeof(float), hipMemcpyDeviceToHost, c->stream);
+        if (e != hipSuccess) rc = hip_fail(c, e, "copy LoRA dot");
+    }
+    if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), nout);
+    if (!rc && !std::isfinite(*lora_dot)) rc = fail(c, PRISM_ERR_NONFINITE, "non-finite LoRA dot");
+    if (rc) {
+        zero(out, nout);
+        *lora_dot = 0.0f;
+    }
+    return rc;
+}
+
+int prism_hip_ffn_chain_lora(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
+                             const float *x, const float *residual, const float *lora_a, int pinned, float *out,
+                             float *lora_dot) {
+    Tally t(c, 3, true);
+    return t(ffn_lora_checked(c, gate, up, down, x, residual, lora_a, pinned, out, lora_dot, t));
 }
 
 int prism_hip_quantize_q8k_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int pinned,
                                   prism_q8k_block *out, void *stream) {
+    Tally t(c, 0, true);
     int rc = check_ready(c);
-    if (rc) return rc;
-    if (!x || !out || cols == 0 || cols % 256) return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_K needs cols % 256 == 0");
+    if (rc) return t(rc);
+    if (!x || !out || cols == 0 || cols % 256) {
+        t.bad_input();
+        return t(fail(c, PRISM_ERR_INVALID_INPUT, "Q8_K needs cols % 256 == 0"));
+    }
     hipStream_t s;
     rc = call_stream(c, stream, &s);
-    return rc ? rc : quantize(c, 0, x, cols, tokens, pinned, out, s);
+    return t(rc ? rc : quantize(c, 0, x, cols, tokens, pinned, out, s));
 }
 
 int prism_hip_quantize_q8_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int contract,
                                  prism_q8_block *out, void *stream) {
+    Tally t(c, 0, true);
     int rc = check_ready(c);
-    if (rc) return rc;
-    if (!x || !out || cols == 0 || cols % 32 || contract < 0 || contract > 2)
-        return fail(c, PRISM_ERR_INVALID_INPUT, "Q8_0 needs cols % 32 == 0 and a known contract");
+    if (rc) return t(rc);
+    if (!x || !out || cols == 0 || cols % 32 || contract < 0 || contract > 2) {
+        t.bad_input();
+        return t(fail(c, PRISM_ERR_INVALID_INPUT, "Q8_0 needs cols % 32 == 0 and a known contract"));
+    }
     hipStream_t s;
     rc = call_stream(c, stream, &s);
-    if (rc) return rc;
-    return launch_result(c, launch_quantize_q8_0(x, cols, tokens, contract, out, c->err, s), "quantize");
+    if (rc) return t(rc);
+    return t(launch_result(c, launch_quantize_q8_0(x, cols, tokens, contract, out, c->err, s), "quantize"));
 }
 
-int prism_hip_project_device(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act, uint32_t tokens,
-                             int pinned, float *out, void *stream) {
+static int project_device_checked(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act, uint32_t tokens,
+                                  int pinned, float *out, void *stream, Tally &t) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, path, &w);
     if (rc) return rc;
-    if (!act || !out || tokens == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    if (!act || !out || tokens == 0) {
+        t.bad_input();
+        return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    }
     hipStream_t s;
     rc = call_stream(c, stream, &s);
     if (rc) return rc;
+    t.dispatch();
     if (path == PRISM_PATH_F32)
         return project_f32_dev(c, *w, static_cast<const float *>(act), tokens, pinned, out, c->act, s);
     return matvec(c, *w, path == PRISM_PATH_Q8K ? kActQ8K : kActQ8, act, tokens, pinned, out, s);
 }
 
-int prism_hip_project_device_noalloc(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act,
-                                     uint32_t tokens, int pinned, float *out, void *stream) {
+int prism_hip_project_device(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act, uint32_t tokens,
+                             int pinned, float *out, void *stream) {
+    Tally t(c, 1, path == PRISM_PATH_F32);
+    return t(project_device_checked(c, wid, path, act, tokens, pinned, out, stream, t));
+}
+
+static int project_noalloc_checked(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act,
+                                   uint32_t tokens, int pinned, float *out, void *stream, Tally &t) {
     const Weight *w = nullptr;
     int rc = prepare_weight(c, wid, path, &w);
     if (rc) return rc;
-    if (!act || !out || tokens == 0) return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    if (!act || !out || tokens == 0) {
+        t.bad_input();
+        return fail(c, PRISM_ERR_INVALID_INPUT, "null device pointer");
+    }
     if (!c->noalloc) return fail(c, PRISM_ERR_UNSUPPORTED, c->noalloc_error);
     hipStream_t s;
     rc = call_stream(c, stream, &s);
     if (rc) return rc;
+    t.dispatch();
     Scratch fixed{c, static_cast<uint8_t *>(c->noalloc), c->noalloc_bytes, 0};
     if (path == PRISM_PATH_F32)
         return project_f32_dev(c, *w, static_cast<const float *>(act), tokens, pinned, out, c->act, s, nullptr, &fixed);
     return matvec(c, *w, path == PRISM_PATH_Q8K ? kActQ8K : kActQ8, act, tokens, pinned, out, s, &fixed);
 }
 
-int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
-                               const float *x, const float *residual, int pinned, float *out, float *h,
-                               void *stream) {
+int prism_hip_project_device_noalloc(prism_hip_ctx *c, prism_weight_id wid, int path, const void *act,
+                                     uint32_t tokens, int pinned, float *out, void *stream) {
+    Tally t(c, 1, path == PRISM_PATH_F32);
+    return t(project_noalloc_checked(c, wid, path, act, tokens, pinned, out, stream, t));
+}
+
+static int ffn_device_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
+                              const float *x, const float *residual, int pinned, float *out, float *h, void *stream,
+                              Tally &t) {
     int rc = check_ready(c);
     if (rc) return rc;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
-    if (!g || !u || (did && !d) || !x || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
+    if (!g || !u || (did && !d) || !out) return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
+    if (!x) {
+        t.bad_input();
+        return fail(c, PRISM_ERR_INVALID_INPUT, "bad FFN chain arguments");
+    }
     if (d && d->kind != g->kind) return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs one packed kind");
     hipStream_t s;
     rc = call_stream(c, stream, &s);
     if (rc) return rc;
+    t.dispatch();
     // Without a down projection the call is project_f32_ffn_swiglu: out receives h.
     if (!d) return ffn_chain_impl(c, *g, *u, nullptr, x, nullptr, pinned, nullptr, out, s);
     return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, s);
+}
+
+int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
+                               const float *x, const float *residual, int pinned, float *out, float *h,
+                               void *stream) {
+    Tally t(c, did ? 3 : 2, true);
+    return t(ffn_device_checked(c, gid, uid, did, x, residual, pinned, out, h, stream, t));
 }
 
 int prism_hip_sync(prism_hip_ctx *c, void *stream) {
@@ -826,5 +989,23 @@ int prism_hip_sync(prism_hip_ctx *c, void *stream) {
 }
 
 void *prism_hip_stream(prism_hip_ctx *c) { return c ? static_cast<void *>(c->stream) : nullptr; }
+
+int prism_hip_set_cancellation(prism_hip_ctx *c, const int32_t *flag) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    c->cancel = flag;
+    return PRISM_OK;
+}
+
+int prism_hip_get_statistics(const prism_hip_ctx *c, prism_hip_statistics *out) {
+    if (!c || !out) return PRISM_ERR_INVALID_INPUT;
+    *out = c->stats;
+    return PRISM_OK;
+}
+
+int prism_hip_get_diagnostics(const prism_hip_ctx *c, prism_hip_diagnostics *out) {
+    if (!c || !out) return PRISM_ERR_INVALID_INPUT;
+    *out = c->diag;
+    return PRISM_OK;
+}
 
 }  // extern "C"

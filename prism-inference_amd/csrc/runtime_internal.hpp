@@ -64,12 +64,15 @@ struct prism_hip_ctx {
     std::map<uint64_t, int64_t> by_key;
     int64_t next_id = 1;
     int *err = nullptr;  // device error flag
-    prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre, sk;
+    prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre, sk, lora;
     // This device's copy of the fixed scratch array (static_scratch.hip), looked up at
     // creation; nullptr if the lookup failed.
     void *noalloc = nullptr;
     size_t noalloc_bytes = 0;
     std::string noalloc_error;
+    prism_hip_statistics stats = {};
+    prism_hip_diagnostics diag = {};
+    const int32_t *cancel = nullptr;  // the request owner's cancellation flag, if any
 };
 
 namespace prism {
@@ -191,11 +194,60 @@ struct Scratch {
     }
 };
 
-inline int check_ready(prism_hip_ctx *c) {
+inline bool cancelled(const prism_hip_ctx *c) { return c->cancel && __atomic_load_n(c->cancel, __ATOMIC_ACQUIRE) != 0; }
+
+// Weight management: only a latched fault refuses it (cancellation concerns requests).
+inline int check_live(prism_hip_ctx *c) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
     return PRISM_OK;
 }
+
+inline int check_ready(prism_hip_ctx *c) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    if (c->faulted) return fail(c, PRISM_ERR_DEVICE_FAULT, "device fault latched");
+    if (cancelled(c)) return fail(c, PRISM_ERR_CANCELLED, "cancelled by the request owner");
+    return PRISM_OK;
+}
+
+// One public call, recorded into the context's statistics and diagnostics when it ends
+// (MatvecStatistics::record, src/kernels.rs:1798-1830): n matrices, and whether the call
+// prepares (quantizes) its own F32 activation.  The call marks a rejected activation with
+// bad_input() and the point past every check with dispatch(); operator() records the
+// outcome and passes the return code through.
+struct Tally {
+    prism_hip_ctx *c;
+    uint32_t n;
+    bool prepares;
+    bool input_ok = true, dispatched = false;
+    Tally(prism_hip_ctx *ctx, uint32_t matrices, bool prep) : c(ctx), n(matrices), prepares(prep) {}
+    void bad_input() { input_ok = false; }
+    void dispatch() { dispatched = true; }
+    static void add(uint64_t &v, uint64_t k) { v = v > UINT64_MAX - k ? UINT64_MAX : v + k; }
+    int operator()(int rc) {
+        if (!c) return rc;
+        prism_hip_statistics &s = c->stats;
+        const bool ok = rc == PRISM_OK && dispatched;
+        if (prepares) {
+            add(s.preparations, 1);
+            if (!input_ok) add(s.preparation_failures, 1);
+        }
+        if (n == 0 || !input_ok) {  // a preparation alone, or no matrix could be attempted
+            if (n) c->diag = prism_hip_diagnostics{0, 0};
+            return rc;
+        }
+        add(s.matrix_attempts, n);
+        if (ok) add(s.matrix_successes, n);
+        if (!dispatched) {
+            add(s.rejected_before_dispatch, n);
+        } else {
+            add(s.device_operations, n);
+            if (n > 1) add(s.grouped_dispatches, 1);
+        }
+        c->diag = prism_hip_diagnostics{dispatched ? 1 : 0, ok ? 1 : 0};
+        return rc;
+    }
+};
 
 inline const Weight *find(prism_hip_ctx *c, prism_weight_id w) {
     auto it = c->weights.find(w);

@@ -33,6 +33,7 @@ ERR_RESOURCE = -2
 ERR_NONFINITE = -3
 ERR_DEVICE_FAULT = -4
 ERR_UNSUPPORTED = -5
+ERR_CANCELLED = -6
 
 PATH_Q8K = 0
 PATH_Q8 = 1
@@ -84,6 +85,10 @@ def lib() -> ctypes.CDLL:
         "prism_hip_supports_f32_group": (I, [P, P, U32]),
         "prism_hip_supports_f32_ffn_swiglu": (I, [P, P, P]),
         "prism_hip_supports_f32_ffn_chain": (I, [P, P]),
+        "prism_hip_supports_f32_ffn_chain_lora": (I, [P, P]),
+        "prism_hip_get_statistics": (I, [P, P]),
+        "prism_hip_set_cancellation": (I, [P, P]),
+        "prism_hip_get_diagnostics": (I, [P, P]),
         "prism_hip_supports_tile_tokens": (I, [P]),
         "prism_hip_weight_tiled_bytes": (U64, [P, U32, U64, U64]),
         "prism_hip_weight_repack_tiled": (I, [P, U32, U64, U64, P, U64, P, U64]),
@@ -103,6 +108,7 @@ def lib() -> ctypes.CDLL:
         "prism_hip_project_f32_triple_tokens": (I, [P, P, P, U32, I, P, P, P]),
         "prism_hip_ffn_swiglu": (I, [P, I64, I64, P, I, P]),
         "prism_hip_ffn_chain": (I, [P, I64, I64, I64, P, P, I, P]),
+        "prism_hip_ffn_chain_lora": (I, [P, I64, I64, I64, P, P, P, I, P, P]),
         "prism_hip_ffn_swiglu_tokens": (I, [P, I64, I64, P, U32, I, P]),
         "prism_hip_ffn_chain_tokens": (I, [P, I64, I64, I64, P, P, U32, I, P]),
         "prism_hip_prefill": (I, [P, I64, P, U32, I, P]),
@@ -143,6 +149,21 @@ def lib() -> ctypes.CDLL:
         fn.argtypes = args
     _lib = L
     return L
+
+
+class Statistics(ctypes.Structure):
+    """prism_hip_statistics (include/prism_hip.h): MatvecStatistics, src/kernels.rs:1792-1830."""
+    _fields_ = [(n, ctypes.c_uint64) for n in ("preparations", "preparation_failures", "matrix_attempts",
+                                               "matrix_successes", "rejected_before_dispatch", "device_operations",
+                                               "grouped_dispatches")]
+
+    def as_dict(self) -> dict:
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+class Diagnostics(ctypes.Structure):
+    """prism_hip_diagnostics (include/prism_hip.h): MatvecDiagnostics, src/kernels.rs:1725-1750."""
+    _fields_ = [("dispatched", ctypes.c_int32), ("succeeded", ctypes.c_int32)]
 
 
 class GgufPolicy(ctypes.Structure):
@@ -363,6 +384,25 @@ class Context:
     def supports_f32_ffn_chain(self, gate, up, down) -> bool:
         return bool(lib().prism_hip_supports_f32_ffn_chain(self._h, _descs([gate, up, down])))
 
+    def supports_f32_ffn_chain_lora(self, gate, up, down) -> bool:
+        return bool(lib().prism_hip_supports_f32_ffn_chain_lora(self._h, _descs([gate, up, down])))
+
+    def set_cancellation(self, flag) -> None:
+        """Registers a one-element int32 numpy array as the request's cancellation flag (None
+        unregisters); the array is kept alive here while registered."""
+        self._cancel = flag
+        self._check(lib().prism_hip_set_cancellation(self._h, _ptr(flag) if flag is not None else None))
+
+    def statistics(self) -> dict:
+        st = Statistics()
+        self._check(lib().prism_hip_get_statistics(self._h, ctypes.byref(st)))
+        return st.as_dict()
+
+    def diagnostics(self) -> dict:
+        d = Diagnostics()
+        self._check(lib().prism_hip_get_diagnostics(self._h, ctypes.byref(d)))
+        return {"dispatched": bool(d.dispatched), "succeeded": bool(d.succeeded)}
+
     def supports_tile_tokens(self) -> bool:
         return bool(lib().prism_hip_supports_tile_tokens(self._h))
 
@@ -514,6 +554,18 @@ class Context:
         out = np.full(hidden, 7.0, np.float32)
         rc = lib().prism_hip_ffn_chain(self._h, g, u, d, _ptr(x), _ptr(res), int(pinned), _ptr(out))
         return self._run(rc, out, check)
+
+    def ffn_chain_lora(self, g: int, u: int, d: int, hidden: int, x, lora_a, residual=None, pinned: bool = False,
+                       check=True):
+        """Returns (out, lora_dot); out is zero-filled and the dot 0 on failure."""
+        x = np.ascontiguousarray(x, np.float32)
+        la = np.ascontiguousarray(lora_a, np.float32) if lora_a is not None else None
+        res = np.ascontiguousarray(residual, np.float32) if residual is not None else None
+        out = np.full(hidden, 7.0, np.float32)
+        dot = np.full(1, 7.0, np.float32)
+        rc = lib().prism_hip_ffn_chain_lora(self._h, g, u, d, _ptr(x), _ptr(res), _ptr(la), int(pinned), _ptr(out),
+                                            _ptr(dot))
+        return self._run(rc, out, check), dot[0]
 
     # -- device-pointer dispatch (torch tensors) --
     def quantize_q8k_device(self, x, cols: int, tokens: int, pinned: bool, out, stream=None):

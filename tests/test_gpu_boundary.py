@@ -209,3 +209,92 @@ def test_gpu_caller_owned_tiled_rejects_bad_sizes(ctx):
         ctx.repack_tiled(ph.KIND_Q8_0, 32768, 64, q8, small)
     assert e.value.code == ph.ERR_UNSUPPORTED
     assert not ctx.faulted
+
+
+# ---- LoRA FFN chain (projection.rs:290-326, 653-697) ---------------------------------
+
+@pytest.mark.parametrize("kind", [ph.KIND_PTQ1, ph.KIND_Q2_K])
+def test_gpu_ffn_chain_lora_matches_chain_and_oracle_dot(ctx, kind):
+    """The chain's output equals prism_hip_ffn_chain's bit for bit, and the LoRA A dot
+    equals the oracle's lora_a_dot of the same SwiGLU vector (prism_hip_ffn_swiglu, the
+    same kernels) bit for bit, in both contracts: a sparse factor (every partial sum exact:
+    the workgroup's tree sum), a dense N(0, 1) factor and one spanning 1e-30..1e20 (the
+    index-ordered fallback when the exactness bound fails)."""
+    import oracle
+
+    hidden, ffn = 2048, 6144
+    wg = synth.weights(kind, ffn, hidden, seed=21)
+    wu = synth.weights(kind, ffn, hidden, seed=22)
+    wd = synth.weights(kind, hidden, ffn, seed=23)
+    g, u, d = (ctx.weight(kind, hidden, ffn, wg), ctx.weight(kind, hidden, ffn, wu), ctx.weight(kind, ffn, hidden, wd))
+    assert ctx.supports_f32_ffn_chain_lora((kind, hidden, ffn), (kind, hidden, ffn), (kind, ffn, hidden))
+    x = synth.activations(hidden, seed=24)
+    r = synth.activations(hidden, seed=25)
+    rng = np.random.default_rng(26)
+    sparse = np.zeros(ffn, np.float32)
+    sparse[rng.choice(ffn, 12, replace=False)] = rng.integers(-64, 65, 12) / 64.0
+    dense = rng.standard_normal(ffn).astype(np.float32)
+    wide = (rng.standard_normal(ffn) * 10.0 ** rng.uniform(-30, 20, ffn)).astype(np.float32)
+    for pinned in (False, True):
+        h = ctx.ffn_swiglu(g, u, ffn, x, pinned=pinned)
+        chain = ctx.ffn_chain(g, u, d, hidden, x, r, pinned=pinned)
+        for name, la in (("sparse", sparse), ("dense", dense), ("wide", wide)):
+            out, dot = ctx.ffn_chain_lora(g, u, d, hidden, x, la, r, pinned=pinned)
+            assert_bits_equal(out, chain, f"{name} pinned={pinned} output")
+            want = oracle.lora_a_dot(la, h, pinned)
+            assert_bits_equal(np.float32(dot), np.float32(want), f"{name} pinned={pinned} dot")
+    # 6144 % 16 == 0: the pinned contract takes the lanes; a planted NaN in the factor is
+    # refused before any launch and clears the output.
+    bad = dense.copy()
+    bad[17] = np.nan
+    (rc, out), dot = ctx.ffn_chain_lora(g, u, d, hidden, x, bad, r, pinned=True, check=False)
+    assert rc == ph.ERR_INVALID_INPUT and not out.any() and dot == 0.0
+    assert not ctx.faulted
+    for i in (g, u, d):
+        ctx.release(i)
+
+
+# ---- statistics (MatvecStatistics / MatvecDiagnostics, src/kernels.rs:1725-1830) ------
+
+def test_gpu_statistics_and_diagnostics():
+    """A fresh context counts per matrix: a successful F32 projection (one preparation,
+    one attempt, one success, one device operation), an unknown weight id (rejected
+    before dispatch), a null input (a preparation failure, no matrix attempt), a
+    three-member group (three attempts, one grouped dispatch, one shared preparation) and
+    a prepared Q8_0 call (no preparation).  The diagnostics follow the last call."""
+    c = ph.Context(0)
+    try:
+        zero = {k: 0 for k in ("preparations", "preparation_failures", "matrix_attempts", "matrix_successes",
+                               "rejected_before_dispatch", "device_operations", "grouped_dispatches")}
+        assert c.statistics() == zero
+        assert c.diagnostics() == {"dispatched": False, "succeeded": False}
+        cols, rows = 2048, 256
+        w = synth.ptq1_weights(rows, cols, seed=5)
+        wid = c.weight(ph.KIND_PTQ1, cols, rows, w)
+        x = synth.activations(cols, seed=6)
+        c.project_f32(wid, rows, x)
+        want = dict(zero, preparations=1, matrix_attempts=1, matrix_successes=1, device_operations=1)
+        assert c.statistics() == want
+        assert c.diagnostics() == {"dispatched": True, "succeeded": True}
+        rc, _ = c.project_f32(wid + 1000, rows, x, check=False)
+        assert rc == ph.ERR_INVALID_INPUT
+        want.update(preparations=2, matrix_attempts=2, rejected_before_dispatch=1)
+        assert c.statistics() == want
+        assert c.diagnostics() == {"dispatched": False, "succeeded": False}
+        rc = ph.lib().prism_hip_project_f32(c._h, wid, None, 1, 0, None)
+        assert rc == ph.ERR_INVALID_INPUT
+        want.update(preparations=3, preparation_failures=1)
+        assert c.statistics() == want
+        ids = [c.weight(ph.KIND_PTQ1, cols, r, synth.ptq1_weights(r, cols, seed=r)) for r in (64, 128, 64)]
+        c.project_f32_group(ids, [64, 128, 64], x)
+        want.update(preparations=4, matrix_attempts=5, matrix_successes=4, device_operations=4, grouped_dispatches=1)
+        assert c.statistics() == want
+        import oracle
+
+        act = oracle.quantize_q8_0(x, ph.Q8_SOURCE)
+        c.project_q8(wid, rows, act)
+        want.update(matrix_attempts=6, matrix_successes=5, device_operations=5)
+        assert c.statistics() == want
+        assert c.diagnostics() == {"dispatched": True, "succeeded": True}
+    finally:
+        c.close()

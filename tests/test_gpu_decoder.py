@@ -1,11 +1,14 @@
 """The resident full-attention decoder (prism_hip_decoder_*) against the oracle's
 decode step, with teacher forcing: the oracle replays the tokens the GPU chose.
 
-Parity bar for the full step (logits after 2..28 layers): max |gpu - oracle| over
-a step's logits <= 1e-3 * max |oracle logit| (source SiLU, softmax exp and RoPE
-cos/sin come from different libms; every projection and quantizer is bit-exact),
+Parity bar for the full step (logits after 2..28 layers), both per step:
+- max |gpu - oracle| over the step's logits <= 1e-3 * max |oracle logit|;
+- every logit within 1e-3 of its own magnitude, with an absolute floor of 1e-5 of
+  the step's largest logit (a logit near zero carries the error of its neighbours);
 and every greedy token equal to the oracle's argmax unless the oracle's two logits
-are within that tolerance of each other.
+are within the first tolerance of each other.  Source SiLU, softmax exp and RoPE
+cos/sin come from different libms (every projection and quantizer is bit-exact), so
+bit identity is reported, not required.
 """
 
 import numpy as np
@@ -17,6 +20,7 @@ import synth
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
+FLOOR = 1e-5  # absolute floor of the per-logit check, relative to the step's largest logit
 THREADS = 16
 
 SMALL = dict(hidden=512, ffn=1024, heads=4, kv_heads=2, vocab=2048, layers=2, max_tokens=96)
@@ -30,20 +34,30 @@ def ctx():
 
 
 def check_against_oracle(model, pos, first, toks, logits):
+    """Teacher-forced steps against the oracle; returns the number of steps whose
+    logits were bit-identical."""
     import oracle
 
     od = oracle.Decoder(model, threads=THREADS)
     tok = first
+    identical = 0
     for i in range(len(toks)):
         ref = od.step(tok, pos + i)
         scale = float(np.abs(ref).max())
-        err = float(np.abs(logits[i] - ref).max())
+        diff = np.abs(logits[i].astype(np.float64) - ref.astype(np.float64))
+        err = float(diff.max())
         assert err <= TOL * scale, f"step {i}: max |gpu - oracle| = {err} > {TOL} * {scale}"
+        bound = TOL * np.abs(ref.astype(np.float64)) + FLOOR * scale
+        worst = int(np.argmax(diff - bound))
+        assert diff[worst] <= bound[worst], (f"step {i}: logit {worst}: |gpu - oracle| = {diff[worst]} > "
+                                             f"{TOL} * |{ref[worst]}| + {FLOOR} * {scale}")
         want = oracle.argmax(ref)
         if int(toks[i]) != want:
             gap = abs(float(ref[want]) - float(ref[int(toks[i])]))
             assert gap <= TOL * scale, f"step {i}: token {toks[i]} vs oracle {want} (gap {gap})"
+        identical += int(np.array_equal(logits[i].view(np.uint32), ref.view(np.uint32)))
         tok = int(toks[i])
+    return identical
 
 
 @pytest.mark.parametrize("seed,prefill", [(1, 40), (2, 0), (3, 1)])
@@ -180,3 +194,39 @@ def test_gpu_decoder_profile_and_family_timing(ctx):
         assert np.array_equal(logits.view(np.uint32), logits3.view(np.uint32))
     finally:
         dec.close()
+
+
+def test_gpu_cancellation_flag():
+    """Cancellation (src/runtime.rs:35-60): with a flag registered and clear, a generate
+    runs at most two steps ahead of the device and gives the bits of an unthrottled one;
+    once the flag is set, projections and generates return PRISM_ERR_CANCELLED with zeroed
+    outputs before launching anything (weight uploads still work), and clearing the flag
+    restores service."""
+    c = ph.Context(0)
+    try:
+        model = synth.decoder_model(5, kv_prefill=20, **SMALL)
+        dec = ph.Decoder(c, model, max_steps=16)
+        try:
+            ref_toks, ref_logits, _ = dec.generate(3, 20, 10, graph=True, logits=True)
+            flag = np.zeros(1, np.int32)
+            c.set_cancellation(flag)
+            toks, logits, _ = dec.generate(3, 20, 10, graph=True, logits=True)
+            assert np.array_equal(toks, ref_toks)
+            assert np.array_equal(logits.view(np.uint32), ref_logits.view(np.uint32))
+            flag[0] = 1
+            cols, rows = 2048, 128
+            wid = c.weight(ph.KIND_PTQ1, cols, rows, synth.ptq1_weights(rows, cols, seed=1))
+            rc, out = c.project_f32(wid, rows, synth.activations(cols, seed=2), check=False)
+            assert rc == ph.ERR_CANCELLED and not out.any()
+            with pytest.raises(ph.PrismError) as e:
+                dec.generate(3, 20, 10, graph=True)
+            assert e.value.code == ph.ERR_CANCELLED
+            flag[0] = 0
+            toks, _, _ = dec.generate(3, 20, 10, graph=True)
+            assert np.array_equal(toks, ref_toks)
+            c.set_cancellation(None)
+            assert not c.faulted
+        finally:
+            dec.close()
+    finally:
+        c.close()

@@ -356,3 +356,53 @@ def test_pinned_swiglu_reassociates_the_numerator(oracle):
     pinned = oracle.swiglu(g, u, True)
     swapped = (u * oracle.silu(g, True)).astype(np.float32)
     assert np.count_nonzero(pinned.view(np.uint32) != swapped.view(np.uint32)) > 100
+
+
+# ---- lora_a_dot (src/kernels.rs:2336-2357) ------------------------------------------------
+
+def test_lora_a_dot_exact_when_every_sum_is_representable(oracle):
+    """Small integers: every product and partial sum is exact in binary32, so both
+    contracts return the exact integer dot whatever their order (n = 48 takes the
+    pinned lanes, n = 50 the ordered binary64 sum in both contracts)."""
+    rng = np.random.default_rng(3)
+    for n in (48, 50):
+        a = rng.integers(-20, 21, n).astype(np.float32)
+        h = rng.integers(-20, 21, n).astype(np.float32)
+        want = float(np.dot(a.astype(np.int64), h.astype(np.int64)))
+        for pinned in (False, True):
+            assert float(oracle.lora_a_dot(a, h, pinned)) == want
+
+
+def test_lora_a_dot_source_sums_in_index_order(oracle):
+    """float_dot sums the products in binary64 in index order: 1e20 + 1 - 1e20 + 1 is 1
+    (the first 1 is absorbed: the binary64 spacing at 1e20 is 16384), where the exact sum
+    is 2 and a pairwise sum (1e20 + 1) + (-1e20 + 1) is 0.  Four values are not a multiple
+    of 16, so the pinned contract takes the same ordered sum."""
+    a = np.array([1e20, 1.0, -1e20, 1.0], np.float32)
+    h = np.ones(4, np.float32)
+    for pinned in (False, True):
+        assert float(oracle.lora_a_dot(a, h, pinned)) == 1.0
+
+
+def test_lora_a_dot_pinned_lane_combination(oracle):
+    """pinned_gdn::dot_scalar: element 4r + l of each 16 feeds register r, lane l; lanes
+    combine as (s0 + s2) + (s1 + s3), then (l0 + l1) + (l2 + l3).  With 1e20 in (r0, l0),
+    -1e20 in (r2, l0), 1 in (r1, l0) and 1 in (r0, l1): lane 0 is (1e20 - 1e20) + (1 + 0)
+    = 1, lane 1 is 1, the result 2.  Combining registers as (s0 + s1) + (s2 + s3) would
+    give lane 0 = 0 and a result of 1; the index-ordered sum gives 0."""
+    a = np.zeros(16, np.float32)
+    a[0], a[8], a[4], a[1] = 1e20, -1e20, 1.0, 1.0
+    h = np.ones(16, np.float32)
+    assert float(oracle.lora_a_dot(a, h, True)) == 2.0
+    assert float(oracle.lora_a_dot(a, h, False)) == 0.0
+
+
+def test_lora_a_dot_rejects_nonfinite_input_and_result(oracle):
+    a = np.ones(32, np.float32)
+    h = np.ones(32, np.float32)
+    h[5] = np.nan
+    with pytest.raises(Exception):
+        oracle.lora_a_dot(a, h, False)
+    big = np.full(32, 3e38, np.float32)
+    with pytest.raises(Exception):
+        oracle.lora_a_dot(big, np.ones(32, np.float32), True)
