@@ -449,20 +449,24 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
 
 # ---- CPU baselines (the oracle on the host's cores) --------------------------------------
 
-def _time(fn, budget_s: float, min_runs: int = 1, warm: bool = True):
-    if warm:
+def _time(fn, budget_s: float = 0.0, min_runs: int = 20, warmups: int = 3):
+    """Median seconds of at least `min_runs` timed runs after `warmups` untimed ones
+    (more runs while the budget lasts), and the number of timed runs."""
+    for _ in range(warmups):
         fn()
-    n, t0 = 0, time.perf_counter()
-    while n < min_runs or time.perf_counter() - t0 < budget_s:
+    times, t0 = [], time.perf_counter()
+    while len(times) < min_runs or time.perf_counter() - t0 < budget_s:
+        t = time.perf_counter()
         fn()
-        n += 1
-    return (time.perf_counter() - t0) / n, n
+        times.append(time.perf_counter() - t)
+    return float(np.median(times)), len(times)
 
 
-def cpu_baselines(model: dict, budget_s: float = 1.5):
+def cpu_baselines(model: dict, budget_s: float = 1.0):
     """The oracle (scalar C restatement of the reference's CPU kernels, rows split evenly
     over threads as CpuThreadPool does, src/backend/threadpool.rs:190-196) on the same
-    workloads, at the box's host-core share and at one thread."""
+    workloads, at the box's host-core share and at one thread: the median of at least 20
+    runs after 3 warmups (the one-thread decode step: of 3 runs after one warmup)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
@@ -470,7 +474,7 @@ def cpu_baselines(model: dict, budget_s: float = 1.5):
     res = {"host": host_info(), "threads": T, "kind": "port", "configs": []}
 
     def add(name, unit, work, fn, budget=budget_s, sample=""):
-        row = {"config": name, "unit": unit, "sample": sample}
+        row = {"config": name, "unit": unit, "sample": sample, "statistic": "median"}
         for threads in (T, 1):
             dt, n = _time(lambda: fn(threads), budget)
             row[f"value_{threads}t" if threads == 1 else "value"] = work / dt
@@ -511,10 +515,10 @@ def cpu_baselines(model: dict, budget_s: float = 1.5):
         od.threads = threads
         oracle.argmax(od.step(1, pos[0]))
 
-    row = {"config": "c3 28-layer decode step", "unit": "tokens/s"}
-    dt, n = _time(lambda: step(T), 8.0, 2)
+    row = {"config": "c3 28-layer decode step", "unit": "tokens/s", "statistic": "median"}
+    dt, n = _time(lambda: step(T))
     row.update(value=1.0 / dt, ms=dt * 1e3, runs=n)
-    dt1, n1 = _time(lambda: step(1), 0.0, 1, warm=False)
+    dt1, n1 = _time(lambda: step(1), min_runs=3, warmups=1)
     row.update(value_1t=1.0 / dt1, ms_1t=dt1 * 1e3, runs_1t=n1)
     res["configs"].append(row)
     log(f"cpu c3: {row['value']:.3f} tokens/s at {T} threads, {row['value_1t']:.4f} at 1")
@@ -616,9 +620,9 @@ def main() -> int:
         cpu = {"value": c3["value"], "unit": "tokens/s", "cores": cb["threads"], "kind": "port",
                "value_1_thread": c3["value_1t"], "nproc": cb["host"]["nproc"],
                "cores_available": cb["host"]["cores_available"], "cpu_model": cb["host"]["cpu_model"],
-               "sample": f"{c3['runs']} decode steps at {cb['threads']} threads and {c3['runs_1t']} at one "
-                         f"thread of the scalar C restatement (every projection through the reference's dot "
-                         f"order), rows split evenly over the threads"}
+               "sample": f"median of {c3['runs']} decode steps at {cb['threads']} threads (after 3 warmups) and "
+                         f"of {c3['runs_1t']} at one thread (after one) of the scalar C restatement (every "
+                         f"projection through the reference's dot order), rows split evenly over the threads"}
     ms = dec["ms_per_token"]
     line = {
         "metric": METRIC,
