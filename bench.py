@@ -544,7 +544,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the path would shard by output rows, see DESIGN.md)", file=sys.stderr)
+              "(the path would shard by output rows with an all-gather of the outputs)", file=sys.stderr)
         return 2
     if hiprt.device_count() < 1:
         print("bench.py: no HIP device", file=sys.stderr)
