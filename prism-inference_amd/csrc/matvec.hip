@@ -190,10 +190,11 @@ __device__ __forceinline__ void unit_terms(__amdgpu_buffer_rsrc_t rs, uint32_t r
         if constexpr (O == Op::PTQ1_SRC) {
             int acc[4] = {0, 0, 0, 0};
             ptq1_dots(x, s.a, [&](int q) -> int & { return acc[q >> 3]; });
-            // dot_q8_groups, src/kernels.rs:1043-1064
+            // dot_q8_groups, src/kernels.rs:1043-1064: fl(tt + fl(scale * I)) is one FMA, since
+            // the binary16 scale (11 significant bits) times |I| < 2^13 is exact in binary32.
             float tt = 0.0f;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) tt = tt + s.sc[g] * static_cast<float>(acc[g] - s.sa[g]);
+            for (int g = 0; g < 4; ++g) tt = __builtin_fmaf(s.sc[g], static_cast<float>(acc[g] - s.sa[g]), tt);
             t[0] = d * tt;
         } else if constexpr (O == Op::PTQ1_Q8K) {
             int acc = 0;

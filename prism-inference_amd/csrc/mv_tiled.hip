@@ -422,7 +422,8 @@ __device__ __forceinline__ void unit_terms(const W &w, const void *__restrict__ 
         if constexpr (O == Op::PTQ1_SRC) {
             int acc[4] = {0, 0, 0, 0};
             trits(w, a, [&](int q) -> int & { return acc[q >> 3]; });
-            // dot_q8_groups, src/kernels.rs:1043-1064
+            // dot_q8_groups, src/kernels.rs:1043-1064: fl(tt + fl(scale * I)) is one FMA, since
+            // the binary16 scale (11 significant bits) times |I| < 2^13 is exact in binary32.
             float tt = 0.0f;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -431,7 +432,7 @@ __device__ __forceinline__ void unit_terms(const W &w, const void *__restrict__ 
 #pragma unroll
                     for (int i = 0; i < 8; ++i) s = bsum4(av[g][i], s);
                 }
-                tt = tt + b[g].scale * static_cast<float>(acc[g] - s);
+                tt = __builtin_fmaf(b[g].scale, static_cast<float>(acc[g] - s), tt);
             }
             t[0] = d * tt;
         } else {
@@ -486,7 +487,8 @@ __device__ __forceinline__ void unit_terms(const W &w, const void *__restrict__ 
         }
     } else if constexpr (O == Op::PQ2_Q8) {
         // dot_q8_groups for an odd-group PQ2 row (src/kernels.rs:1043-1064); the pinned
-        // contract keeps this order for PQ2 (:1109-1121).
+        // contract keeps this order for PQ2 (:1109-1121).  One FMA per group: the binary16
+        // scale times |I| <= 32 * 2 * 127 < 2^13 is exact in binary32.
         const Q8Block *b = static_cast<const Q8Block *>(act) + 4 * u;
         float tt = 0.0f;
 #pragma unroll
@@ -496,7 +498,7 @@ __device__ __forceinline__ void unit_terms(const W &w, const void *__restrict__ 
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 pq2_dword(w.c[2 * g + h], av[4 * h], av[4 * h + 1], av[4 * h + 2], av[4 * h + 3], a0, a1, a2, s);
-            tt = tt + b[g].scale * static_cast<float>(a0 + (a1 >> 2) + (a2 >> 4) - s);
+            tt = __builtin_fmaf(b[g].scale, static_cast<float>(a0 + (a1 >> 2) + (a2 >> 4) - s), tt);
         }
         t[0] = h2f(w.d) * tt;
     } else if constexpr (O == Op::Q2K) {
@@ -1585,10 +1587,11 @@ __device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, co
             acc[3] = mfma32(q[6], q[7], f.b[1].z, f.b[1].w, zero);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                // dot_q8_groups, src/kernels.rs:1043-1064
+                // dot_q8_groups, src/kernels.rs:1043-1064: fl(tt + fl(scale * I)) is one FMA, since
+                // the binary16 scale (11 significant bits) times |I| < 2^13 is exact in binary32.
                 float tt = 0.0f;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) tt = tt + as[g] * static_cast<float>(acc[g][v]);
+                for (int g = 0; g < 4; ++g) tt = __builtin_fmaf(as[g], static_cast<float>(acc[g][v]), tt);
                 tv[v][0] = h2f(f.dd[v] >> 16) * tt;
             }
         } else {
@@ -1627,10 +1630,11 @@ __device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, co
         for (int v = 0; v < 4; ++v) {
             const float d = h2f((f.dd[v >> 1] >> (16 * (v & 1))) & 0xffffu);
             if constexpr (O == Op::PQ2_Q8) {
-                // dot_q8_groups for an odd-group PQ2 row, src/kernels.rs:1043-1064
+                // dot_q8_groups for an odd-group PQ2 row, src/kernels.rs:1043-1064 (one FMA per
+                // group: the scale times |I| < 2^13 is exact in binary32)
                 float tt = 0.0f;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) tt = tt + as[g] * static_cast<float>(acc[g][v]);
+                for (int g = 0; g < 4; ++g) tt = __builtin_fmaf(as[g], static_cast<float>(acc[g][v]), tt);
                 tv[v][0] = d * tt;
             } else {
                 // dot_pq2::<FUSED>, src/kernels.rs:941-955
@@ -2182,13 +2186,14 @@ __device__ __forceinline__ void quad_unit(const Raw<O> &w, const uint32_t *qa, c
 #pragma unroll
                 for (int g = 0; g < 4; ++g) acc[g] = mfma4(A[slot(g, i)], W[slot(g, i)], acc[g]);
             if constexpr (O == Op::PTQ1_SRC) {
-                // dot_q8_groups, src/kernels.rs:1043-1064
+                // dot_q8_groups, src/kernels.rs:1043-1064: fl(tt + fl(scale * I)) is one FMA, since
+                // the binary16 scale (11 significant bits) times |I| < 2^13 is exact in binary32.
                 const float d = h2f(ptq1_scale_bits(w));
 #pragma unroll
                 for (int t = 0; t < static_cast<int>(kQuadTok); ++t) {
                     float tt = 0.0f;
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) tt = tt + S[g][t] * static_cast<float>(acc[g][t]);
+                    for (int g = 0; g < 4; ++g) tt = __builtin_fmaf(S[g][t], static_cast<float>(acc[g][t]), tt);
                     if constexpr (TERMS)
                         ch.o[t] = d * tt;
                     else

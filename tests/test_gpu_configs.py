@@ -95,11 +95,11 @@ def test_gpu_c4_12288x4096_every_row(ctx, kind):
 
 
 @pytest.mark.parametrize("M", [128, 512, 2048])
-def test_gpu_c2_prefill_both_contracts_sampled_tokens(ctx, M):
+def test_gpu_c2_prefill_both_contracts_every_token(ctx, M):
     """The prefill workload (PTQ1 6144x2048, M tokens) in both contracts: the source
     contract on the f16-MFMA GEMM, the pinned one (the contract the reference's graph
-    hands the executor) on the int8-MFMA skinny kernel, 16 tokens per launch, each
-    unit decoded once per launch.  Sampled tokens, every row, against the oracle."""
+    hands the executor) on its own GEMM.  Every token and every row against the oracle's
+    per-token matvec (about 1.3 ms of host work per token at 16 threads)."""
     import oracle
 
     rows, cols = 6144, 2048
@@ -108,9 +108,8 @@ def test_gpu_c2_prefill_both_contracts_sampled_tokens(ctx, M):
     wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
     for pinned in (False, True):
         Y = ctx.prefill(wid, rows, X, pinned=pinned)
-        for t in sorted({0, 1, 15, 16, 17, M // 2, M - 1}):
-            ref = oracle.matvec(ph.KIND_PTQ1, cols, rows, w, X[t], pinned, threads=THREADS)
-            assert_bits_equal(Y[t], ref, f"M={M} token {t} pinned={pinned}")
+        ref = oracle.prefill(ph.KIND_PTQ1, cols, rows, w, X, pinned, threads=THREADS)
+        assert_bits_equal(Y, ref, f"M={M} pinned={pinned}")
     ctx.release(wid)
 
 
