@@ -596,14 +596,16 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
 
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 16), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
                                          (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
-                                         (96, 256, 4096), (130, 1152, 1100), (6144, 2048, 1024)])
+                                         (96, 256, 4096), (130, 1152, 1100), (6144, 2048, 1024),
+                                         (6044, 2048, 2048)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     """PTQ1 prefill runs as one f16-MFMA GEMM from 16 tokens on, in both contracts; every
     token row must equal the reference's per-token matvec bit for bit (partial row
     tiles, idle wavefronts of a partial 128-row block, an odd block count, 32, 64 and
     128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
     token groups are a multiple of eight: M = 200, 512, 4096; nine blocks per row at 1152
-    columns, the benchmark's matrix at 1024 tokens).  The pinned contract's
+    columns, the benchmark's matrix at 1024 tokens, a partial last tile at 6044 rows and
+    2048 tokens).  The pinned contract's
     kernel takes each native lane's integer sum from its own masked MFMA and runs the
     four FMA lanes of dot_q8_groups_pinned."""
     import oracle
