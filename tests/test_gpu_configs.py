@@ -127,22 +127,20 @@ def lm_head_weights():
 
 
 @pytest.mark.parametrize("kind", FORMATS)
-def test_gpu_c4_151936x4096_sampled_rows(ctx, lm_head_weights, kind):
-    """The LM-head shape: every 997th row and the last, batch 1, 4 and 16, both
-    contracts, equal to the oracle's matvec of those rows."""
+def test_gpu_c4_151936x4096_every_row(ctx, lm_head_weights, kind):
+    """The LM-head shape: every row, batch 1, 4 and 16, both contracts, equal to the
+    oracle's matvec (20 to 60 ms of host work per token at 16 threads)."""
     import oracle
 
     rows, cols = 151936, 4096
     w = lm_head_weights(kind)
-    sample = np.r_[np.arange(0, rows, 997), rows - 1]
-    wsub = np.ascontiguousarray(w.reshape(rows, -1)[sample]).ravel()
     wid = ctx.weight(kind, cols, rows, w)
     for tokens in (1, 4, 16):
         X = synth.activations(cols, seed=kind + 7 * tokens, tokens=tokens)
         for pinned in (False, True):
-            ref = oracle.prefill(kind, cols, len(sample), wsub, X.reshape(tokens, cols), pinned, threads=THREADS)
+            ref = oracle.prefill(kind, cols, rows, w, X.reshape(tokens, cols), pinned, threads=THREADS)
             got = ctx.project_f32(wid, rows, X, tokens=tokens, pinned=pinned).reshape(tokens, rows)
-            assert_bits_equal(got[:, sample], ref, f"B={tokens} pinned={pinned}")
+            assert_bits_equal(got, ref, f"B={tokens} pinned={pinned}")
     ctx.release(wid)
 
 
