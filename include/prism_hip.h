@@ -247,14 +247,22 @@ int prism_hip_project_f32_triple_tokens(prism_hip_ctx *ctx, const prism_weight_i
 /* project_f32_ffn_swiglu (projection.rs:206-222): out[ffn] = SwiGLU(gate(x), up(x)). */
 int prism_hip_ffn_swiglu(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
                          float *out);
-/* project_f32_ffn_chain (projection.rs:250-287) without the Hadamard transform:
- * out[hidden] = down(SwiGLU(gate(x), up(x))) (+ residual if non-NULL).  Gate, up
- * and down share one packed kind (PQ2, PTQ1, Q2_K, Q8_0, TQ1_0 or TQ2_0). */
+/* project_f32_ffn_chain (src/kernels/projection.rs:271-290):
+ * out[hidden] = down(H(SwiGLU(gate(x), up(x)))) (+ residual if non-NULL).  Gate, up
+ * and down share one packed kind (PQ2, PTQ1, Q2_K, Q8_0, TQ1_0 or TQ2_0).
+ * hadamard_block is the call's hadamard_block_size: 0 (None) or 1 leaves H the identity;
+ * otherwise H is the normalized Sylvester-Walsh-Hadamard transform of every
+ * hadamard_block consecutive SwiGLU values (src/kernels.rs:3952-3987: butterflies with
+ * half = 1, 2, 4, ..., (l, r) -> (l + r, l - r) in binary32, then each value times
+ * 1/sqrt(block)), the rotation the decoder applies ahead of a rotated down projection
+ * (src/graph.rs:1810-1831 picks the block, signs all +1).  A block that is not a power of
+ * two up to 8192 dividing the FFN width is PRISM_ERR_INVALID_INPUT. */
 int prism_hip_ffn_chain(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                        const float *x, const float *residual, int pinned, float *out);
-/* project_f32_ffn_chain_lora (projection.rs:298-326, called from
- * matvec_ffn_chain_lora_with_executor :653-697) without the Hadamard transform: the chain
- * of prism_hip_ffn_chain, plus *lora_dot = lora_a . SwiGLU(gate(x), up(x)) with lora_a[ffn]
+                        const float *x, const float *residual, uint32_t hadamard_block, int pinned, float *out);
+/* project_f32_ffn_chain_lora (src/kernels/projection.rs:303-323, called from
+ * matvec_ffn_chain_lora_with_executor :653-697): the chain of prism_hip_ffn_chain
+ * (hadamard_block as there), plus *lora_dot = lora_a . SwiGLU(gate(x), up(x)) -- the
+ * unrotated SwiGLU vector, as src/graph/prefill_ffn_tests.rs:554-590 orders it -- with lora_a[ffn]
  * (ffn = down's columns), in lora_a_dot's arithmetic (src/kernels.rs:2336-2357): pinned with
  * ffn % 16 == 0, sixteen binary32 FMA lanes combined as pinned_gdn::dot_scalar
  * (src/kernels/pinned_gdn.rs:205-230); otherwise the binary32 products summed in binary64
@@ -262,17 +270,18 @@ int prism_hip_ffn_chain(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_i
  * before any launch (PRISM_ERR_INVALID_INPUT); a non-finite dot or output fails the call.
  * On any error out is zero-filled and *lora_dot is 0. */
 int prism_hip_ffn_chain_lora(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                             const float *x, const float *residual, const float *lora_a, int pinned, float *out,
-                             float *lora_dot);
+                             const float *x, const float *residual, uint32_t hadamard_block, const float *lora_a,
+                             int pinned, float *out, float *lora_dot);
 /* project_f32_ffn_swiglu_tokens (projection.rs:239-259) and project_f32_ffn_chain_tokens
- * (projection.rs:328-355) without the Hadamard transform: x [tokens][hidden], residual
+ * (projection.rs:328-355, hadamard_block as for prism_hip_ffn_chain): x [tokens][hidden], residual
  * (or NULL) and out [tokens][hidden] (SwiGLU: out [tokens][ffn]).  Gate and up run as
  * one sibling group over all tokens, so each weight is read once per batch of tokens;
  * every row equals that token's single-token chain. */
 int prism_hip_ffn_swiglu_tokens(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, const float *x,
                                 uint32_t tokens, int pinned, float *out);
 int prism_hip_ffn_chain_tokens(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                               const float *x, const float *residual, uint32_t tokens, int pinned, float *out);
+                               const float *x, const float *residual, uint32_t tokens, uint32_t hadamard_block,
+                               int pinned, float *out);
 /* Tiled prefill (src/kernels/prefill.rs:200-725): X[tokens][cols] -> out[tokens][rows];
  * every token row is bit-identical to its own project_f32. */
 int prism_hip_prefill(prism_hip_ctx *ctx, prism_weight_id w, const float *x, uint32_t tokens, int pinned,
@@ -296,11 +305,12 @@ int prism_hip_quantize_q8_device(prism_hip_ctx *ctx, const float *x, uint64_t co
  * PRISM_PATH_F32 floats quantized on the fly) into device out[tokens][rows]. */
 int prism_hip_project_device(prism_hip_ctx *ctx, prism_weight_id w, int path, const void *act, uint32_t tokens,
                              int pinned, float *out, void *stream);
-/* FFN chain on device pointers (h may be NULL; when set it receives the SwiGLU vector).
- * down == 0 is project_f32_ffn_swiglu: out receives the SwiGLU vector (ffn floats). */
+/* FFN chain on device pointers (h may be NULL; when set it receives the unrotated SwiGLU
+ * vector; hadamard_block as for prism_hip_ffn_chain).  down == 0 is project_f32_ffn_swiglu:
+ * out receives the SwiGLU vector (ffn floats) and hadamard_block is ignored. */
 int prism_hip_ffn_chain_device(prism_hip_ctx *ctx, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                               const float *x, const float *residual, int pinned, float *out, float *h,
-                               void *stream);
+                               const float *x, const float *residual, uint32_t hadamard_block, int pinned,
+                               float *out, float *h, void *stream);
 /* prism_hip_project_device without any device allocation: every scratch buffer the
  * call's kernels use (the quantized activation, the skinny batch's lane-ordered copy,
  * the prefill token codes) is carved from one fixed, file-scope device array of

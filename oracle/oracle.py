@@ -97,6 +97,8 @@ def lib():
             "po_swiglu": (None, [P, P, S, I]),
             "po_lora_a_dot": (I, [P, P, S, I, P]),
             "po_ffn": (I, [U, S, S, P, P, P, P, P, I, P, P, I]),
+            "po_hadamard": (I, [P, S, U]),
+            "po_ffn_rotated": (I, [U, S, S, P, P, P, P, P, U, I, P, P, I]),
             "po_rms_norm": (I, [P, P, S, ctypes.c_float, P]),
             "po_rope_frequencies": (None, [S, P, P, ctypes.c_float, P, P]),
             "po_norm_rope_f16": (I, [P, P, S, S, P, P, ctypes.c_float]),
@@ -309,14 +311,24 @@ def lora_a_dot(a, h, pinned: bool) -> np.float32:
     return out[0]
 
 
-def ffn(kind: int, hidden: int, ffn_dim: int, wg, wu, wd, x, residual=None, pinned: bool = False, threads: int = 1):
+def hadamard(values, block: int) -> np.ndarray:
+    """Blockwise normalized Walsh-Hadamard rotation (src/kernels.rs:3952-3987)."""
+    v = _f32(values).copy()
+    _check(lib().po_hadamard(_p(v), v.size, block), "hadamard")
+    return v
+
+
+def ffn(kind: int, hidden: int, ffn_dim: int, wg, wu, wd, x, residual=None, pinned: bool = False, threads: int = 1,
+        hadamard_block: int = 0):
+    """The FFN chain; returns (out, the unrotated SwiGLU vector)."""
     wg, wu, wd = _u8(wg), _u8(wu), _u8(wd)
     x = _f32(x)
     out = np.zeros(hidden, np.float32)
     h = np.zeros(ffn_dim, np.float32)
     res = _f32(residual) if residual is not None else None
-    rc = lib().po_ffn(kind, hidden, ffn_dim, _p(wg), _p(wu), _p(wd), _p(x), _p(res) if res is not None else None,
-                      int(pinned), _p(out), _p(h), threads)
+    rc = lib().po_ffn_rotated(kind, hidden, ffn_dim, _p(wg), _p(wu), _p(wd), _p(x),
+                              _p(res) if res is not None else None, hadamard_block, int(pinned), _p(out), _p(h),
+                              threads)
     _check(rc, "ffn")
     return out, h
 

@@ -953,9 +953,38 @@ int po_lora_a_dot(const float *a, const float *input, size_t n, int pinned, floa
 
 /* gate/up projections sharing one preparation, SwiGLU into up, then down
  * (src/graph.rs:3935-3956); optional residual add as the executor chain does. */
-int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const uint8_t *wu,
-           const uint8_t *wd, const float *x, const float *residual, int pinned, float *out,
-           float *h_out, int threads) {
+/* hadamard (src/kernels.rs:3952-3987) over every `block` consecutive values: finite input,
+ * butterflies with half = 1, 2, 4, ... turning (l, r) into (l + r, l - r) in binary32,
+ * then each value times the binary32 1 / sqrt(block); a non-finite result fails. */
+int po_hadamard(float *v, size_t n, uint32_t block) {
+    if (block == 0 || (block & (block - 1)) || n % block) return PO_ERR_INVALID_INPUT;
+    const float norm = 1.0f / sqrtf((float)block);
+    for (size_t b = 0; b < n; b += block) {
+        float *x = v + b;
+        for (uint32_t i = 0; i < block; i++)
+            if (!is_finite(x[i])) return PO_ERR_NONFINITE;
+        for (uint32_t half = 1; half < block; half *= 2)
+            for (uint32_t base = 0; base < block; base += 2 * half)
+                for (uint32_t i = base; i < base + half; i++) {
+                    const float l = x[i], r = x[i + half];
+                    x[i] = l + r;
+                    x[i + half] = l - r;
+                }
+        for (uint32_t i = 0; i < block; i++) {
+            x[i] = x[i] * norm;
+            if (!is_finite(x[i])) return PO_ERR_NONFINITE;
+        }
+    }
+    return PO_OK;
+}
+
+/* The chain with hadamard_block_size (src/kernels/projection.rs:271-290): gate and up
+ * matvecs, SwiGLU, then (block > 1) the blockwise Hadamard rotation of the SwiGLU vector
+ * ahead of the down matvec (src/graph/prefill_ffn_tests.rs:517-547 rotates `mid` before
+ * cpu_matvec(down, ...)); h_out receives the unrotated SwiGLU vector. */
+int po_ffn_rotated(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const uint8_t *wu,
+                   const uint8_t *wd, const float *x, const float *residual, uint32_t hadamard_block,
+                   int pinned, float *out, float *h_out, int threads) {
     float *g = (float *)malloc(sizeof(float) * ffn);
     float *u = (float *)malloc(sizeof(float) * ffn);
     int rc = (g && u) ? PO_OK : PO_ERR_RESOURCE;
@@ -967,6 +996,7 @@ int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const ui
             if (!is_finite(u[i])) rc = PO_ERR_NONFINITE;
     }
     if (!rc && h_out) memcpy(h_out, u, sizeof(float) * ffn);
+    if (!rc && hadamard_block > 1) rc = po_hadamard(u, ffn, hadamard_block);
     if (!rc) rc = po_matvec(kind, ffn, hidden, wd, u, pinned, out, threads);
     if (!rc && residual)
         for (size_t i = 0; i < hidden; i++) {
@@ -977,4 +1007,10 @@ int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const ui
     free(g);
     free(u);
     return rc;
+}
+
+int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const uint8_t *wu,
+           const uint8_t *wd, const float *x, const float *residual, int pinned, float *out,
+           float *h_out, int threads) {
+    return po_ffn_rotated(kind, hidden, ffn, wg, wu, wd, x, residual, 0, pinned, out, h_out, threads);
 }

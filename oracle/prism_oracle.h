@@ -125,6 +125,13 @@ int po_ffn(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const ui
            const uint8_t *wd, const float *x, const float *residual, int pinned, float *out,
            float *h_out, int threads);
 
+/* ---- blockwise normalized Walsh-Hadamard rotation (src/kernels.rs:3952-3987) and the chain
+ * that rotates the SwiGLU vector ahead of down (src/kernels/projection.rs:271-290) ---- */
+int po_hadamard(float *v, size_t n, uint32_t block);
+int po_ffn_rotated(uint32_t kind, size_t hidden, size_t ffn, const uint8_t *wg, const uint8_t *wu,
+                   const uint8_t *wd, const float *x, const float *residual, uint32_t hadamard_block,
+                   int pinned, float *out, float *h_out, int threads);
+
 /* ---- full-attention decode step, source order (decoder_oracle.c) ---- */
 typedef struct {
     size_t hidden, ffn, heads, kv_heads, head_dim, rope, vocab, layers, max_tokens;

@@ -1,5 +1,6 @@
-// ffn.hip -- FFN epilogue kernels: SwiGLU between gate/up and down, residual add, and the
-// LoRA A dot beside the chain.
+// ffn.hip -- FFN epilogue kernels: SwiGLU between gate/up and down, the blockwise Hadamard
+// rotation ahead of a rotated down projection, residual add, and the LoRA A dot beside the
+// chain.
 //
 // Source order  (src/graph.rs:121-131, src/kernels.rs:3365-3368):
 //     up = up * (g / (1 + exp(-g)))
@@ -10,6 +11,8 @@
 // src/kernels/pinned_activations.rs:26-62); it is evaluated here with the same
 // explicit fused multiply-adds, so the pinned epilogue is bit-exact.  exp() is the
 // device libm and matches the host's only to within its error bound.
+#include <cmath>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -104,6 +107,41 @@ __global__ __launch_bounds__(256) void k_lora_dot(const float *__restrict__ a, c
     if (!finite(r)) raise_error(err, kErrNonfinite);
 }
 
+// hadamard (src/kernels.rs:3952-3987) of every `block`-sized block of the SwiGLU rows,
+// out of place: the butterfly stages half = 1, 2, 4, ... each replace (l, r) by (l + r,
+// l - r) in binary32, then every value is multiplied by norm = 1 / sqrt(block) (binary32,
+// computed by the caller as the reference does).  Each value of a stage depends only on the
+// two values of the previous stage it pairs, so the result is the reference's bit for bit
+// whatever thread computes it.  One workgroup per block (grid = blocks of all tokens), the
+// block in LDS; non-finite inputs or outputs raise the error flag.
+__global__ __launch_bounds__(1024) void k_hadamard(const float *__restrict__ in, float *__restrict__ out,
+                                                   uint32_t block, float norm, int *__restrict__ err) {
+    extern __shared__ float hv[];
+    const size_t base = static_cast<size_t>(blockIdx.x) * block;
+    bool bad = false;
+    for (uint32_t i = threadIdx.x; i < block; i += blockDim.x) {
+        const float v = in[base + i];
+        bad |= !finite(v);
+        hv[i] = v;
+    }
+    __syncthreads();
+    for (uint32_t half = 1; half < block; half *= 2) {
+        for (uint32_t p = threadIdx.x; p < block / 2; p += blockDim.x) {
+            const uint32_t i = (p / half) * 2 * half + p % half;
+            const float l = hv[i], r = hv[i + half];
+            hv[i] = l + r;
+            hv[i + half] = l - r;
+        }
+        __syncthreads();
+    }
+    for (uint32_t i = threadIdx.x; i < block; i += blockDim.x) {
+        const float v = hv[i] * norm;
+        bad |= !finite(v);
+        out[base + i] = v;
+    }
+    if (bad) raise_error(err, kErrNonfinite);
+}
+
 __global__ void k_fill_i32(int *p, int v, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -128,6 +166,19 @@ int launch_add_residual(float *out, const float *residual, uint64_t n, int *err,
 int launch_lora_dot(const float *a, const float *h, uint32_t n, int pinned, float *out, int *err, hipStream_t s) {
     if (n == 0) return kLaunchUnsupported;
     hipLaunchKernelGGL(k_lora_dot, dim3(1), dim3(256), 0, s, a, h, n, pinned, out, err);
+    return launch_status();
+}
+
+int launch_hadamard(const float *in, float *out, uint64_t n, uint32_t tokens, uint32_t block, int *err,
+                    hipStream_t s) {
+    if (block < 2 || (block & (block - 1)) || block > kHadamardMaxBlock || n % block) return kLaunchUnsupported;
+    const uint64_t blocks = n / block * tokens;
+    if (blocks == 0 || blocks > 0x7fffffffull) return kLaunchUnsupported;
+    // The reference's normalization: 1 / sqrt(float(block)), each step rounded to binary32.
+    const float norm = 1.0f / std::sqrt(static_cast<float>(block));
+    const uint32_t threads = block / 2 < 1024 ? block / 2 : 1024;
+    hipLaunchKernelGGL(k_hadamard, dim3(static_cast<uint32_t>(blocks)), dim3(threads), sizeof(float) * block, s, in,
+                       out, block, norm, err);
     return launch_status();
 }
 

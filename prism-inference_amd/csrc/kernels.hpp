@@ -89,6 +89,11 @@ int launch_swiglu(const float *gate, const float *up, float *h, uint64_t n, uint
                   hipStream_t s);
 // out += residual, flagging non-finite sums.
 int launch_add_residual(float *out, const float *residual, uint64_t n, int *err, hipStream_t s);
+// Largest Hadamard block of the FFN chains (the block sits in one workgroup's LDS).
+constexpr uint32_t kHadamardMaxBlock = 8192;
+// The normalized blockwise Hadamard rotation of tokens rows of n values, in -> out.
+int launch_hadamard(const float *in, float *out, uint64_t n, uint32_t tokens, uint32_t block, int *err,
+                    hipStream_t s);
 // lora_a_dot of a[0..n) with the SwiGLU vector h into *out (one workgroup).
 int launch_lora_dot(const float *a, const float *h, uint32_t n, int pinned, float *out, int *err, hipStream_t s);
 // p[0..n) = v with a kernel (safe inside captured graphs, unlike a memset node).

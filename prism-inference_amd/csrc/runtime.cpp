@@ -129,13 +129,39 @@ int finish(prism_hip_ctx *c, float *host_out, const float *dev_out, size_t n) {
     return drain(c, c->stream);
 }
 
+// The Hadamard block of a rotated down projection (project_f32_ffn_chain's
+// hadamard_block_size, src/kernels/projection.rs:277-301): 0 or 1 = none; otherwise a power
+// of two from 2 to kHadamardMaxBlock dividing the SwiGLU width, as the GPU precedent accepts
+// (tools/adreno-vulkan/src/executor.rs:2493-2507, there up to 1024).
+bool hadamard_ok(uint32_t hb, uint64_t ffn) {
+    return hb <= 1 || ((hb & (hb - 1)) == 0 && hb <= kHadamardMaxBlock && ffn % hb == 0);
+}
+
+// The down projection's input: the SwiGLU rows hv, or (hb > 1) their blockwise Hadamard
+// rotation in c->hr (the reference rotates the SwiGLU vector ahead of the quantizer,
+// src/graph.rs:4168-4276 with src/kernels.rs:3952-4021); hv itself stays unrotated.
+int down_input(prism_hip_ctx *c, const float *hv, uint64_t ffn, uint32_t tokens, uint32_t hb, hipStream_t s,
+               const float **in) {
+    *in = hv;
+    if (hb <= 1) return PRISM_OK;
+    int rc = ensure(c, c->hr, sizeof(float) * ffn * tokens);
+    if (rc) return rc;
+    float *hr = static_cast<float *>(c->hr.p);
+    rc = launch_result(c, launch_hadamard(hv, hr, ffn, tokens, hb, c->err, s), "hadamard launch");
+    if (!rc) *in = hr;
+    return rc;
+}
+
 int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Weight *d, const float *x,
-                   const float *residual, int pinned, float *out, float *h, hipStream_t s) {
+                   const float *residual, int pinned, float *out, float *h, hipStream_t s, uint32_t hb = 0) {
     // Shapes: gate/up [ffn][hidden], down [hidden][ffn] (projection.rs:571-597).
     if (g.cols != u.cols || g.rows != u.rows || g.kind != u.kind)
         return fail(c, PRISM_ERR_INVALID_INPUT, "gate/up geometry differs");
     if (d && (d->cols != g.rows || d->rows != g.cols))
         return fail(c, PRISM_ERR_INVALID_INPUT, "down geometry does not match gate/up");
+    if (!hadamard_ok(hb, g.rows))
+        return fail(c, PRISM_ERR_INVALID_INPUT, "Hadamard block must be a power of two up to 8192 dividing the FFN width");
+    if (!d) hb = 0;
     float *hv = h;
     int rc = PRISM_OK;
     if (!hv) {
@@ -149,9 +175,10 @@ int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Wei
         MatvecArgs a = f32_args(c, g, x, 1, pinned, hv, nullptr, s);
         a.w2 = static_cast<const uint8_t *>(u.dev);
         // A tiled down matrix on Q8_0 activations takes the SwiGLU vector as blocks the
-        // gate/up epilogue quantizes (its contract, per 32 rows), not as floats.
+        // gate/up epilogue quantizes (its contract, per 32 rows), not as floats -- unless
+        // the vector is rotated first.
         const int dc = d ? contract_for(d->kind, d->cols, pinned) : 0;
-        if (d && d->tiled && dc != 0 && g.rows % 32 == 0) {
+        if (d && d->tiled && dc != 0 && g.rows % 32 == 0 && hb <= 1) {
             rc = ensure(c, c->act2, act_bytes(dc, d->cols, 1));
             if (rc) return rc;
             a.q8_out = c->act2.p;
@@ -188,7 +215,10 @@ int ffn_chain_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Wei
         if (rc) return rc;
     }
     if (!d) return PRISM_OK;
-    return project_f32_dev(c, *d, hv, 1, pinned, out, c->act2, s, residual);
+    const float *din = nullptr;
+    rc = down_input(c, hv, g.rows, 1, hb, s, &din);
+    if (rc) return rc;
+    return project_f32_dev(c, *d, din, 1, pinned, out, c->act2, s, residual);
 }
 
 // Sibling projections of `tokens` token rows of one f32 input (device pointers):
@@ -230,11 +260,14 @@ int group_tokens_impl(prism_hip_ctx *c, const Weight *const *w, uint32_t n, cons
 // over all tokens.  Every token row is its own single-token chain's result.  h, if not
 // NULL, receives the SwiGLU rows; without a down projection `out` is that vector.
 int ffn_tokens_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const Weight *d, const float *x,
-                    const float *residual, uint32_t tokens, int pinned, float *out, float *h, hipStream_t s) {
+                    const float *residual, uint32_t tokens, int pinned, float *out, float *h, hipStream_t s,
+                    uint32_t hb = 0) {
     const prism_tensor_desc dd = d ? desc_of(*d) : prism_tensor_desc{};
     if (!ffn_eligible(desc_of(g), desc_of(u), d ? &dd : nullptr))
         return fail(c, PRISM_ERR_UNSUPPORTED, "FFN chain needs gate/up [ffn][hidden] and down [hidden][ffn] of one packed kind");
-    if (tokens == 1) return ffn_chain_impl(c, g, u, d, x, residual, pinned, d ? out : nullptr, d ? h : out, s);
+    if (!hadamard_ok(hb, g.rows))
+        return fail(c, PRISM_ERR_INVALID_INPUT, "Hadamard block must be a power of two up to 8192 dividing the FFN width");
+    if (tokens == 1) return ffn_chain_impl(c, g, u, d, x, residual, pinned, d ? out : nullptr, d ? h : out, s, hb);
     const size_t nh = sizeof(float) * g.rows * tokens;
     int rc = ensure(c, c->gate, nh);
     if (!rc) rc = ensure(c, c->up, nh);
@@ -251,7 +284,10 @@ int ffn_tokens_impl(prism_hip_ctx *c, const Weight &g, const Weight &u, const We
         rc = launch_result(c, launch_swiglu(gu_out[0], gu_out[1], hv, g.rows, tokens, pinned, c->err, s),
                            "swiglu launch");
     if (rc || !d) return rc;
-    return project_f32_dev(c, *d, hv, tokens, pinned, out, c->act2, s, residual);
+    const float *din = nullptr;
+    rc = down_input(c, hv, g.rows, tokens, hb, s, &din);
+    if (rc) return rc;
+    return project_f32_dev(c, *d, din, tokens, pinned, out, c->act2, s, residual);
 }
 
 }  // namespace
@@ -291,7 +327,7 @@ void prism_hip_destroy(prism_hip_ctx *c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     prism_hip_weight_release_all(c);
-    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->res, &c->pre, &c->sk, &c->lora})
+    for (DevBuf *b : {&c->x, &c->act, &c->act2, &c->out, &c->gate, &c->up, &c->h, &c->hr, &c->res, &c->pre, &c->sk, &c->lora})
         if (b->p) (void)hipFree(b->p);
     if (c->err) (void)hipFree(c->err);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -720,7 +756,8 @@ int prism_hip_project_f32_triple_tokens(prism_hip_ctx *c, const prism_weight_id 
 }
 
 static int ffn_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
-                       const float *x, const float *residual, uint32_t tokens, int pinned, float *out, Tally &t) {
+                       const float *x, const float *residual, uint32_t tokens, int pinned, uint32_t hb, float *out,
+                       Tally &t) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
     // Output length: down's rows, or gate's for the SwiGLU vector; known when those ids are.
@@ -759,16 +796,16 @@ static int ffn_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id ui
     if (!rc)
         rc = ffn_tokens_impl(c, *g, *u, d, static_cast<float *>(c->x.p),
                              residual ? static_cast<float *>(c->res.p) : nullptr, tokens, pinned,
-                             static_cast<float *>(c->out.p), nullptr, c->stream);
+                             static_cast<float *>(c->out.p), nullptr, c->stream, hb);
     if (!rc) rc = finish(c, out, static_cast<float *>(c->out.p), nout);
     if (rc) zero(out, nout);
     return rc;
 }
 
 static int ffn_host(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did, const float *x,
-                    const float *residual, uint32_t tokens, int pinned, float *out) {
+                    const float *residual, uint32_t tokens, int pinned, float *out, uint32_t hb = 0) {
     Tally t(c, did ? 3 : 2, true);
-    return t(ffn_checked(c, gid, uid, did, x, residual, tokens, pinned, out, t));
+    return t(ffn_checked(c, gid, uid, did, x, residual, tokens, pinned, hb, out, t));
 }
 
 int prism_hip_ffn_swiglu(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, const float *x, int pinned,
@@ -782,22 +819,23 @@ int prism_hip_ffn_swiglu_tokens(prism_hip_ctx *c, prism_weight_id gate, prism_we
 }
 
 int prism_hip_ffn_chain(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                        const float *x, const float *residual, int pinned, float *out) {
+                        const float *x, const float *residual, uint32_t hadamard_block, int pinned, float *out) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (down == 0) return Tally(c, 3, true)(fail(c, PRISM_ERR_INVALID_INPUT, "down projection required"));
-    return ffn_host(c, gate, up, down, x, residual, 1, pinned, out);
+    return ffn_host(c, gate, up, down, x, residual, 1, pinned, out, hadamard_block);
 }
 
 int prism_hip_ffn_chain_tokens(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                               const float *x, const float *residual, uint32_t tokens, int pinned, float *out) {
+                               const float *x, const float *residual, uint32_t tokens, uint32_t hadamard_block,
+                               int pinned, float *out) {
     if (!c) return PRISM_ERR_INVALID_INPUT;
     if (down == 0) return Tally(c, 3, true)(fail(c, PRISM_ERR_INVALID_INPUT, "down projection required"));
-    return ffn_host(c, gate, up, down, x, residual, tokens, pinned, out);
+    return ffn_host(c, gate, up, down, x, residual, tokens, pinned, out, hadamard_block);
 }
 
 static int ffn_lora_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
-                            const float *x, const float *residual, const float *lora_a, int pinned, float *out,
-                            float *lora_dot, Tally &t) {
+                            const float *x, const float *residual, uint32_t hb, const float *lora_a, int pinned,
+                            float *out, float *lora_dot, Tally &t) {
     if (lora_dot) *lora_dot = 0.0f;
     if (!c) return PRISM_ERR_INVALID_INPUT;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = find(c, did);
@@ -848,7 +886,7 @@ static int ffn_lora_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_
     if (!rc)
         rc = ffn_chain_impl(c, *g, *u, d, static_cast<const float *>(c->x.p),
                             residual ? static_cast<const float *>(c->res.p) : nullptr, pinned,
-                            static_cast<float *>(c->out.p), hv, c->stream);
+                            static_cast<float *>(c->out.p), hv, c->stream, hb);
     if (!rc)
         rc = launch_result(c, launch_lora_dot(static_cast<const float *>(c->lora.p), hv, static_cast<uint32_t>(nl),
                                               pinned, dot, c->err, c->stream),
@@ -867,10 +905,10 @@ static int ffn_lora_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_
 }
 
 int prism_hip_ffn_chain_lora(prism_hip_ctx *c, prism_weight_id gate, prism_weight_id up, prism_weight_id down,
-                             const float *x, const float *residual, const float *lora_a, int pinned, float *out,
-                             float *lora_dot) {
+                             const float *x, const float *residual, uint32_t hadamard_block, const float *lora_a,
+                             int pinned, float *out, float *lora_dot) {
     Tally t(c, 3, true);
-    return t(ffn_lora_checked(c, gate, up, down, x, residual, lora_a, pinned, out, lora_dot, t));
+    return t(ffn_lora_checked(c, gate, up, down, x, residual, hadamard_block, lora_a, pinned, out, lora_dot, t));
 }
 
 int prism_hip_quantize_q8k_device(prism_hip_ctx *c, const float *x, uint64_t cols, uint32_t tokens, int pinned,
@@ -953,8 +991,8 @@ int prism_hip_project_device_noalloc(prism_hip_ctx *c, prism_weight_id wid, int 
 }
 
 static int ffn_device_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
-                              const float *x, const float *residual, int pinned, float *out, float *h, void *stream,
-                              Tally &t) {
+                              const float *x, const float *residual, uint32_t hb, int pinned, float *out, float *h,
+                              void *stream, Tally &t) {
     int rc = check_ready(c);
     if (rc) return rc;
     const Weight *g = find(c, gid), *u = find(c, uid), *d = did ? find(c, did) : nullptr;
@@ -970,14 +1008,14 @@ static int ffn_device_checked(prism_hip_ctx *c, prism_weight_id gid, prism_weigh
     t.dispatch();
     // Without a down projection the call is project_f32_ffn_swiglu: out receives h.
     if (!d) return ffn_chain_impl(c, *g, *u, nullptr, x, nullptr, pinned, nullptr, out, s);
-    return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, s);
+    return ffn_chain_impl(c, *g, *u, d, x, residual, pinned, out, h, s, hb);
 }
 
 int prism_hip_ffn_chain_device(prism_hip_ctx *c, prism_weight_id gid, prism_weight_id uid, prism_weight_id did,
-                               const float *x, const float *residual, int pinned, float *out, float *h,
-                               void *stream) {
+                               const float *x, const float *residual, uint32_t hadamard_block, int pinned,
+                               float *out, float *h, void *stream) {
     Tally t(c, did ? 3 : 2, true);
-    return t(ffn_device_checked(c, gid, uid, did, x, residual, pinned, out, h, stream, t));
+    return t(ffn_device_checked(c, gid, uid, did, x, residual, hadamard_block, pinned, out, h, stream, t));
 }
 
 int prism_hip_sync(prism_hip_ctx *c, void *stream) {

@@ -64,7 +64,7 @@ struct prism_hip_ctx {
     std::map<uint64_t, int64_t> by_key;
     int64_t next_id = 1;
     int *err = nullptr;  // device error flag
-    prism::rt::DevBuf x, act, act2, out, gate, up, h, res, pre, sk, lora;
+    prism::rt::DevBuf x, act, act2, out, gate, up, h, hr, res, pre, sk, lora;
     // This device's copy of the fixed scratch array (static_scratch.hip), looked up at
     // creation; nullptr if the lookup failed.
     void *noalloc = nullptr;

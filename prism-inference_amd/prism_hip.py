@@ -107,17 +107,17 @@ def lib() -> ctypes.CDLL:
         "prism_hip_project_f32_pair_tokens": (I, [P, P, P, U32, I, P, P]),
         "prism_hip_project_f32_triple_tokens": (I, [P, P, P, U32, I, P, P, P]),
         "prism_hip_ffn_swiglu": (I, [P, I64, I64, P, I, P]),
-        "prism_hip_ffn_chain": (I, [P, I64, I64, I64, P, P, I, P]),
-        "prism_hip_ffn_chain_lora": (I, [P, I64, I64, I64, P, P, P, I, P, P]),
+        "prism_hip_ffn_chain": (I, [P, I64, I64, I64, P, P, U32, I, P]),
+        "prism_hip_ffn_chain_lora": (I, [P, I64, I64, I64, P, P, U32, P, I, P, P]),
         "prism_hip_ffn_swiglu_tokens": (I, [P, I64, I64, P, U32, I, P]),
-        "prism_hip_ffn_chain_tokens": (I, [P, I64, I64, I64, P, P, U32, I, P]),
+        "prism_hip_ffn_chain_tokens": (I, [P, I64, I64, I64, P, P, U32, U32, I, P]),
         "prism_hip_prefill": (I, [P, I64, P, U32, I, P]),
         "prism_hip_mul_mat": (I, [P, I64, P, U32, P]),
         "prism_hip_quantize_q8k_device": (I, [P, P, U64, U32, I, P, P]),
         "prism_hip_quantize_q8_device": (I, [P, P, U64, U32, I, P, P]),
         "prism_hip_project_device": (I, [P, I64, I, P, U32, I, P, P]),
         "prism_hip_project_device_noalloc": (I, [P, I64, I, P, U32, I, P, P]),
-        "prism_hip_ffn_chain_device": (I, [P, I64, I64, I64, P, P, I, P, P, P]),
+        "prism_hip_ffn_chain_device": (I, [P, I64, I64, I64, P, P, U32, I, P, P, P]),
         "prism_hip_sync": (I, [P, P]),
         "prism_hip_stream": (P, [P]),
         "prism_hip_decoder_create": (P, [P, P, U32]),
@@ -534,12 +534,13 @@ class Context:
         return self._run(rc, out, check)
 
     def ffn_chain_tokens(self, g: int, u: int, d: int, hidden: int, X, residual=None, pinned: bool = False,
-                         check=True):
+                         check=True, hadamard_block: int = 0):
+        """hadamard_block: the chain's hadamard_block_size (0 = None)."""
         X = np.ascontiguousarray(X, np.float32)
         res = np.ascontiguousarray(residual, np.float32) if residual is not None else None
         out = np.full((X.shape[0], hidden), 7.0, np.float32)
-        rc = lib().prism_hip_ffn_chain_tokens(self._h, g, u, d, _ptr(X), _ptr(res), X.shape[0], int(pinned),
-                                              _ptr(out))
+        rc = lib().prism_hip_ffn_chain_tokens(self._h, g, u, d, _ptr(X), _ptr(res), X.shape[0], hadamard_block,
+                                              int(pinned), _ptr(out))
         return self._run(rc, out, check)
 
     def ffn_swiglu(self, g: int, u: int, ffn: int, x, pinned: bool = False, check=True):
@@ -548,23 +549,25 @@ class Context:
         rc = lib().prism_hip_ffn_swiglu(self._h, g, u, _ptr(x), int(pinned), _ptr(out))
         return self._run(rc, out, check)
 
-    def ffn_chain(self, g: int, u: int, d: int, hidden: int, x, residual=None, pinned: bool = False, check=True):
+    def ffn_chain(self, g: int, u: int, d: int, hidden: int, x, residual=None, pinned: bool = False, check=True,
+                  hadamard_block: int = 0):
+        """hadamard_block: the chain's hadamard_block_size (0 = None)."""
         x = np.ascontiguousarray(x, np.float32)
         res = np.ascontiguousarray(residual, np.float32) if residual is not None else None
         out = np.full(hidden, 7.0, np.float32)
-        rc = lib().prism_hip_ffn_chain(self._h, g, u, d, _ptr(x), _ptr(res), int(pinned), _ptr(out))
+        rc = lib().prism_hip_ffn_chain(self._h, g, u, d, _ptr(x), _ptr(res), hadamard_block, int(pinned), _ptr(out))
         return self._run(rc, out, check)
 
     def ffn_chain_lora(self, g: int, u: int, d: int, hidden: int, x, lora_a, residual=None, pinned: bool = False,
-                       check=True):
+                       check=True, hadamard_block: int = 0):
         """Returns (out, lora_dot); out is zero-filled and the dot 0 on failure."""
         x = np.ascontiguousarray(x, np.float32)
         la = np.ascontiguousarray(lora_a, np.float32) if lora_a is not None else None
         res = np.ascontiguousarray(residual, np.float32) if residual is not None else None
         out = np.full(hidden, 7.0, np.float32)
         dot = np.full(1, 7.0, np.float32)
-        rc = lib().prism_hip_ffn_chain_lora(self._h, g, u, d, _ptr(x), _ptr(res), _ptr(la), int(pinned), _ptr(out),
-                                            _ptr(dot))
+        rc = lib().prism_hip_ffn_chain_lora(self._h, g, u, d, _ptr(x), _ptr(res), hadamard_block, _ptr(la),
+                                            int(pinned), _ptr(out), _ptr(dot))
         return self._run(rc, out, check), dot[0]
 
     # -- device-pointer dispatch (torch tensors) --
@@ -585,9 +588,9 @@ class Context:
             self._check(rc)
         return rc
 
-    def ffn_chain_device(self, g, u, d, x, residual, pinned, out, h=None, stream=None):
-        self._check(lib().prism_hip_ffn_chain_device(self._h, g, u, d, _ptr(x), _ptr(residual), int(pinned), _ptr(out),
-                                                     _ptr(h), stream))
+    def ffn_chain_device(self, g, u, d, x, residual, pinned, out, h=None, stream=None, hadamard_block: int = 0):
+        self._check(lib().prism_hip_ffn_chain_device(self._h, g, u, d, _ptr(x), _ptr(residual), hadamard_block,
+                                                     int(pinned), _ptr(out), _ptr(h), stream))
 
     def sync(self, stream=None) -> int:
         return lib().prism_hip_sync(self._h, stream)

@@ -107,7 +107,7 @@ def test_gpu_group_tokens_errors_clear_outputs(ctx):
 
 # ---- multi-token FFN (projection.rs:239-259, 328-355) ---------------------------------
 
-@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PTQ1, ph.KIND_PQ2])
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PTQ1, ph.KIND_PQ2, ph.KIND_Q8_0])
 def test_gpu_ffn_tokens(ctx, kind):
     import oracle
 
@@ -249,6 +249,55 @@ def test_gpu_ffn_chain_lora_matches_chain_and_oracle_dot(ctx, kind):
     bad[17] = np.nan
     (rc, out), dot = ctx.ffn_chain_lora(g, u, d, hidden, x, bad, r, pinned=True, check=False)
     assert rc == ph.ERR_INVALID_INPUT and not out.any() and dot == 0.0
+    assert not ctx.faulted
+    for i in (g, u, d):
+        ctx.release(i)
+
+
+# ---- rotated FFN chain: hadamard_block_size (projection.rs:271-355) -------------------
+
+@pytest.mark.parametrize("kind", [ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_Q8_0, ph.KIND_PQ2])
+def test_gpu_ffn_chain_hadamard(ctx, kind):
+    """The SwiGLU vector rotated blockwise ahead of down: pinned bit-exact against the
+    oracle's rotated chain for blocks of 32, 256 and 2048 (the SwiGLU width is 6144), on a
+    single token, three tokens and the LoRA chain (whose dot takes the unrotated vector);
+    block 1 is no rotation; a block that is not a power of two, does not divide 6144 or
+    exceeds 8192 is refused with a zeroed output."""
+    import oracle
+
+    hidden, ffn = 2048, 6144
+    wg = synth.weights(kind, ffn, hidden, seed=31)
+    wu = synth.weights(kind, ffn, hidden, seed=32)
+    wd = synth.weights(kind, hidden, ffn, seed=33)
+    g, u, d = (ctx.weight(kind, hidden, ffn, wg), ctx.weight(kind, hidden, ffn, wu), ctx.weight(kind, ffn, hidden, wd))
+    X = synth.activations(hidden, seed=34, tokens=3).reshape(3, hidden)
+    R = synth.activations(hidden, seed=35, tokens=3).reshape(3, hidden)
+    la = np.random.default_rng(36).standard_normal(ffn).astype(np.float32)
+    plain = ctx.ffn_chain(g, u, d, hidden, X[0], R[0], pinned=True)
+    assert_bits_equal(ctx.ffn_chain(g, u, d, hidden, X[0], R[0], pinned=True, hadamard_block=1), plain, "block 1")
+    _, plain_dot = ctx.ffn_chain_lora(g, u, d, hidden, X[0], la, R[0], pinned=True)
+    for block in (32, 256, 2048):
+        ref, _ = oracle.ffn(kind, hidden, ffn, wg, wu, wd, X[0], R[0], pinned=True, threads=THREADS,
+                            hadamard_block=block)
+        got = ctx.ffn_chain(g, u, d, hidden, X[0], R[0], pinned=True, hadamard_block=block)
+        assert_bits_equal(got, ref, f"block {block}")
+        assert not np.array_equal(got, plain)
+        out, dot = ctx.ffn_chain_lora(g, u, d, hidden, X[0], la, R[0], pinned=True, hadamard_block=block)
+        assert_bits_equal(out, ref, f"lora block {block}")
+        assert_bits_equal(np.float32(dot), np.float32(plain_dot), f"lora dot block {block}")
+        Y = ctx.ffn_chain_tokens(g, u, d, hidden, X, R, pinned=True, hadamard_block=block)
+        assert_bits_equal(Y[0], ref, f"tokens block {block}")
+        for t in (1, 2):
+            assert_bits_equal(Y[t], ctx.ffn_chain(g, u, d, hidden, X[t], R[t], pinned=True, hadamard_block=block),
+                              f"token {t} block {block}")
+    ref, _ = oracle.ffn(kind, hidden, ffn, wg, wu, wd, X[1], None, pinned=False, threads=THREADS, hadamard_block=256)
+    got = ctx.ffn_chain(g, u, d, hidden, X[1], None, pinned=False, hadamard_block=256)
+    assert np.max(np.abs(got - ref)) <= 1e-3 * np.max(np.abs(ref))
+    for bad in (96, 4096, 16384):
+        rc, out = ctx.ffn_chain(g, u, d, hidden, X[0], R[0], pinned=True, check=False, hadamard_block=bad)
+        assert rc == ph.ERR_INVALID_INPUT and not out.any(), bad
+        rc, out = ctx.ffn_chain_tokens(g, u, d, hidden, X, R, pinned=True, check=False, hadamard_block=bad)
+        assert rc == ph.ERR_INVALID_INPUT and not out.any(), bad
     assert not ctx.faulted
     for i in (g, u, d):
         ctx.release(i)

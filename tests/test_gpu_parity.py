@@ -682,7 +682,8 @@ def test_gpu_project_f32_group_siblings(ctx):
 
 # ---- FFN ------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_PTQ1, ph.KIND_TQ1_0, ph.KIND_TQ2_0])
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_PTQ1, ph.KIND_Q8_0, ph.KIND_TQ1_0,
+                                  ph.KIND_TQ2_0])
 def test_gpu_ffn_chain(ctx, kind):
     import oracle
 
