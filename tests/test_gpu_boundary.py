@@ -256,7 +256,8 @@ def test_gpu_ffn_chain_lora_matches_chain_and_oracle_dot(ctx, kind):
 
 # ---- rotated FFN chain: hadamard_block_size (projection.rs:271-355) -------------------
 
-@pytest.mark.parametrize("kind", [ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_Q8_0, ph.KIND_PQ2])
+@pytest.mark.parametrize("kind", [ph.KIND_PTQ1, ph.KIND_Q2_K, ph.KIND_Q8_0, ph.KIND_PQ2, ph.KIND_TQ1_0,
+                                  ph.KIND_TQ2_0])
 def test_gpu_ffn_chain_hadamard(ctx, kind):
     """The SwiGLU vector rotated blockwise ahead of down: pinned bit-exact against the
     oracle's rotated chain for blocks of 32, 256 and 2048 (the SwiGLU width is 6144), on a
@@ -293,6 +294,14 @@ def test_gpu_ffn_chain_hadamard(ctx, kind):
     ref, _ = oracle.ffn(kind, hidden, ffn, wg, wu, wd, X[1], None, pinned=False, threads=THREADS, hadamard_block=256)
     got = ctx.ffn_chain(g, u, d, hidden, X[1], None, pinned=False, hadamard_block=256)
     assert np.max(np.abs(got - ref)) <= 1e-3 * np.max(np.abs(ref))
+    # Device pointers: the same bits, and h receives the unrotated SwiGLU vector.
+    xd, rd = DeviceBuffer.from_numpy(X[0]), DeviceBuffer.from_numpy(R[0])
+    od, hd = DeviceBuffer(hidden * 4), DeviceBuffer(ffn * 4)
+    ctx.ffn_chain_device(g, u, d, xd, rd, True, od, hd, hadamard_block=256)
+    assert ctx.sync() == 0
+    assert_bits_equal(od.to_numpy(np.float32), ctx.ffn_chain(g, u, d, hidden, X[0], R[0], pinned=True,
+                                                            hadamard_block=256), "device block 256")
+    assert_bits_equal(hd.to_numpy(np.float32), ctx.ffn_swiglu(g, u, ffn, X[0], pinned=True), "device h")
     for bad in (96, 4096, 16384):
         rc, out = ctx.ffn_chain(g, u, d, hidden, X[0], R[0], pinned=True, check=False, hadamard_block=bad)
         assert rc == ph.ERR_INVALID_INPUT and not out.any(), bad
