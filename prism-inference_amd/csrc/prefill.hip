@@ -368,6 +368,156 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CT == 4 ? 2
     if (bad) raise_error(err, kErrNonfinite);
 }
 
+// Short prompts on the same tiles: with few token groups the kernel above runs few
+// workgroups, each through every block of its rows with one wavefront per SIMD (about 18 us
+// of GEMM for 6144 x 2048 from 16 to 128 tokens).  Here a workgroup of sixteen wavefronts owns the
+// same 128 rows and 32 tokens, and splits the blocks over four phases: wavefront w is row
+// wavefront w % 4 (32 rows, as above) of phase w / 4, which takes blocks p, p + 4, ...
+// Each phase stages its own block's codes (its four row wavefronts four runs each), so the
+// codes still cross from L2 once per workgroup.  Per round of four blocks, phase 0 adds its
+// own block's term fl(d_w * T) to the outputs it holds, phases 1..3 leave theirs in LDS, and
+// after a barrier phase 0 adds them in block order: Y = Y + fl(d_w * T) block by block, the
+// chain above, so every token row is again its own matvec.
+constexpr uint32_t kPhases = 4;
+
+__global__ __launch_bounds__(64 * 4 * kPhases) void k_prefill_ptq1_split(const uint8_t *__restrict__ W, uint32_t rows,
+                                                                        uint32_t nu, const _Float16 *__restrict__ xh,
+                                                                        const float *__restrict__ sc, uint32_t M,
+                                                                        uint32_t Mp, uint32_t xcd_major,
+                                                                        float *__restrict__ out, int *__restrict__ err) {
+    constexpr uint32_t NT = 32;
+    constexpr uint32_t kRun = NT * 16;  // bytes of one (g, j, h) run of one block
+    // actN[phase][g*2+j][h][token][16 bytes], two ring buffers named statically (as above).
+    __shared__ __attribute__((aligned(16))) uint8_t act0[kPhases][8][2][kRun];
+    __shared__ __attribute__((aligned(16))) uint8_t act1[kPhases][8][2][kRun];
+    __shared__ __attribute__((aligned(16))) float4 scl0[kPhases][NT];
+    __shared__ __attribute__((aligned(16))) float4 scl1[kPhases][NT];
+    // The terms of phases 1..3: [phase - 1][row wavefront][output register][lane].
+    __shared__ float terms[kPhases - 1][4][16][64];
+    const uint32_t lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t rw = wave & 3u, phase = wave >> 2;
+    const uint32_t bx = xcd_major ? blockIdx.y : blockIdx.x;
+    const uint32_t by = xcd_major ? blockIdx.x + 8 * blockIdx.z : blockIdx.y;
+    const uint32_t tile = 2 * bx + (rw >> 1), hw = rw & 1;
+    const uint32_t tiles = (rows + kTile - 1) / kTile;
+    const uint32_t t0 = by * NT;
+    const uint32_t row_bytes = nu * 28;
+    uint32_t trows = 0;
+    if (tile < tiles) {
+        const uint32_t left = rows - tile * kTile;
+        trows = left < kTile ? left : kTile;
+    }
+    const bool active = 32 * hw < trows;  // uniform per wavefront
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rw_ =
+        make_rsrc(W + static_cast<size_t>(active ? tile : 0) * kTile * row_bytes, active ? trp * row_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xh, nu * 8u * Mp * 32u);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc, nu * Mp * 16u);
+    const uint32_t row = 32 * hw + r32, out0 = 32 * hw + 4 * h;  // tile rows
+
+    // Block u's 16 runs (this phase's row wavefront rw moves runs rw, rw + 4, ...; one
+    // instruction per run, lanes past the tokens idle) and the tokens' scales.
+    auto stage = [&](uint32_t u, uint8_t (&act)[kPhases][8][2][kRun], float4 (&scl)[kPhases][NT]) {
+#pragma unroll
+        for (uint32_t k = rw; k < 16; k += 4)
+            if (lane < NT)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(&act[phase][k >> 1][k & 1][0]), 16,
+                                                         ((u * 16 + k) * Mp + t0 + lane) * 16u, 0, 0, 0);
+        if (rw == 0 && lane < NT)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(&scl[phase][0]), 16, (u * Mp + t0 + lane) * 16u,
+                                                     0, 0, 0);
+    };
+
+    v16f o;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] = 0.0f;
+    RawBlock w;
+    if (phase < nu) {
+        stage(phase, act0, scl0);
+        if (active) load_block_codes(rw_, phase * trp * 28u, trp, row, w);
+    }
+    wait_vmcnt0();
+    lds_barrier();
+    // Round r (blocks 4r .. 4r+3) from (act, scl) while round r+1 streams into the others.
+    auto round = [&](uint32_t r, const uint8_t (&act)[kPhases][8][2][kRun], const float4 (&scl)[kPhases][NT],
+                     uint8_t (&act_next)[kPhases][8][2][kRun], float4 (&scl_next)[kPhases][NT]) {
+        const uint32_t u = kPhases * r + phase, un = u + kPhases;
+        const bool mine = u < nu && active;
+        uint32_t aw[4][4][2];
+        float dw = 0.0f;
+        if (mine) {
+            PairDecoder dec(w, h);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) dec.group(g, aw[g]);
+            dw = h ? 0.0f : h2f(w.tl >> 16);
+        }
+        if (un < nu) {
+            stage(un, act_next, scl_next);
+            if (active) load_block_codes(rw_, un * trp * 28u, trp, row, w);
+        }
+        if (mine) {
+            const v16f d = __builtin_amdgcn_mfma_f32_32x32x2f32(dw, h ? 0.0f : 1.0f, v16f{}, 0, 0, 0);
+            const float4 sg4 = scl[phase][r32];
+            const float sg[4] = {sg4.x, sg4.y, sg4.z, sg4.w};
+            v16f tt;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                v16f a = {};
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const v8h bx8 = *reinterpret_cast<const v8h *>(&act[phase][2 * g + j][h][r32 * 16]);
+                    const v8h ax = __builtin_bit_cast(v8h, u32x4{aw[g][0][j], aw[g][1][j], aw[g][2][j], aw[g][3][j]});
+                    a = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, bx8, a, 0, 0, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 16; ++k) tt[k] = g == 0 ? sg[0] * a[k] : __builtin_fmaf(sg[g], a[k], tt[k]);
+            }
+            if (phase == 0) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) o[k] = o[k] + d[k] * tt[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) terms[phase - 1][rw][k][lane] = d[k] * tt[k];
+            }
+        }
+        wait_vmcnt0();  // round r+1's codes, scales and weights have landed
+        lds_barrier();  // every term of round r is in LDS; round r's buffers are free
+        if (phase == 0 && active) {
+#pragma unroll
+            for (uint32_t q = 1; q < kPhases; ++q)
+                if (kPhases * r + q < nu)
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) o[k] = o[k] + terms[q - 1][rw][k][lane];
+        }
+        lds_barrier();  // the terms are read before the next round writes them
+    };
+    const uint32_t rounds = (nu + kPhases - 1) / kPhases;
+    for (uint32_t r = 0; r < rounds; r += 2) {
+        round(r, act0, scl0, act1, scl1);
+        if (r + 1 < rounds) round(r + 1, act1, scl1, act0, scl0);
+    }
+    if (phase != 0 || !active) return;
+    // Y[t][r]: the lane holds token t0 + r32 and tile rows out0 + 8q + 0..3.
+    const uint32_t t = t0 + r32;
+    if (t >= M) return;
+    bool bad = false;
+    float *yr = out + static_cast<size_t>(t) * rows + static_cast<size_t>(tile) * kTile;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t r = out0 + 8 * q + e;
+            if (r < trows) {
+                const float v = o[4 * q + e];
+                yr[r] = v;
+                bad |= !finite(v);
+            }
+        }
+    }
+    if (bad) raise_error(err, kErrNonfinite);
+}
+
 // The pinned contract (dot_q8_groups_pinned, src/kernels.rs:1102-1147) on the same
 // tiles: per (token, row) four binary32 lanes L[l] = fma(I_l, dd_g, L[l]) with
 // dd_g = fl(d_w * A_g.scale), group by group, and (L0 + L1) + (L2 + L3) at the end.  In
@@ -493,6 +643,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 
 uint32_t padded_tokens(uint32_t M) { return (M + kTokAlign - 1) / kTokAlign * kTokAlign; }
 
+// Source-contract prompts up to this many tokens take the block-split kernel.  Measured for
+// 6144 x 2048 (prep + GEMM, us, split against the kernel above): 16 tokens 19.6 / 23.1, 64
+// tokens 20.9 / 24.1, 128 tokens 21.3 / 24.6, 256 tokens 37.1 / 32.5, 512 tokens 55.4 / 44.9.
+// Beyond 128 tokens the four-token-group workgroups of the kernel above fill more CUs.
+constexpr uint32_t kSplitMaxTokens = 128;
+
 }  // namespace
 
 size_t prefill_scratch_bytes(uint64_t cols, uint32_t tokens) {
@@ -549,6 +705,14 @@ int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const floa
     // and beats 128 (two per SIMD, the decode shared by more tokens) up to about 4096
     // tokens (4096: 232 against 241-246 us); 32 (four wavefronts per SIMD) keeps CUs busy
     // on short prompts up to 512 tokens (512: 45.0 against 46.6 us; 768: 65.4 against 64.2).
+    if (M <= kSplitMaxTokens) {
+        const uint32_t groups = Mp / 32;
+        const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;
+        const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
+        hipLaunchKernelGGL(k_prefill_ptq1_split, grid, dim3(64 * 4 * kPhases), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major,
+                           out, err);
+        return launch_status();
+    }
     const uint32_t nt = M >= 4096 ? 128 : M > 512 ? 64 : 32, groups = Mp / nt;
     const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
     const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
