@@ -89,6 +89,13 @@ const char *prism_hip_identity(const prism_hip_ctx *ctx);
 const char *prism_hip_last_error(const prism_hip_ctx *ctx);
 /* 1 once a device fault has latched. */
 int prism_hip_faulted(const prism_hip_ctx *ctx);
+/* Test hook with no counterpart in the reference's trait: latches the context's device
+ * fault from the host, as a lost device or a failed wait would (the Vulkan executor's
+ * latch, tools/adreno-vulkan/src/executor.rs:1507-1530), so that the latched behaviour
+ * (every supports*() 0, operation_capacity 0, every call PRISM_ERR_DEVICE_FAULT with its
+ * output cleared) can be tested without faulting a GPU.  Irreversible for this context;
+ * other contexts are unaffected.  Returns PRISM_OK (PRISM_ERR_INVALID_INPUT for NULL). */
+int prism_hip_inject_fault(prism_hip_ctx *ctx);
 /* Pq2ProjectionExecutor::operation_capacity (projection.rs:20-28): 0 when faulted,
  * UINT64_MAX otherwise (submissions are not rationed). */
 uint64_t prism_hip_operation_capacity(const prism_hip_ctx *ctx);

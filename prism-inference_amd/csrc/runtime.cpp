@@ -337,6 +337,12 @@ void prism_hip_destroy(prism_hip_ctx *c) {
 const char *prism_hip_identity(const prism_hip_ctx *c) { return c ? c->identity.c_str() : ""; }
 const char *prism_hip_last_error(const prism_hip_ctx *c) { return c ? c->last_error.c_str() : "null context"; }
 int prism_hip_faulted(const prism_hip_ctx *c) { return c ? (c->faulted ? 1 : 0) : 1; }
+int prism_hip_inject_fault(prism_hip_ctx *c) {
+    if (!c) return PRISM_ERR_INVALID_INPUT;
+    c->faulted = true;
+    c->last_error = "device fault latched by prism_hip_inject_fault";
+    return PRISM_OK;
+}
 uint64_t prism_hip_operation_capacity(const prism_hip_ctx *c) { return (!c || c->faulted) ? 0 : UINT64_MAX; }
 
 int64_t prism_hip_operation_count(const prism_hip_ctx *c, uint32_t kind, uint64_t cols, uint64_t rows) {

@@ -79,6 +79,7 @@ def lib() -> ctypes.CDLL:
         "prism_hip_identity": (ctypes.c_char_p, [P]),
         "prism_hip_last_error": (ctypes.c_char_p, [P]),
         "prism_hip_faulted": (I, [P]),
+        "prism_hip_inject_fault": (I, [P]),
         "prism_hip_operation_capacity": (U64, [P]),
         "prism_hip_operation_count": (I64, [P, U32, U64, U64]),
         "prism_hip_supports": (I, [P, U32, U64, U64, I]),
@@ -364,6 +365,10 @@ class Context:
     def faulted(self) -> bool:
         return bool(lib().prism_hip_faulted(self._h))
 
+    def inject_fault(self) -> None:
+        """Latch this context's device fault from the host (a test hook)."""
+        self._check(lib().prism_hip_inject_fault(self._h))
+
     def operation_capacity(self) -> int:
         return lib().prism_hip_operation_capacity(self._h)
 
@@ -625,7 +630,8 @@ class Decoder:
                               g["rope_base"], g["eps"])
         self._h = lib().prism_hip_decoder_create(ctx._h, ctypes.byref(geo), max_steps)
         if not self._h:
-            raise PrismError(ERR_INVALID_INPUT, lib().prism_hip_last_error(ctx._h).decode())
+            code = ERR_DEVICE_FAULT if lib().prism_hip_faulted(ctx._h) else ERR_INVALID_INPUT
+            raise PrismError(code, lib().prism_hip_last_error(ctx._h).decode())
         try:
             self.set_weights(model)
             for i, L in enumerate(model["layers"]):

@@ -312,6 +312,51 @@ def test_gpu_ffn_chain_hadamard(ctx, kind):
         ctx.release(i)
 
 
+# ---- latched device fault (tools/adreno-vulkan/src/executor.rs:1507-1530) -------------
+
+def test_gpu_latched_fault_refuses_everything():
+    """A latched fault (forced from the host: no GPU is faulted) makes every eligibility
+    query false and the capacity 0, and every call fails with PRISM_ERR_DEVICE_FAULT and a
+    cleared output, weight uploads and decoders included; another context is unaffected."""
+    P, Q2 = ph.KIND_PTQ1, ph.KIND_Q2_K
+    cols, rows = 2048, 128
+    w = synth.ptq1_weights(rows, cols, seed=41)
+    x = synth.activations(cols, seed=42)
+    c = ph.Context(0)
+    other = ph.Context(0)
+    try:
+        wid = c.weight(P, cols, rows, w)
+        good = c.project_f32(wid, rows, x)
+        assert c.supports(P, cols, rows, ph.PATH_F32) and c.supports_tile_tokens()
+        assert c.operation_capacity() > 0 and c.operation_count(P, cols, rows) == cols * rows
+        c.inject_fault()
+        assert c.faulted and "latched" in c.last_error
+        assert not any(c.supports(P, cols, rows, path) for path in (ph.PATH_Q8K, ph.PATH_Q8, ph.PATH_F32))
+        assert not c.supports_f32_group([(P, cols, rows), (P, cols, rows)])
+        assert not c.supports_f32_ffn_swiglu((Q2, 2048, 6144), (Q2, 2048, 6144))
+        assert not c.supports_f32_ffn_chain((Q2, 2048, 6144), (Q2, 2048, 6144), (Q2, 6144, 2048))
+        assert not c.supports_f32_ffn_chain_lora((Q2, 2048, 6144), (Q2, 2048, 6144), (Q2, 6144, 2048))
+        assert not c.supports_tile_tokens()
+        assert c.operation_capacity() == 0 and c.operation_count(P, cols, rows) == -1
+        for tokens in (1, 4, 32):
+            X = synth.activations(cols, seed=43, tokens=tokens).reshape(tokens, cols)
+            rc, out = c.project_f32(wid, rows, X, tokens=tokens, check=False)
+            assert rc == ph.ERR_DEVICE_FAULT and not out.any(), tokens
+        with pytest.raises(ph.PrismError) as e:
+            c.weight(P, cols, rows, w, key=7)
+        assert e.value.code == ph.ERR_DEVICE_FAULT
+        with pytest.raises(ph.PrismError) as e:
+            ph.Decoder(c, synth.decoder_model(44, kv_prefill=4, hidden=512, ffn=1024, heads=4, kv_heads=2,
+                                              vocab=2048, layers=1, max_tokens=16))
+        assert e.value.code == ph.ERR_DEVICE_FAULT
+        assert not other.faulted
+        oid = other.weight(P, cols, rows, w)
+        assert_bits_equal(other.project_f32(oid, rows, x), good, "other context")
+    finally:
+        c.close()
+        other.close()
+
+
 # ---- statistics (MatvecStatistics / MatvecDiagnostics, src/kernels.rs:1725-1830) ------
 
 def test_gpu_statistics_and_diagnostics():
