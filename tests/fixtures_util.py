@@ -134,3 +134,11 @@ def q8_0_order_kats():
     a = act(np.float16(2 - 2 ** -10), [64, 3])
     cases.append(("C scale product first", w, a, 0x467FE7FA, 0x467FE7FB))
     return cases
+
+
+def mulmat_geometries():
+    """The plain 2-D test_mul_mat cases of test-backend-ops for the path's formats
+    (tests/upstream_prism/backend-ops-geometries.json, filtered by collect_fixtures.py):
+    distinct (type, m, n, k), m rows of A, n columns of B, k the shared width."""
+    data = load_json("backend-ops-mulmat.json")
+    return sorted({(a[0], a[2], a[3], a[4]) for a in (e["Arguments"] for e in data["Eval"])})

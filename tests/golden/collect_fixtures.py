@@ -18,6 +18,8 @@ Sources (paths relative to the reference checkout):
   tests/upstream_prism/pq2-inputs.bin                 15 upstream PQ2 row-shape inputs
   tests/fixtures/upstream-tquants.json                TQ1_0/TQ2_0 encode/decode/dot records
   tests/fixtures/swift-activation-parity.json         pinned SiLU / SwiGLU native captures
+  tests/upstream_prism/backend-ops-geometries.json    MUL_MAT geometries of test-backend-ops
+                                                      (plain 2-D cases of the path's formats)
 """
 
 import hashlib
@@ -85,6 +87,23 @@ def main() -> int:
     with open(os.path.join(OUT, "upstream-kquants-q2k.json"), "w") as f:
         json.dump(reduced, f, indent=1, sort_keys=True)
     provenance["upstream-kquants-q2k.json"] = {"source": rel, "sha256": sha(src), "type_ids": [10], "cases": len(keep)}
+
+    # MUL_MAT geometries (test_mul_mat arguments: type_a, type_b, m, n, k, bs, nr, per, ...):
+    # keep A in Q8_0 (8), Q2_K (10), PQ2 (142) or PTQ1 (143) with an F32 B (type 0) and no
+    # batching, broadcast or permutation -- the 2-D product prism_hip_mul_mat serves.
+    rel = "tests/upstream_prism/backend-ops-geometries.json"
+    src = os.path.join(REF, rel)
+    with open(src) as f:
+        data = json.load(f)
+    keep = [e for e in data["Eval"] if e["Class"] == "test_mul_mat" and e["Arguments"][0] in (8, 10, 142, 143)
+            and e["Arguments"][1] == 0 and e["Arguments"][5] == [1, 1] and e["Arguments"][6] == [1, 1]
+            and e["Arguments"][7] == [0, 1, 2, 3]]
+    reduced = {k: data[k] for k in ("SchemaVersion", "Source", "SourceSha256", "EvalSha256")}
+    reduced["Eval"] = keep
+    with open(os.path.join(OUT, "backend-ops-mulmat.json"), "w") as f:
+        json.dump(reduced, f, indent=1, sort_keys=True)
+    provenance["backend-ops-mulmat.json"] = {"source": rel, "sha256": sha(src), "type_ids": [8, 10, 142, 143],
+                                             "cases": len(keep)}
 
     for name in provenance:
         provenance[name]["local_sha256"] = sha(os.path.join(OUT, name))
