@@ -447,6 +447,58 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
     return r
 
 
+# ---- test-backend-ops' MUL_MAT performance cases -------------------------------------
+
+def bench_backend_ops(ctx: ph.Context, rotate_bytes: int = 512 << 20, calls: int = 40) -> list:
+    """The reference's MUL_MAT performance cases for the path's formats (test-backend-ops'
+    Perf list, tests/upstream_prism/backend-ops-geometries.json, filtered into
+    tests/golden/backend-ops-mulmat.json): A [m][k] packed, B [n][k] F32 in HBM, the whole
+    op as the reference runs it (src/backend/ops.rs:444-466: the GPU quantizes B in the
+    public contract, then the projection), through prism_hip_project_device.  Weights
+    rotated over >= rotate_bytes of copies (beyond the 256 MB MALL); `calls` calls issued one
+    by one from the host and timed with HIP events on the library stream."""
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                           "backend-ops-mulmat.json")) as f:
+        perf = json.load(f)["Perf"]
+    cases = []
+    for e in perf:
+        a = e["Arguments"]
+        g = (a[0], a[2], a[3], a[4])
+        if g not in cases:
+            cases.append(g)
+    shapes = []
+    for kind, m, n, k in cases:
+        if (kind, m, k) not in shapes:
+            shapes.append((kind, m, k))
+    stream = ctx.stream()
+    res = []
+    for kind, m, k in shapes:
+        w = synth.weights(kind, m, k, seed=17)
+        copies = max(2, math.ceil(rotate_bytes / w.size))
+        rot = Rotation(ctx, kind, m, k, w, copies)
+        for n in [c[2] for c in cases if (c[0], c[1], c[3]) == (kind, m, k)]:
+            x = hiprt.DeviceBuffer.from_numpy(synth.activations(k, seed=18, tokens=n))
+            out = hiprt.DeviceBuffer(4 * m * n)
+            for i in range(min(copies, 4)):
+                ctx.project_device(rot.ids[i], ph.PATH_F32, x, n, False, out, stream)
+            assert ctx.sync() == 0
+            e0, e1 = hiprt.Event(), hiprt.Event()
+            e0.record(stream)
+            for i in range(calls):
+                ctx.project_device(rot.ids[i % copies], ph.PATH_F32, x, n, False, out, stream)
+            e1.record(stream)
+            e1.synchronize()
+            assert ctx.sync() == 0
+            t = e0.elapsed_ms(e1) / calls * 1e-3
+            nbytes = w.size + 4 * k * n + 4 * m * n
+            res.append({"type": kind, "m": m, "n": n, "k": k, "us": t * 1e6, "GBps": nbytes / t / 1e9,
+                        "TOPS": 2.0 * m * n * k / t / 1e12, "frac_hbm": nbytes / t / PEAK_HBM})
+            x.free()
+            out.free()
+        rot.release(ctx)
+    return res
+
+
 # ---- CPU baselines (the oracle on the host's cores) --------------------------------------
 
 def _time(fn, budget_s: float = 0.0, min_runs: int = 20, warmups: int = 3):
@@ -539,6 +591,8 @@ def main() -> int:
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
     ap.add_argument("--floor-only", action="store_true", help="time only the launch floor")
+    ap.add_argument("--backend-ops", action="store_true",
+                    help="time only test-backend-ops' MUL_MAT performance cases of the path's formats")
     ap.add_argument("--decode-eager", action="store_true",
                     help="time only decode steps launched kernel by kernel (no graph), for kernel traces")
     args = ap.parse_args()
@@ -553,6 +607,11 @@ def main() -> int:
         return calibrate_copy()
     ctx = ph.Context(0)
     log(ctx.identity)
+    if args.backend_ops:
+        for r in bench_backend_ops(ctx):
+            print(json.dumps(r), flush=True)
+        ctx.close()
+        return 0
     if args.prefill_only or args.matvec_only or args.ffn_only or args.floor_only:
         for spec in filter(None, args.prefill_only.split(",")):
             M, _, contract = spec.partition(":")  # "2048" or "2048:pinned"

@@ -100,6 +100,16 @@ int project(prism_hip_decoder *d, prism_weight_id wid, const float *x, float *ou
     return run_matvec(c, a, true);
 }
 
+// Whether a projection the step gives floats (qkv, o, the gate/up pair) quantizes them in
+// its kernel's prologue at these widths.
+bool prologue_fits(prism_hip_decoder *d, prism_weight_id wid, prism_weight_id up = 0, void *q8_out = nullptr) {
+    prism_hip_ctx *c = d->ctx;
+    MatvecArgs a = f32_args(c, *find(c, wid), nullptr, 1, 0, nullptr, nullptr, c->stream);
+    if (up) a.w2 = static_cast<const uint8_t *>(find(c, up)->dev);
+    a.q8_out = q8_out;
+    return tiled_prologue_fits(a);
+}
+
 // A projection of prepared Q8_0 blocks (the source contract's dot_q8_groups) + residual.
 int project_q8(prism_hip_decoder *d, prism_weight_id wid, const void *act, float *out, const float *residual) {
     prism_hip_ctx *c = d->ctx;
@@ -394,6 +404,8 @@ int prism_hip_decoder_set_layer(prism_hip_decoder *d, uint32_t layer, const uint
     if (!rc) rc = weight(d, &L.gate, slot + 2, PRISM_KIND_PTQ1, H, g.ffn, gate);
     if (!rc) rc = weight(d, &L.up, slot + 3, PRISM_KIND_PTQ1, H, g.ffn, up);
     if (!rc) rc = weight(d, &L.down, slot + 4, PRISM_KIND_PTQ1, g.ffn, H, down);
+    if (!rc && !(prologue_fits(d, L.qkv) && prologue_fits(d, L.o) && prologue_fits(d, L.gate, L.up, d->ffn_q8)))
+        rc = fail(d->ctx, PRISM_ERR_UNSUPPORTED, "decoder projection too wide for the quantizing prologue");
     if (!rc) rc = upload(d, L.norm, norm, sizeof(float) * H);
     if (!rc) rc = upload(d, L.post_norm, post_norm, sizeof(float) * H);
     if (!rc) rc = upload(d, L.q_norm, q_norm, sizeof(float) * D);

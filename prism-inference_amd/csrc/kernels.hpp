@@ -65,6 +65,10 @@ int launch_matvec_tiled(const MatvecArgs &a);
 // Whether a kActF32 tiled call must be given prepared blocks instead (large matrices
 // run a separate quantize kernel; the prologue would repeat it per workgroup).
 bool tiled_needs_prepared(const MatvecArgs &a);
+// Whether a kActF32 tiled call can quantize its input in the kernel's prologue at all (the
+// split kernel's plan fits LDS); callers that always pass floats (the decoder) check it
+// once instead of finding out at launch.
+bool tiled_prologue_fits(const MatvecArgs &a);
 // Device scratch a tiled call needs (the lane-ordered activations of a skinny batch).
 size_t tiled_scratch_bytes(const MatvecArgs &a);
 // Whether (kind, cols, rows) can be stored tiled on a device with `cus` compute units

@@ -2482,15 +2482,22 @@ bool plan_split(uint64_t rows, uint32_t nu, uint32_t cols, bool quant, uint32_t 
         lpr /= 2;
         ks *= 2;
     }
-    const uint32_t rw = kTile / lpr;
+    // activation blocks | terms (| SwiGLU inputs) | 16 doubles for the RMSNorm reduction
+    auto lds = [&](uint32_t groups) -> size_t {
+        const uint32_t rw = kTile / groups;
+        return align16(act_bytes_for<O>(cols)) +
+               align16(static_cast<uint32_t>(sizeof(float) * (nmat * rw * (nu * terms_per_unit<O>() + 1) + 2 * rw))) +
+               16 * sizeof(double);
+    };
+    // Long rows whose terms overflow LDS at this split: more lane groups per row, so a
+    // workgroup holds fewer rows' terms (pinned PTQ1 at 17408 inputs: 16 rows' terms take
+    // 78 KiB, 8 rows' 39 KiB).
+    while (lds(lpr) > kSplitLds && lpr < max_lpr && ks * lpr * 2 <= nu) lpr *= 2;
     pl->ks = ks;
     pl->lpr = lpr;
     pl->lg_ks = static_cast<uint32_t>(__builtin_ctz(ks));
     pl->lg_lpr = static_cast<uint32_t>(__builtin_ctz(lpr));
-    // activation blocks | terms (| SwiGLU inputs) | 16 doubles for the RMSNorm reduction
-    pl->lds = align16(act_bytes_for<O>(cols)) +
-              align16(static_cast<uint32_t>(sizeof(float) * (nmat * rw * (nu * terms_per_unit<O>() + 1) + 2 * rw))) +
-              16 * sizeof(double);
+    pl->lds = lds(lpr);
     return pl->lds <= kSplitLds;
 }
 
@@ -2594,7 +2601,30 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
         return launch_status();
     }
     SplitPlan pl;
-    if (!plan_split<O>(a.rows, nu, p.cols, quant, nmat, a.cus, &pl, a.q8_out ? 2u : 8u)) return -2;
+    if (!plan_split<O>(a.rows, nu, p.cols, quant, nmat, a.cus, &pl, a.q8_out ? 2u : 8u)) {
+        // Rows too wide for the split kernel's LDS (the activation and every unit's terms of a
+        // workgroup's rows): prepared activations take a row-tile kernel, which has no width
+        // limit (f32 input is quantized by the caller first, op_needs_prepared).
+        if (quant || nmat != 1) return -2;
+        const uint32_t grid = static_cast<uint32_t>(tiles < a.cus ? tiles : a.cus);
+        if constexpr (kind_of<O>() == kPTQ1) {
+            // The tile's units over 16 wavefronts with their terms in LDS when they fit beside
+            // the table, else one wavefront per tile.
+            if (const uint32_t lds = lut_spread_lds<O>(static_cast<uint32_t>(tiles), grid, nu))
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutSpread>), dim3(grid), dim3(kLutThreads), lds, a.stream, p, act);
+            else
+                hipLaunchKernelGGL((k_mv_rows_lut<O, kLutWhole>), dim3(grid), dim3(kLutThreads), 0, a.stream, p, act);
+            return launch_status();
+        } else {
+            const uint32_t stride = ((nu - (nu + 1) / 2) * terms_per_unit<O>()) | 1u;
+            if (O != Op::PTQ1_PINNED && nu >= 4 && stride <= 129)
+                hipLaunchKernelGGL(k_mv_rows2<O>, dim3(static_cast<uint32_t>(tiles)), dim3(128),
+                                   kTile * stride * sizeof(float), a.stream, p, stride);
+            else
+                hipLaunchKernelGGL(k_mv_rows<O>, dim3(static_cast<uint32_t>(tiles)), dim3(64), 0, a.stream, p);
+            return launch_status();
+        }
+    }
     p.ks = pl.ks;
     p.lpr = pl.lpr;
     p.lg_ks = pl.lg_ks;
@@ -2674,31 +2704,9 @@ bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t cus) 
     if (!tiled_format(kind, &f) || cols % f.unit_weights) return false;
     const uint64_t row_bytes = cols / f.unit_weights * f.unit_bytes;
     if (row_bytes * kTile >= (1ull << 31)) return false;  // 32-bit in-tile offsets
-    if ((rows + kTile - 1) / kTile >= cus) return true;   // row-tile kernels: any width
-    // Fewer tiles than CUs run the split kernel, whose LDS holds the prepared activation and
-    // the terms of every unit of its rows: every order the kind can take must fit, or the
-    // tensor stays in the native layout (whose kernels have no width limit).
-    MatvecArgs a;
-    a.kind = kind;
-    a.cols = cols;
-    a.rows = rows;
-    a.cus = cus;
-    for (const int fmt : {static_cast<int>(kActQ8K), static_cast<int>(kActQ8)}) {
-        if (fmt == kActQ8K && (cols % 256 || kind == kQ8_0)) continue;
-        if (fmt == kActQ8 && (kind == kQ2_K || kind == kTQ1_0 || kind == kTQ2_0)) continue;
-        for (const int pinned : {0, 1}) {
-            a.act_format = fmt;
-            a.pinned = pinned;
-            const int fits = dispatch(a, [&]<Op O>() {
-                SplitPlan pl;
-                return plan_split<O>(rows, static_cast<uint32_t>(cols / unit_weights<O>()), static_cast<uint32_t>(cols),
-                                     false, 1, cus, &pl)
-                           ? 1
-                           : 0;
-            });
-            if (fits == 0) return false;
-        }
-    }
+    (void)cus;
+    // Every width has a tiled kernel: fewer tiles than CUs run the split kernel where its LDS
+    // holds the activation and every unit's terms of its rows, else a row-tile kernel.
     return true;
 }
 
@@ -3005,6 +3013,18 @@ size_t tiled_scratch_bytes(const MatvecArgs &a) {
         else
             return 0;
     }));
+}
+
+bool tiled_prologue_fits(const MatvecArgs &a) {
+    const bool f32 = a.act_format == kActF32;
+    return f32 && dispatch(a, [&]<Op O>() {
+               SplitPlan pl;
+               return plan_split<O>(a.rows, static_cast<uint32_t>(a.cols / unit_weights<O>()),
+                                    static_cast<uint32_t>(a.cols), true, a.w2 ? 2u : 1u, a.cus, &pl,
+                                    a.q8_out ? 2u : 8u)
+                          ? 1
+                          : 0;
+           }) == 1;
 }
 
 bool tiled_needs_prepared(const MatvecArgs &a) {

@@ -142,3 +142,15 @@ def mulmat_geometries():
     distinct (type, m, n, k), m rows of A, n columns of B, k the shared width."""
     data = load_json("backend-ops-mulmat.json")
     return sorted({(a[0], a[2], a[3], a[4]) for a in (e["Arguments"] for e in data["Eval"])})
+
+
+def mulmat_perf_geometries():
+    """test-backend-ops' MUL_MAT performance cases for the path's formats (the same filter),
+    distinct (type, m, n, k) in file order."""
+    out = []
+    for e in load_json("backend-ops-mulmat.json")["Perf"]:
+        a = e["Arguments"]
+        g = (a[0], a[2], a[3], a[4])
+        if g not in out:
+            out.append(g)
+    return out

@@ -95,11 +95,15 @@ def main() -> int:
     src = os.path.join(REF, rel)
     with open(src) as f:
         data = json.load(f)
-    keep = [e for e in data["Eval"] if e["Class"] == "test_mul_mat" and e["Arguments"][0] in (8, 10, 142, 143)
-            and e["Arguments"][1] == 0 and e["Arguments"][5] == [1, 1] and e["Arguments"][6] == [1, 1]
-            and e["Arguments"][7] == [0, 1, 2, 3]]
-    reduced = {k: data[k] for k in ("SchemaVersion", "Source", "SourceSha256", "EvalSha256")}
+    def plain(e):
+        a = e["Arguments"]
+        return (e["Class"] == "test_mul_mat" and a[0] in (8, 10, 142, 143) and a[1] == 0 and a[5] == [1, 1]
+                and a[6] == [1, 1] and a[7] == [0, 1, 2, 3])
+
+    keep = [e for e in data["Eval"] if plain(e)]
+    reduced = {k: data[k] for k in ("SchemaVersion", "Source", "SourceSha256", "EvalSha256", "PerfSha256")}
     reduced["Eval"] = keep
+    reduced["Perf"] = [e for e in data["Perf"] if plain(e)]
     with open(os.path.join(OUT, "backend-ops-mulmat.json"), "w") as f:
         json.dump(reduced, f, indent=1, sort_keys=True)
     provenance["backend-ops-mulmat.json"] = {"source": rel, "sha256": sha(src), "type_ids": [8, 10, 142, 143],

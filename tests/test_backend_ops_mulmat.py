@@ -30,6 +30,11 @@ def test_mulmat_fixture_is_the_filtered_reference_file():
         a = e["Arguments"]
         assert e["Class"] == "test_mul_mat" and a[0] in (8, 10, 142, 143) and a[1] == 0
         assert a[5] == [1, 1] and a[6] == [1, 1] and a[7] == [0, 1, 2, 3]
+    assert len(data["Perf"]) == 125
+    for e in data["Perf"]:
+        a = e["Arguments"]
+        assert e["Class"] == "test_mul_mat" and a[0] in (8, 10, 142, 143) and a[1] == 0
+        assert a[5] == [1, 1] and a[6] == [1, 1] and a[7] == [0, 1, 2, 3]
     geoms = fx.mulmat_geometries()
     assert len(geoms) == 260
     block = {8: 32, 10: 256, 142: 128, 143: 128}

@@ -774,8 +774,9 @@ def test_gpu_device_calls_reject_a_foreign_stream(ctx):
 @pytest.mark.parametrize("kind", [ph.KIND_PTQ1, ph.KIND_PQ2, ph.KIND_Q8_0])
 def test_gpu_wide_small_matrix_keeps_a_layout_every_order_can_run(ctx, kind):
     """One 64-row tile of 32768 inputs: the small-matrix kernel's LDS cannot hold the
-    pinned PTQ1 terms of such rows, so the tensor keeps the native layout (no width limit)
-    where needed; every contract must run and match the oracle, without a latch."""
+    activation or the pinned PTQ1 terms of such rows, so the input is quantized first and a
+    row-tile kernel (no width limit) takes the tile; every contract must run and match the
+    oracle, without a latch."""
     import oracle
 
     rows, cols = 64, 32768
@@ -789,6 +790,32 @@ def test_gpu_wide_small_matrix_keeps_a_layout_every_order_can_run(ctx, kind):
         act = oracle.quantize_q8_0(x, 2)
         ref = oracle.project_q8(kind, cols, rows, w, act, True, threads=THREADS)
         assert_bits_equal(ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=True), ref, "wide q8 pinned")
+    assert not ctx.faulted
+    ctx.release(wid)
+
+
+@pytest.mark.parametrize("kind,rows,cols", [(ph.KIND_PTQ1, 320 + 5, 17408), (ph.KIND_PQ2, 100, 14336),
+                                            (ph.KIND_Q2_K, 130, 14336), (ph.KIND_Q8_0, 200, 14336),
+                                            (ph.KIND_TQ1_0, 90, 14336), (ph.KIND_TQ2_0, 70, 14336)])
+def test_gpu_wide_rows_few_tiles_every_token_count(ctx, kind, rows, cols):
+    """FFN-down-like widths (14336, 17408 inputs) on a few 64-row tiles, stored tiled: one
+    token takes the row-tile fallback where the split kernel's LDS cannot hold the rows,
+    a few tokens run token by token, and PTQ1 from 16 tokens the prefill GEMM; every
+    output equals the oracle's per-token matvec."""
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=kind + rows)
+    wid = ctx.weight(kind, cols, rows, w)
+    for M in (1, 3, 32):
+        X = synth.activations(cols, seed=M + kind, tokens=M).reshape(M, cols)
+        for pinned in (False, True):
+            ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+            got = ctx.project_f32(wid, rows, X[0], pinned=pinned) if M == 1 else ctx.prefill(wid, rows, X, pinned=pinned)
+            assert_bits_equal(got.reshape(-1), ref.reshape(-1), f"wide kind={kind} {rows}x{cols} M={M} pinned={pinned}")
+    if kind in (ph.KIND_PTQ1, ph.KIND_Q8_0):
+        act = oracle.quantize_q8_0(synth.activations(cols, seed=7), 1)
+        ref = oracle.project_q8(kind, cols, rows, w, act, True, threads=THREADS)
+        assert_bits_equal(ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), pinned=True), ref, "wide q8")
     assert not ctx.faulted
     ctx.release(wid)
 
