@@ -788,7 +788,7 @@ __global__ __launch_bounds__(128) void k_mv_rows2(MvParams p, uint32_t stride) {
     }
 }
 
-// NW wavefronts per 64-row tile (fewer tiles than CUs, prepared activations): wavefront
+// NW wavefronts per 64-row tile (half a tile to four tiles per CU, prepared activations): wavefront
 // k walks the contiguous units [k * nu / NW, (k + 1) * nu / NW); wavefront 0 folds its own
 // units straight into the chain and the others leave their units' terms in LDS (row-major,
 // odd `stride`), which wavefront 0 folds after one barrier in unit order: the unsplit
@@ -2539,8 +2539,11 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
         // Measured, prepared activations (us, split kernel -> spread): 12288x4096 8.6 -> 6.9
         // (pinned 14.0 -> 10.8), 8192x4096 6.7 -> 6.6; fewer tiles or longer rows lose to
         // the split kernel (2048x2048 4.2 -> 4.8, 6144x2048 5.0 -> 5.1, 2048x6144 5.4 -> 7.6).
+        // Rows of up to 64 units from half a tile per CU (against the split kernel below one
+        // tile per CU, the split-pair table kernel above): 10240x5120 10.0 -> 7.3, 12288x5120
+        // 10.1 -> 7.6, 17408x5120 21.3 -> 10.6.
         const uint32_t sgrid = static_cast<uint32_t>(tiles < a.cus ? tiles : a.cus);
-        if (!quant && nmat == 1 && 2 * tiles > a.cus && nu <= 32) {
+        if (!quant && nmat == 1 && 2 * tiles > a.cus && nu <= 64) {
             if (const uint32_t lds = lut_spread_lds<O>(static_cast<uint32_t>(tiles), sgrid, nu)) {
                 hipLaunchKernelGGL((k_mv_rows_lut<O, kLutSpread>), dim3(sgrid), dim3(kLutThreads), lds, a.stream, p,
                                    act);
@@ -2553,7 +2556,10 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
         // 16 units per row, 8 from 8.  Measured (us, split kernel -> N wavefronts), 12288
         // rows x 4096: Q8_0 12.6 -> 12.0, Q2_K 7.4 -> 6.0, PQ2 7.9 -> 6.9, TQ1_0 8.2 -> 6.7,
         // TQ2_0 6.9 -> 5.5; 10240 x 4096 Q8_0 12.2 -> 10.9; 12288 x 2048 Q2_K 5.6 -> 4.2 (8
-        // wavefronts; 4 gave 4.4).
+        // wavefronts; 4 gave 4.4).  One to four tiles per CU: 8 wavefronts per tile, against
+        // the one- or two-wavefront row kernels (us): 17408 x 5120 Q8_0 26.1 -> 24.1, Q2_K 13.0
+        // -> 10.2, PQ2 18.1 -> 11.9; 32768 x 4096 Q2_K 12.4 -> 10.8, PQ2 16.5 -> 11.2 (16
+        // wavefronts per tile lost there: Q2_K 17408 x 5120 13.1).
         auto rowsn = [&]<uint32_t NW>() -> int {
             const uint32_t c1 = nu / NW;
             const uint32_t stride = ((nu - c1) * terms_per_unit<O>()) | 1u;
@@ -2562,8 +2568,8 @@ int launch_op(const MatvecArgs &a, const void *act, float *out) {
                                kTile * stride * sizeof(float), a.stream, p, stride);
             return launch_status();
         };
-        if (!quant && nmat == 1 && tiles < a.cus && 2 * tiles > a.cus && nu >= 8) {
-            const int rc = nu >= 16 ? rowsn.template operator()<16>() : rowsn.template operator()<8>();
+        if (!quant && nmat == 1 && tiles < 4ull * a.cus && 2 * tiles > a.cus && nu >= 8) {
+            const int rc = nu >= 16 && tiles < a.cus ? rowsn.template operator()<16>() : rowsn.template operator()<8>();
             if (rc >= 0) return rc;
         }
     }

@@ -330,14 +330,14 @@ def test_gpu_ptq1_table_decode_matches_oracle(ctx, cols, per_cu):
 
 
 @pytest.mark.parametrize("per_cu4", [3, 6, 14])
-@pytest.mark.parametrize("cols", [384, 4096])
+@pytest.mark.parametrize("cols", [384, 4096, 5120, 8064])
 def test_gpu_ptq1_table_spread_matches_oracle(ctx, cols, per_cu4):
-    """From half a tile to eight tiles per CU, prepared-activation PTQ1 runs table
-    workgroups of one, two or four tiles (per_cu4 / 4 tiles per CU here), each tile's units
-    spread over 16, 8 or 4 wavefronts and their terms folded in unit order from LDS (pinned
-    PTQ1 at 4096 columns only with one tile per workgroup; beyond, its earlier forms):
-    bit-exact in every contract (source, pinned, native-scale pinned Q8_0, and Q8_K), with
-    an odd unit count and a partial last tile."""
+    """From half a tile to eight tiles per CU, prepared-activation PTQ1 rows of up to 64
+    units run table workgroups of one, two or four tiles (per_cu4 / 4 tiles per CU here),
+    each tile's units spread over 16, 8 or 4 wavefronts and their terms folded in unit order
+    from LDS (pinned PTQ1 only where its nine terms per unit fit; beyond, its earlier
+    forms): bit-exact in every contract (source, pinned, native-scale pinned Q8_0, and
+    Q8_K), with odd unit counts (3, 63) and a partial last tile."""
     import oracle
 
     import hiprt
@@ -363,21 +363,23 @@ def test_gpu_ptq1_table_spread_matches_oracle(ctx, cols, per_cu4):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("per_cu4", [3, 6, 15])
 @pytest.mark.parametrize("kind,cols", [(ph.KIND_Q8_0, 2048), (ph.KIND_Q8_0, 4224), (ph.KIND_PQ2, 2048),
                                        (ph.KIND_PQ2, 4224), (ph.KIND_Q2_K, 2048), (ph.KIND_Q2_K, 4352),
                                        (ph.KIND_TQ1_0, 2304), (ph.KIND_TQ1_0, 4096), (ph.KIND_TQ2_0, 2048),
                                        (ph.KIND_TQ2_0, 4352)])
-def test_gpu_rows_n_wavefronts_matches_oracle(ctx, kind, cols):
-    """Between half a tile and one tile per CU, prepared activations of the non-PTQ1
-    formats run 16 wavefronts per tile (8 with 8 to 15 units per row), each walking a
-    contiguous unit range whose terms wavefront 0 folds from LDS in unit order: bit-exact
-    in every contract, with even and odd unit counts and a partial last tile."""
+def test_gpu_rows_n_wavefronts_matches_oracle(ctx, kind, cols, per_cu4):
+    """Between half a tile and four tiles per CU (per_cu4 / 4 here), prepared activations
+    of the non-PTQ1 formats run 16 wavefronts per tile below one tile per CU and 8 from one
+    (8 with 8 to 15 units per row), each walking a contiguous unit range whose terms
+    wavefront 0 folds from LDS in unit order: bit-exact in every contract, with even and
+    odd unit counts and a partial last tile."""
     import oracle
 
     import hiprt
 
     cus = hiprt.cu_count(0)
-    rows = 64 * (3 * cus // 4) + 37
+    rows = 64 * (per_cu4 * cus // 4) + 37
     w = synth.weights(kind, rows, cols, seed=81 + cols) if kind != ph.KIND_PQ2 else \
         synth.pq2_weights(rows, cols, 81 + cols, 4)
     x = synth.activations(cols, seed=82)
