@@ -2957,6 +2957,20 @@ bool skinny_eligible(const MatvecArgs &a) {
     return dispatch(a, [&]<Op O>() { return skinny_supported<O>() ? 1 : 0; }) == 1;
 }
 
+// Two PTQ1 / PQ2 tokens (three PTQ1 tokens from 12288 inputs) of rows of at least 6144 inputs on
+// fewer than two tiles per CU run token by token on the single-token kernels, whose split
+// spreads a long row over lane groups and wavefronts; the batch kernels leave most of their
+// matrix-core width or table workgroup idle there.  Measured (us, f32 input with its
+// quantization; batch kernel -> token by token): PTQ1 5120x17408 49.7 -> 34.5, 4096x14336
+// 29.6 -> 19.1 (three tokens 30.4 -> 26.7), 5120x6144 21.5 -> 17.1; PQ2 4096x14336 25.9 ->
+// 18.1, 5120x17408 37.0 -> 30.6.  Shorter rows lose (PTQ1 6144x5120 16.0 -> 16.4), and so do
+// Q8_0 and Q2_K (4096x14336: 31.4 -> 32.9, 14.2 -> 17.1).
+bool token_by_token(const MatvecArgs &a) {
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile;
+    if (a.w2 || tiles >= 2ull * a.cus || a.cols < 6144 || (a.kind != kPTQ1 && a.kind != kPQ2)) return false;
+    return a.tokens == 2 || (a.tokens == 3 && a.kind == kPTQ1 && a.cols >= 12288);
+}
+
 int launch_matvec_tiled(const MatvecArgs &a) {
     if (a.tile_best) {
         // Only the one-token row-tile path writes the tile maxima (launch_op).
@@ -2966,12 +2980,13 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
-    if (a.act_format != kActF32 && quad_eligible(a))
+    const bool batched = a.act_format != kActF32 && !token_by_token(a);
+    if (batched && quad_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_quad<O>(a, static_cast<uint32_t>(in_stride)); });
-    if (a.act_format != kActF32 && quad_split_eligible(a)) return launch_quad_split(a, static_cast<uint32_t>(in_stride));
-    if (a.act_format != kActF32 && lut_batch_eligible(a))
+    if (batched && quad_split_eligible(a)) return launch_quad_split(a, static_cast<uint32_t>(in_stride));
+    if (batched && lut_batch_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_lut_batch<O>(a, static_cast<uint32_t>(in_stride)); });
-    if (a.act_format != kActF32 && skinny_eligible(a)) {
+    if (batched && skinny_eligible(a)) {
         for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
             const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
             const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;
@@ -2987,7 +3002,7 @@ int launch_matvec_tiled(const MatvecArgs &a) {
         }
         return 0;
     }
-    if (a.act_format != kActF32 && batch_eligible(a)) {
+    if (batched && batch_eligible(a)) {
         for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
             const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
             const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;

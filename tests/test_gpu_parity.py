@@ -801,14 +801,15 @@ def test_gpu_wide_small_matrix_keeps_a_layout_every_order_can_run(ctx, kind):
                                             (ph.KIND_TQ1_0, 90, 14336), (ph.KIND_TQ2_0, 70, 14336)])
 def test_gpu_wide_rows_few_tiles_every_token_count(ctx, kind, rows, cols):
     """FFN-down-like widths (14336, 17408 inputs) on a few 64-row tiles, stored tiled: one
-    token takes the row-tile fallback where the split kernel's LDS cannot hold the rows,
-    a few tokens run token by token, and PTQ1 from 16 tokens the prefill GEMM; every
-    output equals the oracle's per-token matvec."""
+    token takes the split kernel with wider lane groups, or the row-tile fallback where its
+    LDS cannot hold the rows; two or three tokens run token by token (PTQ1, PQ2) or on the
+    batch kernels, and PTQ1 from 16 tokens the prefill GEMM; every output equals the
+    oracle's per-token matvec."""
     import oracle
 
     w = synth.weights(kind, rows, cols, seed=kind + rows)
     wid = ctx.weight(kind, cols, rows, w)
-    for M in (1, 3, 32):
+    for M in (1, 2, 3, 32):
         X = synth.activations(cols, seed=M + kind, tokens=M).reshape(M, cols)
         for pinned in (False, True):
             ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
