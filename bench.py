@@ -420,10 +420,10 @@ def bench_matvec_kernel(ctx: ph.Context, kind: int, rows: int, cols: int, launch
 # ---- config 2: the tiled prefill GEMM ----------------------------------------------------
 
 def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, reps: int = 20,
-                  pinned: bool = False):
+                  pinned: bool = False, kind: int = ph.KIND_PTQ1):
     """The prefill GEMM (quantization prep + GEMM) in the source or the pinned contract."""
-    w = synth.ptq1_weights(rows, cols, seed=9)
-    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
+    w = synth.weights(kind, rows, cols, seed=9)
+    wid = ctx.weight(kind, cols, rows, w)
     X = hiprt.DeviceBuffer.from_numpy(synth.activations(cols, seed=10, tokens=M))
     out = hiprt.DeviceBuffer(4 * rows * M)
     stream = ctx.stream()
@@ -442,7 +442,9 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
     valu_ceiling = PREFILL_OPS_PER_BLOCK * 4 / (PREFILL_VALU_PER_BLOCK * 4) * CUS * ENGINE_HZ
     r = {"M": M, "contract": "pinned" if pinned else "source", "ms": t * 1e3, "TOPS": ops / t / 1e12,
          "frac_int8_peak": ops / t / PEAK_I8, "frac_f16_peak": ops / t / PEAK_F16}
-    if not pinned:  # the instruction-mix ceiling was counted for the source kernel
+    if kind != ph.KIND_PTQ1:
+        r.update(kind=kind, rows=rows, cols=cols)
+    elif not pinned:  # the instruction-mix ceiling was counted for the source kernel
         r.update(valu_issue_ceiling_TOPS=valu_ceiling / 1e12, frac_valu_ceiling=ops / t / valu_ceiling)
     return r
 
@@ -586,7 +588,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="",
-                    help="comma-separated token counts, each optionally ':pinned': time only the prefill GEMM")
+                    help="comma-separated token counts, each optionally ':pinned' and ':q2k' (Q2_K weights, "
+                         "else PTQ1): time only the prefill GEMM")
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
@@ -614,8 +617,9 @@ def main() -> int:
         return 0
     if args.prefill_only or args.matvec_only or args.ffn_only or args.floor_only:
         for spec in filter(None, args.prefill_only.split(",")):
-            M, _, contract = spec.partition(":")  # "2048" or "2048:pinned"
-            print(json.dumps(bench_prefill(ctx, int(M), pinned=contract == "pinned")), flush=True)
+            M, *flags = spec.split(":")  # "2048", "2048:pinned", "2048:q2k", "2048:pinned:q2k"
+            kind = ph.KIND_Q2_K if "q2k" in flags else ph.KIND_PTQ1
+            print(json.dumps(bench_prefill(ctx, int(M), pinned="pinned" in flags, kind=kind)), flush=True)
         for spec in filter(None, args.matvec_only.split(",")):
             kind, rows, cols, *tok = (int(v) for v in spec.split(":"))
             print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols, tokens=tok[0] if tok else 1)), flush=True)
@@ -670,6 +674,11 @@ def main() -> int:
                 r = bench_prefill(ctx, M, pinned=pinned)
                 log(f"prefill {r['contract']} M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
                 extras["prefill_ptq1_6144x2048"].append(r)
+        extras["prefill_q2k_6144x2048"] = []
+        for M in (128, 512, 2048):
+            r = bench_prefill(ctx, M, kind=ph.KIND_Q2_K)
+            log(f"prefill Q2_K M={M}: {r['ms']:.3f} ms, {r['TOPS']:.2f} TOPS")
+            extras["prefill_q2k_6144x2048"].append(r)
     ctx.close()
     cpu = None
     if not args.no_cpu:

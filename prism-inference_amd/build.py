@@ -21,7 +21,7 @@ OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libprism_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["quantize.hip", "matvec.hip", "mv_tiled.hip", "prefill.hip", "ffn.hip", "decode.hip", "static_scratch.hip",
+SOURCES = ["quantize.hip", "matvec.hip", "mv_tiled.hip", "prefill.hip", "prefill_k.hip", "ffn.hip", "decode.hip", "static_scratch.hip",
            "runtime.cpp", "decoder.cpp", "gguf.cpp"]
 
 FLAGS = [

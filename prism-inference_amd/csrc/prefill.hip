@@ -651,7 +651,8 @@ constexpr uint32_t kSplitMaxTokens = 128;
 
 }  // namespace
 
-size_t prefill_scratch_bytes(uint64_t cols, uint32_t tokens) {
+size_t prefill_scratch_bytes(uint32_t kind, uint64_t cols, uint32_t tokens) {
+    if (kind != kPTQ1) return prefill_k_scratch_bytes(cols, tokens);
     const size_t Mp = padded_tokens(tokens);
     return ((Mp * cols * 2 + 255) & ~size_t(255)) + Mp * (cols / 32) * 4;
 }
@@ -662,6 +663,7 @@ size_t prefill_scratch_bytes(uint64_t cols, uint32_t tokens) {
 constexpr uint32_t kPinnedGemmMinTokens = 32;
 
 bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens) {
+    if (kind != kPTQ1) return prefill_k_supported(kind, cols, rows, tokens);
     // The token codes are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols / 128 * 8u * padded_tokens(tokens) * 32u;
     if (pinned && tokens < kPinnedGemmMinTokens) return false;
@@ -669,8 +671,9 @@ bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, 
            (rows * (cols / 128) * 28) < (1ull << 40) && code_bytes < (1ull << 31);
 }
 
-int launch_prefill(const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M, int pinned,
-                   float *out, void *scratch, int *err, hipStream_t s) {
+int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
+                   int pinned, float *out, void *scratch, int *err, hipStream_t s) {
+    if (kind != kPTQ1) return launch_prefill_k(kind, w_tiled, cols, rows, x, M, pinned, out, scratch, err, s);
     const uint32_t K = static_cast<uint32_t>(cols), Mp = padded_tokens(M);
     if (static_cast<uint64_t>(K / 128) * 8u * Mp * 32u >= (1ull << 31)) return kLaunchUnsupported;
     _Float16 *xh = static_cast<_Float16 *>(scratch);

@@ -16,7 +16,8 @@ using namespace prism::rt;
 namespace {
 
 // Token count from which f32 projections of PTQ1 weights run as one tiled-prefill GEMM
-// (prefill_supported has the last word: its own threshold for the pinned contract).
+// (prefill_supported has the last word: its own thresholds for the pinned contract and for
+// Q2_K / PQ2).
 constexpr uint32_t kPrefillMinTokens = 16;
 
 // Quantize device floats with the contract matvec_into would use, then project.  `role`
@@ -27,9 +28,10 @@ int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t 
     Scratch &scr = sc ? *sc : grow;
     if (w.tiled && tokens >= kPrefillMinTokens && prefill_supported(w.kind, w.cols, w.rows, pinned, tokens)) {
         void *pre = nullptr;
-        int rc = scr.get(c->pre, prefill_scratch_bytes(w.cols, tokens), &pre);
+        int rc = scr.get(c->pre, prefill_scratch_bytes(w.kind, w.cols, tokens), &pre);
         if (rc) return rc;
-        rc = launch_result(c, launch_prefill(w.dev, w.cols, w.rows, x, tokens, pinned, out, pre, c->err, s), "prefill launch");
+        rc = launch_result(c, launch_prefill(w.kind, w.dev, w.cols, w.rows, x, tokens, pinned, out, pre, c->err, s),
+                           "prefill launch");
         // The residual joins after the projection, one binary32 add per output (as the
         // row kernels do in their epilogue).
         if (!rc && residual)

@@ -201,13 +201,15 @@ def test_gpu_caller_owned_tiled_rejects_bad_sizes(ctx):
     with pytest.raises(ph.PrismError) as e:
         ctx.weight_tiled_device(ph.KIND_PTQ1, cols, rows, small)
     assert e.value.code == ph.ERR_INVALID_INPUT
-    # one 64-row tile of 32768 Q8_0 inputs has no tiled layout (the small-matrix kernel's
-    # LDS cannot hold its activation): size 0, and the repack refuses it
-    assert ctx.tiled_bytes(ph.KIND_Q8_0, 32768, 64) == 0
+    # Every width has a tiled layout (one 64-row tile of 32768 Q8_0 inputs: the native bytes,
+    # no padding rows), and the repack refuses a destination of another size; only a tensor
+    # whose 64-row tile passes 2 GiB (32-bit in-tile offsets) has none.
+    assert ctx.tiled_bytes(ph.KIND_Q8_0, 32768, 64) == 64 * (32768 // 32) * 34
     q8 = DeviceBuffer.from_numpy(synth.q8_0_weights(64, 32768, seed=2))
     with pytest.raises(ph.PrismError) as e:
         ctx.repack_tiled(ph.KIND_Q8_0, 32768, 64, q8, small)
-    assert e.value.code == ph.ERR_UNSUPPORTED
+    assert e.value.code == ph.ERR_INVALID_INPUT
+    assert ctx.tiled_bytes(ph.KIND_Q8_0, 32 << 20, 64) == 0
     assert not ctx.faulted
 
 

@@ -624,6 +624,32 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2])
+@pytest.mark.parametrize("rows,cols,M", [(200, 2048, 48), (64, 256, 49), (130, 1024, 300), (37, 512, 129),
+                                         (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64)])
+def test_gpu_k_prefill_gemm_equals_per_token_matvec(ctx, kind, rows, cols, M):
+    """Q2_K and PQ2 (Q8_K activations) prefill from 48 tokens runs as one int8-MFMA GEMM, 32
+    or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted codes,
+    msum from a binary16 product of the sub-block mins and sums, the two outer products of
+    the token and row scales; PQ2: each 128-element block's integer dot on signed codes and
+    its outer product of scales, folded unfused or fused by contract.  Every token row
+    equals the reference's per-token matvec bit for bit, in both contracts (partial row
+    tiles, a single-unit row, padding tokens, an all-zero token, the XCD-major grid)."""
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=rows + M)
+    X = synth.activations(cols, seed=M, tokens=M)
+    X[3] *= 1e-3  # a token with small scales
+    X[5] = 0.0    # an all-zero token
+    wid = ctx.weight(kind, cols, rows, w)
+    for pinned in (False, True):
+        ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
+        assert_bits_equal(ctx.prefill(wid, rows, X, pinned=pinned), ref,
+                          f"gemm kind={kind} {rows}x{cols} M={M} pinned={pinned}")
+    assert_bits_equal(ctx.mul_mat(wid, rows, X), oracle.prefill(kind, cols, rows, w, X, False, THREADS), "mul_mat")
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("kind,rows,cols", [(ph.KIND_Q2_K, 151936, 4096), (ph.KIND_Q8_0, 32768, 4096),
                                          (ph.KIND_PQ2, 32768, 4096), (ph.KIND_TQ2_0, 65536, 4096)])
 def test_gpu_large_matvec_sampled_rows_match_oracle(ctx, kind, rows, cols):
