@@ -588,8 +588,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="",
-                    help="comma-separated token counts, each optionally ':pinned' and ':q2k' or ':pq2' (Q2_K "
-                         "or PQ2 weights, else PTQ1): time only the prefill GEMM")
+                    help="comma-separated token counts, each optionally ':pinned' and ':q2k', ':pq2' or ':q8' "
+                         "(Q2_K, PQ2 or Q8_0 weights, else PTQ1): time only the prefill GEMM")
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
@@ -618,7 +618,8 @@ def main() -> int:
     if args.prefill_only or args.matvec_only or args.ffn_only or args.floor_only:
         for spec in filter(None, args.prefill_only.split(",")):
             M, *flags = spec.split(":")  # "2048", "2048:pinned", "2048:q2k", "2048:pinned:pq2"
-            kind = ph.KIND_Q2_K if "q2k" in flags else ph.KIND_PQ2 if "pq2" in flags else ph.KIND_PTQ1
+            kind = {"q2k": ph.KIND_Q2_K, "pq2": ph.KIND_PQ2, "q8": ph.KIND_Q8_0}.get(next(
+                (f for f in flags if f != "pinned"), ""), ph.KIND_PTQ1)
             print(json.dumps(bench_prefill(ctx, int(M), pinned="pinned" in flags, kind=kind)), flush=True)
         for spec in filter(None, args.matvec_only.split(",")):
             kind, rows, cols, *tok = (int(v) for v in spec.split(":"))

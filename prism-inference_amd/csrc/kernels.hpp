@@ -79,7 +79,7 @@ int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols,
 // Tiled-prefill GEMM: quantizes x[M][cols] once and multiplies it by the tiled weights on
 // the matrix cores; every output row is bit-identical to its own per-token matvec.  PTQ1
 // in either contract (the pinned one from kPinnedGemmMinTokens tokens) on the f16 matrix
-// cores (prefill.hip); Q2_K and PQ2 (Q8_K activations) on the int8 matrix cores
+// cores (prefill.hip); Q2_K and PQ2 (Q8_K activations) and Q8_0 on the int8 matrix cores
 // (prefill_k.hip).
 bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens);
 size_t prefill_scratch_bytes(uint32_t kind, uint64_t cols, uint32_t tokens);

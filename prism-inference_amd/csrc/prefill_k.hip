@@ -1,5 +1,5 @@
-// prefill_k.hip -- tiled prefill GEMM for Q2_K and PQ2 weights (Q8_K activations) on the int8
-// matrix cores (gfx950).
+// prefill_k.hip -- tiled prefill GEMM for Q2_K and PQ2 weights (Q8_K activations) and Q8_0
+// weights (Q8_0 activations) on the int8 matrix cores (gfx950).
 //
 // dot_q2_k_block (src/kernels/kquants.rs:162-197, row order :346-430), per 256-element
 // unit u of a row and a token's Q8_K block:
@@ -29,6 +29,10 @@
 // Y = fma(d, s, Y) (fused, the pinned contract) or Y + fl(d * s).  The block's integer
 // dot is four v_mfma_i32_32x32x32_i8 on the signed codes c - 1, d one outer product.
 //
+// dot_legacy (src/kernels.rs:1204-1248), per 32-element block b of a Q8_0 row and the
+// token's Q8_0 block b: Y = Y + fl(fl(ws_b * as_b) * float(I_b)), I_b one K-step on the codes
+// as they are (no decode), the scale product one outer product.
+//
 // Work split: a workgroup of four wavefronts owns 128 weight rows (two 64-row tiles) and
 // NT = 32 * CT tokens, and walks the rows' 256-element units (one Q8_K block each; two
 // PQ2 blocks).  Wavefront w owns 32 rows and decodes them itself into the int8 operand
@@ -37,6 +41,8 @@
 // in exactly that order, stream unit by unit into a double-buffered LDS ring with
 // direct-to-LDS buffer loads, with the tokens' scales and sub-block sums beside them; one
 // barrier per unit hands a buffer from the loads to the readers and back.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "quant_dev.hpp"
@@ -73,13 +79,16 @@ __host__ __device__ constexpr uint32_t q2k_elem(uint32_t s, uint32_t h, uint32_t
 __host__ __device__ constexpr uint32_t pq2_elem(uint32_t s, uint32_t h, uint32_t i) {
     return 128 * (s >> 2) + 16 * (4 * ((s >> 1) & 1) + 2 * h + (s & 1)) + i;
 }
+// Q8_0: K-step s is the 32-element block s of the unit, half h its codes 16h .. 16h+15 (tiled
+// code piece 2 * (s % 4) + h of tiled unit 2u + s / 4), in their own order: no decode.
 
 // ---- activation prep ------------------------------------------------------------------
 // A workgroup of TOK wavefronts quantizes TOK consecutive tokens (one each, 1024 inputs =
-// four Q8_K blocks; pinned selects pinned_q8k_integer's rounding), then writes, per unit u
-// and token t (tokens padded to Mp with zeros):
+// four Q8_K blocks, pinned selecting pinned_q8k_integer's rounding; for Q8_0 weights 32 Q8_0
+// blocks in the source or pinned generic contract), then writes, per 256-element unit u and
+// token t (tokens padded to Mp with zeros):
 //   xq[u][s][h][t][16 bytes]   codes in the kind's operand order (16 slots of 16 bytes),
-//   as[u][t]                   the block scale,
+//   as[u][t]                   the Q8_K block scale (Q8_0: as[u][s][t], the 8 block scales),
 //   bs[u][h][t][8 x f16]       Q2_K only: the sums of sub-blocks 8h .. 8h+7,
 // consecutive threads taking consecutive tokens of one slot, so each slot's TOK tokens
 // leave as one contiguous run.  A quantizer error is raised and the wavefront carries on.
@@ -88,14 +97,20 @@ __global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const float *__rest
                                                              uint32_t K, int pinned, uint8_t *__restrict__ xq,
                                                              float *__restrict__ as, _Float16 *__restrict__ bs,
                                                              int *__restrict__ err) {
-    __shared__ Q8KBlock blk[TOK][4];
+    constexpr bool kQ8 = KIND == kQ8_0;
+    using Blk = typename std::conditional<kQ8, Q8Block[TOK][32], Q8KBlock[TOK][4]>::type;
+    __shared__ Blk blk;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t chunks = (K + 1023) / 1024;
     const uint32_t c = blockIdx.x % chunks, tb = blockIdx.x / chunks * TOK;
-    const uint32_t k0 = c * 1024, nb = (K - k0 < 1024 ? K - k0 : 1024) / kUnit;  // 1..4 blocks
+    const uint32_t k0 = c * 1024, nb = (K - k0 < 1024 ? K - k0 : 1024) / kUnit;  // 1..4 units
     const uint32_t t = tb + wave;
     if (t < M) {
-        const int e = q8k_blocks_wave(x + static_cast<size_t>(t) * K + k0, nb, pinned, blk[wave], lane);
+        int e;
+        if constexpr (kQ8)  // the source (0) or pinned generic (1) contract, 32-element blocks
+            e = q8_0_blocks_wave(x + static_cast<size_t>(t) * K + k0, nb * 8, pinned ? 1 : 0, blk[wave], lane);
+        else
+            e = q8k_blocks_wave(x + static_cast<size_t>(t) * K + k0, nb, pinned, blk[wave], lane);
         if (e && lane == 0) raise_error(err, e);
     }
     __syncthreads();
@@ -105,10 +120,13 @@ __global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const float *__rest
         const uint32_t s = q >> 1, h = q & 1u;
         uint32_t v[4] = {0, 0, 0, 0};
         if (tb + w < M) {
-            const uint8_t *vals = reinterpret_cast<const uint8_t *>(blk[w][ub].values);
+            const uint8_t *vals = kQ8 ? reinterpret_cast<const uint8_t *>(blk[w][8 * ub + s].values) + 16 * h
+                                      : reinterpret_cast<const uint8_t *>(blk[w][ub].values);
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) {
-                if constexpr (KIND == kQ2_K) {
+                if constexpr (kQ8) {
+                    v[j] = *reinterpret_cast<const uint32_t *>(vals + 4 * j);
+                } else if constexpr (KIND == kQ2_K) {
                     v[j] = *reinterpret_cast<const uint32_t *>(vals + q2k_elem(s, h, j));
                 } else {
                     const uint8_t *e = vals + pq2_elem(s, h, j);  // elements e, e+4, e+8, e+12
@@ -136,7 +154,12 @@ __global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const float *__rest
                 make_uint4(p[0], p[1], p[2], p[3]);
         }
     }
-    if (tid < nb * TOK) {
+    if constexpr (kQ8) {
+        for (uint32_t i = tid; i < nb * 8 * TOK; i += 64 * TOK) {  // as[u][s][t]: the 8 block scales
+            const uint32_t w = i % TOK, b = i / TOK;
+            as[(static_cast<size_t>(u0) * 8 + b) * Mp + tb + w] = tb + w < M ? blk[w][b].scale : 0.0f;
+        }
+    } else if (tid < nb * TOK) {
         const uint32_t w = tid % TOK, ub = tid / TOK;
         as[static_cast<size_t>(u0 + ub) * Mp + tb + w] = tb + w < M ? blk[w][ub].scale : 0.0f;
     }
@@ -159,6 +182,11 @@ struct RawK<kPQ2> {
     u32x2 c[2][2];
     uint32_t d[2];
 };
+template <>
+struct RawK<kQ8_0> {
+    u32x4 c[8];    // codes 16h .. 16h+15 of the unit's eight blocks
+    u32x2 sc[2];   // the eight binary16 block scales
+};
 template <uint32_t KIND>
 __device__ __forceinline__ void load_unit_k(__amdgpu_buffer_rsrc_t rs, uint32_t u, uint32_t trp, uint32_t row,
                                             uint32_t h, RawK<KIND> &w) {
@@ -168,6 +196,14 @@ __device__ __forceinline__ void load_unit_k(__amdgpu_buffer_rsrc_t rs, uint32_t 
         for (uint32_t p = 0; p < 4; ++p) w.c[p] = bload2(rs, seg + 16u * p * trp + 16u * row + 8u * h);
         w.sc = bload4(rs, seg + 64u * trp + 16u * row);
         w.dm = bload1(rs, seg + 80u * trp + 4u * row);
+    } else if constexpr (KIND == kQ8_0) {
+#pragma unroll
+        for (uint32_t b = 0; b < 2; ++b) {
+            const uint32_t seg = (2 * u + b) * trp * 136u;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) w.c[4 * b + j] = bload4(rs, seg + 16u * (2 * j + h) * trp + 16u * row);
+            w.sc[b] = bload2(rs, seg + 128u * trp + 8u * row);
+        }
     } else {
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b) {
@@ -196,8 +232,9 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                                                     uint32_t xcd_major, float *__restrict__ out,
                                                     int *__restrict__ err) {
     constexpr uint32_t NT = 32 * CT;
-    constexpr bool kQ2 = KIND == kQ2_K;
+    constexpr bool kQ2 = KIND == kQ2_K, kQ8 = KIND == kQ8_0;
     constexpr uint32_t kSums = kQ2 ? 2 : 0;  // Q2_K: two runs of sub-block sums per unit
+    constexpr uint32_t kScl = kQ8 ? 8 : 1;   // scale runs per unit (Q8_0: one per block)
     // Ring buffers (separate objects, named statically below, so the compiler can tell a
     // read of one from the direct-to-LDS loads in flight into the other): the codes
     // [s][h][token][16 bytes] (each half-wavefront's read covers 512 contiguous bytes),
@@ -206,9 +243,10 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
     __shared__ __attribute__((aligned(16))) uint8_t act1[8][2][NT * 16];
     __shared__ __attribute__((aligned(16))) uint8_t bsm0[kQ2 ? 2 : 1][kQ2 ? NT * 16 : 16];
     __shared__ __attribute__((aligned(16))) uint8_t bsm1[kQ2 ? 2 : 1][kQ2 ? NT * 16 : 16];
-    __shared__ __attribute__((aligned(16))) float scl0[NT];
-    __shared__ __attribute__((aligned(16))) float scl1[NT];
+    __shared__ __attribute__((aligned(16))) float scl0[kScl][NT];
+    __shared__ __attribute__((aligned(16))) float scl1[kScl][NT];
     using Bsm = uint8_t[kQ2 ? 2 : 1][kQ2 ? NT * 16 : 16];
+    using Scl = float[kScl][NT];
     const uint32_t lane = threadIdx.x & 63, r32 = lane & 31, h = lane >> 5;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Workgroups go to the eight XCDs round-robin in dispatch order (x fastest), each with
@@ -220,7 +258,7 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
     const uint32_t tile = 2 * bx + (wave >> 1), hw = wave & 1;
     const uint32_t tiles = (rows + kTile - 1) / kTile;
     const uint32_t t0 = by * NT;
-    const uint32_t row_bytes = nu * (kQ2 ? 84u : 68u);
+    const uint32_t row_bytes = nu * (kQ2 ? 84u : kQ8 ? 272u : 68u);
     uint32_t trows = 0;
     if (tile < tiles) {
         const uint32_t left = rows - tile * kTile;
@@ -232,13 +270,13 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
         make_rsrc(W + static_cast<size_t>(active ? tile : 0) * kTile * row_bytes, active ? trp * row_bytes : 0u);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, nu * 256u * Mp);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bs, kQ2 ? nu * 32u * Mp : 0u);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(as, nu * 4u * Mp);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(as, nu * 4u * kScl * Mp);
     const uint32_t row = 32 * hw + r32, out0 = 32 * hw + 4 * h;  // tile rows
 
     // Unit u's token data -> LDS: 16 code runs (and Q2_K's 2 sum runs) of NT * 16 bytes and
     // NT scales, each contiguous in the prepared arrays; one wavefront instruction moves 64
     // tokens' 16 bytes (lanes past a short run idle).
-    auto stage = [&](uint32_t u, uint8_t (&act)[8][2][NT * 16], Bsm &bsm, float (&scl)[NT]) {
+    auto stage = [&](uint32_t u, uint8_t (&act)[8][2][NT * 16], Bsm &bsm, Scl &scl) {
         constexpr uint32_t per = (NT + 63) / 64;  // instructions per run
 #pragma unroll
         for (uint32_t k = wave; k < (16 + kSums) * per; k += 4) {
@@ -254,12 +292,15 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                 }
             }
         }
-        if (wave == 3) {
+        // Scale run r by wavefront 3 - r % 4.
+#pragma unroll
+        for (uint32_t r = 0; r < kScl; ++r) {
+            if (wave != 3 - r % 4) continue;
 #pragma unroll
             for (uint32_t c = 0; c < per; ++c)
                 if (64 * c + lane < NT)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(&scl[64 * c]), 4,
-                                                             (u * Mp + t0 + 64 * c + lane) * 4u, 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(&scl[r][64 * c]), 4,
+                                                             ((u * kScl + r) * Mp + t0 + 64 * c + lane) * 4u, 0, 0, 0);
         }
     };
 
@@ -274,11 +315,12 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
     if (active) load_unit_k<KIND>(rw, 0, trp, row, h, w);
     wait_vmcnt0();
     lds_barrier();
-    auto unit = [&](uint32_t u, const uint8_t (&act)[8][2][NT * 16], const Bsm &bsm, const float (&scl)[NT],
-                    uint8_t (&act_n)[8][2][NT * 16], Bsm &bsm_n, float (&scl_n)[NT]) {
+    auto unit = [&](uint32_t u, const uint8_t (&act)[8][2][NT * 16], const Bsm &bsm, const Scl &scl,
+                    uint8_t (&act_n)[8][2][NT * 16], Bsm &bsm_n, Scl &scl_n) {
         u32x4 aw[8];  // the weight operand of each K-step
         v8h mn;       // Q2_K: min_g of sub-blocks 8h .. 8h+7
         float d0 = 0.0f, d1 = 0.0f;  // Q2_K: d, dmin; PQ2: the two blocks' scales (half 0; zero in half 1)
+        u32x2 wsc[2];                // Q8_0: the eight block scales
         if (active) {
             if constexpr (kQ2) {
                 uint32_t m[16];  // sc_g in both 16-bit lanes
@@ -300,6 +342,11 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                     mn[k] = static_cast<_Float16>(static_cast<float>((w.sc[2 * h + (k >> 2)] >> (8 * (k & 3) + 4)) & 15u));
                 d0 = h ? 0.0f : h2f(w.dm & 0xffffu);
                 d1 = h ? 0.0f : h2f(w.dm >> 16);
+            } else if constexpr (kQ8) {
+#pragma unroll
+                for (uint32_t s = 0; s < 8; ++s) aw[s] = w.c[s];
+                wsc[0] = w.sc[0];
+                wsc[1] = w.sc[1];
             } else {
                 // Codes 0..2 -> signed bytes c - 1: +0x7f per byte (no carry out of a byte),
                 // then the sign bit flipped.
@@ -350,7 +397,7 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
                     const uint32_t tok = 32 * ct + r32;
-                    const float a = h ? 0.0f : scl[tok];
+                    const float a = h ? 0.0f : scl[0][tok];
                     const v16f f1 = __builtin_amdgcn_mfma_f32_32x32x2f32(d0, a, v16f{}, 0, 0, 0);  // fl(as * d)
                     const v16f f2 = __builtin_amdgcn_mfma_f32_32x32x2f32(d1, a, v16f{}, 0, 0, 0);  // fl(as * dmin)
                     const v8h bsum = *reinterpret_cast<const v8h *>(&bsm[h][tok * 16]);
@@ -358,6 +405,28 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
                         o[ct][r] = o[ct][r] + (f1[r] * static_cast<float>(is[ct][r]) - f2[r] * ms[r]);
+                }
+            } else if constexpr (kQ8) {
+                // dot_legacy's chain, block by block: Y = Y + fl(fl(ws_s * as_s) * float(I_s)),
+                // I_s one K-step.
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const float ws = h ? 0.0f : h2f((wsc[s >> 2][(s >> 1) & 1] >> (16 * (s & 1))) & 0xffffu);
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct) {
+                        // Read by every lane: a branch around the read (lanes of half 1 need
+                        // none) lets the compiler sink the chain below all eight blocks' MFMAs,
+                        // whose results then fill the registers.
+                        const float sa = scl[s][32 * ct + r32];
+                        const float a = h ? 0.0f : sa;
+                        const v16f dd = __builtin_amdgcn_mfma_f32_32x32x2f32(ws, a, v16f{}, 0, 0, 0);
+                        const v16i is = kstep(s, ct, v16i{});
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[ct][r] = o[ct][r] + dd[r] * static_cast<float>(is[r]);
+                    }
+                    // One block's products at a time (measured: 2048 tokens 158.8 against 166.4 us
+                    // with the scheduler free to issue later blocks' MFMAs early).
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
                 // Per 128-element block b (K-steps 4b .. 4b+3): I_b and fl(ws_b * as).
@@ -373,7 +442,7 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                     }
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
-                    const float a = h ? 0.0f : scl[32 * ct + r32];
+                    const float a = h ? 0.0f : scl[0][32 * ct + r32];
 #pragma unroll
                     for (int b = 0; b < 2; ++b) {
                         const v16f dd = __builtin_amdgcn_mfma_f32_32x32x2f32(b ? d1 : d0, a, v16f{}, 0, 0, 0);
@@ -426,11 +495,11 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens) {
     const size_t Mp = padded_tokens(tokens), nu = cols / kUnit;
-    return align256(Mp * cols) + align256(nu * Mp * 4) + nu * Mp * 32;
+    return align256(Mp * cols) + align256(nu * Mp * 4 * 8) + nu * Mp * 32;
 }
 
-// Tokens from which Q2_K and PQ2 (Q8_K activations) take the GEMM rather than the skinny
-// kernel (16 tokens per launch).  Measured, Q2_K 6144 x 2048 (us, skinny kernel launches plus
+// Tokens from which Q2_K, PQ2 (Q8_K activations) and Q8_0 take the GEMM rather than the
+// skinny kernel (16 tokens per launch).  Measured, Q2_K 6144 x 2048 (us, skinny kernel launches plus
 // the quantization against prep + GEMM): 16 tokens 9 / 16.3, 32 tokens 14 / 17.4, 64 tokens 24 /
 // 17.4, 2048 tokens 640 / 93.8.
 constexpr uint32_t kGemmMinTokens = 48;
@@ -438,7 +507,7 @@ constexpr uint32_t kGemmMinTokens = 48;
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens) {
     // Codes, sums and scales are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols * padded_tokens(tokens);
-    return (kind == kQ2_K || kind == kPQ2) && cols % kUnit == 0 && cols <= 65536 && rows > 0 &&
+    return (kind == kQ2_K || kind == kPQ2 || kind == kQ8_0) && cols % kUnit == 0 && cols <= 65536 && rows > 0 &&
            rows < (1ull << 31) && code_bytes < (1ull << 31) && tokens >= kGemmMinTokens;
 }
 
@@ -449,12 +518,14 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     uint8_t *base = static_cast<uint8_t *>(scratch);
     uint8_t *xq = base;
     float *as = reinterpret_cast<float *>(base + align256(static_cast<size_t>(Mp) * K));
-    _Float16 *bs = reinterpret_cast<_Float16 *>(reinterpret_cast<uint8_t *>(as) + align256(static_cast<size_t>(nu) * Mp * 4));
+    _Float16 *bs = reinterpret_cast<_Float16 *>(reinterpret_cast<uint8_t *>(as) + align256(static_cast<size_t>(nu) * Mp * 4 * 8));
     constexpr uint32_t kTok = 4;
     static_assert(kTokAlign % kTok == 0, "the prep takes whole token groups");
     const dim3 pgrid(Mp / kTok * ((K + 1023) / 1024)), pblock(64 * kTok);
     if (kind == kQ2_K)
         hipLaunchKernelGGL((k_prefill_k_prep<kQ2_K, kTok>), pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
+    else if (kind == kQ8_0)
+        hipLaunchKernelGGL((k_prefill_k_prep<kQ8_0, kTok>), pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
     else
         hipLaunchKernelGGL((k_prefill_k_prep<kPQ2, kTok>), pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
     if (const int e = launch_status()) return e;
@@ -463,7 +534,9 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     const uint32_t R = static_cast<uint32_t>(rows);
     // Tokens per workgroup (measured, Q2_K 6144 x 2048, us): 64 from 1024 tokens (2048: 93.4
     // against 97.4 with 32; 4096: 184.3 / 200.4), 32 below (128 tokens: 18.0 / 22.3).
-    const uint32_t nt = M > 512 ? 64 : 32, groups = Mp / nt;
+    // Q8_0 keeps 32 (2048 tokens: 158.8 us against 156.4 with 64, whose chain operands take
+    // two wavefronts per SIMD instead of three).
+    const uint32_t nt = M > 512 && kind != kQ8_0 ? 64 : 32, groups = Mp / nt;
     const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
     const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
     auto go = [&](auto kernel) {
@@ -471,6 +544,8 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     };
     if (kind == kQ2_K)
         nt == 64 ? go(k_prefill_kq<kQ2_K, 2, false>) : go(k_prefill_kq<kQ2_K, 1, false>);
+    else if (kind == kQ8_0)
+        go(k_prefill_kq<kQ8_0, 1, false>);
     else if (pinned)
         nt == 64 ? go(k_prefill_kq<kPQ2, 2, true>) : go(k_prefill_kq<kPQ2, 1, true>);
     else

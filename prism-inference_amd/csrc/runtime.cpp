@@ -17,7 +17,7 @@ namespace {
 
 // Token count from which f32 projections of PTQ1 weights run as one tiled-prefill GEMM
 // (prefill_supported has the last word: its own thresholds for the pinned contract and for
-// Q2_K / PQ2).
+// Q2_K / PQ2 / Q8_0).
 constexpr uint32_t kPrefillMinTokens = 16;
 
 // Quantize device floats with the contract matvec_into would use, then project.  `role`

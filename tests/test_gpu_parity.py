@@ -624,17 +624,18 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     ctx.release(wid)
 
 
-@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2])
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0])
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 48), (64, 256, 49), (130, 1024, 300), (37, 512, 129),
                                          (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64)])
 def test_gpu_k_prefill_gemm_equals_per_token_matvec(ctx, kind, rows, cols, M):
-    """Q2_K and PQ2 (Q8_K activations) prefill from 48 tokens runs as one int8-MFMA GEMM, 32
-    or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted codes,
-    msum from a binary16 product of the sub-block mins and sums, the two outer products of
-    the token and row scales; PQ2: each 128-element block's integer dot on signed codes and
-    its outer product of scales, folded unfused or fused by contract.  Every token row
-    equals the reference's per-token matvec bit for bit, in both contracts (partial row
-    tiles, a single-unit row, padding tokens, an all-zero token, the XCD-major grid)."""
+    """Q2_K and PQ2 (Q8_K activations) and Q8_0 prefill from 48 tokens runs as one int8-MFMA
+    GEMM, 32 or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted
+    codes, msum from a binary16 product of the sub-block mins and sums, the two outer products
+    of the token and row scales; PQ2: each 128-element block's integer dot on signed codes and
+    its outer product of scales, folded unfused or fused by contract; Q8_0: each 32-element
+    block's dot and scale product, folded block by block.  Every token row equals the
+    reference's per-token matvec bit for bit, in both contracts (partial row tiles, a
+    single-unit row, padding tokens, an all-zero token, the XCD-major grid)."""
     import oracle
 
     w = synth.weights(kind, rows, cols, seed=rows + M)
