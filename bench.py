@@ -442,7 +442,7 @@ def bench_prefill(ctx: ph.Context, M: int, rows: int = 6144, cols: int = 2048, r
     valu_ceiling = PREFILL_OPS_PER_BLOCK * 4 / (PREFILL_VALU_PER_BLOCK * 4) * CUS * ENGINE_HZ
     r = {"M": M, "contract": "pinned" if pinned else "source", "ms": t * 1e3, "TOPS": ops / t / 1e12,
          "frac_int8_peak": ops / t / PEAK_I8, "frac_f16_peak": ops / t / PEAK_F16}
-    if kind != ph.KIND_PTQ1:
+    if kind != ph.KIND_PTQ1 or (rows, cols) != (6144, 2048):
         r.update(kind=kind, rows=rows, cols=cols)
     elif not pinned:  # the instruction-mix ceiling was counted for the source kernel
         r.update(valu_issue_ceiling_TOPS=valu_ceiling / 1e12, frac_valu_ceiling=ops / t / valu_ceiling)
@@ -588,8 +588,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="",
-                    help="comma-separated token counts, each optionally ':pinned' and ':q2k', ':pq2' or ':q8' "
-                         "(Q2_K, PQ2 or Q8_0 weights, else PTQ1): time only the prefill GEMM")
+                    help="comma-separated token counts, each optionally ':pinned', ':q2k', ':pq2' or ':q8' "
+                         "(Q2_K, PQ2 or Q8_0 weights, else PTQ1) and ':ROWSxCOLS' (else 6144x2048): time only "
+                         "the f32 projection of that many tokens (the prefill GEMM where it applies)")
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
     ap.add_argument("--ffn-only", action="store_true", help="time only the Q2_K FFN step")
@@ -617,10 +618,13 @@ def main() -> int:
         return 0
     if args.prefill_only or args.matvec_only or args.ffn_only or args.floor_only:
         for spec in filter(None, args.prefill_only.split(",")):
-            M, *flags = spec.split(":")  # "2048", "2048:pinned", "2048:q2k", "2048:pinned:pq2"
-            kind = {"q2k": ph.KIND_Q2_K, "pq2": ph.KIND_PQ2, "q8": ph.KIND_Q8_0}.get(next(
-                (f for f in flags if f != "pinned"), ""), ph.KIND_PTQ1)
-            print(json.dumps(bench_prefill(ctx, int(M), pinned="pinned" in flags, kind=kind)), flush=True)
+            # "2048", "2048:pinned", "2048:q2k", "2048:pinned:pq2", "16:q2k:151936x4096"
+            M, *flags = spec.split(":")
+            kinds = {"q2k": ph.KIND_Q2_K, "pq2": ph.KIND_PQ2, "q8": ph.KIND_Q8_0}
+            kind = next((kinds[f] for f in flags if f in kinds), ph.KIND_PTQ1)
+            shape = next(([int(v) for v in f.split("x")] for f in flags if "x" in f), [6144, 2048])
+            print(json.dumps(bench_prefill(ctx, int(M), rows=shape[0], cols=shape[1], pinned="pinned" in flags,
+                                           kind=kind)), flush=True)
         for spec in filter(None, args.matvec_only.split(",")):
             kind, rows, cols, *tok = (int(v) for v in spec.split(":"))
             print(json.dumps(bench_matvec_kernel(ctx, kind, rows, cols, tokens=tok[0] if tok else 1)), flush=True)
