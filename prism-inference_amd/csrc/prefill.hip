@@ -657,16 +657,18 @@ size_t prefill_scratch_bytes(uint32_t kind, uint64_t cols, uint32_t tokens) {
     return ((Mp * cols * 2 + 255) & ~size_t(255)) + Mp * (cols / 32) * 4;
 }
 
-// Tokens from which pinned PTQ1 takes the GEMM rather than the skinny kernel (16 tokens
-// per launch, each unit decoded once per launch).  Measured, 6144 x 2048: 16 tokens 33
-// against 24 us, 32 tokens 34 against 45 us, 2048 tokens 275 against 2629 us.
-constexpr uint32_t kPinnedGemmMinTokens = 32;
+// Tokens from which PTQ1 takes the GEMM rather than the skinny kernel (16 tokens per launch,
+// each unit decoded once per launch).  Measured, pinned, 6144 x 2048: 16 tokens 33 against 24
+// us, 32 tokens 34 against 45 us, 2048 tokens 275 against 2629 us.  Source (f32 input with its
+// quantization, GEMM / skinny, us): 6144 x 2048 16 tokens 18.9 / 13.9, 32 tokens 19.7 / 24.5;
+// 12288 x 4096 30.2 / 20.9 and 31.4 / 39.3; 151936 x 4096 139 / 93 and 144 / 183.
+constexpr uint32_t kPinnedGemmMinTokens = 32, kSourceGemmMinTokens = 32;
 
 bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens) {
     if (kind != kPTQ1) return prefill_k_supported(kind, cols, rows, tokens);
     // The token codes are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols / 128 * 8u * padded_tokens(tokens) * 32u;
-    if (pinned && tokens < kPinnedGemmMinTokens) return false;
+    if (tokens < (pinned ? kPinnedGemmMinTokens : kSourceGemmMinTokens)) return false;
     return kind == kPTQ1 && cols % 128 == 0 && cols <= 65536 && rows > 0 &&
            (rows * (cols / 128) * 28) < (1ull << 40) && code_bytes < (1ull << 31);
 }
@@ -698,7 +700,7 @@ int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t r
     const auto W = static_cast<const uint8_t *>(w_tiled);
     const uint32_t R = static_cast<uint32_t>(rows), nu = K / 128;
     if (pinned) {
-        const uint32_t groups = Mp / 32;
+        const uint32_t groups = (M + 31) / 32;  // token groups holding real tokens
         const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;
         const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
         hipLaunchKernelGGL(k_prefill_ptq1_pinned, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
@@ -709,14 +711,14 @@ int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t r
     // tokens (4096: 232 against 241-246 us); 32 (four wavefronts per SIMD) keeps CUs busy
     // on short prompts up to 512 tokens (512: 45.0 against 46.6 us; 768: 65.4 against 64.2).
     if (M <= kSplitMaxTokens) {
-        const uint32_t groups = Mp / 32;
+        const uint32_t groups = (M + 31) / 32;  // token groups holding real tokens
         const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;
         const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
         hipLaunchKernelGGL(k_prefill_ptq1_split, grid, dim3(64 * 4 * kPhases), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major,
                            out, err);
         return launch_status();
     }
-    const uint32_t nt = M >= 4096 ? 128 : M > 512 ? 64 : 32, groups = Mp / nt;
+    const uint32_t nt = M >= 4096 ? 128 : M > 512 ? 64 : 32, groups = (M + nt - 1) / nt;
     const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
     const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
     if (nt == 128)

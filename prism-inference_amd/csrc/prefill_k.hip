@@ -499,16 +499,20 @@ size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens) {
 }
 
 // Tokens from which Q2_K, PQ2 (Q8_K activations) and Q8_0 take the GEMM rather than the
-// skinny kernel (16 tokens per launch).  Measured, Q2_K 6144 x 2048 (us, skinny kernel launches plus
-// the quantization against prep + GEMM): 16 tokens 9 / 16.3, 32 tokens 14 / 17.4, 64 tokens 24 /
-// 17.4, 2048 tokens 640 / 93.8.
-constexpr uint32_t kGemmMinTokens = 48;
+// skinny kernel (16 tokens per launch).  Measured (f32 input with its quantization, us, skinny /
+// GEMM): Q2_K 6144 x 2048 16 tokens 8.0 / 15.8, 32 tokens 11.4 / 16.8, 64 tokens 24 / 17.4,
+// 2048 tokens 640 / 93.8; 12288 x 4096 32 tokens Q2_K 23.5 / 26.3, Q8_0 36.3 / 39.7.  Large
+// matrices leave the skinny kernel sooner: 151936 x 4096 16 tokens Q2_K 70.5 / 68.7, PQ2 74.1
+// / 57.8, Q8_0 169.5 / 144.5; 32 tokens Q2_K 137 / 74, PQ2 147 / 63, Q8_0 338 / 154.
+constexpr uint32_t kGemmMinTokens = 48, kGemmMinTokensLarge = 16;
+constexpr uint64_t kLargeRows = 65536;
 
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens) {
     // Codes, sums and scales are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols * padded_tokens(tokens);
     return (kind == kQ2_K || kind == kPQ2 || kind == kQ8_0) && cols % kUnit == 0 && cols <= 65536 && rows > 0 &&
-           rows < (1ull << 31) && code_bytes < (1ull << 31) && tokens >= kGemmMinTokens;
+           rows < (1ull << 31) && code_bytes < (1ull << 31) &&
+           tokens >= (rows >= kLargeRows ? kGemmMinTokensLarge : kGemmMinTokens);
 }
 
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
@@ -536,7 +540,8 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     // against 97.4 with 32; 4096: 184.3 / 200.4), 32 below (128 tokens: 18.0 / 22.3).
     // Q8_0 keeps 32 (2048 tokens: 158.8 us against 156.4 with 64, whose chain operands take
     // two wavefronts per SIMD instead of three).
-    const uint32_t nt = M > 512 && kind != kQ8_0 ? 64 : 32, groups = Mp / nt;
+    // Only the token groups that hold real tokens are launched (the prep pads to Mp).
+    const uint32_t nt = M > 512 && kind != kQ8_0 ? 64 : 32, groups = (M + nt - 1) / nt;
     const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
     const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
     auto go = [&](auto kernel) {

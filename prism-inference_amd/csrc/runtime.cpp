@@ -15,9 +15,8 @@ using namespace prism::rt;
 
 namespace {
 
-// Token count from which f32 projections of PTQ1 weights run as one tiled-prefill GEMM
-// (prefill_supported has the last word: its own thresholds for the pinned contract and for
-// Q2_K / PQ2 / Q8_0).
+// Token count below which no f32 projection runs as a tiled-prefill GEMM (prefill_supported
+// has the last word: its own thresholds per kind, contract and matrix size).
 constexpr uint32_t kPrefillMinTokens = 16;
 
 // Quantize device floats with the contract matvec_into would use, then project.  `role`

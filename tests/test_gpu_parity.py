@@ -596,12 +596,12 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
         ctx.release(wid)
 
 
-@pytest.mark.parametrize("rows,cols,M", [(200, 2048, 16), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
+@pytest.mark.parametrize("rows,cols,M", [(200, 2048, 32), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
                                          (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
                                          (96, 256, 4096), (130, 1152, 1100), (6144, 2048, 1024),
                                          (6044, 2048, 2048)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
-    """PTQ1 prefill runs as one f16-MFMA GEMM from 16 tokens on, in both contracts; every
+    """PTQ1 prefill runs as one f16-MFMA GEMM from 32 tokens on, in both contracts; every
     token row must equal the reference's per-token matvec bit for bit (partial row
     tiles, idle wavefronts of a partial 128-row block, an odd block count, 32, 64 and
     128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
@@ -626,10 +626,11 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
 
 @pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0])
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 48), (64, 256, 49), (130, 1024, 300), (37, 512, 129),
-                                         (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64)])
+                                         (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64),
+                                         (65536 + 37, 256, 16)])
 def test_gpu_k_prefill_gemm_equals_per_token_matvec(ctx, kind, rows, cols, M):
-    """Q2_K and PQ2 (Q8_K activations) and Q8_0 prefill from 48 tokens runs as one int8-MFMA
-    GEMM, 32 or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted
+    """Q2_K and PQ2 (Q8_K activations) and Q8_0 prefill from 48 tokens (16 on matrices of at
+    least 65536 rows) runs as one int8-MFMA GEMM, 32 or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted
     codes, msum from a binary16 product of the sub-block mins and sums, the two outer products
     of the token and row scales; PQ2: each 128-element block's integer dot on signed codes and
     its outer product of scales, folded unfused or fused by contract; Q8_0: each 32-element
@@ -830,7 +831,7 @@ def test_gpu_wide_rows_few_tiles_every_token_count(ctx, kind, rows, cols):
     """FFN-down-like widths (14336, 17408 inputs) on a few 64-row tiles, stored tiled: one
     token takes the split kernel with wider lane groups, or the row-tile fallback where its
     LDS cannot hold the rows; two or three tokens run token by token (PTQ1, PQ2) or on the
-    batch kernels, and PTQ1 from 16 tokens the prefill GEMM; every output equals the
+    batch kernels, and PTQ1 from 32 tokens the prefill GEMM; every output equals the
     oracle's per-token matvec."""
     import oracle
 
