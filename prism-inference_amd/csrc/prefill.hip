@@ -648,6 +648,9 @@ uint32_t padded_tokens(uint32_t M) { return (M + kTokAlign - 1) / kTokAlign * kT
 // tokens 20.9 / 24.1, 128 tokens 21.3 / 24.6, 256 tokens 37.1 / 32.5, 512 tokens 55.4 / 44.9.
 // Beyond 128 tokens the four-token-group workgroups of the kernel above fill more CUs.
 constexpr uint32_t kSplitMaxTokens = 128;
+// Workgroup rows (128 weight rows each) from which a matrix counts as large for the choice of
+// tokens per workgroup (32768 rows).
+constexpr uint32_t kLargeRowBlocks = 256;
 
 }  // namespace
 
@@ -710,6 +713,31 @@ int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t r
     // and beats 128 (two per SIMD, the decode shared by more tokens) up to about 4096
     // tokens (4096: 232 against 241-246 us); 32 (four wavefronts per SIMD) keeps CUs busy
     // on short prompts up to 512 tokens (512: 45.0 against 46.6 us; 768: 65.4 against 64.2).
+    // Large matrices (at least kLargeRowBlocks workgroup rows) re-read their weights once per
+    // token group, from HBM: there the workgroups take as many tokens as keep at least 512 of
+    // them (1024 beyond 512 tokens) in the grid, and short prompts skip the block-split kernel.
+    // Measured, 151936 x 4096 (us, the small-matrix choice -> this one): 32 tokens 145 -> 114,
+    // 64 tokens 282 -> 168, 128 tokens 523 -> 312, 512 tokens 1365 -> 1065; 32768 x 4096: 64
+    // tokens 62 -> 56, 128 tokens 119 -> 78, 256 tokens 180 -> 132.
+    if (gx >= kLargeRowBlocks) {
+        const uint32_t want = M > 512 ? 1024 : 512, mr = (M + 31) / 32 * 32;
+        uint32_t nt = 32;
+        for (uint32_t c : {128u, 64u})
+            if (c <= mr && static_cast<uint64_t>(gx) * ((M + c - 1) / c) >= want) {
+                nt = c;
+                break;
+            }
+        const uint32_t groups = (M + nt - 1) / nt;
+        const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;
+        const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
+        if (nt == 128)
+            hipLaunchKernelGGL(k_prefill_ptq1<4>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
+        else if (nt == 64)
+            hipLaunchKernelGGL(k_prefill_ptq1<2>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
+        else
+            hipLaunchKernelGGL(k_prefill_ptq1<1>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
+        return launch_status();
+    }
     if (M <= kSplitMaxTokens) {
         const uint32_t groups = (M + 31) / 32;  // token groups holding real tokens
         const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;

@@ -539,9 +539,12 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     // Tokens per workgroup (measured, Q2_K 6144 x 2048, us): 64 from 1024 tokens (2048: 93.4
     // against 97.4 with 32; 4096: 184.3 / 200.4), 32 below (128 tokens: 18.0 / 22.3).
     // Q8_0 keeps 32 (2048 tokens: 158.8 us against 156.4 with 64, whose chain operands take
-    // two wavefronts per SIMD instead of three).
-    // Only the token groups that hold real tokens are launched (the prep pads to Mp).
-    const uint32_t nt = M > 512 && kind != kQ8_0 ? 64 : 32, groups = (M + nt - 1) / nt;
+    // two wavefronts per SIMD instead of three).  Large matrices take 64 already while that
+    // keeps 512 workgroups (their weights are re-read once per token group; Q2_K 151936 x
+    // 4096, us: 128 tokens 273 -> 249, 512 tokens 987 -> 860; 32768 x 4096, 128 tokens 61.6
+    // -> 53.8).  Only the token groups that hold real tokens are launched (the prep pads to Mp).
+    const bool wide = M > 512 || (static_cast<uint64_t>(gx) * ((M + 63) / 64) >= 512 && M > 32);
+    const uint32_t nt = wide && kind != kQ8_0 ? 64 : 32, groups = (M + nt - 1) / nt;
     const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;  // grid y and z limits
     const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);
     auto go = [&](auto kernel) {

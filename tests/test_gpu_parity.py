@@ -599,7 +599,8 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 32), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
                                          (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
                                          (96, 256, 4096), (130, 1152, 1100), (6144, 2048, 1024),
-                                         (6044, 2048, 2048)])
+                                         (6044, 2048, 2048), (32768 + 37, 256, 64), (32768 + 37, 256, 100),
+                                         (32768 + 37, 256, 130)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     """PTQ1 prefill runs as one f16-MFMA GEMM from 32 tokens on, in both contracts; every
     token row must equal the reference's per-token matvec bit for bit (partial row
@@ -607,7 +608,8 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
     token groups are a multiple of eight: M = 200, 512, 4096; nine blocks per row at 1152
     columns, the benchmark's matrix at 1024 tokens, a partial last tile at 6044 rows and
-    2048 tokens).  The pinned contract's
+    2048 tokens; at 32805 rows the large-matrix choice of 32, 64 and 128 tokens per
+    workgroup).  The pinned contract's
     kernel takes each native lane's integer sum from its own masked MFMA and runs the
     four FMA lanes of dot_q8_groups_pinned."""
     import oracle
@@ -627,7 +629,7 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
 @pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0])
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 48), (64, 256, 49), (130, 1024, 300), (37, 512, 129),
                                          (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64),
-                                         (65536 + 37, 256, 16)])
+                                         (65536 + 37, 256, 16), (32768 + 37, 256, 128)])
 def test_gpu_k_prefill_gemm_equals_per_token_matvec(ctx, kind, rows, cols, M):
     """Q2_K and PQ2 (Q8_K activations) and Q8_0 prefill from 48 tokens (16 on matrices of at
     least 65536 rows) runs as one int8-MFMA GEMM, 32 or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted
