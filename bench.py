@@ -588,8 +588,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--prefill-only", default="",
-                    help="comma-separated token counts, each optionally ':pinned', ':q2k', ':pq2' or ':q8' "
-                         "(Q2_K, PQ2 or Q8_0 weights, else PTQ1) and ':ROWSxCOLS' (else 6144x2048): time only "
+                    help="comma-separated token counts, each optionally ':pinned', ':q2k', ':pq2', ':q8', "
+                         "':tq1' or ':tq2' (Q2_K, PQ2, Q8_0, TQ1_0 or TQ2_0 weights, else PTQ1) and ':ROWSxCOLS' (else 6144x2048): time only "
                          "the f32 projection of that many tokens (the prefill GEMM where it applies)")
     ap.add_argument("--matvec-only", default="",
                     help="comma-separated kind:rows:cols[:tokens]: time only these matvecs")
@@ -620,7 +620,8 @@ def main() -> int:
         for spec in filter(None, args.prefill_only.split(",")):
             # "2048", "2048:pinned", "2048:q2k", "2048:pinned:pq2", "16:q2k:151936x4096"
             M, *flags = spec.split(":")
-            kinds = {"q2k": ph.KIND_Q2_K, "pq2": ph.KIND_PQ2, "q8": ph.KIND_Q8_0}
+            kinds = {"q2k": ph.KIND_Q2_K, "pq2": ph.KIND_PQ2, "q8": ph.KIND_Q8_0, "tq1": ph.KIND_TQ1_0,
+                     "tq2": ph.KIND_TQ2_0}
             kind = next((kinds[f] for f in flags if f in kinds), ph.KIND_PTQ1)
             shape = next(([int(v) for v in f.split("x")] for f in flags if "x" in f), [6144, 2048])
             print(json.dumps(bench_prefill(ctx, int(M), rows=shape[0], cols=shape[1], pinned="pinned" in flags,

@@ -1154,11 +1154,6 @@ struct SkParams {
     uint32_t act_stride;  // prepared blocks: bytes per token
 };
 
-template <Op O>
-constexpr bool skinny_supported() {
-    return O != Op::TQ1 && O != Op::TQ2;
-}
-
 // binary32 terms per unit and (row, token) element of the skinny kernel: those of the
 // row kernels, except pinned PTQ1, whose four group scales are already multiplied by
 // the token's block scales: 8 dwords of packed 16-bit lane sums, then the four dd_g.
@@ -1225,7 +1220,12 @@ __device__ __forceinline__ uint32_t trit_quad(uint32_t x, uint32_t pl, uint32_t 
 // Activation operand bytes per lane and unit in the lane-ordered copy (k_sk_prep).
 template <Op O>
 constexpr uint32_t sk_lane_bytes() {
-    return O == Op::Q2K ? 64 : 32;
+    return O == Op::Q2K || O == Op::TQ1 || O == Op::TQ2 ? 64 : 32;
+}
+// 256-element units with one Q8_K block each.
+template <Op O>
+constexpr bool sk_super_block() {
+    return O == Op::Q2K || O == Op::TQ1 || O == Op::TQ2;
 }
 
 template <Op O>
@@ -1242,6 +1242,22 @@ struct SkFrag<Op::Q2K> {
     u32x4 q;   // code bytes 16s..16s+15 of the A row
     u32x2 sc;  // its scale bytes 8(s/2)..+7
     u32x4 dm;  // d | dmin << 16 of the four output rows
+    u32x4 b[4];
+    u32x4 as;
+};
+template <>
+struct SkFrag<Op::TQ2> {
+    u32x4 q;   // code bytes 16s..16s+15 of the A row
+    u32x2 dd;  // binary16 scales of the four output rows
+    u32x4 b[4];
+    u32x4 as;
+};
+template <>
+struct SkFrag<Op::TQ1> {
+    u32x2 c01;    // code bytes 8s..8s+7 of the A row
+    uint32_t c2;  // its code bytes 32+4s..35+4s
+    uint32_t tl;  // its code bytes 48..51 (the lane group's byte: 48+s)
+    u32x2 dd;     // binary16 scales of the four output rows
     u32x4 b[4];
     u32x4 as;
 };
@@ -1304,8 +1320,16 @@ __device__ __forceinline__ uint32_t sk_elem(uint32_t s, uint32_t k, uint32_t &st
     stride = 1;
     if constexpr (O == Op::Q8_0) {
         return 32u * (k >> 1) + 8u * s + 4u * (k & 1u);
-    } else if constexpr (O == Op::Q2K) {
+    } else if constexpr (O == Op::Q2K || O == Op::TQ2) {
         return 128u * (s >> 1) + 32u * (k >> 2) + 16u * (s & 1u) + 4u * (k & 3u);
+    } else if constexpr (O == Op::TQ1) {
+        // Digits 0..4 of code bytes 8s..8s+3 and 8s+4..8s+7 (elements b + 32k), of code
+        // bytes 32+4s..35+4s (elements 160 + 4s + 16k), then the four digits of code byte
+        // 48+s (elements 240 + s + 4k: stride 4).
+        if (k < 10) return 8u * s + 4u * (k >= 5) + 32u * (k % 5);
+        if (k < 15) return 160u + 4u * s + 16u * (k - 10);
+        stride = 4;
+        return 240u + s;
     } else if constexpr (kind_of<O>() == kPTQ1) {
         return ptq1_plan(s).off[k];
     } else {
@@ -1322,7 +1346,7 @@ template <Op O>
 __device__ __forceinline__ const int8_t *sk_value(const uint8_t *a, uint32_t u, uint32_t e) {
     if constexpr (sk_q8_groups<O>())
         return reinterpret_cast<const Q8Block *>(a)[4u * u + (e >> 5)].values + (e & 31u);
-    else if constexpr (O == Op::Q2K)
+    else if constexpr (sk_super_block<O>())
         return reinterpret_cast<const Q8KBlock *>(a)[u].values + e;
     else
         return reinterpret_cast<const Q8KBlock *>(a)[u >> 1].values + 128u * (u & 1u) + e;
@@ -1359,7 +1383,7 @@ __global__ __launch_bounds__(256) void k_sk_prep(const uint8_t *__restrict__ act
         float sc;
         if constexpr (sk_q8_groups<O>())
             sc = reinterpret_cast<const Q8Block *>(a)[4u * u + g].scale;
-        else if constexpr (O == Op::Q2K)
+        else if constexpr (sk_super_block<O>())
             sc = reinterpret_cast<const Q8KBlock *>(a)[u].scale;
         else
             sc = reinterpret_cast<const Q8KBlock *>(a)[u >> 1].scale;
@@ -1382,11 +1406,26 @@ __device__ __forceinline__ void sk_load_act_raw(SkFrag<O> &f, const uint8_t *a, 
         }
         f.as = u32x4{__float_as_uint(blk[0].scale), __float_as_uint(blk[1].scale), __float_as_uint(blk[2].scale),
                      __float_as_uint(blk[3].scale)};
-    } else if constexpr (O == Op::Q2K) {
+    } else if constexpr (O == Op::Q2K || O == Op::TQ2) {
         const Q8KBlock *blk = reinterpret_cast<const Q8KBlock *>(a) + u;
 #pragma unroll
         for (int p = 0; p < 4; ++p)
             f.b[p] = *reinterpret_cast<const u32x4a *>(blk->values + 128u * (s >> 1) + 32u * p + 16u * (s & 1u));
+        f.as.x = __float_as_uint(blk->scale);
+    } else if constexpr (O == Op::TQ1) {
+        const Q8KBlock *blk = reinterpret_cast<const Q8KBlock *>(a) + u;
+        const int8_t *v = blk->values;
+        uint32_t x[16];
+#pragma unroll
+        for (uint32_t k = 0; k < 15; ++k) {
+            uint32_t stride;
+            x[k] = *reinterpret_cast<const uint32_t *>(v + sk_elem<O>(s, k, stride));
+        }
+        x[15] = static_cast<uint8_t>(v[240u + s]) | static_cast<uint32_t>(static_cast<uint8_t>(v[244u + s])) << 8 |
+                static_cast<uint32_t>(static_cast<uint8_t>(v[248u + s])) << 16 |
+                static_cast<uint32_t>(static_cast<uint8_t>(v[252u + s])) << 24;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) f.b[p] = u32x4{x[4 * p], x[4 * p + 1], x[4 * p + 2], x[4 * p + 3]};
         f.as.x = __float_as_uint(blk->scale);
     } else if constexpr (kind_of<O>() == kPTQ1) {
         uint32_t x[8];
@@ -1458,6 +1497,14 @@ __device__ __forceinline__ void sk_load(SkFrag<O> &f, const SkLane &L, uint32_t 
         f.q = bload4(L.rs, seg + 16u * s * L.trp + 16u * L.ra);
         f.sc = bload2(L.rs, seg + 64u * L.trp + 16u * L.ra + 8u * (s >> 1));
         f.dm = bload4(L.rs, seg + 80u * L.trp + 4u * L.rc);
+    } else if constexpr (O == Op::TQ2) {
+        f.q = bload4(L.rs, seg + 16u * s * L.trp + 16u * L.ra);
+        f.dd = bload2(L.rs, seg + 64u * L.trp + 2u * L.rc);
+    } else if constexpr (O == Op::TQ1) {
+        f.c01 = bload2(L.rs, seg + 16u * (s >> 1) * L.trp + 16u * L.ra + 8u * (s & 1u));
+        f.c2 = bload1(L.rs, seg + 32u * L.trp + 16u * L.ra + 4u * s);
+        f.tl = bload1(L.rs, seg + 48u * L.trp + 4u * L.ra);
+        f.dd = bload2(L.rs, seg + 52u * L.trp + 2u * L.rc);
     } else if constexpr (kind_of<O>() == kPTQ1) {
         f.a = bload1(L.rs, seg + 16u * L.ra + 4u * s);
         const u32x2 bb = bload2(L.rs, seg + 16u * L.trp + 8u * L.ra);
@@ -1523,6 +1570,45 @@ __device__ __forceinline__ void sk_terms(const SkFrag<O> &f, const SkLane &L, co
             const float as = __uint_as_float(f.as.x);
             tv[v][0] = (as * h2f(f.dm[v] & 0xffffu)) * static_cast<float>(isum[v]) -
                        (as * h2f(f.dm[v] >> 16)) * static_cast<float>(msum[v]);
+        }
+    } else if constexpr (O == Op::TQ1 || O == Op::TQ2) {
+        // The unit's integer dot over the lane groups' 64 elements each: signed fields
+        // c - 1 (TQ2_0, Q2_K's element order) or signed digits t - 1 (TQ1_0, sk_elem's).
+        u32x4 a[4];
+        if constexpr (O == Op::TQ2) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) a[p][d] = code_map((f.q[d] >> (2 * p)) & 0x03030303u, 0x020100ffu);
+        } else {
+            uint32_t q[16];
+            auto digits = [&](uint32_t x, int n0) {  // digits 0..4 of four code bytes
+                uint32_t Lw = x & 0x00ff00ffu, Hw = (x >> 8) & 0x00ff00ffu;
+#pragma unroll
+                for (int k = 0; k < 5; ++k) {
+                    const uint32_t mL = Lw * 3u, mH = Hw * 3u;
+                    q[n0 + k] = code_map(perm(mH, mL, sel(1, 5, 3, 7)), 0x000100ffu);
+                    Lw = mL & 0x00ff00ffu;
+                    Hw = mH & 0x00ff00ffu;
+                }
+            };
+            digits(f.c01.x, 0);
+            digits(f.c01.y, 5);
+            digits(f.c2, 10);
+            // Code byte 48+s in all four bytes, byte k taking digit k.
+            q[15] = trit_quad(((f.tl >> (8u * s)) & 0xffu) * 0x01010101u, 1u | (9u << 16), 3u | (27u << 16));
+#pragma unroll
+            for (int p = 0; p < 4; ++p) a[p] = u32x4{q[4 * p], q[4 * p + 1], q[4 * p + 2], q[4 * p + 3]};
+        }
+        v4i acc = mfma64(a[0], f.b[0], zero);
+        acc = mfma64(a[1], f.b[1], acc);
+        acc = mfma64(a[2], f.b[2], acc);
+        acc = mfma64(a[3], f.b[3], acc);
+        const float as = __uint_as_float(f.as.x);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            // dot(), src/kernels/tquants.rs:283
+            tv[v][0] = static_cast<float>(acc[v]) * (h2f((f.dd[v >> 1] >> (16 * (v & 1))) & 0xffffu) * as);
         }
     } else if constexpr (kind_of<O>() == kPTQ1) {
         // A_s digits 0..4, sequentially (remainder times 3 per digit).
@@ -2753,24 +2839,20 @@ int launch_batch(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t a
 constexpr uint64_t kSkinnyMinRows = 1024;
 
 // The row-tile batch kernel (one wavefront per 64-row tile runs every token's chain, each
-// unit decoded once per batch): large matrices, and TQ1_0 / TQ2_0 (no skinny kernel)
-// from eight tokens on smaller ones.  Measured: TQ1_0 6144x2048 x 16 tokens 45 us
-// against 75 us token by token; 12288x4096 x 4 tokens 34 us against 29 us.
+// unit decoded once per batch): large matrices the skinny kernel leaves (pinned PTQ1 up
+// to four tokens).
 bool batch_eligible(const MatvecArgs &a) {
-    if (a.tokens < 2 || a.w2) return false;
-    if (a.rows >= kBatchMinRows) return true;
-    const bool tq = a.kind == kTQ1_0 || a.kind == kTQ2_0;
-    return tq && a.rows >= kSkinnyMinRows && a.tokens >= 8;
+    return a.tokens >= 2 && !a.w2 && a.rows >= kBatchMinRows;
 }
 
 // Whether a skinny batch first copies its activations into lane order (one more launch,
 // then contiguous loads) instead of gathering them from the prepared blocks in every
 // wavefront.  Measured on 2048..151936 rows: the copy pays from 8192 rows or from 5
-// tokens; Q2_K's 256-element units halve its gathers, and the copy pays only from
-// 32768 rows.
+// tokens; Q2_K's 256-element units halve its gathers (as TQ2_0's, in the same order), and
+// the copy pays only from 32768 rows.
 template <Op O>
 bool skinny_lane_ordered(uint64_t rows, uint32_t ntok) {
-    if constexpr (O == Op::Q2K) return rows >= 32768;
+    if constexpr (O == Op::Q2K || O == Op::TQ2) return rows >= 32768;
     return rows >= 8192 || ntok > 4;
 }
 
@@ -2948,13 +3030,16 @@ bool skinny_eligible(const MatvecArgs &a) {
     if (a.tokens < 2 || a.w2 || a.rows < kSkinnyMinRows || lut_batch_eligible(a) || quad_eligible(a) ||
         quad_split_eligible(a))
         return false;
-    // Pinned PTQ1 (four masked MFMAs per group) on large matrices: up to four tokens the
-    // row-tile batch kernel is faster (151936x4096 x 4: 148 against 165 us), from 16 the
-    // skinny kernel (171 against 558 us).
+    // Pinned PTQ1 (four masked MFMAs per group) and TQ1_0 / TQ2_0 (digits decoded for 16
+    // rows per wavefront) on large matrices: up to four tokens the row-tile batch kernel is
+    // faster (151936x4096 x 4: pinned PTQ1 148 against 165 us, TQ2_0 56.8 against 61.3, TQ1_0
+    // 72.3 against 72.7; x 2: TQ2_0 40.6 against 60.9), from eight the skinny kernel (TQ1_0
+    // 73.7 against 116; pinned PTQ1 x 16: 171 against 558).
     const bool pinned_q8 = a.kind == kPTQ1 && a.pinned && a.act_format != kActQ8K &&
                            !(a.act_format == kActF32 && a.qcontract_is_q8k);
-    if (pinned_q8 && a.rows >= kBatchMinRows && a.tokens <= 4) return false;
-    return dispatch(a, [&]<Op O>() { return skinny_supported<O>() ? 1 : 0; }) == 1;
+    const bool tq = a.kind == kTQ1_0 || a.kind == kTQ2_0;
+    if ((pinned_q8 || tq) && a.rows >= kBatchMinRows && a.tokens <= 4) return false;
+    return dispatch(a, [&]<Op>() { return 1; }) == 1;  // a kind and contract of the tiled kernels
 }
 
 // Two PTQ1 / PQ2 tokens (three PTQ1 tokens from 12288 inputs) of rows of at least 6144 inputs on
@@ -2993,10 +3078,7 @@ int launch_matvec_tiled(const MatvecArgs &a) {
             float *out = a.out + a.rows * tok;
             const float *res = a.residual ? a.residual + a.rows * tok : nullptr;
             const int rc = dispatch(a, [&]<Op O>() {
-                if constexpr (skinny_supported<O>())
-                    return launch_skinny<O>(a, act, n, static_cast<uint32_t>(in_stride), out, res);
-                else
-                    return -2;
+                return launch_skinny<O>(a, act, n, static_cast<uint32_t>(in_stride), out, res);
             });
             if (rc) return rc;
         }
@@ -3028,12 +3110,7 @@ int launch_matvec_tiled(const MatvecArgs &a) {
 
 size_t tiled_scratch_bytes(const MatvecArgs &a) {
     if (!skinny_eligible(a)) return 0;
-    return static_cast<size_t>(dispatch(a, [&]<Op O>() {
-        if constexpr (skinny_supported<O>())
-            return static_cast<int>(skinny_scratch<O>(a));
-        else
-            return 0;
-    }));
+    return static_cast<size_t>(dispatch(a, [&]<Op O>() { return static_cast<int>(skinny_scratch<O>(a)); }));
 }
 
 bool tiled_prologue_fits(const MatvecArgs &a) {

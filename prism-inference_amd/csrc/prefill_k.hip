@@ -1,5 +1,5 @@
-// prefill_k.hip -- tiled prefill GEMM for Q2_K and PQ2 weights (Q8_K activations) and Q8_0
-// weights (Q8_0 activations) on the int8 matrix cores (gfx950).
+// prefill_k.hip -- tiled prefill GEMM for Q2_K, PQ2, TQ1_0 and TQ2_0 weights (Q8_K
+// activations) and Q8_0 weights (Q8_0 activations) on the int8 matrix cores (gfx950).
 //
 // dot_q2_k_block (src/kernels/kquants.rs:162-197, row order :346-430), per 256-element
 // unit u of a row and a token's Q8_K block:
@@ -32,6 +32,10 @@
 // dot_legacy (src/kernels.rs:1204-1248), per 32-element block b of a Q8_0 row and the
 // token's Q8_0 block b: Y = Y + fl(fl(ws_b * as_b) * float(I_b)), I_b one K-step on the codes
 // as they are (no decode), the scale product one outer product.
+//
+// TQ1_0 / TQ2_0 dot (src/kernels/tquants.rs:255-285), per 256-element unit and the token's
+// Q8_K block: Y = Y + float(I) * fl(d * as), I = sum (t - 1) * a over the unit (eight K-steps
+// on the signed codes), fl(d * as) one outer product.
 //
 // Work split: a workgroup of four wavefronts owns 128 weight rows (two 64-row tiles) and
 // NT = 32 * CT tokens, and walks the rows' 256-element units (one Q8_K block each; two
@@ -81,6 +85,52 @@ __host__ __device__ constexpr uint32_t pq2_elem(uint32_t s, uint32_t h, uint32_t
 }
 // Q8_0: K-step s is the 32-element block s of the unit, half h its codes 16h .. 16h+15 (tiled
 // code piece 2 * (s % 4) + h of tiled unit 2u + s / 4), in their own order: no decode.
+// TQ2_0: bits 2k of code byte 32q + b hold element 128q + 32k + b (dot_tq2_block).  K-step s
+// takes piece p = s / 2 (bytes 16p .. 16p+15) and fields k = 2 * (s % 2) + {0, 1}; dword i is
+// bytes 8h + 4 * (i % 2) .. +3 of the piece at field 2 * (s % 2) + i / 2: the four
+// consecutive elements starting at
+__host__ __device__ constexpr uint32_t tq2_elem(uint32_t s, uint32_t h, uint32_t i) {
+    const uint32_t p = s >> 1, k = 2 * (s & 1) + (i >> 1);
+    return 128 * (p >> 1) + 32 * k + 16 * (p & 1) + 8 * h + 4 * (i & 1);
+}
+// TQ1_0: base-3 digit k of code byte b holds element b + 32k (b < 32, k < 5), 160 + (b - 32)
+// + 16k (32 <= b < 48) or 240 + (b - 48) + 4k (48 <= b < 52, k < 4) (dot_tq1_block).  Half h
+// takes bytes 8h .. 8h+7 of the three 16-byte pieces (six code dwords of five digits) and bytes
+// 2h, 2h+1 of the 4-byte piece (four digits each).  Operand dword n = 4s + i (0..31) is digit
+// n % 5 of code dword c = n / 5 (piece c / 2, bytes 8h + 4 * (c % 2) .. +3) for n < 30, and
+// for n = 30 + m digits 2m, 2m + 1 of the two short-piece bytes.  Byte j of it holds element
+__host__ __device__ constexpr uint32_t tq1_elem(uint32_t s, uint32_t h, uint32_t i, uint32_t j) {
+    const uint32_t n = 4 * s + i;
+    if (n >= 30) return 240 + 2 * h + (j & 1) + 4 * (2 * (n - 30) + (j >> 1));
+    const uint32_t c = n / 5, k = n % 5, p = c >> 1, b = 8 * h + 4 * (c & 1) + j;
+    return p < 2 ? 16 * p + b + 32 * k : 160 + b + 16 * k;
+}
+
+// Each order names every element of the unit exactly once over its 256 byte slots (eight
+// K-steps, two halves, four dwords of four bytes), byte j of an operand dword at elem(s, h, i, j).
+template <typename F>
+constexpr bool names_every_element_once(F elem) {
+    bool seen[256] = {};
+    for (uint32_t s = 0; s < 8; ++s)
+        for (uint32_t h = 0; h < 2; ++h)
+            for (uint32_t i = 0; i < 4; ++i)
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const uint32_t e = elem(s, h, i, j);
+                    if (e >= 256 || seen[e]) return false;
+                    seen[e] = true;
+                }
+    return true;
+}
+static_assert(names_every_element_once([](uint32_t s, uint32_t h, uint32_t i, uint32_t j) {
+    return q2k_elem(s, h, i) + j;
+}));
+static_assert(names_every_element_once([](uint32_t s, uint32_t h, uint32_t i, uint32_t j) {
+    return pq2_elem(s, h, i) + 4 * j;
+}));
+static_assert(names_every_element_once([](uint32_t s, uint32_t h, uint32_t i, uint32_t j) {
+    return tq2_elem(s, h, i) + j;
+}));
+static_assert(names_every_element_once(tq1_elem));
 
 // ---- activation prep ------------------------------------------------------------------
 // A workgroup of TOK wavefronts quantizes TOK consecutive tokens (one each, 1024 inputs =
@@ -128,6 +178,11 @@ __global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const float *__rest
                     v[j] = *reinterpret_cast<const uint32_t *>(vals + 4 * j);
                 } else if constexpr (KIND == kQ2_K) {
                     v[j] = *reinterpret_cast<const uint32_t *>(vals + q2k_elem(s, h, j));
+                } else if constexpr (KIND == kTQ2_0) {
+                    v[j] = *reinterpret_cast<const uint32_t *>(vals + tq2_elem(s, h, j));
+                } else if constexpr (KIND == kTQ1_0) {
+#pragma unroll
+                    for (uint32_t b = 0; b < 4; ++b) v[j] |= static_cast<uint32_t>(vals[tq1_elem(s, h, j, b)]) << (8 * b);
                 } else {
                     const uint8_t *e = vals + pq2_elem(s, h, j);  // elements e, e+4, e+8, e+12
                     v[j] = static_cast<uint32_t>(e[0]) | static_cast<uint32_t>(e[4]) << 8 |
@@ -187,6 +242,22 @@ struct RawK<kQ8_0> {
     u32x4 c[8];    // codes 16h .. 16h+15 of the unit's eight blocks
     u32x2 sc[2];   // the eight binary16 block scales
 };
+template <>
+struct RawK<kTQ2_0> {
+    u32x2 c[4];  // bytes 8h .. 8h+7 of the four code pieces
+    uint32_t d;  // binary16 scale
+};
+template <>
+struct RawK<kTQ1_0> {
+    u32x2 c[3];     // bytes 8h .. 8h+7 of the three 16-byte code pieces
+    uint32_t tail;  // the 4-byte code piece (code bytes 48 .. 51)
+    uint32_t d;
+};
+// Bytes per row of a tiled 256-element unit: the native block.
+template <uint32_t KIND>
+constexpr uint32_t unit_bytes_k() {
+    return KIND == kQ2_K ? 84 : KIND == kQ8_0 ? 272 : KIND == kPQ2 ? 68 : KIND == kTQ2_0 ? 66 : 54;
+}
 template <uint32_t KIND>
 __device__ __forceinline__ void load_unit_k(__amdgpu_buffer_rsrc_t rs, uint32_t u, uint32_t trp, uint32_t row,
                                             uint32_t h, RawK<KIND> &w) {
@@ -204,6 +275,13 @@ __device__ __forceinline__ void load_unit_k(__amdgpu_buffer_rsrc_t rs, uint32_t 
             for (uint32_t j = 0; j < 4; ++j) w.c[4 * b + j] = bload4(rs, seg + 16u * (2 * j + h) * trp + 16u * row);
             w.sc[b] = bload2(rs, seg + 128u * trp + 8u * row);
         }
+    } else if constexpr (KIND == kTQ2_0 || KIND == kTQ1_0) {
+        constexpr uint32_t P = KIND == kTQ2_0 ? 4 : 3, kScale = KIND == kTQ2_0 ? 64 : 52;
+        const uint32_t seg = u * trp * unit_bytes_k<KIND>();
+#pragma unroll
+        for (uint32_t p = 0; p < P; ++p) w.c[p] = bload2(rs, seg + 16u * p * trp + 16u * row + 8u * h);
+        if constexpr (KIND == kTQ1_0) w.tail = bload1(rs, seg + 48u * trp + 4u * row);
+        w.d = __builtin_amdgcn_raw_buffer_load_b16(rs, static_cast<int>(seg + kScale * trp + 2u * row), 0, 0);
     } else {
 #pragma unroll
         for (uint32_t b = 0; b < 2; ++b) {
@@ -232,7 +310,7 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                                                     uint32_t xcd_major, float *__restrict__ out,
                                                     int *__restrict__ err) {
     constexpr uint32_t NT = 32 * CT;
-    constexpr bool kQ2 = KIND == kQ2_K, kQ8 = KIND == kQ8_0;
+    constexpr bool kQ2 = KIND == kQ2_K, kQ8 = KIND == kQ8_0, kTQ = KIND == kTQ1_0 || KIND == kTQ2_0;
     constexpr uint32_t kSums = kQ2 ? 2 : 0;  // Q2_K: two runs of sub-block sums per unit
     constexpr uint32_t kScl = kQ8 ? 8 : 1;   // scale runs per unit (Q8_0: one per block)
     // Ring buffers (separate objects, named statically below, so the compiler can tell a
@@ -258,7 +336,7 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
     const uint32_t tile = 2 * bx + (wave >> 1), hw = wave & 1;
     const uint32_t tiles = (rows + kTile - 1) / kTile;
     const uint32_t t0 = by * NT;
-    const uint32_t row_bytes = nu * (kQ2 ? 84u : kQ8 ? 272u : 68u);
+    const uint32_t row_bytes = nu * unit_bytes_k<KIND>();
     uint32_t trows = 0;
     if (tile < tiles) {
         const uint32_t left = rows - tile * kTile;
@@ -347,6 +425,42 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                 for (uint32_t s = 0; s < 8; ++s) aw[s] = w.c[s];
                 wsc[0] = w.sc[0];
                 wsc[1] = w.sc[1];
+            } else if constexpr (KIND == kTQ2_0) {
+                // Fields c (0..3) -> signed bytes c - 1, as for PQ2.
+#pragma unroll
+                for (uint32_t s = 0; s < 8; ++s)
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; ++i) {
+                        const uint32_t k = 2 * (s & 1) + (i >> 1);
+                        aw[s][i] = (((w.c[s >> 1][i & 1] >> (2 * k)) & 0x03030303u) + 0x7f7f7f7fu) ^ 0x80808080u;
+                    }
+                d0 = h ? 0.0f : h2f(w.d & 0xffffu);
+            } else if constexpr (KIND == kTQ1_0) {
+                // Base-3 digits of four code bytes at a time: with a byte y in each 16-bit lane,
+                // y * 3 carries the next digit into the lane's high byte and leaves the rest of
+                // the base-3 fraction (y * 3 mod 256) in its low byte.  The digits d (0..2)
+                // then select d - 1 as a signed byte from {0xff, 0x00, 0x01}.
+                uint32_t op[32];
+                auto digits = [&](uint32_t x, int nd, uint32_t *dst) {
+                    uint32_t L = x & 0x00ff00ffu, H = (x >> 8) & 0x00ff00ffu;
+#pragma unroll
+                    for (int k = 0; k < nd; ++k) {
+                        const uint32_t mL = L * 3u, mH = H * 3u;  // no carry out of a lane: 255 * 3 < 2^16
+                        dst[k] = perm(0u, 0x000100ffu, perm(mH, mL, 0x07030501u));  // high bytes, in byte order
+                        L = mL & 0x00ff00ffu;
+                        H = mH & 0x00ff00ffu;
+                    }
+                };
+#pragma unroll
+                for (uint32_t c = 0; c < 6; ++c) digits(w.c[c >> 1][c & 1], 5, op + 5 * c);
+                uint32_t t4[4];
+                digits(w.tail, 4, t4);
+                const uint32_t pick = h ? 0x07060302u : 0x05040100u;  // bytes 2h, 2h+1 of two digit dwords
+                op[30] = perm(t4[1], t4[0], pick);
+                op[31] = perm(t4[3], t4[2], pick);
+#pragma unroll
+                for (uint32_t n = 0; n < 32; ++n) aw[n >> 2][n & 3] = op[n];
+                d0 = h ? 0.0f : h2f(w.d & 0xffffu);
             } else {
                 // Codes 0..2 -> signed bytes c - 1: +0x7f per byte (no carry out of a byte),
                 // then the sign bit flipped.
@@ -372,7 +486,7 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
                 return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, aw[s]), __builtin_bit_cast(v4i, bx),
                                                              acc, 0, 0, 0);
             };
-            if constexpr (kQ2) {
+            if constexpr (kQ2 || kTQ) {
                 // isum: each token group's chain of eight K-steps; the chains run side by side
                 // (a dependent MFMA waits for its predecessor's result), and a single token
                 // group splits its chain into even and odd K-steps, added at the end (exact).
@@ -394,17 +508,27 @@ __global__ __launch_bounds__(256) void k_prefill_kq(const uint8_t *__restrict__ 
 #pragma unroll
                         for (int ct = 0; ct < CT; ++ct) is[ct] = kstep(s, ct, is[ct]);
                 }
+                if constexpr (kTQ) {
 #pragma unroll
-                for (int ct = 0; ct < CT; ++ct) {
-                    const uint32_t tok = 32 * ct + r32;
-                    const float a = h ? 0.0f : scl[0][tok];
-                    const v16f f1 = __builtin_amdgcn_mfma_f32_32x32x2f32(d0, a, v16f{}, 0, 0, 0);  // fl(as * d)
-                    const v16f f2 = __builtin_amdgcn_mfma_f32_32x32x2f32(d1, a, v16f{}, 0, 0, 0);  // fl(as * dmin)
-                    const v8h bsum = *reinterpret_cast<const v8h *>(&bsm[h][tok * 16]);
-                    const v16f ms = __builtin_amdgcn_mfma_f32_32x32x16_f16(mn, bsum, v16f{}, 0, 0, 0);
+                    for (int ct = 0; ct < CT; ++ct) {
+                        const float a = h ? 0.0f : scl[0][32 * ct + r32];
+                        const v16f dd = __builtin_amdgcn_mfma_f32_32x32x2f32(d0, a, v16f{}, 0, 0, 0);  // fl(d * as)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        o[ct][r] = o[ct][r] + (f1[r] * static_cast<float>(is[ct][r]) - f2[r] * ms[r]);
+                        for (int r = 0; r < 16; ++r) o[ct][r] = o[ct][r] + static_cast<float>(is[ct][r]) * dd[r];
+                    }
+                } else {
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct) {
+                        const uint32_t tok = 32 * ct + r32;
+                        const float a = h ? 0.0f : scl[0][tok];
+                        const v16f f1 = __builtin_amdgcn_mfma_f32_32x32x2f32(d0, a, v16f{}, 0, 0, 0);  // fl(as * d)
+                        const v16f f2 = __builtin_amdgcn_mfma_f32_32x32x2f32(d1, a, v16f{}, 0, 0, 0);  // fl(as * dmin)
+                        const v8h bsum = *reinterpret_cast<const v8h *>(&bsm[h][tok * 16]);
+                        const v16f ms = __builtin_amdgcn_mfma_f32_32x32x16_f16(mn, bsum, v16f{}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            o[ct][r] = o[ct][r] + (f1[r] * static_cast<float>(is[ct][r]) - f2[r] * ms[r]);
+                    }
                 }
             } else if constexpr (kQ8) {
                 // dot_legacy's chain, block by block: Y = Y + fl(fl(ws_s * as_s) * float(I_s)),
@@ -498,21 +622,22 @@ size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens) {
     return align256(Mp * cols) + align256(nu * Mp * 4 * 8) + nu * Mp * 32;
 }
 
-// Tokens from which Q2_K, PQ2 (Q8_K activations) and Q8_0 take the GEMM rather than the
-// skinny kernel (16 tokens per launch).  Measured (f32 input with its quantization, us, skinny /
-// GEMM): Q2_K 6144 x 2048 16 tokens 8.0 / 15.8, 32 tokens 11.4 / 16.8, 64 tokens 24 / 17.4,
-// 2048 tokens 640 / 93.8; 12288 x 4096 32 tokens Q2_K 23.5 / 26.3, Q8_0 36.3 / 39.7.  Large
-// matrices leave the skinny kernel sooner: 151936 x 4096 16 tokens Q2_K 70.5 / 68.7, PQ2 74.1
-// / 57.8, Q8_0 169.5 / 144.5; 32 tokens Q2_K 137 / 74, PQ2 147 / 63, Q8_0 338 / 154.
+// Tokens from which the GEMM takes over from the skinny kernel (16 tokens per launch).
+// Measured (f32 input with its quantization, us, skinny / GEMM): Q2_K 6144 x 2048 16 tokens
+// 8.0 / 15.8, 32 tokens 11.4 / 16.8, 64 tokens 24 / 17.4, 2048 tokens 640 / 93.8; 12288 x
+// 4096 32 tokens Q2_K 23.5 / 26.3, Q8_0 36.3 / 39.7, TQ2_0 22.2 / 21.1, TQ1_0 27.5 / 24.2;
+// 6144 x 2048 32 tokens TQ2_0 10.9 / 14.2, TQ1_0 16.9 / 15.7, 16 tokens TQ1_0 11.0 / 15.2.
+// Large matrices leave the skinny kernel sooner: 151936 x 4096 16 tokens Q2_K 70.5 / 68.7,
+// PQ2 74.1 / 57.8, Q8_0 169.5 / 144.5; 32 tokens Q2_K 137 / 74, PQ2 147 / 63, Q8_0 338 / 154.
 constexpr uint32_t kGemmMinTokens = 48, kGemmMinTokensLarge = 16;
 constexpr uint64_t kLargeRows = 65536;
 
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens) {
     // Codes, sums and scales are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols * padded_tokens(tokens);
-    return (kind == kQ2_K || kind == kPQ2 || kind == kQ8_0) && cols % kUnit == 0 && cols <= 65536 && rows > 0 &&
-           rows < (1ull << 31) && code_bytes < (1ull << 31) &&
-           tokens >= (rows >= kLargeRows ? kGemmMinTokensLarge : kGemmMinTokens);
+    const bool kinds = kind == kQ2_K || kind == kPQ2 || kind == kQ8_0 || kind == kTQ1_0 || kind == kTQ2_0;
+    return kinds && cols % kUnit == 0 && cols <= 65536 && rows > 0 && rows < (1ull << 31) &&
+           code_bytes < (1ull << 31) && tokens >= (rows >= kLargeRows ? kGemmMinTokensLarge : kGemmMinTokens);
 }
 
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
@@ -526,12 +651,16 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     constexpr uint32_t kTok = 4;
     static_assert(kTokAlign % kTok == 0, "the prep takes whole token groups");
     const dim3 pgrid(Mp / kTok * ((K + 1023) / 1024)), pblock(64 * kTok);
-    if (kind == kQ2_K)
-        hipLaunchKernelGGL((k_prefill_k_prep<kQ2_K, kTok>), pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
-    else if (kind == kQ8_0)
-        hipLaunchKernelGGL((k_prefill_k_prep<kQ8_0, kTok>), pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
-    else
-        hipLaunchKernelGGL((k_prefill_k_prep<kPQ2, kTok>), pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
+    auto prep = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
+    };
+    switch (kind) {
+        case kQ2_K: prep(k_prefill_k_prep<kQ2_K, kTok>); break;
+        case kQ8_0: prep(k_prefill_k_prep<kQ8_0, kTok>); break;
+        case kTQ1_0: prep(k_prefill_k_prep<kTQ1_0, kTok>); break;
+        case kTQ2_0: prep(k_prefill_k_prep<kTQ2_0, kTok>); break;
+        default: prep(k_prefill_k_prep<kPQ2, kTok>);
+    }
     if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
     const auto W = static_cast<const uint8_t *>(w_tiled);
@@ -552,6 +681,10 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     };
     if (kind == kQ2_K)
         nt == 64 ? go(k_prefill_kq<kQ2_K, 2, false>) : go(k_prefill_kq<kQ2_K, 1, false>);
+    else if (kind == kTQ1_0)
+        nt == 64 ? go(k_prefill_kq<kTQ1_0, 2, false>) : go(k_prefill_kq<kTQ1_0, 1, false>);
+    else if (kind == kTQ2_0)
+        nt == 64 ? go(k_prefill_kq<kTQ2_0, 2, false>) : go(k_prefill_kq<kTQ2_0, 1, false>);
     else if (kind == kQ8_0)
         go(k_prefill_kq<kQ8_0, 1, false>);
     else if (pinned)

@@ -470,16 +470,18 @@ def test_gpu_ptq1_table_batch_matches_per_token_oracle(ctx, cols, tokens):
 @pytest.mark.parametrize("rows", [1024 + 53, 20480 + 37, 40960 + 37, 65536 + 37, 131072 + 37])
 @pytest.mark.parametrize("kind,cols", [(ph.KIND_PTQ1, 128), (ph.KIND_PTQ1, 384), (ph.KIND_PTQ1, 512), (ph.KIND_PQ2, 512),
                                        (ph.KIND_PQ2, 384), (ph.KIND_Q2_K, 512), (ph.KIND_Q8_0, 256),
-                                       (ph.KIND_TQ1_0, 512), (ph.KIND_TQ2_0, 256)])
+                                       (ph.KIND_TQ1_0, 512), (ph.KIND_TQ2_0, 256), (ph.KIND_TQ1_0, 1280),
+                                       (ph.KIND_TQ2_0, 768)])
 def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     """2..17 tokens run weights-once on the int8 matrix cores, 16 rows per block: the
     row counts cover 8, 4, 2 and 1 wavefronts per block (K split over the workgroup,
     terms folded through LDS), and rows x tokens cover both activation sources (prepared
     blocks gathered directly, or a lane-ordered copy); pinned PTQ1 takes four masked
     MFMAs per group (one per native lane subset), at most two wavefronts per block;
-    TQ1_0 / TQ2_0 run the row-tile batch kernel.  Each token's row must equal its own matvec, in
-    every contract, with partial chunks of the 16-token batch, a partial last tile and
-    16-row block."""
+    TQ1_0 / TQ2_0 take each unit's integer from four MFMAs on signed digits or fields (TQ1_0's
+    last byte of each lane group gathered at stride 4).  Each token's row must equal its own
+    matvec, in every contract, with partial chunks of the 16-token batch, a partial last tile
+    and 16-row block."""
     import oracle
 
     w = synth.weights(kind, rows, cols, seed=41) if kind != ph.KIND_PQ2 else synth.pq2_weights(rows, cols, 41, 4)
@@ -626,19 +628,21 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
     ctx.release(wid)
 
 
-@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0])
+@pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0, ph.KIND_TQ1_0, ph.KIND_TQ2_0])
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 48), (64, 256, 49), (130, 1024, 300), (37, 512, 129),
                                          (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64),
-                                         (65536 + 37, 256, 16), (32768 + 37, 256, 128)])
+                                         (300, 1280, 16), (65536 + 37, 256, 16), (32768 + 37, 256, 128)])
 def test_gpu_k_prefill_gemm_equals_per_token_matvec(ctx, kind, rows, cols, M):
-    """Q2_K and PQ2 (Q8_K activations) and Q8_0 prefill from 48 tokens (16 on matrices of at
-    least 65536 rows) runs as one int8-MFMA GEMM, 32 or 64 tokens per workgroup.  Q2_K: isum from the matrix cores on scale-weighted
+    """Q2_K, PQ2, TQ1_0 and TQ2_0 (Q8_K activations) and Q8_0 prefill runs as one int8-MFMA
+    GEMM, 32 or 64 tokens per workgroup: from 48 tokens (16 on matrices of at least 65536
+    rows; 16 tokens of 300 rows take the skinny kernel).  Q2_K: isum from the matrix cores on scale-weighted
     codes, msum from a binary16 product of the sub-block mins and sums, the two outer products
     of the token and row scales; PQ2: each 128-element block's integer dot on signed codes and
     its outer product of scales, folded unfused or fused by contract; Q8_0: each 32-element
-    block's dot and scale product, folded block by block.  Every token row equals the
-    reference's per-token matvec bit for bit, in both contracts (partial row tiles, a
-    single-unit row, padding tokens, an all-zero token, the XCD-major grid)."""
+    block's dot and scale product, folded block by block; TQ1_0 / TQ2_0: the unit's integer
+    dot on the signed base-3 digits or 2-bit fields and one outer product of scales.  Every
+    token row equals the reference's per-token matvec bit for bit, in both contracts (partial
+    row tiles, a single-unit row, padding tokens, an all-zero token, the XCD-major grid)."""
     import oracle
 
     w = synth.weights(kind, rows, cols, seed=rows + M)
