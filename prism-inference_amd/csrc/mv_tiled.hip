@@ -2849,16 +2849,21 @@ bool batch_eligible(const MatvecArgs &a) {
 // then contiguous loads) instead of gathering them from the prepared blocks in every
 // wavefront.  Measured on 2048..151936 rows: the copy pays from 8192 rows or from 5
 // tokens; Q2_K's 256-element units halve its gathers (as TQ2_0's, in the same order), and
-// the copy pays only from 32768 rows.
+// the copy pays only from 32768 rows.  PQ2 and Q8_0 rows of 12288 inputs or more take it
+// from two tokens (us, gathered / copied: PQ2 5120 x 17408 3 tokens 37.6 / 30.1, 4096 x
+// 14336 4 tokens 26.5 / 24.6; Q8_0 4096 x 14336 2 tokens 31.6 / 28.6); PTQ1 there is mixed
+// (4096 x 14336 4 tokens 31.3 / 38.4, 5120 x 17408 55.4 / 45.9) and keeps the rule above.
 template <Op O>
-bool skinny_lane_ordered(uint64_t rows, uint32_t ntok) {
+bool skinny_lane_ordered(uint64_t rows, uint64_t cols, uint32_t ntok) {
     if constexpr (O == Op::Q2K || O == Op::TQ2) return rows >= 32768;
+    if constexpr (O == Op::Q8_0 || kind_of<O>() == kPQ2)
+        if (cols >= 12288) return true;
     return rows >= 8192 || ntok > 4;
 }
 
 template <Op O>
 size_t skinny_scratch(const MatvecArgs &a) {
-    if (!skinny_lane_ordered<O>(a.rows, a.tokens < kBatchMax ? a.tokens : kBatchMax)) return 0;
+    if (!skinny_lane_ordered<O>(a.rows, a.cols, a.tokens < kBatchMax ? a.tokens : kBatchMax)) return 0;
     const uint64_t nu = a.cols / unit_weights<O>();
     return nu * 64u * (sk_lane_bytes<O>() + 4u);
 }
@@ -2866,7 +2871,7 @@ size_t skinny_scratch(const MatvecArgs &a) {
 template <Op O>
 int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t act_stride, float *out,
                   const float *residual) {
-    const bool sw = skinny_lane_ordered<O>(a.rows, ntok);
+    const bool sw = skinny_lane_ordered<O>(a.rows, a.cols, ntok);
     if (sw && (!a.scratch || a.scratch_bytes < skinny_scratch<O>(a))) return -2;
     const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
     if (sw) {

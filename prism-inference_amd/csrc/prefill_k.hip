@@ -629,15 +629,21 @@ size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens) {
 // 6144 x 2048 32 tokens TQ2_0 10.9 / 14.2, TQ1_0 16.9 / 15.7, 16 tokens TQ1_0 11.0 / 15.2.
 // Large matrices leave the skinny kernel sooner: 151936 x 4096 16 tokens Q2_K 70.5 / 68.7,
 // PQ2 74.1 / 57.8, Q8_0 169.5 / 144.5; 32 tokens Q2_K 137 / 74, PQ2 147 / 63, Q8_0 338 / 154.
-constexpr uint32_t kGemmMinTokens = 48, kGemmMinTokensLarge = 16;
-constexpr uint64_t kLargeRows = 65536;
+// From 16384 rows, 17 tokens (two skinny launches) already take the GEMM: 17 / 32 tokens,
+// Q2_K 17408 x 5120 36.0 / 31.2 and 41.8 / 32.1, 32768 x 4096 44.8 / 27.6 and 45.3 / 29.0;
+// PQ2 16384 x 4096 30.6 / 23.0, Q8_0 24576 x 4096 57.8 / 40.7, TQ1_0 17408 x 5120 41.6 /
+// 27.8 (17 tokens); at 12288 x 4096 the skinny kernel keeps Q2_K, Q8_0 and TQ2_0 (Q2_K 21.3 /
+// 25.3, Q8_0 36.3 / 39.0).
+constexpr uint32_t kGemmMinTokens = 48, kGemmMinTokensMid = 17, kGemmMinTokensLarge = 16;
+constexpr uint64_t kMidRows = 16384, kLargeRows = 65536;
 
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens) {
     // Codes, sums and scales are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols * padded_tokens(tokens);
     const bool kinds = kind == kQ2_K || kind == kPQ2 || kind == kQ8_0 || kind == kTQ1_0 || kind == kTQ2_0;
     return kinds && cols % kUnit == 0 && cols <= 65536 && rows > 0 && rows < (1ull << 31) &&
-           code_bytes < (1ull << 31) && tokens >= (rows >= kLargeRows ? kGemmMinTokensLarge : kGemmMinTokens);
+           code_bytes < (1ull << 31) &&
+           tokens >= (rows >= kLargeRows ? kGemmMinTokensLarge : rows >= kMidRows ? kGemmMinTokensMid : kGemmMinTokens);
 }
 
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,

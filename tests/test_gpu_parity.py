@@ -631,11 +631,12 @@ def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
 @pytest.mark.parametrize("kind", [ph.KIND_Q2_K, ph.KIND_PQ2, ph.KIND_Q8_0, ph.KIND_TQ1_0, ph.KIND_TQ2_0])
 @pytest.mark.parametrize("rows,cols,M", [(200, 2048, 48), (64, 256, 49), (130, 1024, 300), (37, 512, 129),
                                          (6144, 2048, 128), (192, 512, 1030), (100, 768, 513), (6044, 4096, 64),
-                                         (300, 1280, 16), (65536 + 37, 256, 16), (32768 + 37, 256, 128)])
+                                         (300, 1280, 16), (65536 + 37, 256, 16), (32768 + 37, 256, 128),
+                                         (16384 + 37, 512, 20)])
 def test_gpu_k_prefill_gemm_equals_per_token_matvec(ctx, kind, rows, cols, M):
     """Q2_K, PQ2, TQ1_0 and TQ2_0 (Q8_K activations) and Q8_0 prefill runs as one int8-MFMA
-    GEMM, 32 or 64 tokens per workgroup: from 48 tokens (16 on matrices of at least 65536
-    rows; 16 tokens of 300 rows take the skinny kernel).  Q2_K: isum from the matrix cores on scale-weighted
+    GEMM, 32 or 64 tokens per workgroup: from 48 tokens (17 on matrices of at least 16384
+    rows, 16 from 65536 rows; 16 tokens of 300 rows take the skinny kernel).  Q2_K: isum from the matrix cores on scale-weighted
     codes, msum from a binary16 product of the sub-block mins and sums, the two outer products
     of the token and row scales; PQ2: each 128-element block's integer dot on signed codes and
     its outer product of scales, folded unfused or fused by contract; Q8_0: each 32-element
