@@ -78,13 +78,13 @@ bool tiled_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t cus);
 int launch_repack(const void *native, void *tiled, uint32_t kind, uint64_t cols, uint64_t rows, hipStream_t s);
 // Tiled-prefill GEMM: quantizes x[M][cols] once and multiplies it by the tiled weights on
 // the matrix cores; every output row is bit-identical to its own per-token matvec.  PTQ1
-// in either contract (the pinned one from kPinnedGemmMinTokens tokens) on the f16 matrix
-// cores (prefill.hip); Q2_K and PQ2 (Q8_K activations) and Q8_0 on the int8 matrix cores
-// (prefill_k.hip).
+// in either contract on the f16 matrix cores (prefill.hip); Q2_K, PQ2, TQ1_0 and TQ2_0 (Q8_K
+// activations) and Q8_0 on the int8 matrix cores (prefill_k.hip).
 bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens);
 size_t prefill_scratch_bytes(uint32_t kind, uint64_t cols, uint32_t tokens);
+// cus: the device's compute units (the block-split kernel runs one workgroup per CU).
 int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
-                   int pinned, float *out, void *scratch, int *err, hipStream_t s);
+                   int pinned, float *out, void *scratch, int *err, hipStream_t s, uint32_t cus);
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens);
 size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens);
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,

@@ -1150,8 +1150,9 @@ struct SkParams {
     float *out;         // [ntok][rows]
     const float *residual;
     int *err;
-    uint32_t rows, nu, ntok;
-    uint32_t act_stride;  // prepared blocks: bytes per token
+    uint32_t rows, nu, ntok;  // ntok: every chunk's tokens (16 per chunk, the last one fewer)
+    uint32_t act_stride;      // prepared blocks: bytes per token
+    uint32_t sw_chunk;        // bytes from one chunk's activations in `sw` to the next's
 };
 
 // binary32 terms per unit and (row, token) element of the skinny kernel: those of the
@@ -1362,6 +1363,11 @@ __global__ __launch_bounds__(256) void k_sk_prep(const uint8_t *__restrict__ act
                                                  uint32_t nu, uint32_t *__restrict__ sw) {
     constexpr uint32_t LD = sk_lane_bytes<O>() / 4;
     const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    // Chunk blockIdx.y: tokens 16y .. 16y + 15 of the batch, its copy nu * 64 * (LD + 1)
+    // dwords after the previous chunk's.
+    act += static_cast<size_t>(16u * blockIdx.y) * act_stride;
+    ntok = ntok - 16u * blockIdx.y < 16u ? ntok - 16u * blockIdx.y : 16u;
+    sw += static_cast<size_t>(blockIdx.y) * nu * 64u * (LD + 1u);
     if (idx < nu * 64u * LD) {
         const uint32_t k = idx % LD, lane = (idx / LD) & 63u, u = idx / (LD * 64u);
         const uint32_t i = lane & 15u, tok = i < ntok ? i : ntok - 1u;
@@ -1754,6 +1760,9 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
     const uint32_t left = p.rows - tile * kTile;
     const uint32_t trows = left < kTile ? left : kTile;
     if (16u * quarter >= trows) return;
+    // Chunk blockIdx.y: tokens 16y .. 16y + ntok - 1.
+    const uint32_t t0 = 16u * blockIdx.y, ntok = p.ntok - t0 < 16u ? p.ntok - t0 : 16u;
+    const uint8_t *sw = p.sw + static_cast<size_t>(blockIdx.y) * p.sw_chunk;
     SkLane L;
     L.s = lane >> 4;
     L.lane = lane;
@@ -1763,16 +1772,16 @@ __global__ __launch_bounds__(64 * KS) void k_mv_skinny(SkParams p) {
     L.ra = 16u * quarter + i;
     L.rc = 16u * quarter + 4u * L.s;
     if constexpr (SW) {
-        L.sw = p.sw;
-        L.scales = p.sw + static_cast<size_t>(p.nu) * 64u * sk_lane_bytes<O>();
+        L.sw = sw;
+        L.scales = sw + static_cast<size_t>(p.nu) * 64u * sk_lane_bytes<O>();
     } else {
-        L.sw = p.sw + static_cast<size_t>(i < p.ntok ? i : p.ntok - 1u) * p.act_stride;
+        L.sw = sw + static_cast<size_t>(i < ntok ? i : ntok - 1u) * p.act_stride;
         L.scales = nullptr;
     }
     const Ptq1Plan pp = ptq1_plan(L.s);
-    const size_t obase = static_cast<size_t>(tile) * kTile + 16u * quarter;
+    const size_t obase = static_cast<size_t>(t0) * p.rows + static_cast<size_t>(tile) * kTile + 16u * quarter;
     auto store = [&](uint32_t tok, uint32_t r, float v) {  // r: row within the 16-row block
-        if (tok < p.ntok && 16u * quarter + r < trows) {
+        if (tok < ntok && 16u * quarter + r < trows) {
             const size_t at = static_cast<size_t>(tok) * p.rows + obase + r;
             if (p.residual) v = v + p.residual[at];
             p.out[at] = v;
@@ -2861,27 +2870,39 @@ bool skinny_lane_ordered(uint64_t rows, uint64_t cols, uint32_t ntok) {
     return rows >= 8192 || ntok > 4;
 }
 
+// 16-token chunks per skinny launch: the chunks run side by side (grid y), each a batch
+// of its own, so a launch of up to kSkChunks * 16 tokens fills the chip where one chunk
+// leaves it latency-bound.  Four chunks keep the lane-ordered copies under 10 MB at
+// 65536 inputs.
+constexpr uint32_t kSkChunks = 4;
+
 template <Op O>
 size_t skinny_scratch(const MatvecArgs &a) {
     if (!skinny_lane_ordered<O>(a.rows, a.cols, a.tokens < kBatchMax ? a.tokens : kBatchMax)) return 0;
     const uint64_t nu = a.cols / unit_weights<O>();
-    return nu * 64u * (sk_lane_bytes<O>() + 4u);
+    const uint64_t chunks = (a.tokens + kBatchMax - 1) / kBatchMax;
+    return nu * 64u * (sk_lane_bytes<O>() + 4u) * (chunks < kSkChunks ? chunks : kSkChunks);
 }
 
+// ntok: up to kSkChunks * 16 tokens, one chunk of 16 per grid row.
 template <Op O>
 int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t act_stride, float *out,
                   const float *residual) {
-    const bool sw = skinny_lane_ordered<O>(a.rows, a.cols, ntok);
+    const uint32_t chunks = (ntok + kBatchMax - 1) / kBatchMax;
+    if (chunks > kSkChunks) return -2;
+    const bool sw = skinny_lane_ordered<O>(a.rows, a.cols, ntok < kBatchMax ? ntok : kBatchMax);
     if (sw && (!a.scratch || a.scratch_bytes < skinny_scratch<O>(a))) return -2;
     const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
+    const uint32_t sw_chunk = nu * 64u * (sk_lane_bytes<O>() + 4u);
     if (sw) {
         const uint32_t nprep = nu * 64u * (sk_lane_bytes<O>() / 4u);
-        hipLaunchKernelGGL(k_sk_prep<O>, dim3((nprep + 255u) / 256u), dim3(256), 0, a.stream,
+        hipLaunchKernelGGL(k_sk_prep<O>, dim3((nprep + 255u) / 256u, chunks), dim3(256), 0, a.stream,
                            static_cast<const uint8_t *>(act), act_stride, ntok, nu, static_cast<uint32_t *>(a.scratch));
     }
     SkParams p{};
     p.w = a.w;
     p.sw = static_cast<const uint8_t *>(sw ? a.scratch : act);
+    p.sw_chunk = sw ? sw_chunk : kBatchMax * act_stride;
     p.act_stride = act_stride;
     p.out = out;
     p.residual = residual;
@@ -2898,7 +2919,7 @@ int launch_skinny(const MatvecArgs &a, const void *act, uint32_t ntok, uint32_t 
     // element cap it at two wavefronts per block (48 KiB).
     constexpr int kMaxKs = sk_terms_per_unit<O>() > 8 ? 2 : 8;
     if (ks > kMaxKs) ks = kMaxKs;
-    const dim3 grid(static_cast<uint32_t>(blocks)), block(64 * ks);
+    const dim3 grid(static_cast<uint32_t>(blocks), chunks), block(64 * ks);
     auto go = [&]<bool SWv>() {
         if (ks == 1) hipLaunchKernelGGL((k_mv_skinny<O, SWv, 1>), grid, block, 0, a.stream, p);
         else if (ks == 2) hipLaunchKernelGGL((k_mv_skinny<O, SWv, 2>), grid, block, 0, a.stream, p);
@@ -3077,8 +3098,8 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     if (batched && lut_batch_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_lut_batch<O>(a, static_cast<uint32_t>(in_stride)); });
     if (batched && skinny_eligible(a)) {
-        for (uint32_t tok = 0; tok < a.tokens; tok += kBatchMax) {
-            const uint32_t n = a.tokens - tok < kBatchMax ? a.tokens - tok : kBatchMax;
+        for (uint32_t tok = 0; tok < a.tokens; tok += kSkChunks * kBatchMax) {
+            const uint32_t n = a.tokens - tok < kSkChunks * kBatchMax ? a.tokens - tok : kSkChunks * kBatchMax;
             const void *act = static_cast<const uint8_t *>(a.act) + in_stride * tok;
             float *out = a.out + a.rows * tok;
             const float *res = a.residual ? a.residual + a.rows * tok : nullptr;

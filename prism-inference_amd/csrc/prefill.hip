@@ -660,24 +660,25 @@ size_t prefill_scratch_bytes(uint32_t kind, uint64_t cols, uint32_t tokens) {
     return ((Mp * cols * 2 + 255) & ~size_t(255)) + Mp * (cols / 32) * 4;
 }
 
-// Tokens from which PTQ1 takes the GEMM rather than the skinny kernel (16 tokens per launch,
-// each unit decoded once per launch).  Measured, pinned, 6144 x 2048: 16 tokens 33 against 24
-// us, 32 tokens 34 against 45 us, 2048 tokens 275 against 2629 us.  Source (f32 input with its
-// quantization, GEMM / skinny, us): 6144 x 2048 16 tokens 18.9 / 13.9, 32 tokens 19.7 / 24.5;
-// 12288 x 4096 30.2 / 20.9 and 31.4 / 39.3; 151936 x 4096 139 / 93 and 144 / 183.
-constexpr uint32_t kPinnedGemmMinTokens = 32, kSourceGemmMinTokens = 32;
+// Tokens from which PTQ1 takes the GEMM rather than the skinny kernel (up to four 16-token
+// chunks side by side per launch, each unit decoded once per chunk).  Measured (f32 input
+// with its quantization, GEMM / skinny, us): 16 tokens 6144 x 2048 18.9 / 13.9, 12288 x 4096
+// 30.2 / 20.9, 151936 x 4096 139 / 93; 32 tokens source 6144 x 2048 20.0 / 17.3, 12288 x 4096
+// 31.6 / 31.8, 17408 x 5120 38.2 / 46.6, 32768 x 4096 41.7 / 54.8; pinned 6144 x 2048 31.6 /
+// 27.0, 12288 x 4096 56.7 / 73.7; 48 tokens source 6144 x 2048 20.3 / 21.4, pinned 32.3 / 42.4.
+static uint32_t ptq1_gemm_min_tokens(uint64_t rows) { return rows < 8192 ? 33 : 32; }
 
 bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, uint32_t tokens) {
     if (kind != kPTQ1) return prefill_k_supported(kind, cols, rows, tokens);
     // The token codes are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols / 128 * 8u * padded_tokens(tokens) * 32u;
-    if (tokens < (pinned ? kPinnedGemmMinTokens : kSourceGemmMinTokens)) return false;
+    if (tokens < ptq1_gemm_min_tokens(rows)) return false;
     return kind == kPTQ1 && cols % 128 == 0 && cols <= 65536 && rows > 0 &&
            (rows * (cols / 128) * 28) < (1ull << 40) && code_bytes < (1ull << 31);
 }
 
 int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
-                   int pinned, float *out, void *scratch, int *err, hipStream_t s) {
+                   int pinned, float *out, void *scratch, int *err, hipStream_t s, uint32_t cus) {
     if (kind != kPTQ1) return launch_prefill_k(kind, w_tiled, cols, rows, x, M, pinned, out, scratch, err, s);
     const uint32_t K = static_cast<uint32_t>(cols), Mp = padded_tokens(M);
     if (static_cast<uint64_t>(K / 128) * 8u * Mp * 32u >= (1ull << 31)) return kLaunchUnsupported;
@@ -738,7 +739,9 @@ int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t r
             hipLaunchKernelGGL(k_prefill_ptq1<1>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
         return launch_status();
     }
-    if (M <= kSplitMaxTokens) {
+    // The block-split kernel holds one workgroup per CU: with more workgroups than CUs its
+    // grid runs in two rounds (17408 x 5120, 48 tokens: 69.1 us against 38.2 at 32 tokens).
+    if (M <= kSplitMaxTokens && static_cast<uint64_t>(gx) * ((M + 31) / 32) <= cus) {
         const uint32_t groups = (M + 31) / 32;  // token groups holding real tokens
         const uint32_t xcd_major = groups % 8 == 0 && gx <= 65535;
         const dim3 grid = xcd_major ? dim3(8, gx, groups / 8) : dim3(gx, groups);

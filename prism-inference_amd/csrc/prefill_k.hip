@@ -622,28 +622,29 @@ size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens) {
     return align256(Mp * cols) + align256(nu * Mp * 4 * 8) + nu * Mp * 32;
 }
 
-// Tokens from which the GEMM takes over from the skinny kernel (16 tokens per launch).
-// Measured (f32 input with its quantization, us, skinny / GEMM): Q2_K 6144 x 2048 16 tokens
-// 8.0 / 15.8, 32 tokens 11.4 / 16.8, 64 tokens 24 / 17.4, 2048 tokens 640 / 93.8; 12288 x
-// 4096 32 tokens Q2_K 23.5 / 26.3, Q8_0 36.3 / 39.7, TQ2_0 22.2 / 21.1, TQ1_0 27.5 / 24.2;
-// 6144 x 2048 32 tokens TQ2_0 10.9 / 14.2, TQ1_0 16.9 / 15.7, 16 tokens TQ1_0 11.0 / 15.2.
-// Large matrices leave the skinny kernel sooner: 151936 x 4096 16 tokens Q2_K 70.5 / 68.7,
-// PQ2 74.1 / 57.8, Q8_0 169.5 / 144.5; 32 tokens Q2_K 137 / 74, PQ2 147 / 63, Q8_0 338 / 154.
-// From 16384 rows, 17 tokens (two skinny launches) already take the GEMM: 17 / 32 tokens,
-// Q2_K 17408 x 5120 36.0 / 31.2 and 41.8 / 32.1, 32768 x 4096 44.8 / 27.6 and 45.3 / 29.0;
-// PQ2 16384 x 4096 30.6 / 23.0, Q8_0 24576 x 4096 57.8 / 40.7, TQ1_0 17408 x 5120 41.6 /
-// 27.8 (17 tokens); at 12288 x 4096 the skinny kernel keeps Q2_K, Q8_0 and TQ2_0 (Q2_K 21.3 /
-// 25.3, Q8_0 36.3 / 39.0).
-constexpr uint32_t kGemmMinTokens = 48, kGemmMinTokensMid = 17, kGemmMinTokensLarge = 16;
-constexpr uint64_t kMidRows = 16384, kLargeRows = 65536;
+// Tokens from which the GEMM takes over from the skinny kernel, which runs up to four
+// 16-token chunks side by side per launch.  Measured (f32 input with its quantization, us,
+// skinny / GEMM):
+// - below 8192 rows the skinny kernel stays ahead to 64 tokens (6144 x 2048, 48 tokens: Q2_K
+//   10.8 / 17.6, PQ2 14.1 / 15.6, Q8_0 16.8 / 23.7, TQ2_0 10.2 / 14.4; 64 tokens: Q2_K 12.1 /
+//   17.3);
+// - below 16384 rows to 48 tokens (12288 x 4096, 48 tokens: Q2_K 27.1 / 28.2, PQ2 26.1 /
+//   24.0; 64 tokens: Q2_K 33.7 / 27.3, Q8_0 52.7 / 41.3);
+// - from 16384 rows the GEMM wins from 17 tokens (17 / 32 tokens: Q2_K 32768 x 4096 38.4 /
+//   26.9 and 38.3 / 28.3, PQ2 17408 x 5120 30.6 / 26.8 and 30.7 / 28.4, TQ2_0 17408 x 5120
+//   26.5 / 23.6; Q8_0 17408 x 5120 48.3 / 47.6);
+// - from 65536 rows from 16 (151936 x 4096: Q2_K 70.5 / 68.7, PQ2 74.1 / 57.8, Q8_0 169.5 /
+//   144.5).
+static uint32_t gemm_min_tokens(uint64_t rows) {
+    return rows >= 65536 ? 16 : rows >= 16384 ? 17 : rows >= 8192 ? 48 : 65;
+}
 
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens) {
     // Codes, sums and scales are addressed with 32-bit buffer offsets.
     const uint64_t code_bytes = cols * padded_tokens(tokens);
     const bool kinds = kind == kQ2_K || kind == kPQ2 || kind == kQ8_0 || kind == kTQ1_0 || kind == kTQ2_0;
     return kinds && cols % kUnit == 0 && cols <= 65536 && rows > 0 && rows < (1ull << 31) &&
-           code_bytes < (1ull << 31) &&
-           tokens >= (rows >= kLargeRows ? kGemmMinTokensLarge : rows >= kMidRows ? kGemmMinTokensMid : kGemmMinTokens);
+           code_bytes < (1ull << 31) && tokens >= gemm_min_tokens(rows);
 }
 
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,

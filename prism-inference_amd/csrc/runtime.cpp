@@ -29,7 +29,7 @@ int project_f32_dev(prism_hip_ctx *c, const Weight &w, const float *x, uint32_t 
         void *pre = nullptr;
         int rc = scr.get(c->pre, prefill_scratch_bytes(w.kind, w.cols, tokens), &pre);
         if (rc) return rc;
-        rc = launch_result(c, launch_prefill(w.kind, w.dev, w.cols, w.rows, x, tokens, pinned, out, pre, c->err, s),
+        rc = launch_result(c, launch_prefill(w.kind, w.dev, w.cols, w.rows, x, tokens, pinned, out, pre, c->err, s, c->cus),
                            "prefill launch");
         // The residual joins after the projection, one binary32 add per output (as the
         // row kernels do in their epilogue).

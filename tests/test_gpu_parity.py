@@ -598,20 +598,21 @@ def test_gpu_prefill_and_mul_mat_equal_per_token_matvec(ctx):
         ctx.release(wid)
 
 
-@pytest.mark.parametrize("rows,cols,M", [(200, 2048, 32), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
+@pytest.mark.parametrize("rows,cols,M", [(200, 2048, 33), (64, 384, 37), (130, 1024, 300), (6144, 2048, 128),
                                          (192, 512, 1030), (96, 256, 4100), (100, 256, 200), (320, 512, 512),
                                          (96, 256, 4096), (130, 1152, 1100), (6144, 2048, 1024),
                                          (6044, 2048, 2048), (32768 + 37, 256, 64), (32768 + 37, 256, 100),
-                                         (32768 + 37, 256, 130)])
+                                         (32768 + 37, 256, 130), (8192 + 37, 256, 32), (17408 + 37, 256, 48)])
 def test_gpu_prefill_gemm_equals_per_token_matvec(ctx, rows, cols, M):
-    """PTQ1 prefill runs as one f16-MFMA GEMM from 32 tokens on, in both contracts; every
-    token row must equal the reference's per-token matvec bit for bit (partial row
-    tiles, idle wavefronts of a partial 128-row block, an odd block count, 32, 64 and
-    128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
+    """PTQ1 prefill runs as one f16-MFMA GEMM from 32 tokens on (33 below 8192 rows), in both
+    contracts; every token row must equal the reference's per-token matvec bit for bit
+    (partial row tiles, idle wavefronts of a partial 128-row block, an odd block count, 32,
+    64 and 128 tokens per workgroup, padding tokens, and the XCD-major grid, taken when the
     token groups are a multiple of eight: M = 200, 512, 4096; nine blocks per row at 1152
     columns, the benchmark's matrix at 1024 tokens, a partial last tile at 6044 rows and
     2048 tokens; at 32805 rows the large-matrix choice of 32, 64 and 128 tokens per
-    workgroup).  The pinned contract's
+    workgroup; at 17445 rows and 48 tokens more block-split workgroups than CUs, so the
+    plain kernel).  The pinned contract's
     kernel takes each native lane's integer sum from its own masked MFMA and runs the
     four FMA lanes of dot_q8_groups_pinned."""
     import oracle
@@ -772,6 +773,28 @@ def test_gpu_errors_clear_output_and_do_not_latch(ctx):
     ctx.release(good)
 
 
+@pytest.mark.parametrize("kind,size", [(ph.KIND_TQ1_0, 54), (ph.KIND_TQ2_0, 66)])
+@pytest.mark.parametrize("tokens", [1, 4, 64])
+def test_gpu_tq_nonfinite_scale_fails_every_path(ctx, kind, size, tokens):
+    """A TQ block whose binary16 scale is infinite makes the reference's dot fail (scale(),
+    src/kernels.rs:152-154; src/kernels/tquants.rs:282): the one-token matvec, the skinny
+    batch (4 tokens) and the int8 prefill GEMM (64 tokens) report NONFINITE, leave the output
+    cleared and do not latch."""
+    rows, cols = 2048, 512
+    w = bytearray(synth.weights(kind, rows, cols, seed=7).tobytes())
+    at = (1000 * (cols // 256) + 1) * size + size - 2  # row 1000, second block's scale
+    w[at:at + 2] = (0x7C00).to_bytes(2, "little")
+    wid = ctx.weight(kind, cols, rows, bytes(w))
+    X = synth.activations(cols, seed=8, tokens=tokens).reshape(tokens, cols)
+    rc, out = ctx.project_f32(wid, rows, X[0] if tokens == 1 else X, tokens=tokens, check=False)
+    assert rc == ph.ERR_NONFINITE and not np.asarray(out).any()
+    assert not ctx.faulted
+    good = ctx.weight(kind, cols, rows, synth.weights(kind, rows, cols, seed=7))
+    assert np.isfinite(ctx.project_f32(good, rows, X[0] if tokens == 1 else X, tokens=tokens)).all()
+    ctx.release(wid)
+    ctx.release(good)
+
+
 def test_gpu_failed_calls_clear_outputs(ctx):
     """Every failing projection zero-fills the outputs whose length it knows, whatever the
     failure: an ineligible path (Q8_K activations for a Q8_0 weight), a bad extent, an
@@ -838,13 +861,13 @@ def test_gpu_wide_rows_few_tiles_every_token_count(ctx, kind, rows, cols):
     """FFN-down-like widths (14336, 17408 inputs) on a few 64-row tiles, stored tiled: one
     token takes the split kernel with wider lane groups, or the row-tile fallback where its
     LDS cannot hold the rows; two or three tokens run token by token (PTQ1, PQ2) or on the
-    batch kernels, and PTQ1 from 32 tokens the prefill GEMM; every output equals the
+    batch kernels, and PTQ1 from 33 tokens the prefill GEMM; every output equals the
     oracle's per-token matvec."""
     import oracle
 
     w = synth.weights(kind, rows, cols, seed=kind + rows)
     wid = ctx.weight(kind, cols, rows, w)
-    for M in (1, 2, 3, 32):
+    for M in (1, 2, 3, 33):
         X = synth.activations(cols, seed=M + kind, tokens=M).reshape(M, cols)
         for pinned in (False, True):
             ref = oracle.prefill(kind, cols, rows, w, X, pinned, threads=THREADS)
