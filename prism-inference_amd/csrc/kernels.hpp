@@ -55,6 +55,9 @@ struct MatvecArgs {
     uint32_t cus = 256;           // compute units of the device
     void *scratch = nullptr;      // tiled only: tiled_scratch_bytes() of device memory
     size_t scratch_bytes = 0;
+    // Scratch the caller can provide at most (a fixed buffer); kernel choices that need more
+    // fall back to ones that need less.
+    size_t scratch_cap = ~size_t(0);
 };
 
 // Return launch_status() values (0, kLaunchUnsupported, or a hipError_t).
@@ -89,6 +92,12 @@ bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t t
 size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens);
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
                      int pinned, float *out, void *scratch, int *err, hipStream_t s);
+// The same GEMM on prepared activations (M tokens of act_stride bytes): Q8_K blocks for
+// Q2_K, PQ2 (pinned: the fused chain), TQ1_0 and TQ2_0, Q8_0 blocks for Q8_0; the blocks'
+// codes, scales and sums are taken as they are.
+int launch_prefill_k_blocks(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const void *act,
+                            uint32_t act_stride, uint32_t M, int pinned, float *out, void *scratch, int *err,
+                            hipStream_t s);
 int launch_quantize_q8k(const float *x, uint64_t cols, uint32_t tokens, int pinned, void *out, int *err,
                         hipStream_t s);
 int launch_quantize_q8_0(const float *x, uint64_t cols, uint32_t tokens, int contract, void *out, int *err,

@@ -135,18 +135,19 @@ static_assert(names_every_element_once(tq1_elem));
 // ---- activation prep ------------------------------------------------------------------
 // A workgroup of TOK wavefronts quantizes TOK consecutive tokens (one each, 1024 inputs =
 // four Q8_K blocks, pinned selecting pinned_q8k_integer's rounding; for Q8_0 weights 32 Q8_0
-// blocks in the source or pinned generic contract), then writes, per 256-element unit u and
+// blocks in the source or pinned generic contract), or with BLOCKS copies the tokens' prepared
+// blocks of those inputs (src_stride bytes per token), then writes, per 256-element unit u and
 // token t (tokens padded to Mp with zeros):
 //   xq[u][s][h][t][16 bytes]   codes in the kind's operand order (16 slots of 16 bytes),
 //   as[u][t]                   the Q8_K block scale (Q8_0: as[u][s][t], the 8 block scales),
 //   bs[u][h][t][8 x f16]       Q2_K only: the sums of sub-blocks 8h .. 8h+7,
 // consecutive threads taking consecutive tokens of one slot, so each slot's TOK tokens
 // leave as one contiguous run.  A quantizer error is raised and the wavefront carries on.
-template <uint32_t KIND, uint32_t TOK>
-__global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp,
-                                                             uint32_t K, int pinned, uint8_t *__restrict__ xq,
-                                                             float *__restrict__ as, _Float16 *__restrict__ bs,
-                                                             int *__restrict__ err) {
+template <uint32_t KIND, uint32_t TOK, bool BLOCKS>
+__global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const void *__restrict__ src, uint32_t src_stride,
+                                                             uint32_t M, uint32_t Mp, uint32_t K, int pinned,
+                                                             uint8_t *__restrict__ xq, float *__restrict__ as,
+                                                             _Float16 *__restrict__ bs, int *__restrict__ err) {
     constexpr bool kQ8 = KIND == kQ8_0;
     using Blk = typename std::conditional<kQ8, Q8Block[TOK][32], Q8KBlock[TOK][4]>::type;
     __shared__ Blk blk;
@@ -156,12 +157,21 @@ __global__ __launch_bounds__(64 * TOK) void k_prefill_k_prep(const float *__rest
     const uint32_t k0 = c * 1024, nb = (K - k0 < 1024 ? K - k0 : 1024) / kUnit;  // 1..4 units
     const uint32_t t = tb + wave;
     if (t < M) {
-        int e;
-        if constexpr (kQ8)  // the source (0) or pinned generic (1) contract, 32-element blocks
-            e = q8_0_blocks_wave(x + static_cast<size_t>(t) * K + k0, nb * 8, pinned ? 1 : 0, blk[wave], lane);
-        else
-            e = q8k_blocks_wave(x + static_cast<size_t>(t) * K + k0, nb, pinned, blk[wave], lane);
-        if (e && lane == 0) raise_error(err, e);
+        if constexpr (BLOCKS) {
+            constexpr uint32_t kUnitBytes = kQ8 ? 8 * sizeof(Q8Block) : sizeof(Q8KBlock);  // per 256 inputs
+            const uint32_t *from = reinterpret_cast<const uint32_t *>(
+                static_cast<const uint8_t *>(src) + static_cast<size_t>(t) * src_stride + (k0 / kUnit) * kUnitBytes);
+            uint32_t *to = reinterpret_cast<uint32_t *>(&blk[wave]);
+            for (uint32_t i = lane; i < nb * kUnitBytes / 4; i += 64) to[i] = from[i];
+        } else {
+            const float *x = static_cast<const float *>(src) + static_cast<size_t>(t) * K + k0;
+            int e;
+            if constexpr (kQ8)  // the source (0) or pinned generic (1) contract, 32-element blocks
+                e = q8_0_blocks_wave(x, nb * 8, pinned ? 1 : 0, blk[wave], lane);
+            else
+                e = q8k_blocks_wave(x, nb, pinned, blk[wave], lane);
+            if (e && lane == 0) raise_error(err, e);
+        }
     }
     __syncthreads();
     const uint32_t u0 = k0 / kUnit;
@@ -647,8 +657,11 @@ bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t t
            code_bytes < (1ull << 31) && tokens >= gemm_min_tokens(rows);
 }
 
-int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
-                     int pinned, float *out, void *scratch, int *err, hipStream_t s) {
+// The prep (quantizing f32 input, or with BLOCKS copying prepared blocks of src_stride bytes
+// per token) and the GEMM.
+template <bool BLOCKS>
+static int launch_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const void *src,
+                    uint32_t src_stride, uint32_t M, int pinned, float *out, void *scratch, int *err, hipStream_t s) {
     if (!prefill_k_supported(kind, cols, rows, M)) return kLaunchUnsupported;
     const uint32_t K = static_cast<uint32_t>(cols), Mp = padded_tokens(M), nu = K / kUnit;
     uint8_t *base = static_cast<uint8_t *>(scratch);
@@ -659,14 +672,14 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     static_assert(kTokAlign % kTok == 0, "the prep takes whole token groups");
     const dim3 pgrid(Mp / kTok * ((K + 1023) / 1024)), pblock(64 * kTok);
     auto prep = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, pgrid, pblock, 0, s, x, M, Mp, K, pinned, xq, as, bs, err);
+        hipLaunchKernelGGL(kernel, pgrid, pblock, 0, s, src, src_stride, M, Mp, K, pinned, xq, as, bs, err);
     };
     switch (kind) {
-        case kQ2_K: prep(k_prefill_k_prep<kQ2_K, kTok>); break;
-        case kQ8_0: prep(k_prefill_k_prep<kQ8_0, kTok>); break;
-        case kTQ1_0: prep(k_prefill_k_prep<kTQ1_0, kTok>); break;
-        case kTQ2_0: prep(k_prefill_k_prep<kTQ2_0, kTok>); break;
-        default: prep(k_prefill_k_prep<kPQ2, kTok>);
+        case kQ2_K: prep(k_prefill_k_prep<kQ2_K, kTok, BLOCKS>); break;
+        case kQ8_0: prep(k_prefill_k_prep<kQ8_0, kTok, BLOCKS>); break;
+        case kTQ1_0: prep(k_prefill_k_prep<kTQ1_0, kTok, BLOCKS>); break;
+        case kTQ2_0: prep(k_prefill_k_prep<kTQ2_0, kTok, BLOCKS>); break;
+        default: prep(k_prefill_k_prep<kPQ2, kTok, BLOCKS>);
     }
     if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
@@ -699,6 +712,17 @@ int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t
     else
         nt == 64 ? go(k_prefill_kq<kPQ2, 2, false>) : go(k_prefill_kq<kPQ2, 1, false>);
     return launch_status();
+}
+
+int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
+                     int pinned, float *out, void *scratch, int *err, hipStream_t s) {
+    return launch_k<false>(kind, w_tiled, cols, rows, x, 0, M, pinned, out, scratch, err, s);
+}
+
+int launch_prefill_k_blocks(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const void *act,
+                            uint32_t act_stride, uint32_t M, int pinned, float *out, void *scratch, int *err,
+                            hipStream_t s) {
+    return launch_k<true>(kind, w_tiled, cols, rows, act, act_stride, M, pinned, out, scratch, err, s);
 }
 
 }  // namespace prism

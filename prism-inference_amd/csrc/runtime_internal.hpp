@@ -307,6 +307,10 @@ inline MatvecArgs matvec_args(prism_hip_ctx *c, const Weight &w, int act_format,
 inline int run_matvec(prism_hip_ctx *c, const MatvecArgs &args, bool tiled, Scratch *sc = nullptr) {
     MatvecArgs a = args;
     if (tiled) {
+        if (sc && sc->base) {  // a fixed buffer: what is left of it bounds the kernel choice
+            const size_t at = (sc->used + 255) & ~size_t(255);
+            a.scratch_cap = at < sc->cap ? sc->cap - at : 0;
+        }
         const size_t need = tiled_scratch_bytes(a);
         if (need) {
             Scratch grow{c};
