@@ -88,6 +88,11 @@ size_t prefill_scratch_bytes(uint32_t kind, uint64_t cols, uint32_t tokens);
 // cus: the device's compute units (the block-split kernel runs one workgroup per CU).
 int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
                    int pinned, float *out, void *scratch, int *err, hipStream_t s, uint32_t cus);
+// The same GEMMs on prepared activations (M tokens of act_stride bytes): Q8_0 blocks for PTQ1
+// (pinned: the pinned chain) and Q8_0, Q8_K blocks for the other kinds (launch_prefill_k_blocks).
+int launch_prefill_blocks(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const void *act,
+                          uint32_t act_stride, uint32_t M, int pinned, float *out, void *scratch, int *err,
+                          hipStream_t s, uint32_t cus);
 bool prefill_k_supported(uint32_t kind, uint64_t cols, uint64_t rows, uint32_t tokens);
 size_t prefill_k_scratch_bytes(uint64_t cols, uint32_t tokens);
 int launch_prefill_k(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,

@@ -3052,18 +3052,19 @@ int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
     return launch_status();
 }
 
-// Prepared activations of many tokens on the int8 GEMM (prefill_k.hip), from the token counts
-// at which it beats the skinny kernel for f32 input: Q8_K blocks for Q2_K, PQ2, TQ1_0 and
-// TQ2_0, Q8_0 blocks for Q8_0 (151936 x 4096, 16 tokens, us, skinny -> GEMM: Q2_K 79.6 ->
-// 71.4, Q8_0 167.8 -> 136.4).  Not with a residual, and not when the caller's scratch cannot
-// hold the token codes.
+// Prepared activations of many tokens on the prefill GEMMs, from the token counts at which
+// they beat the skinny kernel for f32 input: Q8_K blocks for Q2_K, PQ2, TQ1_0 and TQ2_0, Q8_0
+// blocks for Q8_0 (int8 GEMM, prefill_k.hip) and PTQ1 in either order (f16 GEMM,
+// prefill.hip).  Measured, 151936 x 4096, 16 tokens, us, skinny -> GEMM: Q2_K 79.6 -> 71.4,
+// Q8_0 167.8 -> 136.4.  Not with a residual, and not when the caller's scratch cannot hold the
+// token codes.
 bool gemm_eligible(const MatvecArgs &a) {
     if (a.act_format == kActF32 || a.w2 || a.residual || a.tile_best || a.tokens < 2) return false;
     const bool fits = a.act_format == kActQ8K
                           ? a.kind == kQ2_K || a.kind == kPQ2 || a.kind == kTQ1_0 || a.kind == kTQ2_0
-                          : a.kind == kQ8_0;
-    return fits && prefill_k_supported(a.kind, a.cols, a.rows, a.tokens) &&
-           prefill_k_scratch_bytes(a.cols, a.tokens) <= a.scratch_cap;
+                          : a.kind == kQ8_0 || a.kind == kPTQ1;
+    return fits && prefill_supported(a.kind, a.cols, a.rows, a.pinned, a.tokens) &&
+           prefill_scratch_bytes(a.kind, a.cols, a.tokens) <= a.scratch_cap;
 }
 
 bool skinny_eligible(const MatvecArgs &a) {
@@ -3107,9 +3108,9 @@ int launch_matvec_tiled(const MatvecArgs &a) {
                                                        : sizeof(Q8Block) * (a.cols / 32);
     const bool batched = a.act_format != kActF32 && !token_by_token(a);
     if (batched && gemm_eligible(a)) {
-        if (!a.scratch || a.scratch_bytes < prefill_k_scratch_bytes(a.cols, a.tokens)) return -2;
-        return launch_prefill_k_blocks(a.kind, a.w, a.cols, a.rows, a.act, static_cast<uint32_t>(in_stride), a.tokens,
-                                       a.pinned, a.out, a.scratch, a.err, a.stream);
+        if (!a.scratch || a.scratch_bytes < prefill_scratch_bytes(a.kind, a.cols, a.tokens)) return -2;
+        return launch_prefill_blocks(a.kind, a.w, a.cols, a.rows, a.act, static_cast<uint32_t>(in_stride), a.tokens,
+                                     a.pinned, a.out, a.scratch, a.err, a.stream, a.cus);
     }
     if (batched && quad_eligible(a))
         return dispatch(a, [&]<Op O>() { return launch_quad<O>(a, static_cast<uint32_t>(in_stride)); });
@@ -3154,7 +3155,8 @@ int launch_matvec_tiled(const MatvecArgs &a) {
 }
 
 size_t tiled_scratch_bytes(const MatvecArgs &a) {
-    if (a.act_format != kActF32 && !token_by_token(a) && gemm_eligible(a)) return prefill_k_scratch_bytes(a.cols, a.tokens);
+    if (a.act_format != kActF32 && !token_by_token(a) && gemm_eligible(a))
+        return prefill_scratch_bytes(a.kind, a.cols, a.tokens);
     if (!skinny_eligible(a)) return 0;
     return static_cast<size_t>(dispatch(a, [&]<Op O>() { return static_cast<int>(skinny_scratch<O>(a)); }));
 }

@@ -81,10 +81,13 @@ __host__ __device__ constexpr uint32_t pair_base(uint32_t g, uint32_t q, uint32_
 // workgroups.  A quantizer error is raised and the wavefront carries on (the call then
 // reports it and clears the output).  TOK = 16 fills whole 128-byte lines per pinned slot;
 // short prompts take TOK = 4, which spreads their few tokens over four times as many CUs.
-template <bool PINNED, uint32_t TOK>
-__global__ __launch_bounds__(64 * TOK) void k_prefill_prep(const float *__restrict__ x, uint32_t M, uint32_t Mp,
-                                                           uint32_t K, _Float16 *__restrict__ xh,
-                                                           float *__restrict__ sc, int *__restrict__ err) {
+// With BLOCKS the tokens' prepared Q8_0 blocks (src_stride bytes per token) are copied instead
+// of quantizing f32 input.
+template <bool PINNED, uint32_t TOK, bool BLOCKS>
+__global__ __launch_bounds__(64 * TOK) void k_prefill_prep(const void *__restrict__ src, uint32_t src_stride,
+                                                           uint32_t M, uint32_t Mp, uint32_t K,
+                                                           _Float16 *__restrict__ xh, float *__restrict__ sc,
+                                                           int *__restrict__ err) {
     __shared__ Q8Block blk[TOK][32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t chunks = (K + 1023) / 1024;
@@ -92,9 +95,17 @@ __global__ __launch_bounds__(64 * TOK) void k_prefill_prep(const float *__restri
     const uint32_t k0 = c * 1024, n = K - k0 < 1024 ? K - k0 : 1024;  // multiple of 128
     const uint32_t t = tb + wave;
     if (t < M) {
-        // Contract 0: source (round half away); 2: pinned PTQ1 native scale (quant_dev.hpp).
-        const int e = q8_0_blocks_wave(x + static_cast<size_t>(t) * K + k0, n / 32, PINNED ? 2 : 0, blk[wave], lane);
-        if (e && lane == 0) raise_error(err, e);
+        if constexpr (BLOCKS) {
+            const uint32_t *from = reinterpret_cast<const uint32_t *>(
+                static_cast<const uint8_t *>(src) + static_cast<size_t>(t) * src_stride + (k0 / 32) * sizeof(Q8Block));
+            uint32_t *to = reinterpret_cast<uint32_t *>(&blk[wave]);
+            for (uint32_t i = lane; i < n / 32 * sizeof(Q8Block) / 4; i += 64) to[i] = from[i];
+        } else {
+            // Contract 0: source (round half away); 2: pinned PTQ1 native scale (quant_dev.hpp).
+            const float *x = static_cast<const float *>(src) + static_cast<size_t>(t) * K + k0;
+            const int e = q8_0_blocks_wave(x, n / 32, PINNED ? 2 : 0, blk[wave], lane);
+            if (e && lane == 0) raise_error(err, e);
+        }
     }
     __syncthreads();
     if (lane < n / 32) {
@@ -677,9 +688,11 @@ bool prefill_supported(uint32_t kind, uint64_t cols, uint64_t rows, int pinned, 
            (rows * (cols / 128) * 28) < (1ull << 40) && code_bytes < (1ull << 31);
 }
 
-int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
-                   int pinned, float *out, void *scratch, int *err, hipStream_t s, uint32_t cus) {
-    if (kind != kPTQ1) return launch_prefill_k(kind, w_tiled, cols, rows, x, M, pinned, out, scratch, err, s);
+// The prep (quantizing f32 input, or with BLOCKS copying prepared Q8_0 blocks of src_stride
+// bytes per token) and the PTQ1 GEMM.
+template <bool BLOCKS>
+static int launch_ptq1(const void *w_tiled, uint64_t cols, uint64_t rows, const void *src, uint32_t src_stride,
+                       uint32_t M, int pinned, float *out, void *scratch, int *err, hipStream_t s, uint32_t cus) {
     const uint32_t K = static_cast<uint32_t>(cols), Mp = padded_tokens(M);
     if (static_cast<uint64_t>(K / 128) * 8u * Mp * 32u >= (1ull << 31)) return kLaunchUnsupported;
     _Float16 *xh = static_cast<_Float16 *>(scratch);
@@ -694,11 +707,14 @@ int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t r
     const bool wide = pinned && Mp >= 1024;
     const dim3 pgrid(static_cast<uint32_t>(items / (wide ? 16 : 4))), pblock(wide ? 1024 : 256);
     if (wide)
-        hipLaunchKernelGGL((k_prefill_prep<true, 16>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
+        hipLaunchKernelGGL((k_prefill_prep<true, 16, BLOCKS>), pgrid, pblock, 0, s, src, src_stride, M, Mp, K, xh, sc,
+                           err);
     else if (pinned)
-        hipLaunchKernelGGL((k_prefill_prep<true, 4>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
+        hipLaunchKernelGGL((k_prefill_prep<true, 4, BLOCKS>), pgrid, pblock, 0, s, src, src_stride, M, Mp, K, xh, sc,
+                           err);
     else
-        hipLaunchKernelGGL((k_prefill_prep<false, 4>), pgrid, pblock, 0, s, x, M, Mp, K, xh, sc, err);
+        hipLaunchKernelGGL((k_prefill_prep<false, 4, BLOCKS>), pgrid, pblock, 0, s, src, src_stride, M, Mp, K, xh, sc,
+                           err);
     if (const int e = launch_status()) return e;
     const uint32_t gx = static_cast<uint32_t>((rows + kRowsPerWg - 1) / kRowsPerWg);
     const auto W = static_cast<const uint8_t *>(w_tiled);
@@ -759,6 +775,20 @@ int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t r
     else
         hipLaunchKernelGGL(k_prefill_ptq1<1>, grid, dim3(256), 0, s, W, R, nu, xh, sc, M, Mp, xcd_major, out, err);
     return launch_status();
+}
+
+int launch_prefill(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const float *x, uint32_t M,
+                   int pinned, float *out, void *scratch, int *err, hipStream_t s, uint32_t cus) {
+    if (kind != kPTQ1) return launch_prefill_k(kind, w_tiled, cols, rows, x, M, pinned, out, scratch, err, s);
+    return launch_ptq1<false>(w_tiled, cols, rows, x, 0, M, pinned, out, scratch, err, s, cus);
+}
+
+int launch_prefill_blocks(uint32_t kind, const void *w_tiled, uint64_t cols, uint64_t rows, const void *act,
+                          uint32_t act_stride, uint32_t M, int pinned, float *out, void *scratch, int *err,
+                          hipStream_t s, uint32_t cus) {
+    if (kind != kPTQ1)
+        return launch_prefill_k_blocks(kind, w_tiled, cols, rows, act, act_stride, M, pinned, out, scratch, err, s);
+    return launch_ptq1<true>(w_tiled, cols, rows, act, act_stride, M, pinned, out, scratch, err, s, cus);
 }
 
 }  // namespace prism

@@ -517,6 +517,41 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("kind,rows,cols,tokens", [(ph.KIND_PTQ1, 200, 1024, 40), (ph.KIND_PTQ1, 6144 + 37, 512, 100),
+                                                   (ph.KIND_Q8_0, 300, 512, 70), (ph.KIND_Q2_K, 300, 512, 70),
+                                                   (ph.KIND_PQ2, 300, 512, 70), (ph.KIND_TQ1_0, 300, 512, 70),
+                                                   (ph.KIND_TQ2_0, 300, 512, 70), (ph.KIND_Q2_K, 65536 + 37, 256, 16)])
+def test_gpu_prepared_activations_gemm_matches_oracle(ctx, kind, rows, cols, tokens):
+    """Prepared multi-token activations take the prefill GEMMs from their token thresholds, with
+    a prep that copies the blocks instead of quantizing: PTQ1 with Q8_0 blocks of each contract
+    in both chain orders (f16 GEMM), Q8_0 with Q8_0 blocks, Q2_K, PQ2 (both chains), TQ1_0 and
+    TQ2_0 with Q8_K blocks (int8 GEMM).  Every token row equals the oracle's matvec on that
+    token's blocks, bit for bit."""
+    import oracle
+
+    w = synth.weights(kind, rows, cols, seed=rows + tokens) if kind != ph.KIND_PQ2 else \
+        synth.pq2_weights(rows, cols, rows, 4)
+    wid = ctx.weight(kind, cols, rows, w)
+    X = synth.activations(cols, seed=tokens + kind, tokens=tokens).reshape(tokens, cols)
+    nq8, nq8k = cols // 32, cols // 256
+    if kind in (ph.KIND_PTQ1, ph.KIND_Q8_0):
+        for contract, pinned in ((0, False), (2, True), (1, False)) if kind == ph.KIND_PTQ1 else ((1, False), (0, True)):
+            act = np.concatenate([oracle.quantize_q8_0(X[t], contract) for t in range(tokens)])
+            ref = np.stack([oracle.project_q8(kind, cols, rows, w, act[t * nq8:(t + 1) * nq8], pinned, threads=THREADS)
+                            for t in range(tokens)])
+            got = ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens, pinned=pinned)
+            assert_bits_equal(got, ref, f"prepared q8 kind={kind} tokens={tokens} contract={contract} pinned={pinned}")
+    else:
+        for fused in (False, True):
+            act = np.concatenate([oracle.quantize_q8k(X[t], fused) for t in range(tokens)])
+            ref = np.stack([oracle.project_q8k(kind, cols, rows, w, act[t * nq8k:(t + 1) * nq8k], fused,
+                                               threads=THREADS) for t in range(tokens)])
+            got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens, fused=fused)
+            assert_bits_equal(got, ref, f"prepared q8k kind={kind} tokens={tokens} fused={fused}")
+    assert not ctx.faulted
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("kind,cols,rows", [(ph.KIND_PTQ1, 128, 65536 + 37), (ph.KIND_PTQ1, 640, 65536 + 37),
                                             (ph.KIND_PTQ1, 384, 131072 + 5), (ph.KIND_Q8_0, 128, 65536 + 37),
                                             (ph.KIND_Q8_0, 640, 65536 + 1), (ph.KIND_Q8_0, 384, 131072 + 63),
