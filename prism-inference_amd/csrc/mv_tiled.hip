@@ -1123,6 +1123,89 @@ __global__ __launch_bounds__(64) void k_mv_rows_batch(MvParams p, const void *__
     }
 }
 
+// ---- long rows on few tiles: split-K through global memory -----------------------------
+// With fewer tiles than CUs and long rows, one workgroup per tile walks a long serial chain of
+// units.  Here the units are split over workgroups instead: k_mv_terms (one wavefront per
+// tile and range of upw units) computes every unit's terms of the tile's rows for every token
+// and stores them at terms[((t * nu + u) * TPU + j) * rp + row] (rp: rows rounded up to whole
+// tiles); k_mv_fold then folds each (token, row) element's terms in unit order -- the unsplit
+// chain, so every output equals its matvec bit for bit.
+template <Op O>
+__global__ __launch_bounds__(64) void k_mv_terms(MvParams p, const void *__restrict__ act, uint32_t act_stride,
+                                                 uint32_t ntok, uint32_t upw, float *__restrict__ terms, uint32_t rp) {
+    constexpr uint32_t UB = unit_bytes<O>();
+    constexpr int TPU = terms_per_unit<O>();
+    const uint32_t lane = threadIdx.x, tile = blockIdx.x;
+    const uint32_t nu = p.nu, row_bytes = nu * UB;
+    const uint32_t u0 = blockIdx.y * upw, u1 = u0 + upw < nu ? u0 + upw : nu;
+    const uint32_t left = p.rows - tile * kTile;
+    const uint32_t trows = left < kTile ? left : kTile;
+    const uint32_t trp = (trows + 7u) & ~7u;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
+    float *tr = terms + static_cast<size_t>(tile) * kTile + lane;  // rows past the matrix: zero weights, never folded
+    auto step = [&](const Raw<O> &w, uint32_t u) {
+        for (uint32_t t = 0; t < ntok; ++t) {
+            const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
+            float tt[TPU];
+            unit_terms<O>(w, a, u, tt);
+#pragma unroll
+            for (int j = 0; j < TPU; ++j) tr[((static_cast<size_t>(t) * nu + u) * TPU + j) * rp] = tt[j];
+        }
+    };
+    Raw<O> A, B;
+    uint32_t u = u0;
+    load_unit<O>(A, rs, u * trp * UB, trp, lane);
+    while (u + 1 < u1) {
+        load_unit<O>(B, rs, (u + 1) * trp * UB, trp, lane);
+        step(A, u);
+        if (u + 2 < u1) load_unit<O>(A, rs, (u + 2) * trp * UB, trp, lane);
+        step(B, u + 1);
+        u += 2;
+    }
+    if (u < u1) step(A, u);
+}
+
+// Rows per k_mv_fold workgroup whose terms fit kFoldLds (0: none do).
+constexpr uint32_t kFoldLds = 64 * 1024;
+template <Op O>
+uint32_t fold_rows(uint32_t nu) {
+    for (uint32_t rf = 64; rf >= 8; rf >>= 1)
+        if (static_cast<uint64_t>(rf) * nu * terms_per_unit<O>() * sizeof(float) <= kFoldLds) return rf;
+    return 0;
+}
+
+// Workgroup (block of rf rows, token t): every unit's terms of its rows staged in LDS with
+// all loads issued at once (consecutive threads take consecutive rows of one term), then rf
+// threads fold their row's terms in unit order.
+template <Op O>
+__global__ __launch_bounds__(256) void k_mv_fold(MvParams p, const void *__restrict__ act, uint32_t act_stride,
+                                                 const float *__restrict__ terms, uint32_t rp, uint32_t rf) {
+    constexpr int TPU = terms_per_unit<O>();
+    extern __shared__ float staged[];  // [nu * TPU][rf]
+    const uint32_t t = blockIdx.y, row0 = blockIdx.x * rf, n = p.nu * TPU;
+    const float *src = terms + static_cast<size_t>(t) * n * rp + row0;
+    for (uint32_t i = threadIdx.x; i < n * rf; i += 256) {
+        const uint32_t k = i / rf, r = i % rf;
+        staged[i] = src[static_cast<size_t>(k) * rp + r];
+    }
+    __syncthreads();
+    const uint32_t r = threadIdx.x;
+    if (r >= rf || row0 + r >= p.rows) return;
+    const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
+    Chain<O> ch;
+    for (uint32_t u = 0; u < p.nu; ++u) {
+        float tt[TPU];
+#pragma unroll
+        for (int j = 0; j < TPU; ++j) tt[j] = staged[(u * TPU + j) * rf + r];
+        ch.fold(tt, a, u);
+    }
+    const size_t at = static_cast<size_t>(t) * p.rows + row0 + r;
+    float o = ch.result();
+    if (p.residual) o = o + p.residual[at];
+    p.out[at] = o;
+    if (!finite(o)) raise_error(p.err, kErrNonfinite);
+}
+
 // Row count from which a skinny batch runs weights-once: one wavefront per tile needs
 // several tiles per SIMD before the per-token chains stop dominating (measured: at
 // 12288 rows token-by-token launches are faster, at 151936 weights-once is 1.5-4x).
@@ -3052,6 +3135,57 @@ int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
     return launch_status();
 }
 
+// Long rows on few tiles take the two-pass split-K (k_mv_terms + k_mv_fold) for source-order
+// PTQ1 (prepared Q8_0 blocks, one term per unit) at two to eight tokens, where the other paths
+// run token by token or leave the skinny kernel's 16-token width mostly empty.  Measured
+// (prepared activations, us, before -> split-K): 5120 x 17408 2 tokens 31.2 -> 21.0, 4 tokens
+// 53.0 -> 28.1; 6144 x 16384 28.9 -> 21.3 and 51.7 -> 29.7; 4096 x 14336 4 tokens 27.8 -> 20.5, 8
+// tokens 34.3 -> 31.4; 2048 x 16384 4 / 8 tokens 32.3 -> 18.2 and 36.4 -> 23.2.  It loses at one
+// token (two launches: 4096 x 14336 8.9 -> 15.4), at two tokens below 5120 rows, from eight
+// tokens above 4096 rows and at sixteen (12288 x 8192 30.1 -> 68.3); the terms it stores grow
+// with tokens x units x terms per unit, so the other formats (Q8_0 4 terms per unit: 5120 x
+// 17408 16 tokens 37.5 -> 165.2; PQ2 4 tokens 27.7 -> 35.2) and the pinned order (9 terms)
+// keep their kernels.
+constexpr uint32_t kSplitKUnits = 4, kSplitKMinUnits = 64;
+
+size_t splitk_scratch(const MatvecArgs &a) {
+    const uint64_t rp = (a.rows + kTile - 1) / kTile * kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
+    return a.tokens * nu * terms_per_unit<Op::PTQ1_SRC>() * rp * sizeof(float);
+}
+
+bool splitk_eligible(const MatvecArgs &a) {
+    if (a.kind != kPTQ1 || a.act_format != kActQ8 || a.pinned || a.w2 || a.tile_best) return false;
+    const uint64_t tiles = (a.rows + kTile - 1) / kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
+    if (tiles >= a.cus || nu < kSplitKMinUnits || !fold_rows<Op::PTQ1_SRC>(static_cast<uint32_t>(nu))) return false;
+    const bool tokens = a.tokens == 2 ? a.rows >= 5120 : a.tokens >= 3 && (a.tokens <= 4 || (a.tokens <= 8 && a.rows <= 4096));
+    return tokens && splitk_scratch(a) <= a.scratch_cap;
+}
+
+template <Op O>
+int launch_splitk(const MatvecArgs &a, uint32_t act_stride) {
+    const uint32_t nu = static_cast<uint32_t>(a.cols / unit_weights<O>());
+    const uint32_t rf = fold_rows<O>(nu);
+    if (!rf || !a.scratch || a.scratch_bytes < splitk_scratch(a)) return -2;
+    const uint32_t tiles = static_cast<uint32_t>((a.rows + kTile - 1) / kTile), rp = tiles * kTile;
+    MvParams p{};
+    p.w[0] = p.w[1] = a.w;
+    p.rows = static_cast<uint32_t>(a.rows);
+    p.nu = nu;
+    p.cols = static_cast<uint32_t>(a.cols);
+    p.out = a.out;
+    p.residual = a.residual;
+    p.err = a.err;
+    float *terms = static_cast<float *>(a.scratch);
+    const uint32_t chunks = (nu + kSplitKUnits - 1) / kSplitKUnits;
+    hipLaunchKernelGGL(k_mv_terms<O>, dim3(tiles, chunks), dim3(64), 0, a.stream, p, a.act, act_stride, a.tokens,
+                       kSplitKUnits, terms, rp);
+    if (const int e = launch_status()) return e;
+    const uint32_t lds = rf * nu * terms_per_unit<O>() * static_cast<uint32_t>(sizeof(float));
+    hipLaunchKernelGGL(k_mv_fold<O>, dim3((p.rows + rf - 1) / rf, a.tokens), dim3(256), lds, a.stream, p, a.act,
+                       act_stride, terms, rp, rf);
+    return launch_status();
+}
+
 // Prepared activations of many tokens on the prefill GEMMs, from the token counts at which
 // they beat the skinny kernel for f32 input: Q8_K blocks for Q2_K, PQ2, TQ1_0 and TQ2_0, Q8_0
 // blocks for Q8_0 (int8 GEMM, prefill_k.hip) and PTQ1 in either order (f16 GEMM,
@@ -3106,6 +3240,7 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
+    if (splitk_eligible(a)) return launch_splitk<Op::PTQ1_SRC>(a, static_cast<uint32_t>(in_stride));
     const bool batched = a.act_format != kActF32 && !token_by_token(a);
     if (batched && gemm_eligible(a)) {
         if (!a.scratch || a.scratch_bytes < prefill_scratch_bytes(a.kind, a.cols, a.tokens)) return -2;
@@ -3155,6 +3290,7 @@ int launch_matvec_tiled(const MatvecArgs &a) {
 }
 
 size_t tiled_scratch_bytes(const MatvecArgs &a) {
+    if (splitk_eligible(a)) return splitk_scratch(a);
     if (a.act_format != kActF32 && !token_by_token(a) && gemm_eligible(a))
         return prefill_scratch_bytes(a.kind, a.cols, a.tokens);
     if (!skinny_eligible(a)) return 0;

@@ -517,6 +517,31 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [(5120 + 37, 17408, 2), (2048 + 5, 8192, 3), (2048 + 5, 8192, 4),
+                                              (4096 - 3, 8192, 8), (1000, 16384, 6)])
+def test_gpu_splitk_long_rows_match_oracle(ctx, rows, cols, tokens):
+    """Long PTQ1 rows on few tiles at two to eight tokens (source order) take the two-pass
+    split-K: one wavefront per (tile, four units) stores each unit's term per (token, row) in
+    global memory, and a fold kernel adds them in unit order.  Prepared source blocks and f32
+    input (quantized first) equal the oracle's per-token matvec bit for bit (a partial last
+    tile, 64 to 136 units per row)."""
+    import oracle
+
+    w = synth.ptq1_weights(rows, cols, seed=rows + tokens)
+    wid = ctx.weight(ph.KIND_PTQ1, cols, rows, w)
+    X = synth.activations(cols, seed=tokens, tokens=tokens).reshape(tokens, cols)
+    nq8 = cols // 32
+    act = np.concatenate([oracle.quantize_q8_0(X[t], 0) for t in range(tokens)])
+    ref = np.stack([oracle.project_q8(ph.KIND_PTQ1, cols, rows, w, act[t * nq8:(t + 1) * nq8], False, threads=THREADS)
+                    for t in range(tokens)])
+    assert_bits_equal(ctx.project_q8(wid, rows, act.view(ph.Q8_DTYPE), tokens=tokens), ref,
+                      f"split-K prepared {rows}x{cols} tokens={tokens}")
+    ref = oracle.prefill(ph.KIND_PTQ1, cols, rows, w, X, False, threads=THREADS)
+    assert_bits_equal(ctx.project_f32(wid, rows, X, tokens=tokens), ref, f"split-K f32 {rows}x{cols} tokens={tokens}")
+    assert not ctx.faulted
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("kind,rows,cols,tokens", [(ph.KIND_PTQ1, 200, 1024, 40), (ph.KIND_PTQ1, 6144 + 37, 512, 100),
                                                    (ph.KIND_Q8_0, 300, 512, 70), (ph.KIND_Q2_K, 300, 512, 70),
                                                    (ph.KIND_PQ2, 300, 512, 70), (ph.KIND_TQ1_0, 300, 512, 70),
