@@ -224,7 +224,8 @@ uint64_t prism_hip_resident_bytes(const prism_hip_ctx *ctx);
 /* Pq2ProjectionExecutor::project (projection.rs:46-57): PQ2 with cols%256==0 and
  * prepared Q8_K codes, `fused` selects mul_add accumulation.  Also accepts Q2_K
  * (kquants::dot) and PTQ1 (dot_ptq1_q8k, src/kernels.rs:999-1037).  act holds
- * tokens*cols/256 blocks; out receives [tokens][rows]. */
+ * tokens*cols/256 blocks, each with the sums of its codes in `sums` (as every Q8_K
+ * quantizer writes them; Q2_K reads them); out receives [tokens][rows]. */
 int prism_hip_project_q8k(prism_hip_ctx *ctx, prism_weight_id w, const prism_q8k_block *act, uint64_t nblocks,
                           uint32_t tokens, int fused, float *out);
 /* Pq2ProjectionExecutor::project_q8 (projection.rs:68-87): PTQ1 or odd-group PQ2
