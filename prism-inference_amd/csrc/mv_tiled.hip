@@ -3145,8 +3145,15 @@ int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
 // tokens above 4096 rows and at sixteen (12288 x 8192 30.1 -> 68.3); the terms it stores grow
 // with tokens x units x terms per unit, so the other formats (Q8_0 4 terms per unit: 5120 x
 // 17408 16 tokens 37.5 -> 165.2; PQ2 4 tokens 27.7 -> 35.2) and the pinned order (9 terms)
-// keep their kernels.
-constexpr uint32_t kSplitKUnits = 4, kSplitKMinUnits = 64;
+// keep their kernels.  Shorter rows (32 to 63 units) take it on up to half a tile per CU, at
+// two or three tokens, and at four from 48 units (5120 x 6144, 2 / 4 tokens 14.2 -> 11.7 and
+// 21.3 -> 13.9; 6144 x 5120 2 tokens 13.1 -> 11.3; at 8 tokens prepared input gains, 21.0 ->
+// 18.6, but f32 input loses, 23.5 -> 24.4), and two or three tokens on one to two tiles per
+// CU, where the quad-split
+// kernel's one workgroup per tile runs in two rounds (17408 x 5120 25.0 -> 16.0 and 18.9;
+// 24576 x 5120 25.3 -> 20.0 and 23.6); between half a tile and one tile per CU that kernel
+// stays ahead (10240 x 5120 4 tokens 13.4 against 16.3).
+constexpr uint32_t kSplitKUnits = 4, kSplitKMinUnits = 32;
 
 size_t splitk_scratch(const MatvecArgs &a) {
     const uint64_t rp = (a.rows + kTile - 1) / kTile * kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
@@ -3156,9 +3163,18 @@ size_t splitk_scratch(const MatvecArgs &a) {
 bool splitk_eligible(const MatvecArgs &a) {
     if (a.kind != kPTQ1 || a.act_format != kActQ8 || a.pinned || a.w2 || a.tile_best) return false;
     const uint64_t tiles = (a.rows + kTile - 1) / kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
-    if (tiles >= a.cus || nu < kSplitKMinUnits || !fold_rows<Op::PTQ1_SRC>(static_cast<uint32_t>(nu))) return false;
-    const bool tokens = a.tokens == 2 ? a.rows >= 5120 : a.tokens >= 3 && (a.tokens <= 4 || (a.tokens <= 8 && a.rows <= 4096));
-    return tokens && splitk_scratch(a) <= a.scratch_cap;
+    if (nu < kSplitKMinUnits || !fold_rows<Op::PTQ1_SRC>(static_cast<uint32_t>(nu))) return false;
+    const uint32_t n = a.tokens;
+    bool take = false;
+    if (tiles >= 2ull * a.cus)
+        take = false;
+    else if (tiles > a.cus)
+        take = n >= 2 && n <= 3;
+    else if (nu >= 64)
+        take = n == 2 ? a.rows >= 5120 : n >= 3 && (n <= 4 || (n <= 8 && a.rows <= 4096));
+    else
+        take = 2 * tiles <= a.cus && n >= 2 && (n <= 3 || (n <= 4 && nu >= 48));
+    return take && splitk_scratch(a) <= a.scratch_cap;
 }
 
 template <Op O>

@@ -518,13 +518,14 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
 
 
 @pytest.mark.parametrize("rows,cols,tokens", [(5120 + 37, 17408, 2), (2048 + 5, 8192, 3), (2048 + 5, 8192, 4),
-                                              (4096 - 3, 8192, 8), (1000, 16384, 6)])
+                                              (4096 - 3, 8192, 8), (1000, 16384, 6), (17408 + 37, 5120, 2),
+                                              (17408 + 37, 5120, 3), (5120 + 3, 6144, 4), (6144 + 5, 5120, 3)])
 def test_gpu_splitk_long_rows_match_oracle(ctx, rows, cols, tokens):
     """Long PTQ1 rows on few tiles at two to eight tokens (source order) take the two-pass
     split-K: one wavefront per (tile, four units) stores each unit's term per (token, row) in
     global memory, and a fold kernel adds them in unit order.  Prepared source blocks and f32
     input (quantized first) equal the oracle's per-token matvec bit for bit (a partial last
-    tile, 64 to 136 units per row)."""
+    tile, 40 to 136 units per row, fewer and more tiles than CUs)."""
     import oracle
 
     w = synth.ptq1_weights(rows, cols, seed=rows + tokens)
