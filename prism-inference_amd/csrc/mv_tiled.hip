@@ -1144,12 +1144,22 @@ __global__ __launch_bounds__(64) void k_mv_terms(MvParams p, const void *__restr
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w[0] + static_cast<size_t>(tile) * kTile * row_bytes, trp * row_bytes);
     float *tr = terms + static_cast<size_t>(tile) * kTile + lane;  // rows past the matrix: zero weights, never folded
     auto step = [&](const Raw<O> &w, uint32_t u) {
-        for (uint32_t t = 0; t < ntok; ++t) {
-            const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
-            float tt[TPU];
-            unit_terms<O>(w, a, u, tt);
+        // A PTQ1 unit's trits are extracted once for all tokens.
+        auto unit = [&](const auto &dec) {
+            for (uint32_t t = 0; t < ntok; ++t) {
+                const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
+                float tt[TPU];
+                unit_terms<O, false, std::remove_cvref_t<decltype(dec)>>(dec, a, u, tt);
 #pragma unroll
-            for (int j = 0; j < TPU; ++j) tr[((static_cast<size_t>(t) * nu + u) * TPU + j) * rp] = tt[j];
+                for (int j = 0; j < TPU; ++j) tr[((static_cast<size_t>(t) * nu + u) * TPU + j) * rp] = tt[j];
+            }
+        };
+        if constexpr (kind_of<O>() == kPTQ1) {
+            Ptq1Dec D;
+            ptq1_decode(w.x, D);
+            unit(D);
+        } else {
+            unit(w);
         }
     };
     Raw<O> A, B;
@@ -1179,24 +1189,43 @@ uint32_t fold_rows(uint32_t nu) {
 // threads fold their row's terms in unit order.
 template <Op O>
 __global__ __launch_bounds__(256) void k_mv_fold(MvParams p, const void *__restrict__ act, uint32_t act_stride,
-                                                 const float *__restrict__ terms, uint32_t rp, uint32_t rf) {
+                                                 const float *__restrict__ terms, uint32_t rp, uint32_t lg_rf) {
     constexpr int TPU = terms_per_unit<O>();
+    constexpr uint32_t kBatch = 8;  // loads in flight per thread, and LDS reads ahead of the chain
     extern __shared__ float staged[];  // [nu * TPU][rf]
-    const uint32_t t = blockIdx.y, row0 = blockIdx.x * rf, n = p.nu * TPU;
+    const uint32_t rf = 1u << lg_rf, t = blockIdx.y, row0 = blockIdx.x * rf, n = p.nu * TPU;
     const float *src = terms + static_cast<size_t>(t) * n * rp + row0;
-    for (uint32_t i = threadIdx.x; i < n * rf; i += 256) {
-        const uint32_t k = i / rf, r = i % rf;
-        staged[i] = src[static_cast<size_t>(k) * rp + r];
+    const uint32_t total = n * rf;
+    for (uint32_t i0 = threadIdx.x; i0 < total; i0 += 256 * kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (uint32_t b = 0; b < kBatch; ++b) {
+            const uint32_t i = i0 + 256 * b;
+            v[b] = i < total ? src[static_cast<size_t>(i >> lg_rf) * rp + (i & (rf - 1))] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t b = 0; b < kBatch; ++b)
+            if (i0 + 256 * b < total) staged[i0 + 256 * b] = v[b];
     }
     __syncthreads();
     const uint32_t r = threadIdx.x;
     if (r >= rf || row0 + r >= p.rows) return;
     const void *a = static_cast<const uint8_t *>(act) + static_cast<size_t>(t) * act_stride;
     Chain<O> ch;
-    for (uint32_t u = 0; u < p.nu; ++u) {
+    uint32_t u = 0;
+    for (; u + kBatch <= p.nu; u += kBatch) {
+        float tt[kBatch][TPU];
+#pragma unroll
+        for (uint32_t b = 0; b < kBatch; ++b)
+#pragma unroll
+            for (int j = 0; j < TPU; ++j) tt[b][j] = staged[(((u + b) * TPU + j) << lg_rf) + r];
+#pragma unroll
+        for (uint32_t b = 0; b < kBatch; ++b) ch.fold(tt[b], a, u + b);
+    }
+    for (; u < p.nu; ++u) {
         float tt[TPU];
 #pragma unroll
-        for (int j = 0; j < TPU; ++j) tt[j] = staged[(u * TPU + j) * rf + r];
+        for (int j = 0; j < TPU; ++j) tt[j] = staged[((u * TPU + j) << lg_rf) + r];
         ch.fold(tt, a, u);
     }
     const size_t at = static_cast<size_t>(t) * p.rows + row0 + r;
@@ -3198,7 +3227,7 @@ int launch_splitk(const MatvecArgs &a, uint32_t act_stride) {
     if (const int e = launch_status()) return e;
     const uint32_t lds = rf * nu * terms_per_unit<O>() * static_cast<uint32_t>(sizeof(float));
     hipLaunchKernelGGL(k_mv_fold<O>, dim3((p.rows + rf - 1) / rf, a.tokens), dim3(256), lds, a.stream, p, a.act,
-                       act_stride, terms, rp, rf);
+                       act_stride, terms, rp, static_cast<uint32_t>(__builtin_ctz(rf)));
     return launch_status();
 }
 
