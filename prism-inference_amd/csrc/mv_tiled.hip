@@ -3167,22 +3167,21 @@ int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
 // Long rows on few tiles take the two-pass split-K (k_mv_terms + k_mv_fold) for source-order
 // PTQ1 (prepared Q8_0 blocks, one term per unit) at two to eight tokens, where the other paths
 // run token by token or leave the skinny kernel's 16-token width mostly empty.  Measured
-// (prepared activations, us, before -> split-K): 5120 x 17408 2 tokens 31.2 -> 21.0, 4 tokens
-// 53.0 -> 28.1; 6144 x 16384 28.9 -> 21.3 and 51.7 -> 29.7; 4096 x 14336 4 tokens 27.8 -> 20.5, 8
-// tokens 34.3 -> 31.4; 2048 x 16384 4 / 8 tokens 32.3 -> 18.2 and 36.4 -> 23.2.  It loses at one
-// token (two launches: 4096 x 14336 8.9 -> 15.4), at two tokens below 5120 rows, from eight
-// tokens above 4096 rows and at sixteen (12288 x 8192 30.1 -> 68.3); the terms it stores grow
-// with tokens x units x terms per unit, so the other formats (Q8_0 4 terms per unit: 5120 x
-// 17408 16 tokens 37.5 -> 165.2; PQ2 4 tokens 27.7 -> 35.2) and the pinned order (9 terms)
-// keep their kernels.  Shorter rows (32 to 63 units) take it on up to half a tile per CU, at
-// two or three tokens, and at four from 48 units (5120 x 6144, 2 / 4 tokens 14.2 -> 11.7 and
-// 21.3 -> 13.9; 6144 x 5120 2 tokens 13.1 -> 11.3; at 8 tokens prepared input gains, 21.0 ->
-// 18.6, but f32 input loses, 23.5 -> 24.4), and two or three tokens on one to two tiles per
-// CU, where the quad-split
-// kernel's one workgroup per tile runs in two rounds (17408 x 5120 25.0 -> 16.0 and 18.9;
-// 24576 x 5120 25.3 -> 20.0 and 23.6); between half a tile and one tile per CU that kernel
-// stays ahead (10240 x 5120 4 tokens 13.4 against 16.3).
-constexpr uint32_t kSplitKUnits = 4, kSplitKMinUnits = 32;
+// (prepared activations, us, before -> split-K): 5120 x 17408 2 / 4 / 8 tokens 31.2 -> 21.0,
+// 53.0 -> 28.1, 43.1 -> 35.3; 6144 x 16384 8 tokens 40.4 -> 35.4; 4096 x 14336 4 tokens 27.8 ->
+// 20.5; 2048 x 16384 4 tokens 32.3 -> 18.2; 5120 x 6144 2 / 8 tokens 14.2 -> 11.7, 20.1 ->
+// 17.7; 17408 x 5120 2 / 4 tokens 25.0 -> 16.0, 25.5 -> 20.3, where the quad-split kernel's
+// one workgroup per tile runs in two rounds.  Rows under 64 units take it up to three tokens
+// (four from 48 units): with f32 input the separate quantizing launch outweighs the gain from
+// eight tokens (6144 x 5120 21.2 -> 23.4).  It loses at one token (two launches: 4096 x
+// 14336 8.8 -> 12.8), at two tokens on small matrices (2048 x 8192 10.4 -> 12.1), from five
+// tokens above half a tile per CU (12288 x 8192 8 tokens 29.1 -> 32.8), at sixteen (5120 x
+// 17408 43.5 -> 67.8), and between half a tile and one tile per CU on rows under 64 units,
+// where the quad-split kernel fits one round (10240 x 5120 4 tokens 13.4 against 16.3).  The
+// terms it stores grow with tokens x units x terms per unit, so the other formats (Q8_0 4
+// terms per unit: 5120 x 17408 16 tokens 37.5 -> 165.2; PQ2 4 tokens 27.7 -> 35.2) and the
+// pinned order (9 terms) keep their kernels.
+constexpr uint32_t kSplitKUnits = 4, kSplitKMinUnits = 40;
 
 size_t splitk_scratch(const MatvecArgs &a) {
     const uint64_t rp = (a.rows + kTile - 1) / kTile * kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
@@ -3194,15 +3193,18 @@ bool splitk_eligible(const MatvecArgs &a) {
     const uint64_t tiles = (a.rows + kTile - 1) / kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
     if (nu < kSplitKMinUnits || !fold_rows<Op::PTQ1_SRC>(static_cast<uint32_t>(nu))) return false;
     const uint32_t n = a.tokens;
-    bool take = false;
-    if (tiles >= 2ull * a.cus)
+    const bool half = 2 * tiles <= a.cus;  // at most half a tile per CU
+    bool take;
+    if (n < 2 || n > 8 || tiles >= 2ull * a.cus)
         take = false;
     else if (tiles > a.cus)
-        take = n >= 2 && n <= 3;
+        take = n <= 4;
+    else if (n == 2 && nu >= 64)
+        take = a.rows >= 5120;
     else if (nu >= 64)
-        take = n == 2 ? a.rows >= 5120 : n >= 3 && (n <= 4 || (n <= 8 && a.rows <= 4096));
-    else
-        take = 2 * tiles <= a.cus && n >= 2 && (n <= 3 || (n <= 4 && nu >= 48));
+        take = n <= 4 || half;
+    else  // shorter rows: f32 input pays a separate quantizing launch here (6144 x 5120, 8 tokens, 21.2 -> 23.4)
+        take = half && (n <= 3 || (n == 4 && nu >= 48));
     return take && splitk_scratch(a) <= a.scratch_cap;
 }
 

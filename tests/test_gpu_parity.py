@@ -519,7 +519,8 @@ def test_gpu_skinny_batch_matches_per_token_oracle(ctx, kind, cols, rows):
 
 @pytest.mark.parametrize("rows,cols,tokens", [(5120 + 37, 17408, 2), (2048 + 5, 8192, 3), (2048 + 5, 8192, 4),
                                               (4096 - 3, 8192, 8), (1000, 16384, 6), (17408 + 37, 5120, 2),
-                                              (17408 + 37, 5120, 3), (5120 + 3, 6144, 4), (6144 + 5, 5120, 3)])
+                                              (17408 + 37, 5120, 4), (5120 + 3, 6144, 4), (6144 + 5, 5120, 3),
+                                              (5120 + 37, 17408, 8)])
 def test_gpu_splitk_long_rows_match_oracle(ctx, rows, cols, tokens):
     """Long PTQ1 rows on few tiles at two to eight tokens (source order) take the two-pass
     split-K: one wavefront per (tile, four units) stores each unit's term per (token, row) in
