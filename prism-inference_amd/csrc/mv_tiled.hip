@@ -3165,7 +3165,7 @@ int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
 }
 
 // Long rows on few tiles take the two-pass split-K (k_mv_terms + k_mv_fold) for source-order
-// PTQ1 (prepared Q8_0 blocks, one term per unit) at two to eight tokens, where the other paths
+// PTQ1 (prepared Q8_0 blocks, one term per unit; PQ2 below) at two to eight tokens, where the other paths
 // run token by token or leave the skinny kernel's 16-token width mostly empty.  Measured
 // (prepared activations, us, before -> split-K): 5120 x 17408 2 / 4 / 8 tokens 31.2 -> 21.0,
 // 53.0 -> 28.1, 43.1 -> 35.3; 6144 x 16384 8 tokens 40.4 -> 35.4; 4096 x 14336 4 tokens 27.8 ->
@@ -3179,19 +3179,33 @@ int launch_quad_split(const MatvecArgs &a, uint32_t act_stride) {
 // 17408 43.5 -> 67.8), and between half a tile and one tile per CU on rows under 64 units,
 // where the quad-split kernel fits one round (10240 x 5120 4 tokens 13.4 against 16.3).  The
 // terms it stores grow with tokens x units x terms per unit, so the other formats (Q8_0 4
-// terms per unit: 5120 x 17408 16 tokens 37.5 -> 165.2; PQ2 4 tokens 27.7 -> 35.2) and the
-// pinned order (9 terms) keep their kernels.
+// terms per unit: 5120 x 17408 16 tokens 37.5 -> 165.2) and the pinned orders (PTQ1 9 terms,
+// fused PQ2 2) keep their kernels.
 constexpr uint32_t kSplitKUnits = 4, kSplitKMinUnits = 40;
 
+// Both users (source PTQ1, unfused PQ2) have 128-weight units and one term per unit.
+static_assert(unit_weights<Op::PTQ1_SRC>() == unit_weights<Op::PQ2_UNFUSED>() &&
+              terms_per_unit<Op::PTQ1_SRC>() == 1 && terms_per_unit<Op::PQ2_UNFUSED>() == 1, "split-K terms layout");
 size_t splitk_scratch(const MatvecArgs &a) {
     const uint64_t rp = (a.rows + kTile - 1) / kTile * kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
     return a.tokens * nu * terms_per_unit<Op::PTQ1_SRC>() * rp * sizeof(float);
 }
 
+// PQ2 in the unfused order (Q8_K activations, one term per unit) takes it at two tokens from
+// 5120 rows, where it otherwise runs token by token (prepared, us: 5120 x 17408 27.5 -> 19.4,
+// 6144 x 16384 25.5 -> 20.1; the reference's case with f32 input 31.0 -> 23.1).  From three
+// tokens its skinny kernel stays ahead with f32 input, whose quantizing launch split-K adds to
+// (4096 x 14336, 4 tokens: 25.0 against 26.6; prepared 22.2 against 21.1).
+static bool splitk_pq2(const MatvecArgs &a, uint64_t tiles, uint64_t nu) {
+    return a.act_format == kActQ8K && !a.pinned && tiles < a.cus && nu >= 64 && a.tokens == 2 && a.rows >= 5120;
+}
+
 bool splitk_eligible(const MatvecArgs &a) {
-    if (a.kind != kPTQ1 || a.act_format != kActQ8 || a.pinned || a.w2 || a.tile_best) return false;
+    if ((a.kind != kPTQ1 && a.kind != kPQ2) || a.w2 || a.tile_best) return false;
     const uint64_t tiles = (a.rows + kTile - 1) / kTile, nu = a.cols / unit_weights<Op::PTQ1_SRC>();
     if (nu < kSplitKMinUnits || !fold_rows<Op::PTQ1_SRC>(static_cast<uint32_t>(nu))) return false;
+    if (a.kind == kPQ2) return splitk_pq2(a, tiles, nu) && splitk_scratch(a) <= a.scratch_cap;
+    if (a.act_format != kActQ8 || a.pinned) return false;
     const uint32_t n = a.tokens;
     const bool half = 2 * tiles <= a.cus;  // at most half a tile per CU
     bool take;
@@ -3287,7 +3301,9 @@ int launch_matvec_tiled(const MatvecArgs &a) {
     const size_t in_stride = a.act_format == kActF32 ? sizeof(float) * a.cols
                              : a.act_format == kActQ8K ? sizeof(Q8KBlock) * ((a.cols + 255) / 256)
                                                        : sizeof(Q8Block) * (a.cols / 32);
-    if (splitk_eligible(a)) return launch_splitk<Op::PTQ1_SRC>(a, static_cast<uint32_t>(in_stride));
+    if (splitk_eligible(a))
+        return a.kind == kPQ2 ? launch_splitk<Op::PQ2_UNFUSED>(a, static_cast<uint32_t>(in_stride))
+                              : launch_splitk<Op::PTQ1_SRC>(a, static_cast<uint32_t>(in_stride));
     const bool batched = a.act_format != kActF32 && !token_by_token(a);
     if (batched && gemm_eligible(a)) {
         if (!a.scratch || a.scratch_bytes < prefill_scratch_bytes(a.kind, a.cols, a.tokens)) return -2;

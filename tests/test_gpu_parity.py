@@ -544,6 +544,29 @@ def test_gpu_splitk_long_rows_match_oracle(ctx, rows, cols, tokens):
     ctx.release(wid)
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [(5120 + 37, 17408, 2), (6144 + 5, 16384, 2), (4096 - 3, 14336, 3)])
+def test_gpu_splitk_pq2_matches_oracle(ctx, rows, cols, tokens):
+    """Long PQ2 rows on few tiles with Q8_K activations in the unfused order take the two-pass
+    split-K at two tokens from 5120 rows; the fused order and three tokens keep their kernels.  Prepared blocks in both orders and f32 input equal the oracle's
+    per-token matvec bit for bit."""
+    import oracle
+
+    w = synth.pq2_weights(rows, cols, rows + tokens, 4)
+    wid = ctx.weight(ph.KIND_PQ2, cols, rows, w)
+    X = synth.activations(cols, seed=tokens + 3, tokens=tokens).reshape(tokens, cols)
+    nq8k = cols // 256
+    for fused in (False, True):
+        act = np.concatenate([oracle.quantize_q8k(X[t], fused) for t in range(tokens)])
+        ref = np.stack([oracle.project_q8k(ph.KIND_PQ2, cols, rows, w, act[t * nq8k:(t + 1) * nq8k], fused,
+                                           threads=THREADS) for t in range(tokens)])
+        got = ctx.project_q8k(wid, rows, act.view(ph.Q8K_DTYPE), tokens=tokens, fused=fused)
+        assert_bits_equal(got, ref, f"split-K PQ2 prepared {rows}x{cols} tokens={tokens} fused={fused}")
+    ref = oracle.prefill(ph.KIND_PQ2, cols, rows, w, X, False, threads=THREADS)
+    assert_bits_equal(ctx.project_f32(wid, rows, X, tokens=tokens), ref, f"split-K PQ2 f32 {rows}x{cols} tokens={tokens}")
+    assert not ctx.faulted
+    ctx.release(wid)
+
+
 @pytest.mark.parametrize("kind,rows,cols,tokens", [(ph.KIND_PTQ1, 200, 1024, 40), (ph.KIND_PTQ1, 6144 + 37, 512, 100),
                                                    (ph.KIND_Q8_0, 300, 512, 70), (ph.KIND_Q2_K, 300, 512, 70),
                                                    (ph.KIND_PQ2, 300, 512, 70), (ph.KIND_TQ1_0, 300, 512, 70),
