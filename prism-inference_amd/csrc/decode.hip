@@ -29,6 +29,11 @@ constexpr uint32_t kValueDims = 16;     // dimensions per value workgroup
 constexpr uint32_t kValueGroups = 256;  // position groups per value workgroup (x kValueDims/4 threads)
 constexpr uint32_t kMaxTokens = 8192;   // KV cache positions the value kernel's LDS allows
 
+// Score maxima slots per head: one per wavefront (16 positions) of each score workgroup.
+__host__ __device__ constexpr uint32_t maxima_slots(uint32_t max_tokens) {
+    return 4u * ((max_tokens + kScoreChunk - 1u) / kScoreChunk);
+}
+
 __device__ __forceinline__ uint16_t f16_bits(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
@@ -107,7 +112,9 @@ __device__ __forceinline__ bool pow2(uint32_t v) { return v != 0 && (v & (v - 1u
 // workgroup of every KV head appends the current key and value to the binary16
 // caches, and the four lanes of quad t score position chunk*64 + t <= pos (a quarter
 // of the dimensions each): f16_dot(q, k) * (1/sqrt(head)) with the current key taken
-// from LDS.  Every global
+// from LDS.  Each wavefront also leaves the largest of its 16 scores (-inf for none) in
+// maxima[head][4 * chunk + wavefront], so the softmax needs no workgroup-wide maximum.
+// Every global
 // read that does not depend on another (the cached key row, the head inputs, norm
 // weights, RoPE factors, the value to append) is issued before the first is used.
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
@@ -171,6 +178,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
         p.vcache[at] = f16_bits(v);
     }
     const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(kHead));
+    float smax = -__builtin_inff();
     if (t <= pos) {  // uniform over a quad
         // The terms are binary16 x binary16 products, exact in binary32, summed in
         // binary64: four partial sums per lane, then the quad's four lanes.  Only the
@@ -197,8 +205,14 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
         double d = (s[0] + s[1]) + (s[2] + s[3]);
         d += dpp_d<kDppXor1>(d);
         d += dpp_d<kDppXor2>(d);
-        if (part == 0) p.scores[static_cast<size_t>(h) * p.max_tokens + t] = static_cast<float>(d) * scale;
+        smax = static_cast<float>(d) * scale;
+        if (part == 0) p.scores[static_cast<size_t>(h) * p.max_tokens + t] = smax;
     }
+    // Every lane of the workgroup is still here (the returns above are uniform).  fmaxf
+    // passes over a NaN score; the softmax total then reports it.
+    smax = wave_max(smax);
+    if ((tid & 63u) == 0)
+        p.maxima[static_cast<size_t>(h) * maxima_slots(p.max_tokens) + 4u * chunk + (tid >> 6)] = smax;
     if (e) raise_error(p.err, e);  // any element: an overflow can hit one element only
 }
 
@@ -209,7 +223,10 @@ constexpr uint32_t kValueAhead = 8;
 
 // Grid (heads, kHead / kValueDims), 1024 threads; SPT scores per thread
 // (SPT * 1024 >= max_tokens).  softmax_round_f16 (src/kernels.rs:4431-4462) of the
-// head's pos+1 scores -- every workgroup recomputes it -- then source_value_tile
+// head's pos+1 scores -- every workgroup recomputes it; each wavefront takes the maximum
+// from the score kernel's per-wavefront maxima itself, and the reference's refusal of a
+// NaN or +inf score or a -inf maximum shows as a non-finite total (each such case puts a
+// NaN into the sum, and otherwise the total lies in [1, pos+1]) -- then source_value_tile
 // (src/kernels.rs:2971-3011) for this workgroup's kValueDims dimensions:
 // out[d] = sum_t p_t v_t[d] in binary64.  Each term is a binary16 x binary16
 // product, exact in binary32, and a binary64 sum of such terms is exact unless they
@@ -220,7 +237,6 @@ constexpr uint32_t kValueAhead = 8;
 // waited for, so the kernel's inputs arrive in one memory round trip.
 template <uint32_t SPT>
 __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
-    __shared__ float redf[16];
     __shared__ double redd[16];
     __shared__ float prob[kMaxTokens];
     __shared__ double acc[16][kValueDims];
@@ -247,8 +263,18 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
         const uint32_t i = tid + k * 1024u;
         sv[k] = sc[i < last ? i : last];
     }
+    // The head's score maxima: 4 per 64 positions, at most 64 * SPT; slots past the
+    // position hold stale values and are masked below.
+    const uint32_t slots = maxima_slots(p.max_tokens);
+    const float *mxs = p.maxima + static_cast<size_t>(h) * slots;
+    float mx[SPT];
+#pragma unroll
+    for (uint32_t k = 0; k < SPT; ++k) {
+        const uint32_t i = lane + 64u * k;
+        mx[k] = mxs[i < slots ? i : slots - 1u];
+    }
     const uint32_t pos = vector_load(&p.state->pos);
-    // Scores and position first: memory counters complete in issue order, and the
+    // Scores, maxima and position first: memory counters complete in issue order, and the
     // softmax must not wait for the value rows.
     __builtin_amdgcn_sched_barrier(0);
     // Thread (g, q): positions g, g+128, ... of dimensions d0+4q .. d0+4q+3.
@@ -265,24 +291,12 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     // value loads below it, after the wait for the position.)
     const bool ok = pos < p.max_tokens;
     const uint32_t n = ok ? pos + 1 : 1;
+    const uint32_t live = 4u * ((n - 1u) / kScoreChunk + 1u);  // the slots of chunks 0 .. pos/64
     float m = -__builtin_inff();
-    bool bad = false;
 #pragma unroll
-    for (uint32_t k = 0; k < SPT; ++k) {
-        if (tid + k * 1024u < n) {
-            bad |= (sv[k] != sv[k]) || sv[k] == __builtin_inff();
-            m = fmaxf(m, sv[k]);
-        }
-    }
+    for (uint32_t k = 0; k < SPT; ++k)
+        if (lane + 64u * k < live) m = fmaxf(m, mx[k]);
     m = wave_max(m);
-    if (lane == 0) redf[wave] = m;
-    __syncthreads();
-    m = redf[0];
-    for (uint32_t v = 1; v < nw; ++v) m = fmaxf(m, redf[v]);
-    if (__syncthreads_or(bad) || !finite(m)) {
-        if (tid == 0 && slice == 0 && ok) raise_error(p.err, kErrNonfinite);
-        return;
-    }
     double tot = 0.0;
 #pragma unroll
     for (uint32_t k = 0; k < SPT; ++k) {
@@ -297,6 +311,10 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     __syncthreads();
     tot = 0.0;
     for (uint32_t v = 0; v < nw; ++v) tot += redd[v];
+    if (!__builtin_isfinite(tot)) {  // uniform
+        if (tid == 0 && slice == 0 && ok) raise_error(p.err, kErrNonfinite);
+        return;
+    }
     const float inv = static_cast<float>(1.0 / tot);
 #pragma unroll
     for (uint32_t k = 0; k < SPT; ++k) {
@@ -500,6 +518,8 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_embed(const TileBest 
 }
 
 }  // namespace
+
+uint32_t attn_maxima_per_head(uint32_t max_tokens) { return maxima_slots(max_tokens); }
 
 size_t argmax_scratch_bytes(uint64_t vocab) { return sizeof(TileBest) * ((vocab + kTile - 1) / kTile); }
 

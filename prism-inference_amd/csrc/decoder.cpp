@@ -35,7 +35,7 @@ struct prism_hip_decoder {
     prism_weight_id lm_head = 0;
     float *output_norm = nullptr;
     float *hidden[2] = {nullptr, nullptr};
-    float *qkv = nullptr, *att = nullptr, *scores = nullptr, *logits = nullptr;
+    float *qkv = nullptr, *att = nullptr, *scores = nullptr, *maxima = nullptr, *logits = nullptr;
     void *ffn_q8 = nullptr;  // the SwiGLU vector's Q8_0 blocks
     float *logits_all = nullptr;
     size_t logits_all_steps = 0;
@@ -147,6 +147,7 @@ AttnArgs attn_args(prism_hip_decoder *d) {
     AttnArgs at{};
     at.qkv = d->qkv;
     at.scores = d->scores;
+    at.maxima = d->maxima;
     at.out = d->att;
     at.state = d->state;
     at.heads = static_cast<uint32_t>(g.heads);
@@ -354,6 +355,9 @@ prism_hip_decoder *prism_hip_decoder_create(prism_hip_ctx *c, const prism_decode
     if (!rc) rc = dalloc(d, &d->att, sizeof(float) * g->heads * D);
     if (!rc) rc = dalloc(d, &d->ffn_q8, sizeof(prism_q8_block) * (g->ffn / 32));
     if (!rc) rc = dalloc(d, &d->scores, sizeof(float) * g->heads * g->max_tokens);
+    if (!rc)
+        rc = dalloc(d, &d->maxima,
+                    sizeof(float) * g->heads * attn_maxima_per_head(static_cast<uint32_t>(g->max_tokens)));
     if (!rc) rc = dalloc(d, &d->logits, sizeof(float) * g->vocab);
     if (!rc) rc = dalloc(d, &d->lm_act, sizeof(prism_q8_block) * (H / 32));
     if (!rc) rc = dalloc(d, &d->state, sizeof(DecodeState));

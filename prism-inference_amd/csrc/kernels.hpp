@@ -141,6 +141,7 @@ struct AttnArgs {
     const float *q_norm, *k_norm;  // per-head RMSNorm weights [D]
     uint16_t *kcache, *vcache;   // binary16 [max_tokens][kv*D]
     float *scores;               // [heads][max_tokens]
+    float *maxima;               // [heads][attn_maxima_per_head(max_tokens)]: each score wavefront's largest
     float *out;                  // attended [heads*D]
     const DecodeState *state;
     uint32_t heads, kv_heads, head_dim, rope, max_tokens;
@@ -151,6 +152,9 @@ struct AttnArgs {
 // q/k norm + RoPE + KV append + scores, then softmax + values: two launches
 // (launch_attn_scores, then launch_attn_values).
 int launch_attention(const AttnArgs &a);
+// Slots of AttnArgs::maxima per head: one per 16-position wavefront of a 64-position score
+// workgroup.
+uint32_t attn_maxima_per_head(uint32_t max_tokens);
 int launch_attn_scores(const AttnArgs &a);
 int launch_attn_values(const AttnArgs &a);
 // Final RMSNorm + Q8_0 (source) quantization of n values into q8_out.

@@ -106,6 +106,32 @@ def test_gpu_decoder_full_width_matches_oracle(ctx):
     check_against_oracle(model, 1024, 1, toks, logits)
 
 
+@pytest.mark.parametrize("graph", [False, True])
+def test_gpu_decoder_nan_cached_key_is_refused(ctx, graph):
+    """A NaN element in a cached key makes that position's score NaN for the query heads
+    of its KV head: softmax_round_f16 refuses it (src/kernels.rs:4431-4462), so the step
+    reports NONFINITE and the outputs are zero-filled.  The same decoder then runs a
+    clean cache again."""
+    model = synth.decoder_model(7, kv_prefill=40, **SMALL)
+    layer = model["layers"][1]
+    clean = np.array(layer["k_prefill"], np.uint16, copy=True)
+    bad = clean.copy()
+    bad.reshape(40, -1)[17, 3] = 0x7E00  # binary16 NaN: position 17, KV head 0, dimension 3
+    layer["k_prefill"] = bad
+    dec = ph.Decoder(ctx, model, max_steps=8)
+    try:
+        with pytest.raises(ph.PrismError) as ei:
+            dec.generate(5, 40, 3, graph=graph, logits=True)
+        assert ei.value.code == ph.ERR_NONFINITE
+        layer["k_prefill"] = clean
+        dec.close()
+        dec = ph.Decoder(ctx, model, max_steps=8)
+        toks, logits, _ = dec.generate(5, 40, 3, graph=graph, logits=True)
+    finally:
+        dec.close()
+    check_against_oracle(model, 40, 5, toks, logits)
+
+
 def test_gpu_decoder_rejects_bad_arguments(ctx):
     model = synth.decoder_model(6, kv_prefill=8, **SMALL)
     dec = ph.Decoder(ctx, model, max_steps=4)
