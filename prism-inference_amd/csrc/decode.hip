@@ -257,10 +257,17 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     const uint32_t kh = h / group, kw = p.kv_heads * kHead;
     const uint32_t last = p.max_tokens - 1;
     const float *sc = p.scores + static_cast<size_t>(h) * p.max_tokens;
+    // Thread (g, q) sums positions g, g + kValueGroups, ... of dimensions d0+4q .. d0+4q+3, and
+    // takes the softmax of positions g + kValueGroups * (q + kQuads * j): the probability of
+    // its k-th value position is then held by lane q = k % kQuads of its own quad (register
+    // k / kQuads) and reaches it by a DPP broadcast instead of an LDS round trip.
+    constexpr uint32_t kQuads = kValueDims / 4;
+    static_assert(kQuads == 4 && kValueAhead % kQuads == 0, "quad broadcast below");
+    const uint32_t g = tid / kQuads, q = tid % kQuads;
     float sv[SPT];
 #pragma unroll
     for (uint32_t k = 0; k < SPT; ++k) {
-        const uint32_t i = tid + k * 1024u;
+        const uint32_t i = g + kValueGroups * (q + kQuads * k);
         sv[k] = sc[i < last ? i : last];
     }
     // The head's score maxima: 4 per 64 positions, at most 64 * SPT; slots past the
@@ -277,8 +284,6 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     // Scores, maxima and position first: memory counters complete in issue order, and the
     // softmax must not wait for the value rows.
     __builtin_amdgcn_sched_barrier(0);
-    // Thread (g, q): positions g, g+128, ... of dimensions d0+4q .. d0+4q+3.
-    const uint32_t g = tid / (kValueDims / 4), q = tid % (kValueDims / 4);
     const uint16_t *vb = p.vcache + kh * kHead + d0 + 4 * q;
     uint2 w[kValueAhead];
 #pragma unroll
@@ -300,7 +305,7 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     double tot = 0.0;
 #pragma unroll
     for (uint32_t k = 0; k < SPT; ++k) {
-        if (tid + k * 1024u < n) {
+        if (g + kValueGroups * (q + kQuads * k) < n) {
             const float e = exp_f32(sv[k] - m);
             sv[k] = e;
             tot += static_cast<double>(e);
@@ -316,12 +321,18 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
         return;
     }
     const float inv = static_cast<float>(1.0 / tot);
+    // Contexts past the kValueAhead * kValueGroups positions held in registers also stage
+    // every probability in LDS for the loop below.
+    constexpr bool kLong = SPT * 1024u > kValueAhead * kValueGroups;
+    float pr[SPT];
 #pragma unroll
     for (uint32_t k = 0; k < SPT; ++k) {
-        const uint32_t i = tid + k * 1024u;
-        if (i < n) prob[i] = round_f16(sv[k] * inv);
+        const uint32_t i = g + kValueGroups * (q + kQuads * k);
+        pr[k] = i < n ? round_f16(sv[k] * inv) : 0.0f;
+        if constexpr (kLong)
+            if (i < n) prob[i] = pr[k];
     }
-    __syncthreads();
+    if constexpr (kLong) __syncthreads();
     double a[4] = {0.0, 0.0, 0.0, 0.0};
     auto accumulate = [&](const uint2 &r, float pr) {
         a[0] += static_cast<double>(pr * h2f(r.x & 0xffffu));
@@ -332,25 +343,33 @@ __global__ __launch_bounds__(1024) void k_attn_values(AttnArgs p) {
     // Rows past the position (stale cache rows) are zeroed here, where they are first
     // used: zeroing them earlier would wait for these loads before the softmax.
 #pragma unroll
-    for (uint32_t k = 0; k < kValueAhead; ++k) {
-        const uint32_t i = g + k * kValueGroups;
-        const bool in = i < n;
-        accumulate(in ? w[k] : make_uint2(0, 0), in ? prob[i] : 0.0f);
+    for (uint32_t j = 0; j < kValueAhead / kQuads; ++j) {
+        // Positions of register j >= SPT lie past the cache (>= SPT * 1024 > n - 1).
+        const float v = j < SPT ? pr[j < SPT ? j : 0] : 0.0f;
+        const float b[kQuads] = {dpp_f<0x00>(v), dpp_f<0x55>(v), dpp_f<0xAA>(v), dpp_f<0xFF>(v)};
+#pragma unroll
+        for (uint32_t qq = 0; qq < kQuads; ++qq) {
+            const uint32_t k = kQuads * j + qq, i = g + k * kValueGroups;
+            const bool in = i < n;
+            accumulate(in ? w[k] : make_uint2(0, 0), in ? b[qq] : 0.0f);
+        }
     }
     // Longer contexts: the remaining positions, eight rows loaded per batch before any
     // is used.
-    for (uint32_t i0 = g + kValueAhead * kValueGroups; i0 < n; i0 += 8 * kValueGroups) {
-        uint2 r[8];
-        float pr[8];
+    if constexpr (kLong) {
+        for (uint32_t i0 = g + kValueAhead * kValueGroups; i0 < n; i0 += 8 * kValueGroups) {
+            uint2 r[8];
+            float pv[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t i = i0 + k * kValueGroups;
-            const bool in = i < n;
-            r[k] = in ? *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i) * kw) : make_uint2(0, 0);
-            pr[k] = in ? prob[i] : 0.0f;
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t i = i0 + k * kValueGroups;
+                const bool in = i < n;
+                r[k] = in ? *reinterpret_cast<const uint2 *>(vb + static_cast<size_t>(i) * kw) : make_uint2(0, 0);
+                pv[k] = in ? prob[i] : 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) accumulate(r[k], pv[k]);
         }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) accumulate(r[k], pr[k]);
     }
     // A wavefront holds sixteen groups of the same four quads (lane = 4 * group + quad):
     // fold them with row rotations by 4 and 8 (DPP) and shuffles across rows, then the

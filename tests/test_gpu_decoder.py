@@ -73,6 +73,19 @@ def test_gpu_decoder_small_matches_oracle(ctx, seed, prefill):
     check_against_oracle(model, prefill, 7, toks, logits)
 
 
+@pytest.mark.parametrize("max_tokens,prefill", [(2500, 2100), (4200, 4000)])
+def test_gpu_decoder_long_cache_matches_oracle(ctx, max_tokens, prefill):
+    """Caches longer than 2048 positions: the value kernel's four- and eight-score-per-thread
+    forms, whose positions past 2048 take their probabilities from LDS."""
+    model = synth.decoder_model(8, kv_prefill=prefill, **dict(SMALL, max_tokens=max_tokens))
+    dec = ph.Decoder(ctx, model, max_steps=4)
+    try:
+        toks, logits, _ = dec.generate(3, prefill, 3, graph=True, logits=True)
+    finally:
+        dec.close()
+    check_against_oracle(model, prefill, 3, toks, logits)
+
+
 def test_gpu_decoder_graph_replay_equals_eager(ctx):
     """The captured graph (position and token read from device memory) gives the same
     bits as launching every kernel each step, on a second generate as well."""
