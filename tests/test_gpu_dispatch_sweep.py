@@ -30,14 +30,20 @@ TOKENS = [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 48, 64, 100, 130, 300]
 MAX_WORK = 3e8  # rows * cols * tokens per case
 
 
-def _cases(n: int = 160, seed: int = 20261202):
+# Wide rows (the reference's MUL_MAT widths among them): the split-K, token-by-token and
+# quad-split regions, with more token counts between the batch kernels' thresholds.
+COLS_WIDE = [5120, 6144, 12288, 14336, 17408]
+TOKENS_WIDE = TOKENS + [6, 7, 9, 12, 20, 40, 65, 96]
+
+
+def _cases(n: int = 160, seed: int = 20261202, cols_list=COLS, tokens_list=TOKENS):
     rng = np.random.default_rng(seed)
     out = []
     while len(out) < n:
         kind = KINDS[int(rng.integers(len(KINDS)))]
         rows = ROWS[int(rng.integers(len(ROWS)))]
-        cols = COLS[int(rng.integers(len(COLS)))]
-        tokens = TOKENS[int(rng.integers(len(TOKENS)))]
+        cols = cols_list[int(rng.integers(len(cols_list)))]
+        tokens = tokens_list[int(rng.integers(len(tokens_list)))]
         if cols % synth.LAYOUT[kind][0] or rows * cols * tokens > MAX_WORK:
             continue
         out.append((kind, rows, cols, tokens, bool(rng.integers(2))))
@@ -51,7 +57,8 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("kind,rows,cols,tokens,pinned", _cases())
+@pytest.mark.parametrize("kind,rows,cols,tokens,pinned",
+                         _cases() + _cases(100, 20261203, COLS_WIDE, TOKENS_WIDE))
 def test_gpu_dispatch_sweep_matches_oracle(ctx, kind, rows, cols, tokens, pinned):
     import oracle
 
