@@ -50,41 +50,39 @@ __device__ __forceinline__ void rope_freqs(DecodeState *st, uint32_t pos, const 
     st->sn[i] = sin_f32(angle);
 }
 
-// rms_norm_rope_round_f16_into::<false> (src/kernels.rs:3679-3733) of two heads at
-// once: threads 0..127 take the query head, threads 128..255 the KV head's key, one
-// element each (x, the norm weight w and the element's RoPE pair cos/sin already
-// loaded).  Per head: binary64 sum of the binary32 squares (wavefront butterfly,
-// then the two wavefronts in order), mean rounded to binary32, 1/sqrt(mean + eps),
-// (x * scale) * w, rotation of the first `rope` dimensions (element i with i + rope/2),
-// rounding to binary16.  The results land in dst[0] (query) and dst[1] (key).
-// Returns the thread's error bits.
-__device__ int norm_rope_pair(float x, float w, float c, float sn, uint32_t rope, float eps,
-                              float (*dst)[kHead], float (*tmp)[kHead], double *red) {
-    const uint32_t tid = threadIdx.x, which = tid >> 7, d = tid & (kHead - 1);
-    const double s = wave_sum(static_cast<double>(x * x));
-    if ((tid & 63u) == 0) red[tid >> 6] = s;
-    __syncthreads();
-    const double t = (0.0 + red[2 * which]) + red[2 * which + 1];
-    const float mean = static_cast<float>(t / static_cast<double>(kHead));
-    float scale = 1.0f / __builtin_sqrtf(mean + eps);
-    scale = (finite(scale) && scale > 0.0f) ? scale : 0.0f;
-    int e = scale == 0.0f ? kErrNonfinite : 0;
-    const float v = (x * scale) * w;
-    tmp[which][d] = v;
-    if (!finite(v)) e |= kErrNonfinite;
-    __syncthreads();
-    const uint32_t half = rope / 2;
-    float r;
-    if (d < half)
-        r = tmp[which][d] * c - tmp[which][d + half] * sn;
-    else if (d < rope)
-        r = tmp[which][d - half] * sn + tmp[which][d] * c;
-    else
-        r = tmp[which][d];
-    if (!finite(r)) e |= kErrNonfinite;
-    r = round_f16(r);
-    if (!finite(r)) e |= kErrNonfinite;
-    dst[which][d] = r;
+// rms_norm_rope_round_f16_into::<false> (src/kernels.rs:3679-3733) of two heads, one
+// wavefront each: wavefront 0 takes the query head, wavefront 1 the KV head's key
+// (wavefronts 2 and 3 only meet the closing barrier).  Lane l holds two elements of its
+// head, the rotation pair (l, l + rope/2) when l < rope/2 and else (2l, 2l + 1), both past
+// the rotated dimensions (x, the norm weights w and the pair's cos/sin already loaded), so
+// the sum of squares is one wavefront butterfly and the rotation stays in the lane.  Per
+// head: binary64 sum of the binary32 squares, mean rounded to binary32, 1/sqrt(mean + eps),
+// (x * scale) * w, the rotation (x_a c - x_b s, x_a s + x_b c), rounding to binary16.  The
+// results land in dst[0] (query) and dst[1] (key).  Returns the thread's error bits.
+__device__ int norm_rope_wave(const float (&x)[2], const float (&w)[2], float c, float sn, bool rot, uint32_t ia,
+                              uint32_t ib, float eps, float (*dst)[kHead]) {
+    const uint32_t wave = threadIdx.x >> 6;
+    int e = 0;
+    if (wave < 2) {  // wave-uniform
+        const double s = wave_sum(static_cast<double>(x[0] * x[0]) + static_cast<double>(x[1] * x[1]));
+        const float mean = static_cast<float>(s / static_cast<double>(kHead));
+        float scale = 1.0f / __builtin_sqrtf(mean + eps);
+        scale = (finite(scale) && scale > 0.0f) ? scale : 0.0f;
+        if (scale == 0.0f) e = kErrNonfinite;
+        const float va = (x[0] * scale) * w[0], vb = (x[1] * scale) * w[1];
+        if (!finite(va) || !finite(vb)) e |= kErrNonfinite;
+        float ra = va, rb = vb;
+        if (rot) {
+            ra = va * c - vb * sn;
+            rb = va * sn + vb * c;
+        }
+        if (!finite(ra) || !finite(rb)) e |= kErrNonfinite;
+        ra = round_f16(ra);
+        rb = round_f16(rb);
+        if (!finite(ra) || !finite(rb)) e |= kErrNonfinite;
+        dst[wave][ia] = ra;
+        dst[wave][ib] = rb;
+    }
     __syncthreads();
     return e;
 }
@@ -118,8 +116,7 @@ __device__ __forceinline__ bool pow2(uint32_t v) { return v != 0 && (v & (v - 1u
 // read that does not depend on another (the cached key row, the head inputs, norm
 // weights, RoPE factors, the value to append) is issued before the first is used.
 __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
-    __shared__ float hv[2][kHead], tmp[2][kHead];  // [0] query, [1] current key
-    __shared__ double red[4];
+    __shared__ float hv[2][kHead];  // [0] query, [1] current key
     const uint32_t tid = threadIdx.x, group = p.heads / p.kv_heads;
     uint32_t h = blockIdx.x, chunk = blockIdx.y, unit, member;
     const uint32_t lg_kv = __builtin_ctz(p.kv_heads), lg_group = __builtin_ctz(group);
@@ -134,14 +131,18 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
     // is waited for: the normalization's inputs first (memory counters complete in issue
     // order, so the norm waits only for these), then the cached key row of this
     // thread's position (row 0 past the cache, never used).
-    const uint32_t which = tid >> 7, d = tid & (kHead - 1);
-    const float x = p.qkv[which ? qw + kh * kHead + d : h * kHead + d];
+    // The norm's two elements of this lane (norm_rope_wave; wavefronts 2 and 3 read
+    // wavefront 0 and 1's and do not use them).
+    const uint32_t lane = tid & 63u, which = (tid >> 6) & 1u, half = p.rope / 2;
+    const bool rot = lane < half;
+    const uint32_t ia = rot ? lane : 2u * lane, ib = rot ? lane + half : 2u * lane + 1u;
+    const uint32_t base = which ? qw + kh * kHead : h * kHead;
+    const float x[2] = {p.qkv[base + ia], p.qkv[base + ib]};
     // Both norm weights are read: selecting the pointer per thread would read it from
     // the kernel-argument memory with a vector load, one more round trip.
-    const float qn = p.q_norm[d], kn = p.k_norm[d], nw = which ? kn : qn;
-    const uint32_t half = p.rope / 2, j = d < half ? d : d - half;
-    const bool rot = d < p.rope;
-    const float c = rot ? p.state->cs[j] : 1.0f, sn = rot ? p.state->sn[j] : 0.0f;
+    const float qa = p.q_norm[ia], qb = p.q_norm[ib], ka = p.k_norm[ia], kb = p.k_norm[ib];
+    const float nw[2] = {which ? ka : qa, which ? kb : qb};
+    const float c = rot ? p.state->cs[lane] : 1.0f, sn = rot ? p.state->sn[lane] : 0.0f;
     const bool append = h % group == 0 && chunk == 0 && tid < kHead;
     const float vin = append ? p.qkv[qw + kw + kh * kHead + tid] : 0.0f;
     constexpr uint32_t kPart = kHead / kScoreLanes;  // dimensions per lane
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs p) {
 
     // The norm needs no position; the exits come after it, so that no load above is
     // moved below them.
-    int e = norm_rope_pair(x, nw, c, sn, p.rope, p.eps, hv, tmp, red);
+    int e = norm_rope_wave(x, nw, c, sn, rot, ia, ib, p.eps, hv);
     if (pos >= p.max_tokens) {  // uniform: every workgroup leaves
         if (tid == 0 && h == 0 && chunk == 0) raise_error(p.err, kErrInput);
         return;
